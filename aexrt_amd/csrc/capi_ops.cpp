@@ -1,0 +1,456 @@
+// Op-level C ABI of libaexrt_hip.so: argument validation, host-side weight
+// repack, and dispatch of one hot-path kernel per call.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/aexrt_hip.h"
+#include "internal.h"
+#include "kernels.h"
+
+namespace aexrt {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+const char* last_error() { return g_last_error.c_str(); }
+
+bool check_hip(hipError_t e, const char* what) {
+    if (e == hipSuccess) return true;
+    set_error(std::string(what) + ": " + hipGetErrorString(e));
+    return false;
+}
+
+bool is_int8_algorithm(uint32_t a) { return a == 51u || a == 52u || a == 53u; }
+bool is_winograd_algorithm(uint32_t a) { return a == 40u || a == 46u; }
+
+static inline uint32_t round_up(uint32_t v, uint32_t m) { return (v + m - 1u) / m * m; }
+
+// Reference int8 eligibility, native/aexrt_d3d12_runtime.cpp:9399-9422, plus
+// in_channels % 16 == 0: amax is tracked per 16-channel group here, and the
+// reference itself only scans C/16 full groups (9406 + 21631-21640), so a
+// C % 16 tail would be quantized against a partial amax.
+bool can_use_int8(const AexrtConv2DDesc& d, uint32_t kernel_elems) {
+    if (d.groups != 1 || (d.in_channels % 4u) != 0 || (d.out_channels % 4u) != 0) return false;
+    if ((d.in_channels % 16u) != 0) return false;
+    if (kernel_elems == 1u) {
+        if (d.kernel_h != 1 || d.kernel_w != 1 || d.stride_h != 1 || d.stride_w != 1 || d.pad_top != 0 ||
+            d.pad_left != 0 || d.dilation_h != 1 || d.dilation_w != 1)
+            return false;
+        return (d.out_channels % 8u) == 0 && d.in_h == d.out_h && d.in_w == d.out_w;
+    }
+    if (kernel_elems == 9u) {
+        if (d.kernel_h != 3 || d.kernel_w != 3 || d.dilation_h != 1 || d.dilation_w != 1 || d.pad_top != 1 ||
+            d.pad_left != 1)
+            return false;
+        if (d.stride_h == 2 && d.stride_w == 2)
+            return d.in_h >= d.out_h * 2u - 1u && d.in_w >= d.out_w * 2u - 1u;
+        if (d.stride_h != 1 || d.stride_w != 1) return false;
+        return d.in_h == d.out_h && d.in_w == d.out_w;
+    }
+    return false;
+}
+
+uint32_t int8_kernel_elems(uint32_t algorithm) { return algorithm == 51u ? 1u : 9u; }
+
+bool winograd_shape_ok(const AexrtConv2DDesc& d) {
+    return d.kernel_h == 3 && d.kernel_w == 3 && d.stride_h == 1 && d.stride_w == 1 && d.pad_top == 1 &&
+           d.pad_left == 1 && d.dilation_h == 1 && d.dilation_w == 1 && d.groups == 1 &&
+           (d.in_channels % 4u) == 0 && (d.out_h % 2u) == 0 && (d.out_w % 2u) == 0 && d.in_h == d.out_h &&
+           d.in_w == d.out_w;
+}
+
+bool generic_shape_ok(const AexrtConv2DDesc& d) {
+    if (d.groups != 1 || d.dilation_h != 1 || d.dilation_w != 1) return false;
+    if (d.stride_h != d.stride_w || d.pad_top != d.pad_left || d.kernel_h == 0 || d.kernel_w == 0) return false;
+    const int64_t oh = ((int64_t)d.in_h + 2 * d.pad_top - d.kernel_h) / d.stride_h + 1;
+    const int64_t ow = ((int64_t)d.in_w + 2 * d.pad_left - d.kernel_w) / d.stride_w + 1;
+    return oh == d.out_h && ow == d.out_w;
+}
+
+WeightGeom weight_geom(const AexrtConv2DDesc& d, uint32_t algorithm) {
+    WeightGeom g{};
+    g.ocp = round_up(d.out_channels, 16u);
+    if (is_winograd_algorithm(algorithm)) {
+        g.kp = round_up(d.in_channels, 32u);
+        g.elem_bytes = 2;
+        g.nbytes = 16ull * g.ocp * g.kp * 2ull;
+    } else {
+        const uint32_t k = d.kernel_h * d.kernel_w * d.in_channels;
+        g.kp = round_up(k, 64u);
+        g.elem_bytes = is_int8_algorithm(algorithm) ? 1 : 2;
+        g.nbytes = (uint64_t)g.ocp * g.kp * g.elem_bytes;
+    }
+    return g;
+}
+
+// Half-away-from-zero round (std::round), the reference's weight rounding
+// (engine.py:2454-2455, native/aexrt_d3d12_runtime.cpp:21736).
+static inline float round_half_away(float v) { return std::round(v); }
+
+// Per output channel quantization of an fp32 weight (the runtime fallback of
+// native/aexrt_d3d12_runtime.cpp:21716-21741 for engines without layout 8).
+static void quantize_weight_host(const float* w, uint32_t oc, uint32_t per_oc, int8_t* q, float* scale) {
+    for (uint32_t o = 0; o < oc; ++o) {
+        const float* row = w + (uint64_t)o * per_oc;
+        float amax = 0.0f;
+        for (uint32_t i = 0; i < per_oc; ++i) amax = std::max(amax, std::fabs(row[i]));
+        const float s = amax > 0.0f ? amax / 127.0f : 1.0f;
+        const float inv = 1.0f / s;
+        scale[o] = s;
+        for (uint32_t i = 0; i < per_oc; ++i) {
+            float v = round_half_away(row[i] * inv);
+            v = std::min(127.0f, std::max(-127.0f, v));
+            q[(uint64_t)o * per_oc + i] = (int8_t)v;
+        }
+    }
+}
+
+static inline float half_bits_to_float(uint16_t h) {
+    _Float16 v;
+    std::memcpy(&v, &h, 2);
+    return (float)v;
+}
+static inline uint16_t float_to_half_bits(float f) {
+    _Float16 v = (_Float16)f;
+    uint16_t h;
+    std::memcpy(&h, &v, 2);
+    return h;
+}
+
+// Expands any supported source layout to fp32 [oc][ic][kh][kw].
+static bool source_to_f32(const AexrtConv2DDesc& d, uint32_t layout, const void* src, uint64_t nbytes,
+                          std::vector<float>& out) {
+    const uint32_t oc = d.out_channels, ic = d.in_channels, kk = d.kernel_h * d.kernel_w;
+    const uint64_t elems = (uint64_t)oc * ic * kk;
+    out.assign(elems, 0.0f);
+    if (layout == AEXRT_HIP_SRC_RAW_F32) {
+        if (nbytes < elems * 4) return false;
+        std::memcpy(out.data(), src, elems * 4);
+        return true;
+    }
+    const uint16_t* h = static_cast<const uint16_t*>(src);
+    if (layout == AEXRT_HIP_SRC_RAW_F16) {
+        if (nbytes < elems * 2) return false;
+        for (uint64_t i = 0; i < elems; ++i) out[i] = half_bits_to_float(h[i]);
+        return true;
+    }
+    if (layout == AEXRT_HIP_SRC_LAYOUT_OC4_F16) {  // [oc/4][ic][9][4]
+        if (kk != 9 || oc % 4 || nbytes < elems * 2) return false;
+        for (uint32_t o = 0; o < oc; ++o)
+            for (uint32_t c = 0; c < ic; ++c)
+                for (uint32_t k = 0; k < 9; ++k)
+                    out[((uint64_t)o * ic + c) * 9 + k] =
+                        half_bits_to_float(h[(((uint64_t)(o / 4) * ic + c) * 9 + k) * 4 + (o % 4)]);
+        return true;
+    }
+    if (layout == AEXRT_HIP_SRC_LAYOUT_OC8_F16) {  // [oc/8][ic][8]
+        if (kk != 1 || oc % 8 || nbytes < elems * 2) return false;
+        for (uint32_t o = 0; o < oc; ++o)
+            for (uint32_t c = 0; c < ic; ++c)
+                out[(uint64_t)o * ic + c] = half_bits_to_float(h[((uint64_t)(o / 8) * ic + c) * 8 + (o % 8)]);
+        return true;
+    }
+    return false;
+}
+
+}  // namespace aexrt
+
+using namespace aexrt;
+
+extern "C" {
+
+uint32_t aexrt_hip_abi_version(void) { return 1u; }
+
+const char* aexrt_hip_get_last_error(void) { return last_error(); }
+
+int aexrt_hip_can_use_conv_int8(const AexrtConv2DDesc* desc, uint32_t kernel_elems) {
+    return desc && can_use_int8(*desc, kernel_elems) ? 1 : 0;
+}
+
+int aexrt_hip_conv_weight_bytes(const AexrtConv2DDesc* desc, uint32_t algorithm, uint64_t* out_nbytes) {
+    if (!desc || !out_nbytes) {
+        set_error("conv_weight_bytes: null argument");
+        return 0;
+    }
+    *out_nbytes = weight_geom(*desc, algorithm).nbytes;
+    return 1;
+}
+
+int aexrt_hip_pack_conv_weight(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t src_layout,
+                               const void* src, uint64_t src_nbytes, void* dst, uint64_t dst_nbytes,
+                               float* scale_out) {
+    if (!desc || !src || !dst) {
+        set_error("pack_conv_weight: null argument");
+        return 0;
+    }
+    const AexrtConv2DDesc& d = *desc;
+    const WeightGeom g = weight_geom(d, algorithm);
+    if (dst_nbytes < g.nbytes) {
+        set_error("pack_conv_weight: destination too small");
+        return 0;
+    }
+    std::memset(dst, 0, g.nbytes);
+    const uint32_t oc = d.out_channels, ic = d.in_channels, kh = d.kernel_h, kw = d.kernel_w, kk = kh * kw;
+    if (is_int8_algorithm(algorithm)) {
+        if (!scale_out) {
+            set_error("pack_conv_weight: int8 needs scale_out");
+            return 0;
+        }
+        std::vector<int8_t> q((uint64_t)oc * ic * kk);
+        if (src_layout == AEXRT_HIP_SRC_LAYOUT_INT8) {
+            const uint64_t need = q.size() + 4ull * oc;
+            if (src_nbytes < need) {
+                set_error("pack_conv_weight: layout 8 payload too small");
+                return 0;
+            }
+            std::memcpy(q.data(), src, q.size());
+            std::memcpy(scale_out, static_cast<const uint8_t*>(src) + q.size(), 4ull * oc);
+        } else {
+            std::vector<float> w;
+            if (!source_to_f32(d, src_layout, src, src_nbytes, w)) {
+                set_error("pack_conv_weight: unsupported source layout for int8");
+                return 0;
+            }
+            quantize_weight_host(w.data(), oc, ic * kk, q.data(), scale_out);
+        }
+        int8_t* out = static_cast<int8_t*>(dst);
+        for (uint32_t o = 0; o < oc; ++o)
+            for (uint32_t c = 0; c < ic; ++c)
+                for (uint32_t k = 0; k < kk; ++k)
+                    out[(uint64_t)o * g.kp + (uint64_t)k * ic + c] = q[((uint64_t)o * ic + c) * kk + k];
+        return 1;
+    }
+    uint16_t* out = static_cast<uint16_t*>(dst);
+    if (is_winograd_algorithm(algorithm)) {
+        // U as [16][OCp][Cp] fp16 from layout 3 (fp16) / 5 (fp32) [oc][ic][4][4].
+        if (src_layout == AEXRT_HIP_SRC_LAYOUT_WINO_F16 || src_layout == AEXRT_HIP_SRC_LAYOUT_WINO_F32) {
+            const uint64_t elems = (uint64_t)oc * ic * 16;
+            const bool f16 = src_layout == AEXRT_HIP_SRC_LAYOUT_WINO_F16;
+            if (src_nbytes < elems * (f16 ? 2 : 4)) {
+                set_error("pack_conv_weight: Winograd payload too small");
+                return 0;
+            }
+            for (uint32_t o = 0; o < oc; ++o)
+                for (uint32_t c = 0; c < ic; ++c)
+                    for (uint32_t r = 0; r < 16; ++r) {
+                        const uint64_t si = ((uint64_t)o * ic + c) * 16 + r;
+                        const float v = f16 ? half_bits_to_float(static_cast<const uint16_t*>(src)[si])
+                                            : static_cast<const float*>(src)[si];
+                        out[((uint64_t)r * g.ocp + o) * g.kp + c] = float_to_half_bits(v);
+                    }
+            return 1;
+        }
+        // Raw 3x3 weights: U = G g G^T on the fp16-rounded source.
+        std::vector<float> w;
+        if (kk != 9 || !source_to_f32(d, src_layout, src, src_nbytes, w)) {
+            set_error("pack_conv_weight: unsupported source layout for Winograd");
+            return 0;
+        }
+        static const float G[4][3] = {{1.f, 0.f, 0.f}, {.5f, .5f, .5f}, {.5f, -.5f, .5f}, {0.f, 0.f, 1.f}};
+        for (uint32_t o = 0; o < oc; ++o)
+            for (uint32_t c = 0; c < ic; ++c) {
+                float gg[3][3], t[3][4];
+                for (int i = 0; i < 9; ++i)
+                    gg[i / 3][i % 3] = half_bits_to_float(float_to_half_bits(w[((uint64_t)o * ic + c) * 9 + i]));
+                for (int k = 0; k < 3; ++k)
+                    for (int b = 0; b < 4; ++b) t[k][b] = gg[k][0] * G[b][0] + gg[k][1] * G[b][1] + gg[k][2] * G[b][2];
+                for (int a = 0; a < 4; ++a)
+                    for (int b = 0; b < 4; ++b) {
+                        const float u = G[a][0] * t[0][b] + G[a][1] * t[1][b] + G[a][2] * t[2][b];
+                        out[((uint64_t)(a * 4 + b) * g.ocp + o) * g.kp + c] = float_to_half_bits(u);
+                    }
+            }
+        return 1;
+    }
+    std::vector<float> w;
+    if (!source_to_f32(d, src_layout, src, src_nbytes, w)) {
+        set_error("pack_conv_weight: unsupported source layout for fp16 conv");
+        return 0;
+    }
+    for (uint32_t o = 0; o < oc; ++o)
+        for (uint32_t c = 0; c < ic; ++c)
+            for (uint32_t k = 0; k < kk; ++k)
+                out[(uint64_t)o * g.kp + (uint64_t)k * ic + c] = float_to_half_bits(w[((uint64_t)o * ic + c) * kk + k]);
+    return 1;
+}
+
+int aexrt_hip_conv2d(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t flags, const AexrtHipTensorView* x,
+                     const void* weight, const float* w_scale, const float* bias, const AexrtHipTensorView* residual,
+                     const AexrtHipTensorView* y, int32_t* acc_out, void* stream) {
+    if (!desc || !x || !y || !weight || !bias || !x->data || !y->data) {
+        set_error("conv2d: null argument");
+        return 0;
+    }
+    std::string why;
+    ConvParams p{};
+    if (!build_conv_params(*desc, algorithm, flags, *x, weight, w_scale, bias, residual, *y, acc_out, p, why)) {
+        set_error("conv2d: " + why);
+        return 0;
+    }
+    return launch_conv(p, algorithm, static_cast<hipStream_t>(stream)) ? 1 : 0;
+}
+
+int aexrt_hip_amax_slots(const AexrtHipTensorView* x, uint32_t batch, uint32_t height, uint32_t width,
+                         uint32_t channels, void* stream) {
+    if (!x || !x->data || !x->amax_slots || channels % 16 || x->c_stride % 8 || x->n_stride % 8) {
+        set_error("amax_slots: bad view (need slots, C % 16 == 0, 8-element strides)");
+        return 0;
+    }
+    return check_hip(launch_amax_slots_nhwc(static_cast<const __half*>(x->data), x->n_stride, x->c_stride,
+                                            (int)batch, (int)(height * width), (int)channels, x->amax_slots,
+                                            static_cast<hipStream_t>(stream)),
+                     "amax_slots")
+               ? 1
+               : 0;
+}
+
+int aexrt_hip_amax_nchw(const void* x, uint32_t is_f16, uint32_t batch, uint32_t channels, uint32_t plane,
+                        uint32_t* out, void* stream) {
+    if (!x || !out) {
+        set_error("amax_nchw: null argument");
+        return 0;
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (!check_hip(launch_fill_u32(out, channels / 16 + 1, 0u, s), "amax_nchw zero")) return 0;
+    return check_hip(launch_amax_strips_nchw(x, is_f16 != 0, (int)batch, (int)channels, (int)plane, out, s),
+                     "amax_nchw")
+               ? 1
+               : 0;
+}
+
+int aexrt_hip_quantize(const AexrtHipTensorView* x, uint32_t batch, uint32_t height, uint32_t width,
+                       uint32_t channels, int8_t* q, void* stream) {
+    if (!x || !x->data || !x->amax_slots || !q || channels % 16 || x->c_stride % 8 || x->n_stride % 8) {
+        set_error("quantize: bad view (need slots, C % 16 == 0, 8-element strides)");
+        return 0;
+    }
+    return check_hip(launch_quantize_nhwc(static_cast<const __half*>(x->data), x->n_stride, x->c_stride,
+                                          (int)batch, (int)(height * width), (int)channels, x->amax_slots,
+                                          (int)(channels / 16), q, static_cast<hipStream_t>(stream)),
+                     "quantize")
+               ? 1
+               : 0;
+}
+
+int aexrt_hip_quant_pack_nchw(const void* x, uint32_t is_f16, uint32_t batch, uint32_t channels, uint32_t plane,
+                              const uint32_t* amax, uint32_t per_group, uint32_t* packed, void* stream) {
+    if (!x || !amax || !packed || channels % 4) {
+        set_error("quant_pack_nchw: bad arguments");
+        return 0;
+    }
+    return check_hip(launch_quant_pack_nchw(x, is_f16 != 0, (int)batch, (int)channels, (int)plane, amax,
+                                            per_group != 0, packed, static_cast<hipStream_t>(stream)),
+                     "quant_pack_nchw")
+               ? 1
+               : 0;
+}
+
+int aexrt_hip_fill_u32(uint32_t* dst, uint64_t count, uint32_t value, void* stream) {
+    if (!dst && count) {
+        set_error("fill_u32: null destination");
+        return 0;
+    }
+    return check_hip(launch_fill_u32(dst, (int64_t)count, value, static_cast<hipStream_t>(stream)), "fill_u32")
+               ? 1
+               : 0;
+}
+
+int aexrt_hip_nchw_f32_to_nhwc(const float* x, uint32_t batch, uint32_t channels, uint32_t plane,
+                               const AexrtHipTensorView* y, void* stream) {
+    if (!x || !y || !y->data) {
+        set_error("nchw_f32_to_nhwc: null argument");
+        return 0;
+    }
+    return check_hip(launch_nchw_f32_to_nhwc_f16(x, static_cast<__half*>(y->data), y->n_stride, y->c_stride,
+                                                 (int)batch, (int)channels, (int)plane, y->amax_slots,
+                                                 static_cast<hipStream_t>(stream)),
+                     "nchw_f32_to_nhwc")
+               ? 1
+               : 0;
+}
+
+int aexrt_hip_nhwc_to_nchw_f32(const AexrtHipTensorView* x, uint32_t is_f16, uint32_t batch, uint32_t channels,
+                               uint32_t plane, float* y, void* stream) {
+    if (!x || !x->data || !y) {
+        set_error("nhwc_to_nchw_f32: null argument");
+        return 0;
+    }
+    return check_hip(launch_nhwc_to_nchw_f32(x->data, is_f16 != 0, x->n_stride, x->c_stride, y, (int)batch,
+                                             (int)channels, (int)plane, static_cast<hipStream_t>(stream)),
+                     "nhwc_to_nchw_f32")
+               ? 1
+               : 0;
+}
+
+static bool vec_view_ok(const AexrtHipTensorView* v) {
+    return v && v->data && (reinterpret_cast<uintptr_t>(v->data) % 16) == 0 && v->c_stride % 8 == 0 &&
+           v->n_stride % 8 == 0;
+}
+
+int aexrt_hip_copy(const AexrtHipTensorView* src, const AexrtHipTensorView* dst, uint32_t batch, uint32_t plane,
+                   uint32_t channels, void* stream) {
+    if (!vec_view_ok(src) || !vec_view_ok(dst) || channels % 8) {
+        set_error("copy: views need 16-byte alignment and C % 8 == 0");
+        return 0;
+    }
+    return check_hip(launch_copy_nhwc(static_cast<const __half*>(src->data), src->n_stride, src->c_stride,
+                                      static_cast<__half*>(dst->data), dst->n_stride, dst->c_stride, (int)batch,
+                                      (int)plane, (int)channels, dst->amax_slots, static_cast<hipStream_t>(stream)),
+                     "copy")
+               ? 1
+               : 0;
+}
+
+int aexrt_hip_maxpool(const AexrtHipTensorView* x, const AexrtHipTensorView* y, uint32_t batch, uint32_t channels,
+                      uint32_t in_h, uint32_t in_w, uint32_t out_h, uint32_t out_w, uint32_t kernel, uint32_t stride,
+                      uint32_t pad, void* stream) {
+    if (!vec_view_ok(x) || !vec_view_ok(y) || channels % 8 || stride == 0) {
+        set_error("maxpool: views need 16-byte alignment and C % 8 == 0");
+        return 0;
+    }
+    return check_hip(launch_maxpool_nhwc(static_cast<const __half*>(x->data), x->n_stride, x->c_stride,
+                                         static_cast<__half*>(y->data), y->n_stride, y->c_stride, (int)batch,
+                                         (int)in_h, (int)in_w, (int)channels, (int)out_h, (int)out_w, (int)kernel,
+                                         (int)stride, (int)pad, y->amax_slots, static_cast<hipStream_t>(stream)),
+                     "maxpool")
+               ? 1
+               : 0;
+}
+
+int aexrt_hip_resize_nearest(const AexrtHipTensorView* x, const AexrtHipTensorView* y, uint32_t batch,
+                             uint32_t channels, uint32_t in_h, uint32_t in_w, uint32_t out_h, uint32_t out_w,
+                             void* stream) {
+    if (!vec_view_ok(x) || !vec_view_ok(y) || channels % 8) {
+        set_error("resize: views need 16-byte alignment and C % 8 == 0");
+        return 0;
+    }
+    return check_hip(launch_resize_nearest_nhwc(static_cast<const __half*>(x->data), x->n_stride, x->c_stride,
+                                                static_cast<__half*>(y->data), y->n_stride, y->c_stride,
+                                                (int)batch, (int)in_h, (int)in_w, (int)channels, (int)out_h,
+                                                (int)out_w, y->amax_slots, static_cast<hipStream_t>(stream)),
+                     "resize")
+               ? 1
+               : 0;
+}
+
+int aexrt_hip_add(const AexrtHipTensorView* a, const AexrtHipTensorView* b, const AexrtHipTensorView* y,
+                  uint32_t batch, uint32_t plane, uint32_t channels, void* stream) {
+    if (!vec_view_ok(a) || !vec_view_ok(b) || !vec_view_ok(y) || channels % 8) {
+        set_error("add: views need 16-byte alignment and C % 8 == 0");
+        return 0;
+    }
+    return check_hip(launch_add_nhwc(static_cast<const __half*>(a->data), a->n_stride, a->c_stride,
+                                     static_cast<const __half*>(b->data), b->n_stride, b->c_stride,
+                                     static_cast<__half*>(y->data), y->n_stride, y->c_stride, (int)batch,
+                                     (int)plane, (int)channels, y->amax_slots, static_cast<hipStream_t>(stream)),
+                     "add")
+               ? 1
+               : 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,49 @@
+// Shared device helpers for the gfx950 kernels of the W8A8 conv path.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace aexrt {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// Activation amax is kept per 16-channel group ("slot") of every tensor as the
+// bit pattern of a non-negative float, so that an unsigned atomicMax orders
+// the values.  A view or concat over 16-aligned channel ranges takes the max
+// of its slots; the per-tensor amax is the max over all slots.
+constexpr int kAmaxGroup = 16;
+
+__device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+// Per-tensor quantizer of the reference's pack pass: s = 127/amax (IEEE fp32
+// division, computed once by the caller), q = round-half-even(x * s), kept as
+// the low byte of the saturated int32 (the D3D float->int cast saturates; the
+// clamp makes the conversion defined for any input, NaN included).
+__device__ __forceinline__ int32_t quant_int(float x, float s) {
+    const float p = x * s;
+    float r = __builtin_rintf(p);
+    r = fminf(fmaxf(r, -2147483648.0f), 2147483520.0f);
+    return (int32_t)r;
+}
+
+__device__ __forceinline__ uint32_t pack4_q(float a, float b, float c, float d, float s) {
+    return ((uint32_t)quant_int(a, s) & 0xFFu) | (((uint32_t)quant_int(b, s) & 0xFFu) << 8) |
+           (((uint32_t)quant_int(c, s) & 0xFFu) << 16) | (((uint32_t)quant_int(d, s) & 0xFFu) << 24);
+}
+
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
+
+}  // namespace aexrt

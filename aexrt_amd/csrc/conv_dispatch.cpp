@@ -1,0 +1,144 @@
+// Conv dispatch: maps a reference algorithm id and descriptor onto one of the
+// three gfx950 kernels (int8 MFMA, fp16 MFMA, fp16 Winograd) and checks
+// every assumption the kernel makes about shapes, views and alignment before
+// anything is launched.
+#include <cstdint>
+#include <string>
+
+#include "internal.h"
+
+namespace aexrt {
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) % 16) == 0; }
+
+bool build_conv_params(const AexrtConv2DDesc& d, uint32_t algorithm, uint32_t flags, const AexrtHipTensorView& x,
+                       const void* weight, const float* w_scale, const float* bias,
+                       const AexrtHipTensorView* residual, const AexrtHipTensorView& y, int32_t* acc_out,
+                       ConvParams& p, std::string& why) {
+    if (!generic_shape_ok(d)) {
+        why = "unsupported conv geometry (groups/dilation/asymmetric stride or pad, or inconsistent out size)";
+        return false;
+    }
+    if (d.batch == 0 || d.in_channels == 0 || d.out_channels == 0 || d.out_h == 0 || d.out_w == 0) {
+        why = "empty convolution";
+        return false;
+    }
+    const bool int8 = is_int8_algorithm(algorithm);
+    const bool wino = is_winograd_algorithm(algorithm);
+    const bool nchw_in = (flags & AEXRT_HIP_CONV_IN_NCHW_F32) != 0;
+    if (int8) {
+        if (!can_use_int8(d, int8_kernel_elems(algorithm))) {
+            why = "descriptor is not eligible for the planned int8 kernel";
+            return false;
+        }
+        if ((algorithm == 52u && d.stride_h != 1) || (algorithm == 53u && d.stride_h != 2)) {
+            why = "int8 kernel id does not match the stride";
+            return false;
+        }
+        if (!x.amax_slots || !w_scale) {
+            why = "int8 conv needs the input amax slots and the weight scales";
+            return false;
+        }
+        if (nchw_in) {
+            why = "int8 conv reads NHWC fp16 activations only";
+            return false;
+        }
+    }
+    if (wino) {
+        if (!winograd_shape_ok(d)) {
+            why = "Winograd F(2x2,3x3) needs 3x3 s1 p1, C % 4 == 0 and even output dims";
+            return false;
+        }
+        if (!(flags & AEXRT_HIP_CONV_SILU)) {
+            why = "Winograd kernels always apply SiLU (reference kernels 40/46)";
+            return false;
+        }
+        if (nchw_in) {
+            why = "Winograd reads NHWC fp16 activations only";
+            return false;
+        }
+        if (!aligned16(x.data) || x.c_stride % 4 || x.n_stride % 4) {
+            why = "Winograd input view must be 8-byte aligned with 4-element strides";
+            return false;
+        }
+    }
+    if (!int8 && !wino && !nchw_in) {
+        if (d.in_channels % 8) {
+            why = "fp16 conv on an NHWC view needs C % 8 == 0";
+            return false;
+        }
+    }
+    if (!nchw_in && !wino) {
+        if (d.in_channels % 8 || !aligned16(x.data) || x.c_stride % 8 || x.n_stride % 8) {
+            why = "NHWC input view must be 16-byte aligned with 8-element strides and C % 8 == 0";
+            return false;
+        }
+    }
+    if (!nchw_in && (uint32_t)x.c_stride < d.in_channels) {
+        why = "input c_stride smaller than in_channels";
+        return false;
+    }
+    if ((uint32_t)y.c_stride < d.out_channels) {
+        why = "output c_stride smaller than out_channels";
+        return false;
+    }
+    if ((flags & AEXRT_HIP_CONV_RESIDUAL) && (!residual || !residual->data)) {
+        why = "residual flag without a residual view";
+        return false;
+    }
+    if (acc_out && !int8) {
+        why = "acc_out is only produced by int8 kernels";
+        return false;
+    }
+    const WeightGeom g = weight_geom(d, algorithm);
+    p = ConvParams{};
+    p.x = x.data;
+    p.x_nstride = nchw_in ? (int64_t)d.in_channels * d.in_h * d.in_w : x.n_stride;
+    p.x_cstride = nchw_in ? 1 : x.c_stride;
+    p.loader = nchw_in ? kLoaderNchwF32 : kLoaderNhwc;
+    p.x_slots = x.amax_slots;
+    p.x_nslots = (int)(d.in_channels / 16);
+    p.w = weight;
+    p.Kp = (int)g.kp;
+    p.OCp = (int)g.ocp;
+    p.w_scale = w_scale;
+    p.bias = bias;
+    p.y = y.data;
+    p.y_nstride = y.n_stride;
+    p.y_cstride = y.c_stride;
+    p.y_slots = y.amax_slots;
+    if (residual && (flags & AEXRT_HIP_CONV_RESIDUAL)) {
+        p.res = static_cast<const __half*>(residual->data);
+        p.r_nstride = residual->n_stride;
+        p.r_cstride = residual->c_stride;
+    }
+    p.acc_out = acc_out;
+    p.N = (int)d.batch;
+    p.H = (int)d.in_h;
+    p.W = (int)d.in_w;
+    p.C = (int)d.in_channels;
+    p.OH = (int)d.out_h;
+    p.OW = (int)d.out_w;
+    p.OC = (int)d.out_channels;
+    p.KH = (int)d.kernel_h;
+    p.KW = (int)d.kernel_w;
+    p.S = (int)d.stride_h;
+    p.P = (int)d.pad_top;
+    p.K = p.KH * p.KW * p.C;
+    const int64_t m = (int64_t)d.batch * d.out_h * d.out_w;
+    if (m > INT32_MAX / 2) {
+        why = "too many output positions for one launch";
+        return false;
+    }
+    p.M = (int)m;
+    p.flags = (int)(flags & (AEXRT_HIP_CONV_SILU | AEXRT_HIP_CONV_RESIDUAL | AEXRT_HIP_CONV_OUT_F32));
+    return true;
+}
+
+bool launch_conv(const ConvParams& p, uint32_t algorithm, hipStream_t stream) {
+    if (is_winograd_algorithm(algorithm)) return check_hip(launch_winograd_f2x2(p, stream), "winograd conv");
+    return check_hip(launch_conv_igemm(p, is_int8_algorithm(algorithm), stream),
+                     is_int8_algorithm(algorithm) ? "int8 conv" : "fp16 conv");
+}
+
+}  // namespace aexrt

@@ -1,0 +1,39 @@
+// Host-side internals shared by the op-level C ABI and the model runtime.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "../../include/aexrt_hip.h"
+#include "kernels.h"
+
+namespace aexrt {
+
+void set_error(const std::string& msg);
+const char* last_error();
+bool check_hip(hipError_t e, const char* what);
+
+bool is_int8_algorithm(uint32_t algorithm);
+bool is_winograd_algorithm(uint32_t algorithm);
+uint32_t int8_kernel_elems(uint32_t algorithm);
+bool can_use_int8(const AexrtConv2DDesc& d, uint32_t kernel_elems);
+bool winograd_shape_ok(const AexrtConv2DDesc& d);
+bool generic_shape_ok(const AexrtConv2DDesc& d);
+
+// Geometry of a repacked conv weight.
+struct WeightGeom {
+    uint32_t ocp;        // output channels rounded up to 16
+    uint32_t kp;         // K rounded up to 64 (igemm) / C rounded up to 32 (Winograd)
+    uint32_t elem_bytes;
+    uint64_t nbytes;
+};
+WeightGeom weight_geom(const AexrtConv2DDesc& d, uint32_t algorithm);
+
+// Validates one convolution and fills the kernel parameters.
+bool build_conv_params(const AexrtConv2DDesc& d, uint32_t algorithm, uint32_t flags, const AexrtHipTensorView& x,
+                       const void* weight, const float* w_scale, const float* bias,
+                       const AexrtHipTensorView* residual, const AexrtHipTensorView& y, int32_t* acc_out,
+                       ConvParams& p, std::string& why);
+bool launch_conv(const ConvParams& p, uint32_t algorithm, hipStream_t stream);
+
+}  // namespace aexrt

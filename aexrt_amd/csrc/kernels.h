@@ -1,0 +1,91 @@
+// Launch interfaces of the gfx950 kernels (host side of the library).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace aexrt {
+
+enum ConvFlags : int {
+    kConvSilu = 1,      // SiLU after bias
+    kConvResidual = 2,  // + residual tensor after the activation
+    kConvOutF32 = 4,    // store fp32 instead of fp16
+};
+
+enum Loader : int {
+    kLoaderNhwc = 0,     // fp16 NHWC activation view, C % 8 == 0
+    kLoaderNchwF32 = 1,  // fp32 NCHW network input (fp16 path only)
+};
+
+// One convolution launch.  Activation views address element (n, h, w, c) at
+// n*nstride + (h*W + w)*cstride + c relative to their data pointer.
+struct ConvParams {
+    const void* x;
+    int64_t x_nstride;
+    int32_t x_cstride;
+    int32_t loader;
+    const uint32_t* x_slots;  // amax slots of the input channel range (int8 only)
+    int32_t x_nslots;
+    const void* w;            // [OCp][Kp], int8 or fp16
+    int32_t Kp, OCp;
+    const float* w_scale;     // [OC], int8 only
+    const float* bias;        // [OC]
+    void* y;
+    int64_t y_nstride;
+    int32_t y_cstride;
+    uint32_t* y_slots;        // amax slots of the output channels, may be null
+    const __half* res;        // residual view, same geometry as y
+    int64_t r_nstride;
+    int32_t r_cstride;
+    int32_t* acc_out;         // optional int32 accumulators [M][OC] (int8)
+    int N, H, W, C, OH, OW, OC, KH, KW, S, P;
+    int K, M;
+    int flags;
+};
+
+hipError_t launch_conv_igemm(const ConvParams& p, bool int8, hipStream_t stream);
+
+// Winograd F(2x2,3x3), fp16 MFMA.  U is [16][OCp][Cp] fp16 (Cp = C rounded up
+// to 32).  Same views/flags as ConvParams (w = U, Kp = Cp).
+hipError_t launch_winograd_f2x2(const ConvParams& p, hipStream_t stream);
+
+// ---- quantization / amax ---------------------------------------------------
+
+// amax slots of an NHWC fp16 view: slots[g] |= max|x| over channels 16g..16g+15
+// (atomicMax, caller clears).  C % 16 == 0.
+hipError_t launch_amax_slots_nhwc(const __half* x, int64_t nstride, int32_t cstride, int N, int HW,
+                                  int C, uint32_t* slots, hipStream_t stream);
+// The reference's amax buffer over an NCHW tensor (fp16 or fp32): slot 0 =
+// whole tensor, slot 1+g = memory strip [g*16*N*HW, (g+1)*16*N*HW).
+hipError_t launch_amax_strips_nchw(const void* x, bool f16, int N, int C, int HW, uint32_t* slots,
+                                   hipStream_t stream);
+// int8 NHWC (dense) from an fp16 NHWC view with the per-tensor amax of nslots slots.
+hipError_t launch_quantize_nhwc(const __half* x, int64_t nstride, int32_t cstride, int N, int HW, int C,
+                                const uint32_t* slots, int nslots, int8_t* q, hipStream_t stream);
+// The reference's NC/4HW4 pack (per-tensor slot 0, or per_group slots 1+icg/4).
+hipError_t launch_quant_pack_nchw(const void* x, bool f16, int N, int C, int HW, const uint32_t* slots,
+                                  bool per_group, uint32_t* packed, hipStream_t stream);
+
+// ---- glue ------------------------------------------------------------------
+hipError_t launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t stream);
+// dst view (channels [0,C)) = src view; amax slots of dst updated when non-null.
+hipError_t launch_copy_nhwc(const __half* src, int64_t s_nstride, int32_t s_cstride, __half* dst,
+                            int64_t d_nstride, int32_t d_cstride, int N, int HW, int C,
+                            uint32_t* dst_slots, hipStream_t stream);
+hipError_t launch_maxpool_nhwc(const __half* x, int64_t x_nstride, int32_t x_cstride, __half* y,
+                               int64_t y_nstride, int32_t y_cstride, int N, int H, int W, int C,
+                               int OH, int OW, int k, int s, int pad, uint32_t* y_slots,
+                               hipStream_t stream);
+hipError_t launch_resize_nearest_nhwc(const __half* x, int64_t x_nstride, int32_t x_cstride, __half* y,
+                                      int64_t y_nstride, int32_t y_cstride, int N, int H, int W, int C,
+                                      int OH, int OW, uint32_t* y_slots, hipStream_t stream);
+hipError_t launch_add_nhwc(const __half* a, int64_t a_nstride, int32_t a_cstride, const __half* b,
+                           int64_t b_nstride, int32_t b_cstride, __half* y, int64_t y_nstride,
+                           int32_t y_cstride, int N, int HW, int C, uint32_t* y_slots, hipStream_t stream);
+// fp32 NCHW <-> fp16 NHWC views.
+hipError_t launch_nchw_f32_to_nhwc_f16(const float* x, __half* y, int64_t y_nstride, int32_t y_cstride,
+                                       int N, int C, int HW, uint32_t* y_slots, hipStream_t stream);
+hipError_t launch_nhwc_to_nchw_f32(const void* x, bool f16, int64_t x_nstride, int32_t x_cstride, float* y,
+                                   int N, int C, int HW, hipStream_t stream);
+
+}  // namespace aexrt

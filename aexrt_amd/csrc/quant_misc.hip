@@ -1,0 +1,444 @@
+// Activation amax / quantization kernels and the glue ops of the replay
+// stream (copy for concat, maxpool, nearest resize, add, layout changes).
+//
+// All of them are HBM-bound streaming kernels: 16-byte vector accesses along
+// the contiguous channel dimension of NHWC views, grid-stride loops sized to
+// the CU count, and amax reductions that go wave shuffle -> LDS -> one
+// atomicMax per block and 16-channel group (never one workgroup per group, so
+// low-channel / large-plane tensors still fill the chip).
+#include "common.h"
+#include "kernels.h"
+
+namespace aexrt {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxSlots = 128;  // up to 2048 channels per view
+
+inline int grid_for(int64_t work, int per_block = kThreads) {
+    int64_t g = (work + per_block - 1) / per_block;
+    if (g < 1) g = 1;
+    if (g > 256 * 16) g = 256 * 16;  // 16 waves-of-blocks per CU is plenty
+    return (int)g;
+}
+
+__device__ __forceinline__ void slots_init(uint32_t* s, int n) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) s[i] = 0u;
+    __syncthreads();
+}
+
+__device__ __forceinline__ void slots_flush(const uint32_t* s, int n, uint32_t* g) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += blockDim.x)
+        if (s[i]) atomicMax(g + i, s[i]);
+}
+
+__device__ __forceinline__ float max8_abs(const uint4& v) {
+    const __half2* h = reinterpret_cast<const __half2*>(&v);
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float2 f = __half22float2(h[i]);
+        m = fmaxf(m, fmaxf(fabsf(f.x), fabsf(f.y)));
+    }
+    return m;
+}
+
+// ---- amax --------------------------------------------------------------------
+
+__global__ __launch_bounds__(kThreads) void amax_slots_nhwc_kernel(
+    const __half* x, int64_t nstride, int32_t cstride, int HW, int C, int64_t chunks,
+    uint32_t* slots) {
+    __shared__ uint32_t ls[kMaxSlots];
+    const int CC = C / 8;
+    const int G = C / 16;
+    slots_init(ls, G);
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    const bool fixed = (step % CC) == 0;  // each thread then always sees one chunk column
+    float run = 0.0f;
+    int my_g = -1;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
+        const int64_t pix = e / CC;
+        const int cc = (int)(e - pix * CC);
+        const int64_t n = pix / HW;
+        const int64_t pp = pix - n * HW;
+        const uint4 v = *reinterpret_cast<const uint4*>(x + n * nstride + pp * cstride + cc * 8);
+        const float m = max8_abs(v);
+        if (fixed) {
+            run = fmaxf(run, m);
+            my_g = cc >> 1;
+        } else {
+            atomicMax(&ls[cc >> 1], f2u(m));
+        }
+    }
+    if (fixed && my_g >= 0) atomicMax(&ls[my_g], f2u(run));
+    slots_flush(ls, G, slots);
+}
+
+// Reference amax buffer over NCHW memory (RT:3219-3259): slot 0 = max over the
+// scanned strips, slot 1+g = strip g of 16*N*HW elements.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void amax_strips_kernel(const T* x, int64_t strip, int G,
+                                                             uint32_t* slots) {
+    __shared__ uint32_t ls[kMaxSlots + 1];
+    slots_init(ls, G + 1);
+    const int64_t total = strip * G;
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += step) {
+        float v;
+        if constexpr (sizeof(T) == 2) v = __half2float(reinterpret_cast<const __half*>(x)[i]);
+        else v = reinterpret_cast<const float*>(x)[i];
+        const uint32_t b = f2u(fabsf(v));
+        const int g = (int)(i / strip);
+        atomicMax(&ls[1 + g], b);
+        atomicMax(&ls[0], b);
+    }
+    slots_flush(ls, G + 1, slots);
+}
+
+__device__ __forceinline__ float slots_amax(const uint32_t* slots, int n) {
+    uint32_t am = 0;
+    for (int i = 0; i < n; ++i) am = max(am, slots[i]);
+    return u2f(am);
+}
+
+// ---- quantize -----------------------------------------------------------------
+
+__global__ __launch_bounds__(kThreads) void quantize_nhwc_kernel(
+    const __half* x, int64_t nstride, int32_t cstride, int HW, int C, int64_t chunks,
+    const uint32_t* slots, int nslots, int8_t* q) {
+    const float a = slots_amax(slots, nslots);
+    const float s = a > 0.0f ? 127.0f / a : 0.0f;
+    const int CC = C / 8;
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
+        const int64_t pix = e / CC;
+        const int cc = (int)(e - pix * CC);
+        const int64_t n = pix / HW;
+        const int64_t pp = pix - n * HW;
+        const uint4 v = *reinterpret_cast<const uint4*>(x + n * nstride + pp * cstride + cc * 8);
+        uint2 o = make_uint2(0u, 0u);
+        if (a > 0.0f) {
+            const __half2* h = reinterpret_cast<const __half2*>(&v);
+            float2 f0 = __half22float2(h[0]), f1 = __half22float2(h[1]);
+            float2 f2 = __half22float2(h[2]), f3 = __half22float2(h[3]);
+            o.x = pack4_q(f0.x, f0.y, f1.x, f1.y, s);
+            o.y = pack4_q(f2.x, f2.y, f3.x, f3.y, s);
+        }
+        *reinterpret_cast<uint2*>(q + pix * C + cc * 8) = o;
+    }
+}
+
+// Reference NC/4HW4 pack (RT:3314-3346).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void quant_pack_nchw_kernel(const T* x, int C, int HW,
+                                                                 int64_t total4, const uint32_t* slots,
+                                                                 int per_group, uint32_t* packed) {
+    const int icg_count = C / 4;
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total4; idx += step) {
+        const int pos = (int)(idx % HW);
+        const int64_t t = idx / HW;
+        const int icg = (int)(t % icg_count);
+        const int64_t n = t / icg_count;
+        const float a = u2f(per_group ? slots[icg / 4 + 1] : slots[0]);
+        if (!(a > 0.0f)) {
+            packed[idx] = 0u;
+            continue;
+        }
+        const float s = 127.0f / a;
+        const int64_t base = ((n * icg_count + icg) * 4) * HW + pos;
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if constexpr (sizeof(T) == 2) v[j] = __half2float(reinterpret_cast<const __half*>(x)[base + j * HW]);
+            else v[j] = reinterpret_cast<const float*>(x)[base + j * HW];
+        }
+        packed[idx] = pack4_q(v[0], v[1], v[2], v[3], s);
+    }
+}
+
+// ---- glue -------------------------------------------------------------------------
+
+__global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t v) {
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) p[i] = v;
+}
+
+__global__ __launch_bounds__(kThreads) void copy_nhwc_kernel(
+    const __half* src, int64_t s_nstride, int32_t s_cstride, __half* dst, int64_t d_nstride,
+    int32_t d_cstride, int HW, int C, int64_t chunks, uint32_t* dst_slots) {
+    __shared__ uint32_t ls[kMaxSlots];
+    const int G = dst_slots ? C / 16 : 0;
+    slots_init(ls, G);
+    const int CC = C / 8;
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
+        const int64_t pix = e / CC;
+        const int cc = (int)(e - pix * CC);
+        const int64_t n = pix / HW;
+        const int64_t pp = pix - n * HW;
+        const uint4 v = *reinterpret_cast<const uint4*>(src + n * s_nstride + pp * s_cstride + cc * 8);
+        *reinterpret_cast<uint4*>(dst + n * d_nstride + pp * d_cstride + cc * 8) = v;
+        if (G) atomicMax(&ls[cc >> 1], f2u(max8_abs(v)));
+    }
+    if (G) slots_flush(ls, G, dst_slots);
+}
+
+__global__ __launch_bounds__(kThreads) void maxpool_nhwc_kernel(
+    const __half* x, int64_t x_nstride, int32_t x_cstride, __half* y, int64_t y_nstride,
+    int32_t y_cstride, int H, int W, int C, int OH, int OW, int k, int s, int pad, int64_t chunks,
+    uint32_t* y_slots) {
+    __shared__ uint32_t ls[kMaxSlots];
+    const int G = y_slots ? C / 16 : 0;
+    slots_init(ls, G);
+    const int CC = C / 8;
+    const int OHW = OH * OW;
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
+        const int64_t pix = e / CC;
+        const int cc = (int)(e - pix * CC);
+        const int64_t n = pix / OHW;
+        const int pp = (int)(pix - n * OHW);
+        const int oy = pp / OW, ox = pp - (pp / OW) * OW;
+        float m[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m[i] = -INFINITY;
+        for (int ky = 0; ky < k; ++ky) {
+            const int iy = oy * s + ky - pad;
+            if ((unsigned)iy >= (unsigned)H) continue;
+            for (int kx = 0; kx < k; ++kx) {
+                const int ix = ox * s + kx - pad;
+                if ((unsigned)ix >= (unsigned)W) continue;
+                const uint4 v = *reinterpret_cast<const uint4*>(
+                    x + n * x_nstride + ((int64_t)iy * W + ix) * x_cstride + cc * 8);
+                const __half2* h = reinterpret_cast<const __half2*>(&v);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float2 f = __half22float2(h[i]);
+                    m[2 * i] = fmaxf(m[2 * i], f.x);
+                    m[2 * i + 1] = fmaxf(m[2 * i + 1], f.y);
+                }
+            }
+        }
+        uint4 o;
+        __half2* oh = reinterpret_cast<__half2*>(&o);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) oh[i] = __floats2half2_rn(m[2 * i], m[2 * i + 1]);
+        *reinterpret_cast<uint4*>(y + n * y_nstride + (int64_t)pp * y_cstride + cc * 8) = o;
+        if (G) atomicMax(&ls[cc >> 1], f2u(max8_abs(o)));
+    }
+    if (G) slots_flush(ls, G, y_slots);
+}
+
+__global__ __launch_bounds__(kThreads) void resize_nearest_nhwc_kernel(
+    const __half* x, int64_t x_nstride, int32_t x_cstride, __half* y, int64_t y_nstride,
+    int32_t y_cstride, int H, int W, int C, int OH, int OW, int64_t chunks, uint32_t* y_slots) {
+    __shared__ uint32_t ls[kMaxSlots];
+    const int G = y_slots ? C / 16 : 0;
+    slots_init(ls, G);
+    const int CC = C / 8;
+    const int OHW = OH * OW;
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
+        const int64_t pix = e / CC;
+        const int cc = (int)(e - pix * CC);
+        const int64_t n = pix / OHW;
+        const int pp = (int)(pix - n * OHW);
+        const int oy = pp / OW, ox = pp - (pp / OW) * OW;
+        const int iy = (int)((int64_t)oy * H / OH), ix = (int)((int64_t)ox * W / OW);
+        const uint4 v = *reinterpret_cast<const uint4*>(
+            x + n * x_nstride + ((int64_t)iy * W + ix) * x_cstride + cc * 8);
+        *reinterpret_cast<uint4*>(y + n * y_nstride + (int64_t)pp * y_cstride + cc * 8) = v;
+        if (G) atomicMax(&ls[cc >> 1], f2u(max8_abs(v)));
+    }
+    if (G) slots_flush(ls, G, y_slots);
+}
+
+__global__ __launch_bounds__(kThreads) void add_nhwc_kernel(
+    const __half* a, int64_t a_nstride, int32_t a_cstride, const __half* b, int64_t b_nstride,
+    int32_t b_cstride, __half* y, int64_t y_nstride, int32_t y_cstride, int HW, int C, int64_t chunks,
+    uint32_t* y_slots) {
+    __shared__ uint32_t ls[kMaxSlots];
+    const int G = y_slots ? C / 16 : 0;
+    slots_init(ls, G);
+    const int CC = C / 8;
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
+        const int64_t pix = e / CC;
+        const int cc = (int)(e - pix * CC);
+        const int64_t n = pix / HW;
+        const int64_t pp = pix - n * HW;
+        const uint4 va = *reinterpret_cast<const uint4*>(a + n * a_nstride + pp * a_cstride + cc * 8);
+        const uint4 vb = *reinterpret_cast<const uint4*>(b + n * b_nstride + pp * b_cstride + cc * 8);
+        const __half2* ha = reinterpret_cast<const __half2*>(&va);
+        const __half2* hb = reinterpret_cast<const __half2*>(&vb);
+        uint4 o;
+        __half2* ho = reinterpret_cast<__half2*>(&o);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float2 fa = __half22float2(ha[i]), fb = __half22float2(hb[i]);
+            ho[i] = __floats2half2_rn(fa.x + fb.x, fa.y + fb.y);
+        }
+        *reinterpret_cast<uint4*>(y + n * y_nstride + pp * y_cstride + cc * 8) = o;
+        if (G) atomicMax(&ls[cc >> 1], f2u(max8_abs(o)));
+    }
+    if (G) slots_flush(ls, G, y_slots);
+}
+
+__global__ __launch_bounds__(kThreads) void nchw_f32_to_nhwc_f16_kernel(
+    const float* x, __half* y, int64_t y_nstride, int32_t y_cstride, int C, int HW, int64_t total,
+    uint32_t* y_slots) {
+    __shared__ uint32_t ls[kMaxSlots];
+    const int G = y_slots ? C / 16 : 0;
+    slots_init(ls, G);
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += step) {
+        // i enumerates (n, pos, c) so that the fp16 stores are contiguous
+        const int c = (int)(i % C);
+        const int64_t t = i / C;
+        const int64_t pos = t % HW;
+        const int64_t n = t / HW;
+        const __half h = __float2half(x[(n * C + c) * HW + pos]);
+        y[n * y_nstride + pos * y_cstride + c] = h;
+        if (G) atomicMax(&ls[c >> 4], f2u(fabsf(__half2float(h))));
+    }
+    if (G) slots_flush(ls, G, y_slots);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void nhwc_to_nchw_f32_kernel(const T* x, int64_t x_nstride,
+                                                                   int32_t x_cstride, float* y, int C,
+                                                                   int HW, int64_t total) {
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += step) {
+        const int64_t pos = i % HW;
+        const int64_t t = i / HW;
+        const int c = (int)(t % C);
+        const int64_t n = t / C;
+        const int64_t src = n * x_nstride + pos * x_cstride + c;
+        float v;
+        if constexpr (sizeof(T) == 2) v = __half2float(reinterpret_cast<const __half*>(x)[src]);
+        else v = reinterpret_cast<const float*>(x)[src];
+        y[i] = v;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_amax_slots_nhwc(const __half* x, int64_t nstride, int32_t cstride, int N, int HW, int C,
+                                  uint32_t* slots, hipStream_t stream) {
+    if (C % 16 != 0 || C / 16 > kMaxSlots) return hipErrorInvalidValue;
+    const int64_t chunks = (int64_t)N * HW * (C / 8);
+    hipLaunchKernelGGL(amax_slots_nhwc_kernel, dim3(grid_for(chunks)), dim3(kThreads), 0, stream, x,
+                       nstride, cstride, HW, C, chunks, slots);
+    return hipGetLastError();
+}
+
+hipError_t launch_amax_strips_nchw(const void* x, bool f16, int N, int C, int HW, uint32_t* slots,
+                                   hipStream_t stream) {
+    const int G = C / 16;
+    if (G > kMaxSlots) return hipErrorInvalidValue;
+    const int64_t strip = (int64_t)16 * N * HW;
+    const int grid = grid_for(strip * (G > 0 ? G : 1));
+    if (f16)
+        hipLaunchKernelGGL(amax_strips_kernel<__half>, dim3(grid), dim3(kThreads), 0, stream,
+                           reinterpret_cast<const __half*>(x), strip, G, slots);
+    else
+        hipLaunchKernelGGL(amax_strips_kernel<float>, dim3(grid), dim3(kThreads), 0, stream,
+                           reinterpret_cast<const float*>(x), strip, G, slots);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_nhwc(const __half* x, int64_t nstride, int32_t cstride, int N, int HW, int C,
+                                const uint32_t* slots, int nslots, int8_t* q, hipStream_t stream) {
+    if (C % 8 != 0) return hipErrorInvalidValue;
+    const int64_t chunks = (int64_t)N * HW * (C / 8);
+    hipLaunchKernelGGL(quantize_nhwc_kernel, dim3(grid_for(chunks)), dim3(kThreads), 0, stream, x, nstride,
+                       cstride, HW, C, chunks, slots, nslots, q);
+    return hipGetLastError();
+}
+
+hipError_t launch_quant_pack_nchw(const void* x, bool f16, int N, int C, int HW, const uint32_t* slots,
+                                  bool per_group, uint32_t* packed, hipStream_t stream) {
+    if (C % 4 != 0) return hipErrorInvalidValue;
+    const int64_t total4 = (int64_t)N * (C / 4) * HW;
+    const int grid = grid_for(total4);
+    if (f16)
+        hipLaunchKernelGGL(quant_pack_nchw_kernel<__half>, dim3(grid), dim3(kThreads), 0, stream,
+                           reinterpret_cast<const __half*>(x), C, HW, total4, slots, (int)per_group, packed);
+    else
+        hipLaunchKernelGGL(quant_pack_nchw_kernel<float>, dim3(grid), dim3(kThreads), 0, stream,
+                           reinterpret_cast<const float*>(x), C, HW, total4, slots, (int)per_group, packed);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(n)), dim3(kThreads), 0, stream, p, n, v);
+    return hipGetLastError();
+}
+
+hipError_t launch_copy_nhwc(const __half* src, int64_t s_nstride, int32_t s_cstride, __half* dst,
+                            int64_t d_nstride, int32_t d_cstride, int N, int HW, int C, uint32_t* dst_slots,
+                            hipStream_t stream) {
+    if (C % 8 != 0 || (dst_slots && (C % 16 != 0 || C / 16 > kMaxSlots))) return hipErrorInvalidValue;
+    const int64_t chunks = (int64_t)N * HW * (C / 8);
+    hipLaunchKernelGGL(copy_nhwc_kernel, dim3(grid_for(chunks)), dim3(kThreads), 0, stream, src, s_nstride,
+                       s_cstride, dst, d_nstride, d_cstride, HW, C, chunks, dst_slots);
+    return hipGetLastError();
+}
+
+hipError_t launch_maxpool_nhwc(const __half* x, int64_t x_nstride, int32_t x_cstride, __half* y,
+                               int64_t y_nstride, int32_t y_cstride, int N, int H, int W, int C, int OH,
+                               int OW, int k, int s, int pad, uint32_t* y_slots, hipStream_t stream) {
+    if (C % 8 != 0 || (y_slots && (C % 16 != 0 || C / 16 > kMaxSlots))) return hipErrorInvalidValue;
+    const int64_t chunks = (int64_t)N * OH * OW * (C / 8);
+    hipLaunchKernelGGL(maxpool_nhwc_kernel, dim3(grid_for(chunks)), dim3(kThreads), 0, stream, x, x_nstride,
+                       x_cstride, y, y_nstride, y_cstride, H, W, C, OH, OW, k, s, pad, chunks, y_slots);
+    return hipGetLastError();
+}
+
+hipError_t launch_resize_nearest_nhwc(const __half* x, int64_t x_nstride, int32_t x_cstride, __half* y,
+                                      int64_t y_nstride, int32_t y_cstride, int N, int H, int W, int C,
+                                      int OH, int OW, uint32_t* y_slots, hipStream_t stream) {
+    if (C % 8 != 0 || (y_slots && (C % 16 != 0 || C / 16 > kMaxSlots))) return hipErrorInvalidValue;
+    const int64_t chunks = (int64_t)N * OH * OW * (C / 8);
+    hipLaunchKernelGGL(resize_nearest_nhwc_kernel, dim3(grid_for(chunks)), dim3(kThreads), 0, stream, x,
+                       x_nstride, x_cstride, y, y_nstride, y_cstride, H, W, C, OH, OW, chunks, y_slots);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_nhwc(const __half* a, int64_t a_nstride, int32_t a_cstride, const __half* b,
+                           int64_t b_nstride, int32_t b_cstride, __half* y, int64_t y_nstride, int32_t y_cstride,
+                           int N, int HW, int C, uint32_t* y_slots, hipStream_t stream) {
+    if (C % 8 != 0 || (y_slots && (C % 16 != 0 || C / 16 > kMaxSlots))) return hipErrorInvalidValue;
+    const int64_t chunks = (int64_t)N * HW * (C / 8);
+    hipLaunchKernelGGL(add_nhwc_kernel, dim3(grid_for(chunks)), dim3(kThreads), 0, stream, a, a_nstride,
+                       a_cstride, b, b_nstride, b_cstride, y, y_nstride, y_cstride, HW, C, chunks, y_slots);
+    return hipGetLastError();
+}
+
+hipError_t launch_nchw_f32_to_nhwc_f16(const float* x, __half* y, int64_t y_nstride, int32_t y_cstride, int N,
+                                       int C, int HW, uint32_t* y_slots, hipStream_t stream) {
+    if (y_slots && (C % 16 != 0 || C / 16 > kMaxSlots)) return hipErrorInvalidValue;
+    const int64_t total = (int64_t)N * C * HW;
+    hipLaunchKernelGGL(nchw_f32_to_nhwc_f16_kernel, dim3(grid_for(total)), dim3(kThreads), 0, stream, x, y,
+                       y_nstride, y_cstride, C, HW, total, y_slots);
+    return hipGetLastError();
+}
+
+hipError_t launch_nhwc_to_nchw_f32(const void* x, bool f16, int64_t x_nstride, int32_t x_cstride, float* y,
+                                   int N, int C, int HW, hipStream_t stream) {
+    const int64_t total = (int64_t)N * C * HW;
+    if (f16)
+        hipLaunchKernelGGL(nhwc_to_nchw_f32_kernel<__half>, dim3(grid_for(total)), dim3(kThreads), 0, stream,
+                           reinterpret_cast<const __half*>(x), x_nstride, x_cstride, y, C, HW, total);
+    else
+        hipLaunchKernelGGL(nhwc_to_nchw_f32_kernel<float>, dim3(grid_for(total)), dim3(kThreads), 0, stream,
+                           reinterpret_cast<const float*>(x), x_nstride, x_cstride, y, C, HW, total);
+    return hipGetLastError();
+}
+
+}  // namespace aexrt

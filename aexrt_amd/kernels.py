@@ -1,0 +1,218 @@
+"""Host wrappers of the op-level C ABI (one function per hot-path kernel).
+
+PyTorch tensors provide device memory and the stream; every computation runs
+in libaexrt_hip.so.  Activation tensors are NHWC fp16 (``[N, H, W, C]``);
+a channel slice ``t[..., c0:c1]`` is a valid view as long as ``c0`` is a
+multiple of 8 (16 when the view carries amax slots).
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import numpy as np
+
+from . import _lib
+from ._lib import ConvDesc, TensorView, check
+
+SILU = 1
+RESIDUAL = 2
+OUT_F32 = 4
+IN_NCHW_F32 = 8
+
+SRC_RAW_F32 = 0
+SRC_RAW_F16 = 1
+SRC_LAYOUT_OC4_F16 = 2
+SRC_LAYOUT_WINO_F16 = 3
+SRC_LAYOUT_OC8_F16 = 4
+SRC_LAYOUT_WINO_F32 = 5
+SRC_LAYOUT_INT8 = 8
+
+
+def _stream(stream=None):
+    import torch
+
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(int(getattr(stream, "cuda_stream", stream) or 0))
+
+
+def _ptr(t) -> Optional[int]:
+    return None if t is None else int(t.data_ptr())
+
+
+def view(t, slots=None) -> TensorView:
+    """TensorView of an NHWC tensor (or channel slice) ``t`` of shape [N, H, W, C]."""
+    if t.dim() != 4:
+        raise ValueError("activation views are 4-D NHWC")
+    if t.stride(3) != 1 or t.stride(1) != t.shape[2] * t.stride(2):
+        raise ValueError("view must be NHWC with contiguous pixels (channel slices allowed)")
+    return TensorView(data=t.data_ptr(), n_stride=t.stride(0), c_stride=t.stride(2), reserved=0,
+                      amax_slots=_ptr(slots))
+
+
+def new_slots(channels: int, device="cuda"):
+    import torch
+
+    return torch.zeros((channels + 15) // 16, dtype=torch.int32, device=device)
+
+
+def slots_amax(slots) -> float:
+    """Per-tensor amax from a slot tensor (host read)."""
+    a = slots.detach().cpu().numpy().astype(np.int32).view(np.uint32)
+    return float(np.uint32(a.max() if a.size else 0).view(np.float32))
+
+
+def amax_slots(x, slots, stream=None) -> None:
+    n, h, w, c = x.shape
+    v = view(x, slots)
+    check(_lib.lib().aexrt_hip_amax_slots(ctypes.byref(v), n, h, w, c, _stream(stream)), "amax_slots")
+
+
+def amax_nchw(x, stream=None):
+    """Reference amax buffer (C/16 + 1 words) of an NCHW fp16/fp32 tensor."""
+    import torch
+
+    n, c, h, w = x.shape
+    out = torch.empty(c // 16 + 1, dtype=torch.int32, device=x.device)
+    check(_lib.lib().aexrt_hip_amax_nchw(x.data_ptr(), int(x.dtype == torch.float16), n, c, h * w,
+                                          out.data_ptr(), _stream(stream)), "amax_nchw")
+    return out
+
+
+def quantize(x, slots, stream=None):
+    import torch
+
+    n, h, w, c = x.shape
+    q = torch.empty((n, h, w, c), dtype=torch.int8, device=x.device)
+    v = view(x, slots)
+    check(_lib.lib().aexrt_hip_quantize(ctypes.byref(v), n, h, w, c, q.data_ptr(), _stream(stream)),
+          "quantize")
+    return q
+
+
+def quant_pack_nchw(x, amax, per_group: bool = False, stream=None):
+    import torch
+
+    n, c, h, w = x.shape
+    packed = torch.empty(n * (c // 4) * h * w, dtype=torch.int32, device=x.device)
+    check(_lib.lib().aexrt_hip_quant_pack_nchw(x.data_ptr(), int(x.dtype == torch.float16), n, c, h * w,
+                                                amax.data_ptr(), int(per_group), packed.data_ptr(),
+                                                _stream(stream)), "quant_pack_nchw")
+    return packed
+
+
+def can_use_conv_int8(params: Sequence[int], kernel_elems: int) -> bool:
+    d = ConvDesc.from_params(params)
+    return bool(_lib.lib().aexrt_hip_can_use_conv_int8(ctypes.byref(d), kernel_elems))
+
+
+def conv_weight_bytes(params: Sequence[int], algorithm: int) -> int:
+    d = ConvDesc.from_params(params)
+    n = ctypes.c_uint64()
+    check(_lib.lib().aexrt_hip_conv_weight_bytes(ctypes.byref(d), algorithm, ctypes.byref(n)),
+          "conv_weight_bytes")
+    return int(n.value)
+
+
+def pack_conv_weight(params: Sequence[int], algorithm: int, src_layout: int, src: bytes | np.ndarray):
+    """Host repack of a weight payload; returns (packed bytes as uint8 array, scales or None)."""
+    d = ConvDesc.from_params(params)
+    raw = src.tobytes() if isinstance(src, np.ndarray) else bytes(src)
+    nbytes = conv_weight_bytes(params, algorithm)
+    out = np.zeros(nbytes, dtype=np.uint8)
+    scales = np.zeros(d.out_channels, dtype=np.float32) if algorithm in (51, 52, 53) else None
+    buf = ctypes.create_string_buffer(raw, len(raw))
+    check(_lib.lib().aexrt_hip_pack_conv_weight(
+        ctypes.byref(d), algorithm, src_layout, ctypes.cast(buf, ctypes.c_void_p), len(raw),
+        out.ctypes.data, nbytes, None if scales is None else scales.ctypes.data), "pack_conv_weight")
+    return out, scales
+
+
+@dataclass
+class PreparedConv:
+    """Device-resident weights of one conv, ready for :func:`conv2d`."""
+
+    params: list
+    algorithm: int
+    weight: object       # torch uint8 tensor (packed)
+    w_scale: object      # torch float32 [OC] or None
+    bias: object         # torch float32 [OC]
+
+
+def prepare_conv(params, algorithm: int, src_layout: int, src, bias: np.ndarray, device="cuda") -> PreparedConv:
+    import torch
+
+    packed, scales = pack_conv_weight(params, algorithm, src_layout, src)
+    w = torch.from_numpy(packed).to(device)
+    ws = None if scales is None else torch.from_numpy(scales).to(device)
+    b = torch.from_numpy(np.ascontiguousarray(bias, dtype=np.float32)).to(device)
+    return PreparedConv(list(int(v) for v in params), algorithm, w, ws, b)
+
+
+def conv2d(pc: PreparedConv, x, y, *, flags: int = SILU, x_slots=None, y_slots=None, residual=None,
+           acc_out=None, stream=None) -> None:
+    """Runs one conv: x and y are NHWC views (x may be dense fp32 NCHW with IN_NCHW_F32)."""
+    d = ConvDesc.from_params(pc.params)
+    if flags & IN_NCHW_F32:
+        xv = TensorView(data=x.data_ptr(), n_stride=x.stride(0), c_stride=1, reserved=0, amax_slots=None)
+    else:
+        xv = view(x, x_slots)
+    yv = view(y, y_slots)
+    rv = view(residual) if residual is not None else None
+    check(_lib.lib().aexrt_hip_conv2d(
+        ctypes.byref(d), pc.algorithm, flags, ctypes.byref(xv), pc.weight.data_ptr(),
+        _ptr(pc.w_scale), pc.bias.data_ptr(), None if rv is None else ctypes.byref(rv), ctypes.byref(yv),
+        _ptr(acc_out), _stream(stream)), "conv2d")
+
+
+def fill_u32(t, value: int = 0, stream=None) -> None:
+    check(_lib.lib().aexrt_hip_fill_u32(t.data_ptr(), t.numel(), value, _stream(stream)), "fill_u32")
+
+
+def nchw_f32_to_nhwc(x, y, y_slots=None, stream=None) -> None:
+    n, c, h, w = x.shape
+    yv = view(y, y_slots)
+    check(_lib.lib().aexrt_hip_nchw_f32_to_nhwc(x.data_ptr(), n, c, h * w, ctypes.byref(yv),
+                                                 _stream(stream)), "nchw_f32_to_nhwc")
+
+
+def nhwc_to_nchw_f32(x, stream=None):
+    import torch
+
+    n, h, w, c = x.shape
+    y = torch.empty((n, c, h, w), dtype=torch.float32, device=x.device)
+    xv = view(x)
+    check(_lib.lib().aexrt_hip_nhwc_to_nchw_f32(ctypes.byref(xv), int(x.dtype == torch.float16), n, c, h * w,
+                                                 y.data_ptr(), _stream(stream)), "nhwc_to_nchw_f32")
+    return y
+
+
+def copy(src, dst, dst_slots=None, stream=None) -> None:
+    n, h, w, c = src.shape
+    sv, dv = view(src), view(dst, dst_slots)
+    check(_lib.lib().aexrt_hip_copy(ctypes.byref(sv), ctypes.byref(dv), n, h * w, c, _stream(stream)), "copy")
+
+
+def maxpool(x, y, k: int, s: int, p: int, y_slots=None, stream=None) -> None:
+    n, h, w, c = x.shape
+    _, oh, ow, _ = y.shape
+    xv, yv = view(x), view(y, y_slots)
+    check(_lib.lib().aexrt_hip_maxpool(ctypes.byref(xv), ctypes.byref(yv), n, c, h, w, oh, ow, k, s, p,
+                                        _stream(stream)), "maxpool")
+
+
+def resize_nearest(x, y, y_slots=None, stream=None) -> None:
+    n, h, w, c = x.shape
+    _, oh, ow, _ = y.shape
+    xv, yv = view(x), view(y, y_slots)
+    check(_lib.lib().aexrt_hip_resize_nearest(ctypes.byref(xv), ctypes.byref(yv), n, c, h, w, oh, ow,
+                                               _stream(stream)), "resize_nearest")
+
+
+def add(a, b, y, y_slots=None, stream=None) -> None:
+    n, h, w, c = a.shape
+    av, bv, yv = view(a), view(b), view(y, y_slots)
+    check(_lib.lib().aexrt_hip_add(ctypes.byref(av), ctypes.byref(bv), ctypes.byref(yv), n, h * w, c,
+                                    _stream(stream)), "add")

@@ -1,0 +1,188 @@
+/*
+ * aexrt_hip.h -- C ABI of libaexrt_hip.so, the MI355X (gfx950) backend of the
+ * AEXRT W8A8 convolution path.
+ *
+ * Conventions follow the reference's native/aexrt.h: opaque handles, int
+ * return 1 = ok / 0 = failure, a NULL handle on failed creation, and a
+ * diagnostic string from aexrt_hip_get_last_error() (per model:
+ * aexrt_yolo_get_last_error).  Out-structs carry struct_size.  No function
+ * takes a PyTorch type; device memory is passed as plain pointers.
+ *
+ * Two layers:
+ *   1. op-level entry points on device pointers and a hipStream_t (passed as
+ *      void*), one per hot-path kernel: amax, quantize, int8 / fp16 / Winograd
+ *      convolution, and the weight repack they consume;
+ *   2. the model-level API of aexrt.h (device, .aexrt engine load, run,
+ *      errors, timing, conv plan inspection/override), executing the plan on
+ *      HIP kernels with the whole run captured in a HIP graph.
+ */
+#ifndef AEXRT_HIP_H_
+#define AEXRT_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------------- */
+/* Shared types (same field order as native/aexrt.h)                       */
+/* ---------------------------------------------------------------------- */
+
+/* native/aexrt.h:98-115 AexrtConv2DDesc; the 16-u32 replay conv params
+ * (src/aexrt/yolo.py:929-939). */
+typedef struct AexrtConv2DDesc {
+    uint32_t batch;
+    uint32_t in_channels;
+    uint32_t in_h;
+    uint32_t in_w;
+    uint32_t out_channels;
+    uint32_t out_h;
+    uint32_t out_w;
+    uint32_t kernel_h;
+    uint32_t kernel_w;
+    uint32_t stride_h;
+    uint32_t stride_w;
+    uint32_t pad_top;
+    uint32_t pad_left;
+    uint32_t dilation_h;
+    uint32_t dilation_w;
+    uint32_t groups;
+} AexrtConv2DDesc;
+
+/* native/aexrt.h:20-27 */
+typedef struct AexrtYoloDetection {
+    float x1;
+    float y1;
+    float x2;
+    float y2;
+    float score;
+    float class_id;
+} AexrtYoloDetection;
+
+/* An NHWC activation view on the device.  Element (n, h, w, c) of the view is
+ * data[n * n_stride + (h * W + w) * c_stride + c] (elements of the view's
+ * dtype).  amax_slots, when non-NULL, holds one uint32 per 16 channels of
+ * the view: the bit pattern of max|x| over that channel group (all n, h, w).
+ * A channel slice of a larger tensor is a view with a shifted data pointer
+ * and the larger tensor's c_stride. */
+typedef struct AexrtHipTensorView {
+    void* data;
+    int64_t n_stride;
+    int32_t c_stride;
+    uint32_t reserved;
+    uint32_t* amax_slots;
+} AexrtHipTensorView;
+
+/* Conv flags (aexrt_hip_conv2d). */
+#define AEXRT_HIP_CONV_SILU 1u     /* SiLU after bias (CONV_SILU commands)        */
+#define AEXRT_HIP_CONV_RESIDUAL 2u /* + residual view after the activation        */
+#define AEXRT_HIP_CONV_OUT_F32 4u  /* fp32 output view instead of fp16             */
+#define AEXRT_HIP_CONV_IN_NCHW_F32 8u /* x->data is a dense fp32 NCHW tensor (network
+                                       * input of the stem conv; fp16 algorithms only) */
+
+/* Weight source layouts accepted by aexrt_hip_pack_conv_weight: the
+ * reference's packed layouts (src/aexrt/engine.py:59-71) plus raw constants. */
+#define AEXRT_HIP_SRC_RAW_F32 0u          /* [oc][ic][kh][kw] fp32 constant              */
+#define AEXRT_HIP_SRC_RAW_F16 1u          /* [oc][ic][kh][kw] fp16 constant (precision 2) */
+#define AEXRT_HIP_SRC_LAYOUT_OC4_F16 2u   /* layout 2: [oc/4][ic][9][4] fp16              */
+#define AEXRT_HIP_SRC_LAYOUT_WINO_F16 3u  /* layout 3: [oc][ic][4][4] fp16 U = G g G^T    */
+#define AEXRT_HIP_SRC_LAYOUT_OC8_F16 4u   /* layout 4: [oc/8][ic][8] fp16 (1x1)           */
+#define AEXRT_HIP_SRC_LAYOUT_WINO_F32 5u  /* layout 5: [oc][ic][4][4] fp32                */
+#define AEXRT_HIP_SRC_LAYOUT_INT8 8u      /* layout 8: int8 [oc][ic][kk] + oc fp32 scales */
+
+/* ---------------------------------------------------------------------- */
+/* Library / errors                                                        */
+/* ---------------------------------------------------------------------- */
+
+/* Version of this ABI (bumped on incompatible changes). */
+uint32_t aexrt_hip_abi_version(void);
+/* Last error of the calling thread (op-level calls and model creation);
+ * same role as the global fallback of aexrt_yolo_get_last_error
+ * (native/aexrt_d3d12_runtime.cpp:27798-27816). */
+const char* aexrt_hip_get_last_error(void);
+
+/* ---------------------------------------------------------------------- */
+/* Op-level entry points (device pointers; stream = hipStream_t or NULL)   */
+/* ---------------------------------------------------------------------- */
+
+/* a1, producer-side form: atomically folds max|x| of every 16-channel group
+ * of an NHWC fp16 view into x->amax_slots (which the caller clears first).
+ * Replaces the zero + amax dispatches (native/aexrt_d3d12_runtime.cpp:
+ * 3193-3259, recorded at 21622-21644). */
+int aexrt_hip_amax_slots(const AexrtHipTensorView* x, uint32_t batch, uint32_t height,
+                         uint32_t width, uint32_t channels, void* stream);
+
+/* a1, reference form: the reference's amax buffer over an NCHW tensor
+ * (fp16 when is_f16, else fp32).  out[0] = per-tensor max, out[1+g] = max
+ * over memory strip g of 16*N*H*W elements; out has C/16+1 words and is
+ * cleared by this call (native/aexrt_d3d12_runtime.cpp:3219-3259). */
+int aexrt_hip_amax_nchw(const void* x, uint32_t is_f16, uint32_t batch, uint32_t channels,
+                        uint32_t plane, uint32_t* out, void* stream);
+
+/* a2, layout-free form: int8 NHWC (dense, [N*H*W][C]) = round_half_even(
+ * x * 127/amax) with amax = max of the view's amax slots
+ * (native/aexrt_d3d12_runtime.cpp:3337-3344). */
+int aexrt_hip_quantize(const AexrtHipTensorView* x, uint32_t batch, uint32_t height,
+                       uint32_t width, uint32_t channels, int8_t* q, void* stream);
+
+/* a2, reference form: NC/4HW4 uint32 pack of an NCHW tensor with amax[0]
+ * (per_group = 0) or amax[1 + icg/4] (per_group = 1)
+ * (native/aexrt_d3d12_runtime.cpp:3314-3346). */
+int aexrt_hip_quant_pack_nchw(const void* x, uint32_t is_f16, uint32_t batch, uint32_t channels,
+                              uint32_t plane, const uint32_t* amax, uint32_t per_group,
+                              uint32_t* packed, void* stream);
+
+/* a4 (load side): size and host-side repack of a conv weight into the
+ * layout the kernel of `algorithm` consumes.  algorithm is the reference's
+ * AexrtTileFlowConvAlgorithm id (native/aexrt_d3d12_runtime.cpp:8881-8940):
+ * 51/52/53 -> int8 MFMA ([OCp][Kp] int8, K = (ky,kx,c)), 40/46 -> Winograd
+ * ([16][OCp][Cp] fp16), anything else -> fp16 MFMA ([OCp][Kp] fp16).
+ * For int8 the oc scales are written to scale_out (oc floats).  Mirrors the
+ * reference's upload repack (native/aexrt_d3d12_runtime.cpp:21744-21773). */
+int aexrt_hip_conv_weight_bytes(const AexrtConv2DDesc* desc, uint32_t algorithm,
+                                uint64_t* out_nbytes);
+int aexrt_hip_pack_conv_weight(const AexrtConv2DDesc* desc, uint32_t algorithm,
+                               uint32_t src_layout, const void* src, uint64_t src_nbytes,
+                               void* dst, uint64_t dst_nbytes, float* scale_out);
+
+/* a5/a7/a12/a13: one convolution on device views.  x, residual and y are
+ * NHWC views (fp16; y fp32 with AEXRT_HIP_CONV_OUT_F32).  For int8
+ * algorithms the quantization scale comes from x->amax_slots (C/16 slots)
+ * and w_scale holds the oc weight scales; acc_out (optional, int32
+ * [N*OH*OW][OC]) receives the exact accumulators.  When y->amax_slots is
+ * set the epilogue folds max|y| into it.  Replaces record_replay_conv's
+ * dispatch (native/aexrt_d3d12_runtime.cpp:23280-24318). */
+int aexrt_hip_conv2d(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t flags,
+                     const AexrtHipTensorView* x, const void* weight, const float* w_scale,
+                     const float* bias, const AexrtHipTensorView* residual,
+                     const AexrtHipTensorView* y, int32_t* acc_out, void* stream);
+
+/* a10: int8 eligibility of a conv for kernel family kernel_elems (1 or 9),
+ * native/aexrt_d3d12_runtime.cpp:9399-9422, plus this backend's own
+ * requirement in_channels % 16 == 0 (amax is kept per 16 channels). */
+int aexrt_hip_can_use_conv_int8(const AexrtConv2DDesc* desc, uint32_t kernel_elems);
+
+/* Glue ops of the replay stream on NHWC fp16 views. */
+int aexrt_hip_fill_u32(uint32_t* dst, uint64_t count, uint32_t value, void* stream);
+int aexrt_hip_nchw_f32_to_nhwc(const float* x, uint32_t batch, uint32_t channels, uint32_t plane,
+                               const AexrtHipTensorView* y, void* stream);
+int aexrt_hip_nhwc_to_nchw_f32(const AexrtHipTensorView* x, uint32_t is_f16, uint32_t batch,
+                               uint32_t channels, uint32_t plane, float* y, void* stream);
+int aexrt_hip_copy(const AexrtHipTensorView* src, const AexrtHipTensorView* dst, uint32_t batch,
+                   uint32_t plane, uint32_t channels, void* stream);
+int aexrt_hip_maxpool(const AexrtHipTensorView* x, const AexrtHipTensorView* y, uint32_t batch,
+                      uint32_t channels, uint32_t in_h, uint32_t in_w, uint32_t out_h,
+                      uint32_t out_w, uint32_t kernel, uint32_t stride, uint32_t pad, void* stream);
+int aexrt_hip_resize_nearest(const AexrtHipTensorView* x, const AexrtHipTensorView* y,
+                             uint32_t batch, uint32_t channels, uint32_t in_h, uint32_t in_w,
+                             uint32_t out_h, uint32_t out_w, void* stream);
+int aexrt_hip_add(const AexrtHipTensorView* a, const AexrtHipTensorView* b,
+                  const AexrtHipTensorView* y, uint32_t batch, uint32_t plane, uint32_t channels,
+                  void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AEXRT_HIP_H_ */

@@ -1,0 +1,277 @@
+"""GPU parity of every op-level kernel against the CPU oracle (through the C ABI).
+
+int8 tensors, int32 accumulators and amax bit patterns must match exactly;
+fp16 outputs within 1e-2 of the output range; fp32 outputs within 1e-4.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+from aexrt_amd import kernels as K
+from aexrt_amd import packing
+from tests.helpers import c2_input, group16_weight, he_weight, nchw_to_nhwc, nhwc_to_nchw, tol_range
+
+pytestmark = pytest.mark.gpu
+
+FP16_TOL = 1e-2
+FP32_TOL = 1e-4
+
+
+def _dev_nhwc(x_nchw: np.ndarray, cuda, pad_c: int = 0):
+    import torch
+
+    a = nchw_to_nhwc(x_nchw.astype(np.float16))
+    if pad_c:
+        a = np.concatenate([a, np.zeros(a.shape[:3] + (pad_c,), np.float16)], axis=3)
+    return torch.from_numpy(a).to(cuda)
+
+
+def _u32(t) -> np.ndarray:
+    return t.detach().cpu().numpy().view(np.uint32)
+
+
+def test_amax_slots_and_quantize_bit_exact_c2(cuda):
+    import torch
+
+    x = c2_input(seed=1)
+    xd = _dev_nhwc(x, cuda)
+    slots = K.new_slots(128, cuda)
+    K.amax_slots(xd, slots)
+    q = K.quantize(xd, slots)
+    torch.cuda.synchronize()
+    got_slots = _u32(slots)
+    # per-16-channel group max, exact
+    want = np.array([np.float32(np.abs(x[:, g * 16:(g + 1) * 16]).max()).view(np.uint32)
+                     for g in range(8)], dtype=np.uint32)
+    np.testing.assert_array_equal(got_slots, want)
+    a = O.amax(x)
+    assert np.float32(a).view(np.uint32) == got_slots.max()
+    q_ref = O.quantize(x, a)
+    np.testing.assert_array_equal(nhwc_to_nchw(q.cpu().numpy()), q_ref)
+
+
+@pytest.mark.parametrize("n,c,h,w,f16", [(1, 128, 40, 40, True), (2, 48, 9, 7, False), (3, 24, 5, 5, True),
+                                          (1, 8, 4, 4, False)])
+def test_amax_nchw_reference_strips(cuda, n, c, h, w, f16):
+    import torch
+
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((n, c, h, w)).astype(np.float32) * 3
+    if f16:
+        x = x.astype(np.float16).astype(np.float32)
+    xd = torch.from_numpy(x.astype(np.float16 if f16 else np.float32)).to(cuda)
+    got = _u32(K.amax_nchw(xd))
+    np.testing.assert_array_equal(got, O.amax_slots(x))
+
+
+@pytest.mark.parametrize("per_group", [False, True])
+@pytest.mark.parametrize("n", [1, 2])
+def test_quant_pack_nchw_reference_layout(cuda, per_group, n):
+    import torch
+
+    rng = np.random.default_rng(11 + n)
+    x = (rng.standard_normal((n, 64, 12, 10)) * 2).astype(np.float16).astype(np.float32)
+    slots = O.amax_slots(x)
+    xd = torch.from_numpy(x.astype(np.float16)).to(cuda)
+    sd = torch.from_numpy(slots.view(np.int32)).to(cuda)
+    got = K.quant_pack_nchw(xd, sd, per_group=per_group).cpu().numpy().view(np.uint32)
+    np.testing.assert_array_equal(got, O.quant_pack(x, slots, per_group=per_group))
+
+
+INT8_CASES = [
+    # (name, n, ic, h, w, oc, k, s, seed)
+    ("c2_1x1_128_256_40", 1, 128, 40, 40, 256, 1, 1, 1),
+    ("1x1_32_16_ragged", 2, 32, 7, 9, 16, 1, 1, 21),
+    ("3x3s1_64_64_20_b2", 2, 64, 20, 20, 64, 3, 1, 22),
+    ("3x3s1_48_32_odd", 1, 48, 11, 13, 32, 3, 1, 23),
+    ("3x3s2_64_128_160", 1, 64, 160, 160, 128, 3, 2, 2),
+    ("3x3s2_16_32_odd", 3, 16, 17, 15, 32, 3, 2, 24),
+    ("3x3s1_256_256_10", 1, 256, 10, 10, 256, 3, 1, 25),
+]
+
+
+def _run_int8(cuda, n, ic, h, w, oc, k, s, seed, *, silu=True, out_f32=False, x=None):
+    import torch
+
+    rng = np.random.default_rng(seed)
+    if x is None:
+        x = rng.standard_normal((n, ic, h, w)).astype(np.float16).astype(np.float32)
+    wt = group16_weight(rng, oc, ic, k)
+    b = packing.fp16_round(rng.uniform(-0.1, 0.1, oc).astype(np.float32))
+    desc = O.conv_desc(n, ic, h, w, oc, k, s, k // 2)
+    alg = 51 if k == 1 else (53 if s == 2 else 52)
+    pc = K.prepare_conv(desc, alg, K.SRC_LAYOUT_INT8, packing.pack_conv_int8(wt, fp16_engine=True), b,
+                        device=cuda)
+    xd = _dev_nhwc(x, cuda)
+    xs = K.new_slots(ic, cuda)
+    K.amax_slots(xd, xs)
+    _, _, oh, ow = O.out_shape(desc)
+    y = torch.empty((n, oh, ow, oc), dtype=torch.float32 if out_f32 else torch.float16, device=cuda)
+    ys = K.new_slots(oc, cuda)
+    acc = torch.empty((n * oh * ow, oc), dtype=torch.int32, device=cuda)
+    flags = (K.SILU if silu else 0) | (K.OUT_F32 if out_f32 else 0)
+    K.conv2d(pc, xd, y, flags=flags, x_slots=xs, y_slots=ys, acc_out=acc)
+    torch.cuda.synchronize()
+    a, qa, qw, ws, acc_ref, y_ref = O.w8a8_conv(x, wt, b, desc, silu=silu, fp16_engine=True)
+    got_acc = nhwc_to_nchw(acc.cpu().numpy().reshape(n, oh, ow, oc))
+    return dict(acc=got_acc, acc_ref=acc_ref, y=nhwc_to_nchw(y.float().cpu().numpy()), y_ref=y_ref,
+                slots=_u32(ys), y_raw=y, qa=qa, a=a)
+
+
+@pytest.mark.parametrize("case", INT8_CASES, ids=[c[0] for c in INT8_CASES])
+def test_int8_conv_parity(cuda, case):
+    _, n, ic, h, w, oc, k, s, seed = case
+    r = _run_int8(cuda, n, ic, h, w, oc, k, s, seed)
+    np.testing.assert_array_equal(r["acc"], r["acc_ref"])
+    err, allowed = tol_range(r["y_ref"], r["y"], FP16_TOL)
+    assert err <= allowed, (err, allowed)
+    # epilogue amax slots == max |fp16 output| per 16-channel group
+    y = r["y"]
+    want = np.array([np.float32(np.abs(y[:, g * 16:(g + 1) * 16]).max()).view(np.uint32)
+                     for g in range(oc // 16)], dtype=np.uint32)
+    np.testing.assert_array_equal(r["slots"], want)
+
+
+def test_int8_conv_fp32_output_and_linear(cuda):
+    r = _run_int8(cuda, 1, 128, 40, 40, 256, 1, 1, 1, silu=False, out_f32=True, x=c2_input(1))
+    np.testing.assert_array_equal(r["acc"], r["acc_ref"])
+    err, allowed = tol_range(r["y_ref"], r["y"], FP32_TOL)
+    assert err <= allowed, (err, allowed)
+
+
+def test_int8_conv_all_zero_input(cuda):
+    """amax == 0 packs zeros: output is bias (then SiLU), accumulators zero."""
+    x = np.zeros((1, 32, 8, 8), np.float32)
+    r = _run_int8(cuda, 1, 32, 8, 8, 16, 3, 1, 5, x=x)
+    assert not r["acc"].any()
+    err, allowed = tol_range(r["y_ref"], r["y"], FP16_TOL)
+    assert err <= max(allowed, 1e-3)
+
+
+FP16_CASES = [
+    ("stem_nchw_3_16_s2", 2, 3, 64, 64, 16, 3, 2, True),
+    ("1x1_64_64", 1, 64, 20, 20, 64, 1, 1, False),
+    ("3x3s1_80_80_head", 1, 80, 10, 10, 80, 3, 1, False),
+    ("3x3s2_64_128_160", 1, 64, 160, 160, 128, 3, 2, False),
+]
+
+
+@pytest.mark.parametrize("case", FP16_CASES, ids=[c[0] for c in FP16_CASES])
+def test_fp16_conv_parity(cuda, case):
+    import torch
+
+    _, n, ic, h, w, oc, k, s, nchw_in = case
+    rng = np.random.default_rng(31)
+    x = rng.standard_normal((n, ic, h, w)).astype(np.float32)
+    wt = he_weight(rng, oc, ic, k)
+    b = packing.fp16_round(rng.uniform(-0.1, 0.1, oc).astype(np.float32))
+    desc = O.conv_desc(n, ic, h, w, oc, k, s, k // 2)
+    pc = K.prepare_conv(desc, 5, K.SRC_RAW_F32, wt, b, device=cuda)
+    _, _, oh, ow = O.out_shape(desc)
+    y = torch.empty((n, oh, ow, oc), dtype=torch.float16, device=cuda)
+    if nchw_in:
+        xd = torch.from_numpy(x).to(cuda)
+        K.conv2d(pc, xd, y, flags=K.SILU | K.IN_NCHW_F32)
+        x_ref = O.round_f16(x)
+    else:
+        x_ref = O.round_f16(x)
+        xd = _dev_nhwc(x_ref, cuda)
+        K.conv2d(pc, xd, y, flags=K.SILU)
+    torch.cuda.synchronize()
+    y_ref = O.cpu_conv2d(x_ref, O.round_f16(wt), b, desc, silu=True)
+    err, allowed = tol_range(y_ref, nhwc_to_nchw(y.float().cpu().numpy()), FP16_TOL)
+    assert err <= allowed, (err, allowed)
+
+
+def test_fp16_conv_residual_into_channel_slice(cuda):
+    """Bottleneck tail: y[..., 32:64] = silu(conv(x)) + r, written into a wider tensor."""
+    import torch
+
+    rng = np.random.default_rng(41)
+    n, c, h, w = 2, 32, 12, 12
+    x = O.round_f16(rng.standard_normal((n, c, h, w)).astype(np.float32))
+    r = O.round_f16(rng.standard_normal((n, c, h, w)).astype(np.float32))
+    wt = he_weight(rng, c, c, 3)
+    b = packing.fp16_round(rng.uniform(-0.1, 0.1, c).astype(np.float32))
+    desc = O.conv_desc(n, c, h, w, c, 3, 1, 1)
+    pc = K.prepare_conv(desc, 5, K.SRC_RAW_F32, wt, b, device=cuda)
+    big = torch.zeros((n, h, w, 96), dtype=torch.float16, device=cuda)
+    slots = K.new_slots(96, cuda)
+    K.conv2d(pc, _dev_nhwc(x, cuda), big[..., 32:64], flags=K.SILU | K.RESIDUAL, residual=_dev_nhwc(r, cuda),
+             y_slots=slots[2:4])
+    torch.cuda.synchronize()
+    y_ref = O.cpu_conv2d(x, O.round_f16(wt), b, desc, silu=True) + r
+    got = nhwc_to_nchw(big.float().cpu().numpy())
+    err, allowed = tol_range(y_ref, got[:, 32:64], FP16_TOL)
+    assert err <= allowed
+    assert not got[:, :32].any() and not got[:, 64:].any()
+    s = _u32(slots)
+    assert s[0] == 0 and s[1] == 0 and s[4] == 0 and s[5] == 0
+    for g in (2, 3):
+        assert s[g] == np.float32(np.abs(got[:, g * 16:(g + 1) * 16]).max()).view(np.uint32)
+
+
+WINO_CASES = [
+    ("64_64_20", 1, 64, 20, 20, 64),
+    ("96_64_20x18", 1, 96, 20, 18, 64),
+    ("32_48_b2_8x6", 2, 32, 8, 6, 48),
+    ("64_64_40", 1, 64, 40, 40, 64),
+]
+
+
+@pytest.mark.parametrize("case", WINO_CASES, ids=[c[0] for c in WINO_CASES])
+def test_winograd_parity(cuda, case):
+    import torch
+
+    _, n, ic, h, w, oc = case
+    rng = np.random.default_rng(51)
+    x = O.round_f16(rng.standard_normal((n, ic, h, w)).astype(np.float32))
+    wt = he_weight(rng, oc, ic, 3)
+    b = packing.fp16_round(rng.uniform(-0.1, 0.1, oc).astype(np.float32))
+    desc = O.conv_desc(n, ic, h, w, oc, 3, 1, 1)
+    pc = K.prepare_conv(desc, 40, K.SRC_LAYOUT_WINO_F16, packing.pack_winograd_f2x2_fp16(wt), b, device=cuda)
+    y = torch.empty((n, h, w, oc), dtype=torch.float16, device=cuda)
+    K.conv2d(pc, _dev_nhwc(x, cuda), y, flags=K.SILU)
+    torch.cuda.synchronize()
+    u = O.winograd_weight(wt, to_f16=True)
+    y_ref = O.winograd_conv(x, u, b, desc)
+    err, allowed = tol_range(y_ref, nhwc_to_nchw(y.float().cpu().numpy()), FP16_TOL)
+    assert err <= allowed, (err, allowed)
+
+
+def test_glue_ops(cuda):
+    import torch
+
+    rng = np.random.default_rng(61)
+    x = O.round_f16(rng.standard_normal((2, 64, 10, 10)).astype(np.float32))
+    xd = _dev_nhwc(x, cuda)
+    # maxpool k5 s1 p2 (SPPF)
+    y = torch.empty_like(xd)
+    ys = K.new_slots(64, cuda)
+    K.maxpool(xd, y, 5, 1, 2, y_slots=ys)
+    # nearest resize x2
+    up = torch.empty((2, 20, 20, 64), dtype=torch.float16, device=cuda)
+    K.resize_nearest(xd, up)
+    # add
+    s = torch.empty_like(xd)
+    K.add(xd, y, s)
+    # copy into a channel slice
+    big = torch.zeros((2, 10, 10, 128), dtype=torch.float16, device=cuda)
+    K.copy(xd, big[..., 64:])
+    torch.cuda.synchronize()
+    mp = O.maxpool(x, 5, 1, 2)
+    np.testing.assert_array_equal(nhwc_to_nchw(y.float().cpu().numpy()), mp)
+    np.testing.assert_array_equal(_u32(ys), [np.float32(np.abs(mp[:, g * 16:(g + 1) * 16]).max()).view(np.uint32)
+                                             for g in range(4)])
+    np.testing.assert_array_equal(nhwc_to_nchw(up.float().cpu().numpy()), O.resize_nearest(x, 20, 20))
+    np.testing.assert_array_equal(nhwc_to_nchw(s.float().cpu().numpy()), O.round_f16(x + mp))
+    np.testing.assert_array_equal(nhwc_to_nchw(big.float().cpu().numpy())[:, 64:], x)
+    # layout round trip
+    xf = torch.from_numpy(rng.standard_normal((1, 16, 5, 7)).astype(np.float32)).to(cuda)
+    nh = torch.empty((1, 5, 7, 16), dtype=torch.float16, device=cuda)
+    K.nchw_f32_to_nhwc(xf, nh)
+    back = K.nhwc_to_nchw_f32(nh)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(back.cpu().numpy(), O.round_f16(xf.cpu().numpy()))
