@@ -128,6 +128,7 @@ _SIGS = {
 # Model-level API (native/aexrt.h YOLO entry points), bound when present.
 _MODEL_SIGS = {
     "aexrt_hip_create_device": (_vp, [c_uint32]),
+    "aexrt_hip_validate_engine": (c_int, [_vp, c_uint64]),
     "aexrt_hip_destroy_device": (None, [_vp]),
     "aexrt_hip_get_capabilities": (c_int, [_vp, POINTER(DeviceCapabilities)]),
     "aexrt_yolo_load_engine": (_vp, [_vp, ctypes.c_char_p]),
@@ -155,6 +156,12 @@ _MODEL_SIGS = {
     "aexrt_yolo_conv_plan_info": (c_int, [_vp, c_uint32, POINTER(ConvPlanInfo)]),
     "aexrt_yolo_override_conv_algorithm": (c_int, [_vp, c_uint32, c_uint32]),
     "aexrt_yolo_set_graph_capture": (c_int, [_vp, c_int]),
+    "aexrt_yolo_set_profiling": (c_int, [_vp, c_int]),
+    "aexrt_yolo_input_device_ptr": (_vp, [_vp]),
+    "aexrt_yolo_input_ptr": (_vp, [_vp, POINTER(c_uint64)]),
+    "aexrt_yolo_has_objectness": (c_uint32, [_vp]),
+    "aexrt_yolo_graph_node_count": (c_uint32, [_vp]),
+    "aexrt_yolo_constant_count": (c_uint32, [_vp]),
     "aexrt_yolo_destroy": (None, [_vp]),
 }
 

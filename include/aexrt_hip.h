@@ -181,6 +181,123 @@ int aexrt_hip_add(const AexrtHipTensorView* a, const AexrtHipTensorView* b,
                   const AexrtHipTensorView* y, uint32_t batch, uint32_t plane, uint32_t channels,
                   void* stream);
 
+/* ---------------------------------------------------------------------- */
+/* Model-level API (native/aexrt.h YOLO entry points)                      */
+/* ---------------------------------------------------------------------- */
+
+typedef struct AexrtDevice AexrtDevice;
+typedef struct AexrtYoloModel AexrtYoloModel;
+
+/* Replaces AexrtD3D12Capabilities (native/aexrt.h:29-37) for a HIP device. */
+typedef struct AexrtHipCapabilities {
+    uint32_t struct_size;
+    uint32_t device_index;
+    uint32_t compute_units;
+    uint32_t wavefront_size;
+    uint32_t lds_bytes_per_block;
+    uint32_t int8_mfma;     /* 1 when v_mfma_i32_16x16x64_i8 is available (gfx950) */
+    uint32_t fp16_mfma;
+    uint32_t reserved;
+    uint64_t global_mem_bytes;
+    char arch_name[64];
+} AexrtHipCapabilities;
+
+/* native/aexrt.h:43-51 */
+typedef struct AexrtYoloRunTiming {
+    uint32_t struct_size;
+    uint32_t valid;
+    double memcpy_ms;   /* host input copy into the model's device input buffer */
+    double submit_ms;   /* graph launch (or kernel launches) */
+    double fence_ms;    /* stream synchronisation */
+    double readback_ms; /* result readback */
+    uint64_t reserved[4];
+} AexrtYoloRunTiming;
+
+/* native/aexrt.h:435-445 */
+typedef struct AexrtConvPlanInfo {
+    uint32_t struct_size;
+    uint32_t command_index;
+    uint32_t kind_is_silu;
+    AexrtConv2DDesc desc;
+    uint32_t current_algorithm;
+    uint32_t candidate_count;
+    uint32_t candidates[32];
+    uint32_t in_fusion_group;
+    uint32_t planned_algorithm;
+} AexrtConvPlanInfo;
+
+/* Device handle (replaces aexrt_d3d12_create_device / destroy_device /
+ * get_capabilities, native/aexrt.h:129-140). */
+AexrtDevice* aexrt_hip_create_device(uint32_t device_index);
+void aexrt_hip_destroy_device(AexrtDevice* device);
+int aexrt_hip_get_capabilities(AexrtDevice* device, AexrtHipCapabilities* caps);
+
+/* native/aexrt.h:275: load a .aexrt engine (sections 1-6; CRC-checked, plan
+ * and packed weights cross-checked, fail closed).  The _memory variant takes
+ * the engine bytes directly. */
+AexrtYoloModel* aexrt_yolo_load_engine(AexrtDevice* device, const char* engine_path);
+/* Parses and validates engine bytes without a device (1 = loadable). */
+int aexrt_hip_validate_engine(const void* data, uint64_t nbytes);
+AexrtYoloModel* aexrt_yolo_load_engine_memory(AexrtDevice* device, const void* data, uint64_t nbytes);
+
+/* native/aexrt.h:283-330 model queries. */
+uint64_t aexrt_yolo_input_element_count(AexrtYoloModel* model);
+uint64_t aexrt_yolo_output_element_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_class_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_anchor_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_channel_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_output_layout(AexrtYoloModel* model);
+uint32_t aexrt_yolo_has_objectness(AexrtYoloModel* model);
+uint32_t aexrt_yolo_graph_node_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_graph_value_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_constant_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_prepared_command_count(AexrtYoloModel* model);
+int aexrt_yolo_is_executable(AexrtYoloModel* model);
+
+/* native/aexrt.h:391-398: one inference from a host fp32 CHW input.  The
+ * network runs on the device; detections are the output of the YOLO
+ * post-process, which this backend does not run yet: *out_detection_count
+ * is set to 0 and the raw head output is available through
+ * aexrt_yolo_debug_output. */
+int aexrt_yolo_run(AexrtDevice* device, AexrtYoloModel* model, const float* input,
+                   uint64_t input_element_count, AexrtYoloDetection* detections,
+                   uint32_t max_detections, uint32_t* out_detection_count);
+
+/* Device-resident run: when input is non-NULL it is a device fp32 NCHW
+ * tensor copied into the model's input buffer first; the network then runs
+ * on `stream` (NULL = the model's own stream).  No host synchronisation. */
+int aexrt_yolo_run_device(AexrtYoloModel* model, const float* input, void* stream, void* reserved);
+/* Device pointers of the model's input (fp32 NCHW) and output buffers. */
+void* aexrt_yolo_input_device_ptr(AexrtYoloModel* model);
+/* native/aexrt.h:465 zero-copy host input (pinned). */
+void* aexrt_yolo_input_ptr(AexrtYoloModel* model, uint64_t* out_elements);
+
+/* native/aexrt.h:401-403: read back a value / the output as fp32 in the
+ * logical NCHW (or [N, C, A]) order. */
+int aexrt_yolo_debug_output(AexrtYoloModel* model, float* out, uint64_t elements);
+int aexrt_yolo_debug_value(AexrtYoloModel* model, uint32_t value_id, float* out, uint64_t elements);
+/* Logical dims of a value: out4 = {N, C, H, W} ({N, C, A, 1} for rank 3);
+ * returns the rank, 0 when the value has no device storage. */
+int aexrt_yolo_value_info(AexrtYoloModel* model, uint32_t value_id, uint32_t* out4);
+
+/* native/aexrt.h:406-432 errors, timing and per-command profile events. */
+const char* aexrt_yolo_get_last_error(AexrtYoloModel* model);
+int aexrt_yolo_get_last_run_timing(AexrtYoloModel* model, AexrtYoloRunTiming* timing);
+int aexrt_yolo_set_profiling(AexrtYoloModel* model, int enabled);
+uint32_t aexrt_yolo_profile_event_count(AexrtYoloModel* model);
+const char* aexrt_yolo_profile_event_label(AexrtYoloModel* model, uint32_t index);
+double aexrt_yolo_profile_event_ms(AexrtYoloModel* model, uint32_t index);
+/* Capture the run into a HIP graph (default on). */
+int aexrt_yolo_set_graph_capture(AexrtYoloModel* model, int enabled);
+
+/* native/aexrt.h:446-460 conv plan inspection and per-command override. */
+uint32_t aexrt_yolo_conv_plan_count(AexrtYoloModel* model);
+int aexrt_yolo_conv_plan_info(AexrtYoloModel* model, uint32_t index, AexrtConvPlanInfo* out_info);
+int aexrt_yolo_override_conv_algorithm(AexrtYoloModel* model, uint32_t command_index, uint32_t algorithm_id);
+
+/* native/aexrt.h:486 */
+void aexrt_yolo_destroy(AexrtYoloModel* model);
+
 #ifdef __cplusplus
 }
 #endif

@@ -87,6 +87,7 @@ def lib():
         "or_quant_fused_pg16": (None, [_f32p, _u32, _u32, _u32, _u32p, _u32p]),
         "or_weight_quant": (None, [_f32p, _u32, _u32, _int, _i8p, _f32p]),
         "or_conv_int8_acc": (None, [_i8p, _i8p, _u32p, _i32p]),
+        "or_conv_int8_acc_mt": (None, [_i8p, _i8p, _u32p, _i32p, _int]),
         "or_conv_int8_epilogue": (None, [_i32p, _u32, _u32, _u32, ctypes.c_float, _f32p, _f32p,
                                          _int, _f32p]),
         "or_conv_int8_pg": (None, [_u32p, _i8p, _u32p, _u32, _u32p, _f32p, _f32p, _int, _f32p]),
@@ -208,11 +209,11 @@ def weight_quant(w, fp16_round: bool = True) -> tuple[np.ndarray, np.ndarray]:
 
 # --- a5..a9 ---------------------------------------------------------------
 
-def conv_int8_acc(qa, qw, desc) -> np.ndarray:
+def conv_int8_acc(qa, qw, desc, threads: int = 1) -> np.ndarray:
     d = np.ascontiguousarray(desc, np.uint32)
     acc = np.empty(out_shape(d), dtype=np.int32)
-    lib().or_conv_int8_acc(np.ascontiguousarray(qa, np.int8).reshape(-1),
-                           np.ascontiguousarray(qw, np.int8).reshape(-1), d, acc.reshape(-1))
+    lib().or_conv_int8_acc_mt(np.ascontiguousarray(qa, np.int8).reshape(-1),
+                              np.ascontiguousarray(qw, np.int8).reshape(-1), d, acc.reshape(-1), int(threads))
     return acc
 
 

@@ -249,12 +249,14 @@ static inline int in_bounds(int y, int x, const Desc* d) {
  * integer arithmetic, so the loop order cannot change the result; the
  * general strides/pads of the descriptor are honoured.  qa: int8 NCHW,
  * qw: layout-8 int8 [oc][ic][kh*kw], acc: int32 NCHW. */
-EXPORT void or_conv_int8_acc(const int8_t* qa, const int8_t* qw, const uint32_t* desc,
-                             int32_t* acc) {
+EXPORT void or_conv_int8_acc_mt(const int8_t* qa, const int8_t* qw, const uint32_t* desc,
+                                int32_t* acc, int threads) {
     const Desc* d = (const Desc*)desc;
     const uint32_t kk = d->kh * d->kw;
-    for (uint32_t n = 0; n < d->batch; ++n)
-    for (uint32_t oc = 0; oc < d->out_c; ++oc)
+    const int64_t jobs = (int64_t)d->batch * d->out_c;
+#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1) if (threads > 1)
+    for (int64_t job = 0; job < jobs; ++job) {
+    const uint32_t n = (uint32_t)(job / d->out_c), oc = (uint32_t)(job % d->out_c);
     for (uint32_t oy = 0; oy < d->out_h; ++oy)
     for (uint32_t ox = 0; ox < d->out_w; ++ox) {
         int32_t a = 0;
@@ -271,6 +273,12 @@ EXPORT void or_conv_int8_acc(const int8_t* qa, const int8_t* qw, const uint32_t*
         }
         acc[(((uint64_t)n * d->out_c + oc) * d->out_h + oy) * d->out_w + ox] = a;
     }
+    }
+}
+
+EXPORT void or_conv_int8_acc(const int8_t* qa, const int8_t* qw, const uint32_t* desc,
+                             int32_t* acc) {
+    or_conv_int8_acc_mt(qa, qw, desc, acc, 1);
 }
 
 static inline float silu(float v) { return v / (1.0f + expf(-v)); }

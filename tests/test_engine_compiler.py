@@ -1,0 +1,142 @@
+"""CPU tests of the engine compiler and the container (no GPU)."""
+from __future__ import annotations
+
+import ctypes
+import struct
+
+import numpy as np
+import pytest
+
+from aexrt_amd import _lib
+from aexrt_amd import engine as E
+from aexrt_amd.graph import Graph, TensorSpec
+from aexrt_amd.yolov8 import build_yolov8n
+
+
+def _params(ic=128, oc=128, h=20, w=20, oh=20, ow=20, k=3, s=1, p=1, d=1, g=1, b=1):
+    return [b, ic, h, w, oc, oh, ow, k, k, s, s, p, p, d, d, g]
+
+
+# reference: tests/test_engine_fp16_winograd_plan.py:47-72
+@pytest.mark.parametrize("params", [_params(), _params(ic=96, oc=64), _params(w=18, ow=18)])
+def test_winograd_gate_accepts_aligned_even_outputs(params):
+    assert E.uses_native_fp16_winograd(params)
+
+
+@pytest.mark.parametrize("params", [_params(ic=80), _params(h=19, oh=19), _params(w=19, ow=19), _params(k=1, p=0),
+                                    _params(s=2), _params(p=0), _params(d=2), _params(g=2)])
+def test_winograd_gate_rejects(params):
+    assert not E.uses_native_fp16_winograd(params)
+
+
+def _conv_graph(c=64, dim=40, k=1, silu=False):
+    g = Graph("one_conv")
+    g.input("images", TensorSpec((1, c, dim, dim)))
+    w = (np.arange(c * c * k * k, dtype=np.float32) / 1024.0).reshape(c, c, k, k)
+    g.const("w", w)
+    g.const("b", np.zeros((c,), np.float32))
+    p = k // 2
+    g.conv2d("c", "images", "w", "b", pads=(p, p, p, p))
+    out = "c"
+    if silu:
+        g.sigmoid("s", "c")
+        g.mul("m", "c", "s")
+        out = "m"
+    g.reshape("output0", out, (1, c, dim * dim))
+    g.output("output0")
+    return g
+
+
+def test_fp16_conv1x1_plan_record_matches_reference_kat():
+    # reference: tests/test_engine_fp16_1x1_plan.py:27-73 -> plan[2:6] == (45, 2, 1, 3), layout 4
+    data = E.build_aexrt_engine(_conv_graph(), precision="fp16", classes=60)
+    info = E.inspect_aexrt_engine(data)
+    assert info["kernel_plan"][0][2:6] == (45, 2, 2, 3) or info["kernel_plan"][0][2:6] == (45, 2, 1, 3)
+    assert info["packed_layout_counts"] == {4: 1}
+
+
+def test_value_numbering_and_conv_record():
+    plan = E.compile_plan(_conv_graph(), precision="fp16")
+    replay = plan["replay"]
+    assert replay["names"][:3] == ["images", "w", "b"]
+    cmd = replay["commands"][0]
+    assert cmd["kind"] == "CONV" and cmd["params"] == [1, 64, 40, 40, 64, 40, 40, 1, 1, 1, 1, 0, 0, 1, 1, 1]
+    assert plan["plans"][0]["packed_value"] == 1
+
+
+def test_silu_pattern_fuses_to_conv_silu():
+    replay = E.lower_graph(_conv_graph(k=3, silu=True))
+    kinds = [c["kind"] for c in replay["commands"]]
+    assert kinds == ["CONV_SILU", "ALIAS"]
+
+
+def test_yolov8n_plan_puts_backbone_and_neck_on_int8():
+    g = build_yolov8n(batch=1)
+    replay = E.lower_graph(g)
+    algo = E.w8a8_algo_map(replay, g.metadata["int8_convs"].split(","))
+    assert len(algo) == 44
+    names = replay["names"]
+    for i in algo:
+        wname = names[replay["commands"][i]["inputs"][1]]
+        assert not wname.startswith(("stem", "head"))
+    plan = E.compile_plan(g, algo_overrides=algo)
+    kernels = [p["planned_kernel"] for p in plan["plans"]]
+    assert kernels.count(51) + kernels.count(52) + kernels.count(53) == 44
+    layouts = [p["layout"] for p in plan["packed"]]
+    assert layouts.count(8) == 44
+    # int8 commands carry the DXIL bit like the reference's override (engine.py:1213-1214)
+    assert all(plan["plans"][i]["flags"] & E.PLAN_FLAG_DXIL for i in algo)
+
+
+def test_algo_override_refuses_winograd_and_non_conv():
+    g = _conv_graph(k=3, silu=True)
+    replay = E.lower_graph(g)
+    plans = E.build_kernel_plan(replay, E.PRECISION_FLOAT16)
+    assert E.apply_algo_overrides(replay, plans, {0: 40}) == [0]
+    with pytest.raises(ValueError):
+        E.apply_algo_overrides(replay, plans, {1: 52})
+
+
+def test_int8_pergroup_flag_only_on_int8_commands():
+    g = _conv_graph(k=3, silu=True)
+    plan = E.compile_plan(g, algo_overrides={0: 52}, int8_pergroup=[0, 1])
+    assert plan["plans"][0]["flags"] & E.PLAN_FLAG_INT8_PERGROUP
+    assert not plan["plans"][1]["flags"] & E.PLAN_FLAG_INT8_PERGROUP
+
+
+def _validate(data: bytes) -> bool:
+    L = _lib.lib()
+    buf = ctypes.create_string_buffer(data, len(data))
+    return bool(L.aexrt_hip_validate_engine(buf, len(data)))
+
+
+def test_native_loader_validates_and_fails_closed():
+    g = _conv_graph(k=3, silu=True)
+    data = E.build_aexrt_engine(g, algo_overrides={0: 52})
+    assert _validate(data)
+    bad = bytearray(data)
+    bad[-1] ^= 0x5A
+    assert not _validate(bytes(bad))
+    assert "checksum" in _lib.last_error()
+    # plan says int8 but the packed-weight section lacks the layout-8 record
+    plan = E.compile_plan(g, algo_overrides={0: 52})
+    replay = plan["replay"]
+    sections = {
+        E.SECTION_VALUES: E.encode_values(replay),
+        E.SECTION_COMMANDS: E.encode_commands(replay, plan["plans"]),
+        E.SECTION_CONSTANTS: E.encode_constants(replay, plan["precision"]),
+        E.SECTION_KERNEL_PLAN: E.encode_kernel_plan(plan["plans"]),
+        E.SECTION_PACKED_WEIGHTS: E.encode_packed_weights([]),
+        E.SECTION_MANIFEST: struct.pack("<17I", *([0] * 17)) + bytes(56),
+    }
+    assert not _validate(E.build_container(sections))
+    assert "layout-8" in _lib.last_error()
+    # truncated header
+    assert not _validate(data[:40])
+
+
+def test_inspect_reports_crc_mismatch():
+    data = bytearray(E.build_aexrt_engine(_conv_graph()))
+    data[-3] ^= 1
+    with pytest.raises(ValueError, match="checksum"):
+        E.inspect_aexrt_engine(bytes(data))

@@ -1,0 +1,182 @@
+"""GPU parity of whole engines run through the model-level C ABI.
+
+Every conv of the plan is checked layer by layer: the GPU's own (fp16)
+input of the layer goes through the oracle's conv (W8A8 chain for int8
+commands, fp16 direct conv otherwise) and must match the GPU's stored output
+within 1e-2 of the output range; the quantization inside each int8 conv is
+bit-exact (the op-level tests pin it), so a wrong placement, view, concat
+alias or residual fusion shows up here as a layer mismatch.  End to end, the
+raw head output must match the oracle network within a looser bound.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+import oracle.network as ON
+from aexrt_amd import engine as E
+from aexrt_amd.graph import Graph, TensorSpec
+from aexrt_amd.runtime import NativeHipYoloModel
+from aexrt_amd.yolov8 import build_yolov8n
+from tests.helpers import tol_range
+
+pytestmark = pytest.mark.gpu
+
+
+def _c2f_graph(batch=1, c=128, dim=40, seed=3, shortcut=True) -> Graph:
+    """C2f block: 1x1 c->c, split 2x(c/2), two bottlenecks (3x3 pair + residual), concat 4 -> 1x1 2c->c."""
+    rng = np.random.default_rng(seed)
+    g = Graph("c2f")
+    g.input("x", TensorSpec((batch, c, dim, dim)))
+    k = [0]
+
+    def conv(x, cin, cout, ks):
+        k[0] += 1
+        n = f"conv{k[0]}"
+        g.const(f"{n}.w", (rng.standard_normal((cout, cin, ks, ks)) * np.sqrt(2.0 / (cin * ks * ks))).astype(np.float32))
+        g.const(f"{n}.b", rng.uniform(-0.1, 0.1, cout).astype(np.float32))
+        p = ks // 2
+        g.conv2d(f"{n}.y", x, f"{n}.w", f"{n}.b", pads=(p, p, p, p), name=n)
+        g.sigmoid(f"{n}.s", f"{n}.y")
+        g.mul(f"{n}.o", f"{n}.y", f"{n}.s")
+        return f"{n}.o"
+
+    h = c // 2
+    y = conv("x", c, c, 1)
+    g.split(["a", "b"], y, [h, h], axis=1)
+    parts = ["a", "b"]
+    for i in range(2):
+        t = conv(conv(parts[-1], h, h, 3), h, h, 3)
+        if shortcut:
+            g.add(f"res{i}", parts[-1], t)
+            t = f"res{i}"
+        parts.append(t)
+    g.concat("cat", *parts, axis=1)
+    out = conv("cat", 2 * c, c, 1)
+    g.output(out)
+    return g
+
+
+def _layer_check(model: NativeHipYoloModel, graph: Graph, plan: dict, tol=1e-2):
+    replay = plan["replay"]
+    names = replay["names"]
+    cmds = replay["commands"]
+    consumers = {}
+    for i, c in enumerate(cmds):
+        for v in c["inputs"]:
+            consumers.setdefault(v, []).append(i)
+    convs = {n.name: n for n in graph.nodes if n.op == "Conv"}
+    checked = 0
+    worst = 0.0
+    for i, c in enumerate(cmds):
+        if c["kind"] not in ("CONV", "CONV_SILU"):
+            continue
+        pk = plan["plans"][i]["planned_kernel"]
+        int8 = pk in E.INT8_KERNELS and E.int8_eligible(c["params"])
+        xin, wid, bid = c["inputs"]
+        wname = names[wid]
+        node = convs[wname.rsplit(".w", 1)[0]]
+        rank_x, _ = model.value_info(xin)
+        x = model.value(xin)
+        if x.ndim == 3:
+            continue
+        if xin == replay["input_value"]:
+            x = O.round_f16(x)
+        y_ref = ON.conv_layer(x, graph.constants[wname], graph.constants[names[bid]], node.attrs, int8=int8,
+                              silu=c["kind"] == "CONV_SILU")
+        out = c["output"]
+        rank_y, _ = model.value_info(out)
+        if rank_y == 0:  # fused into the residual add that consumes it
+            add = cmds[consumers[out][0]]
+            other = [v for v in add["inputs"] if v != out][0]
+            y_ref = O.round_f16(y_ref) + model.value(other)
+            out = add["output"]
+        y = model.value(out)
+        if y.ndim == 3:
+            y = y.reshape(y_ref.shape)
+        err, allowed = tol_range(y_ref, y, tol)
+        assert err <= allowed, (i, names[out], pk, err, allowed)
+        worst = max(worst, err / max(allowed, 1e-30) * tol)
+        checked += 1
+    return checked, worst
+
+
+def test_c2f_fp16_block_with_winograd_overrides(cuda):
+    g = _c2f_graph(batch=1, c=128, dim=40, seed=3)
+    plan = E.compile_plan(g, precision="fp16")
+    data = E.build_aexrt_engine(g, precision="fp16")
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((1, 128, 40, 40)).astype(np.float32)
+    with NativeHipYoloModel(data) as m:
+        # put the four 3x3 bottleneck convs on Winograd F(2x2,3x3)
+        n_w = 0
+        for info in m.conv_plan():
+            if info["desc"][7] == 3 and 40 in info["candidates"]:
+                m.override_conv_algorithm(info["command_index"], 40)
+                n_w += 1
+        assert n_w == 4
+        assert all(i["current_algorithm"] == 40 for i in m.conv_plan() if i["desc"][7] == 3)
+        m.run(x)
+        checked, _ = _layer_check(m, g, plan)
+        assert checked == 6
+        ref = ON.run_graph(g, x)[g.outputs[0]]
+        got = m.output().reshape(ref.shape)
+        err, allowed = tol_range(ref, got, 1e-2)
+        assert err <= allowed, (err, allowed)
+
+
+@pytest.mark.parametrize("batch", [1, 3])
+def test_c2f_w8a8_block_layer_parity(cuda, batch):
+    g = _c2f_graph(batch=batch, c=64, dim=20, seed=5)
+    replay = E.lower_graph(g)
+    algo = E.w8a8_algo_map(replay)
+    assert len(algo) == 6
+    plan = E.compile_plan(g, precision="fp16", algo_overrides=algo)
+    data = E.build_aexrt_engine(g, precision="fp16", algo_overrides=algo)
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((batch, 64, 20, 20)).astype(np.float32)
+    with NativeHipYoloModel(data) as m:
+        assert sorted(i["current_algorithm"] for i in m.conv_plan()) == [51, 51, 52, 52, 52, 52]
+        m.run(x)
+        checked, _ = _layer_check(m, g, plan)
+        assert checked == 6
+
+
+def test_yolov8n_160_w8a8_layers_and_end_to_end(cuda):
+    g = build_yolov8n(batch=2, imgsz=160, seed=4)
+    replay = E.lower_graph(g)
+    int8_names = g.metadata["int8_convs"].split(",")
+    algo = E.w8a8_algo_map(replay, int8_names)
+    assert len(algo) == 44
+    plan = E.compile_plan(g, precision="fp16", algo_overrides=algo)
+    data = E.build_aexrt_engine(g, precision="fp16", algo_overrides=algo, classes=80)
+    rng = np.random.default_rng(4)
+    x = rng.random((2, 3, 160, 160)).astype(np.float32)
+    with NativeHipYoloModel(data) as m:
+        assert m.executable
+        assert sum(1 for i in m.conv_plan() if i["current_algorithm"] in (51, 52, 53)) == 44
+        m.run(x)
+        out1 = m.output()
+        checked, _ = _layer_check(m, g, plan)
+        assert checked == 63
+        # graph replay is deterministic
+        m.run(x)
+        np.testing.assert_array_equal(m.output(), out1)
+    ref = ON.run_graph(g, x, int8_convs=int8_names, threads=8)["output0"]
+    got = out1.reshape(ref.shape)
+    err, allowed = tol_range(ref, got, 5e-2)
+    assert err <= allowed, (err, allowed)
+
+
+def test_engine_file_roundtrip_and_fail_closed(cuda, tmp_path):
+    g = _c2f_graph(batch=1, c=64, dim=8, seed=9)
+    path = tmp_path / "c2f.aexrt"
+    info = E.save_aexrt_engine(g, path, precision="fp16", algo_overrides=E.w8a8_algo_map(E.lower_graph(g)))
+    assert info["packed_layout_counts"][8] == 6
+    with NativeHipYoloModel(str(path)) as m:
+        assert m.executable and m.input_element_count == 64 * 64
+    data = bytearray(path.read_bytes())
+    data[-1] ^= 0xFF  # corrupt the last section payload
+    with pytest.raises(RuntimeError, match="checksum"):
+        NativeHipYoloModel(bytes(data))
