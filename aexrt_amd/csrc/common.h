@@ -46,4 +46,16 @@ __device__ __forceinline__ uint32_t pack4_q(float a, float b, float c, float d, 
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
 
+// Folds a non-negative value into an amax slot.  Slots only grow during a
+// run, so a value that does not exceed what is already visible cannot change
+// the slot and its atomic is skipped (the value read is one the slot held at
+// some point, never more than its current content).  Every wave of a layer
+// targets the same few slots; without the check those atomics serialize in
+// L2 and dominate the layer's run time.
+__device__ __forceinline__ void slot_max(uint32_t* slot, float v) {
+    const uint32_t b = f2u(v);
+    const uint32_t seen = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (b > seen) atomicMax(slot, b);
+}
+
 }  // namespace aexrt

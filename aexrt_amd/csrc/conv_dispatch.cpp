@@ -25,7 +25,11 @@ bool build_conv_params(const AexrtConv2DDesc& d, uint32_t algorithm, uint32_t fl
     }
     const bool int8 = is_int8_algorithm(algorithm);
     const bool wino = is_winograd_algorithm(algorithm);
-    const bool nchw_in = (flags & AEXRT_HIP_CONV_IN_NCHW_F32) != 0;
+    if (flags & AEXRT_HIP_CONV_IN_NCHW_F32) {
+        why = "convert fp32 NCHW input with aexrt_hip_nchw_f32_to_nhwc first (channels padded to 8)";
+        return false;
+    }
+    const bool out_f32 = (flags & AEXRT_HIP_CONV_OUT_F32) != 0;
     if (int8) {
         if (!can_use_int8(d, int8_kernel_elems(algorithm))) {
             why = "descriptor is not eligible for the planned int8 kernel";
@@ -39,10 +43,6 @@ bool build_conv_params(const AexrtConv2DDesc& d, uint32_t algorithm, uint32_t fl
             why = "int8 conv needs the input amax slots and the weight scales";
             return false;
         }
-        if (nchw_in) {
-            why = "int8 conv reads NHWC fp16 activations only";
-            return false;
-        }
     }
     if (wino) {
         if (!winograd_shape_ok(d)) {
@@ -53,28 +53,28 @@ bool build_conv_params(const AexrtConv2DDesc& d, uint32_t algorithm, uint32_t fl
             why = "Winograd kernels always apply SiLU (reference kernels 40/46)";
             return false;
         }
-        if (nchw_in) {
-            why = "Winograd reads NHWC fp16 activations only";
-            return false;
-        }
         if (!aligned16(x.data) || x.c_stride % 4 || x.n_stride % 4) {
             why = "Winograd input view must be 8-byte aligned with 4-element strides";
             return false;
         }
-    }
-    if (!int8 && !wino && !nchw_in) {
-        if (d.in_channels % 8) {
-            why = "fp16 conv on an NHWC view needs C % 8 == 0";
+    } else {
+        if (d.in_channels % 8 || !aligned16(x.data) || x.c_stride % 8 ||
+            x.n_stride != int64_t(d.in_h) * d.in_w * x.c_stride) {
+            why = "NHWC input view must be 16-byte aligned, C % 8 == 0, c_stride % 8 == 0 and n_stride == H*W*c_stride";
+            return false;
+        }
+        if (d.out_channels % 8 || !aligned16(y.data) || y.c_stride % (out_f32 ? 4 : 8) ||
+            y.n_stride % (out_f32 ? 4 : 8)) {
+            why = "output view must be 16-byte aligned with OC % 8 == 0 and 16-byte aligned strides";
+            return false;
+        }
+        if ((flags & AEXRT_HIP_CONV_RESIDUAL) && residual &&
+            (!aligned16(residual->data) || residual->c_stride % 8 || residual->n_stride % 8)) {
+            why = "residual view must be 16-byte aligned with 8-element strides";
             return false;
         }
     }
-    if (!nchw_in && !wino) {
-        if (d.in_channels % 8 || !aligned16(x.data) || x.c_stride % 8 || x.n_stride % 8) {
-            why = "NHWC input view must be 16-byte aligned with 8-element strides and C % 8 == 0";
-            return false;
-        }
-    }
-    if (!nchw_in && (uint32_t)x.c_stride < d.in_channels) {
+    if ((uint32_t)x.c_stride < d.in_channels) {
         why = "input c_stride smaller than in_channels";
         return false;
     }
@@ -93,9 +93,9 @@ bool build_conv_params(const AexrtConv2DDesc& d, uint32_t algorithm, uint32_t fl
     const WeightGeom g = weight_geom(d, algorithm);
     p = ConvParams{};
     p.x = x.data;
-    p.x_nstride = nchw_in ? (int64_t)d.in_channels * d.in_h * d.in_w : x.n_stride;
-    p.x_cstride = nchw_in ? 1 : x.c_stride;
-    p.loader = nchw_in ? kLoaderNchwF32 : kLoaderNhwc;
+    p.x_nstride = x.n_stride;
+    p.x_cstride = x.c_stride;
+    p.loader = kLoaderNhwc;
     p.x_slots = x.amax_slots;
     p.x_nslots = (int)(d.in_channels / 16);
     p.w = weight;

@@ -14,7 +14,6 @@ enum ConvFlags : int {
 
 enum Loader : int {
     kLoaderNhwc = 0,     // fp16 NHWC activation view, C % 8 == 0
-    kLoaderNchwF32 = 1,  // fp32 NCHW network input (fp16 path only)
 };
 
 // One convolution launch.  Activation views address element (n, h, w, c) at
@@ -41,9 +40,23 @@ struct ConvParams {
     int N, H, W, C, OH, OW, OC, KH, KW, S, P;
     int K, M;
     int flags;
+    // split-K: ksplit blocks per output tile exchange partial tiles through
+    // ws (ksplit * tiles * BM * BN int32) and per-tile arrival counters
+    // (zero between runs; the last block re-arms them)
+    int ksplit = 1;
+    void* ws = nullptr;
+    uint32_t* counters = nullptr;
 };
 
 hipError_t launch_conv_igemm(const ConvParams& p, bool int8, hipStream_t stream);
+// Tile geometry of the igemm kernel (for split-K workspace sizing).
+int conv_block_m();
+int conv_block_n(int oc, bool out_f32);
+int conv_chunk_k(bool int8, int oc, bool out_f32);
+// Input staging of the network's first conv: fp32 NCHW -> fp16 NHWC with the
+// channels zero-padded to a multiple of 8 (one 16-byte store per pixel and
+// 8 channels).  y has c_stride Cp = C rounded up to 8, dense.
+hipError_t launch_nchw_f32_to_nhwc8(const float* x, __half* y, int N, int C, int HW, hipStream_t stream);
 
 // Winograd F(2x2,3x3), fp16 MFMA.  U is [16][OCp][Cp] fp16 (Cp = C rounded up
 // to 32).  Same views/flags as ConvParams (w = U, Kp = Cp).

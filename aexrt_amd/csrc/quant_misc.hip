@@ -23,6 +23,23 @@ inline int grid_for(int64_t work, int per_block = kThreads) {
     return (int)g;
 }
 
+// Grid for a chunk loop over C/8 chunk columns: the grid stride (blocks x
+// 256) is made a multiple of the column count so each thread keeps one
+// column.
+inline int grid_cols(int64_t chunks, int C) {
+    const int cc = C / 8 > 0 ? C / 8 : 1;
+    int a = cc, b = kThreads;
+    while (b) {
+        const int t = a % b;
+        a = b;
+        b = t;
+    }
+    const int r = cc / a;
+    int g = grid_for(chunks);
+    g = (g + r - 1) / r * r;
+    return g;
+}
+
 __device__ __forceinline__ void slots_init(uint32_t* s, int n) {
     for (int i = threadIdx.x; i < n; i += blockDim.x) s[i] = 0u;
     __syncthreads();
@@ -31,8 +48,30 @@ __device__ __forceinline__ void slots_init(uint32_t* s, int n) {
 __device__ __forceinline__ void slots_flush(const uint32_t* s, int n, uint32_t* g) {
     __syncthreads();
     for (int i = threadIdx.x; i < n; i += blockDim.x)
-        if (s[i]) atomicMax(g + i, s[i]);
+        if (s[i]) slot_max(g + i, u2f(s[i]));
 }
+
+// Per-thread running max of one 16-channel group.  The host sizes grids so
+// that the grid stride is a multiple of the chunk columns C/8, which pins
+// every thread to one chunk column (and so one group) for its whole loop;
+// the block then folds one value per thread into LDS.
+struct GroupMax {
+    float v = 0.0f;
+    int g = -1;
+    __device__ __forceinline__ void add(int group, float m, uint32_t* ls) {
+        if (g == group || g < 0) {
+            g = group;
+            v = fmaxf(v, m);
+        } else {
+            atomicMax(&ls[g], f2u(v));
+            g = group;
+            v = m;
+        }
+    }
+    __device__ __forceinline__ void flush(uint32_t* ls) {
+        if (g >= 0) atomicMax(&ls[g], f2u(v));
+    }
+};
 
 __device__ __forceinline__ float max8_abs(const uint4& v) {
     const __half2* h = reinterpret_cast<const __half2*>(&v);
@@ -54,25 +93,17 @@ __global__ __launch_bounds__(kThreads) void amax_slots_nhwc_kernel(
     const int CC = C / 8;
     const int G = C / 16;
     slots_init(ls, G);
+    GroupMax gm;
     const int64_t step = (int64_t)gridDim.x * blockDim.x;
-    const bool fixed = (step % CC) == 0;  // each thread then always sees one chunk column
-    float run = 0.0f;
-    int my_g = -1;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
-        const int64_t pix = e / CC;
-        const int cc = (int)(e - pix * CC);
-        const int64_t n = pix / HW;
-        const int64_t pp = pix - n * HW;
-        const uint4 v = *reinterpret_cast<const uint4*>(x + n * nstride + pp * cstride + cc * 8);
-        const float m = max8_abs(v);
-        if (fixed) {
-            run = fmaxf(run, m);
-            my_g = cc >> 1;
-        } else {
-            atomicMax(&ls[cc >> 1], f2u(m));
-        }
+        const int pix = (int)e / CC;
+        const int cc = (int)e - pix * CC;
+        const int n = pix / HW;
+        const int pp = pix - n * HW;
+        const uint4 v = *reinterpret_cast<const uint4*>(x + n * nstride + (int64_t)pp * cstride + cc * 8);
+        gm.add(cc >> 1, max8_abs(v), ls);
     }
-    if (fixed && my_g >= 0) atomicMax(&ls[my_g], f2u(run));
+    gm.flush(ls);
     slots_flush(ls, G, slots);
 }
 
@@ -85,15 +116,18 @@ __global__ __launch_bounds__(kThreads) void amax_strips_kernel(const T* x, int64
     slots_init(ls, G + 1);
     const int64_t total = strip * G;
     const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    GroupMax gm;
+    float all = 0.0f;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += step) {
         float v;
         if constexpr (sizeof(T) == 2) v = __half2float(reinterpret_cast<const __half*>(x)[i]);
         else v = reinterpret_cast<const float*>(x)[i];
-        const uint32_t b = f2u(fabsf(v));
-        const int g = (int)(i / strip);
-        atomicMax(&ls[1 + g], b);
-        atomicMax(&ls[0], b);
+        const float a = fabsf(v);
+        gm.add(1 + (int)(i / strip), a, ls);
+        all = fmaxf(all, a);
     }
+    gm.flush(ls);
+    if (G > 0) atomicMax(&ls[0], f2u(all));
     slots_flush(ls, G + 1, slots);
 }
 
@@ -113,10 +147,10 @@ __global__ __launch_bounds__(kThreads) void quantize_nhwc_kernel(
     const int CC = C / 8;
     const int64_t step = (int64_t)gridDim.x * blockDim.x;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
-        const int64_t pix = e / CC;
-        const int cc = (int)(e - pix * CC);
-        const int64_t n = pix / HW;
-        const int64_t pp = pix - n * HW;
+        const int pix = (int)e / CC;
+        const int cc = (int)e - pix * CC;
+        const int n = pix / HW;
+        const int pp = pix - n * HW;
         const uint4 v = *reinterpret_cast<const uint4*>(x + n * nstride + pp * cstride + cc * 8);
         uint2 o = make_uint2(0u, 0u);
         if (a > 0.0f) {
@@ -172,17 +206,19 @@ __global__ __launch_bounds__(kThreads) void copy_nhwc_kernel(
     __shared__ uint32_t ls[kMaxSlots];
     const int G = dst_slots ? C / 16 : 0;
     slots_init(ls, G);
+    GroupMax gm;
     const int CC = C / 8;
     const int64_t step = (int64_t)gridDim.x * blockDim.x;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
-        const int64_t pix = e / CC;
-        const int cc = (int)(e - pix * CC);
-        const int64_t n = pix / HW;
-        const int64_t pp = pix - n * HW;
+        const int pix = (int)e / CC;
+        const int cc = (int)e - pix * CC;
+        const int n = pix / HW;
+        const int pp = pix - n * HW;
         const uint4 v = *reinterpret_cast<const uint4*>(src + n * s_nstride + pp * s_cstride + cc * 8);
         *reinterpret_cast<uint4*>(dst + n * d_nstride + pp * d_cstride + cc * 8) = v;
-        if (G) atomicMax(&ls[cc >> 1], f2u(max8_abs(v)));
+        if (G) gm.add(cc >> 1, max8_abs(v), ls);
     }
+    if (G) gm.flush(ls);
     if (G) slots_flush(ls, G, dst_slots);
 }
 
@@ -193,14 +229,15 @@ __global__ __launch_bounds__(kThreads) void maxpool_nhwc_kernel(
     __shared__ uint32_t ls[kMaxSlots];
     const int G = y_slots ? C / 16 : 0;
     slots_init(ls, G);
+    GroupMax gm;
     const int CC = C / 8;
     const int OHW = OH * OW;
     const int64_t step = (int64_t)gridDim.x * blockDim.x;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
-        const int64_t pix = e / CC;
-        const int cc = (int)(e - pix * CC);
-        const int64_t n = pix / OHW;
-        const int pp = (int)(pix - n * OHW);
+        const int pix = (int)e / CC;
+        const int cc = (int)e - pix * CC;
+        const int n = pix / OHW;
+        const int pp = pix - n * OHW;
         const int oy = pp / OW, ox = pp - (pp / OW) * OW;
         float m[8];
 #pragma unroll
@@ -227,8 +264,9 @@ __global__ __launch_bounds__(kThreads) void maxpool_nhwc_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) oh[i] = __floats2half2_rn(m[2 * i], m[2 * i + 1]);
         *reinterpret_cast<uint4*>(y + n * y_nstride + (int64_t)pp * y_cstride + cc * 8) = o;
-        if (G) atomicMax(&ls[cc >> 1], f2u(max8_abs(o)));
+        if (G) gm.add(cc >> 1, max8_abs(o), ls);
     }
+    if (G) gm.flush(ls);
     if (G) slots_flush(ls, G, y_slots);
 }
 
@@ -238,21 +276,23 @@ __global__ __launch_bounds__(kThreads) void resize_nearest_nhwc_kernel(
     __shared__ uint32_t ls[kMaxSlots];
     const int G = y_slots ? C / 16 : 0;
     slots_init(ls, G);
+    GroupMax gm;
     const int CC = C / 8;
     const int OHW = OH * OW;
     const int64_t step = (int64_t)gridDim.x * blockDim.x;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
-        const int64_t pix = e / CC;
-        const int cc = (int)(e - pix * CC);
-        const int64_t n = pix / OHW;
-        const int pp = (int)(pix - n * OHW);
+        const int pix = (int)e / CC;
+        const int cc = (int)e - pix * CC;
+        const int n = pix / OHW;
+        const int pp = pix - n * OHW;
         const int oy = pp / OW, ox = pp - (pp / OW) * OW;
         const int iy = (int)((int64_t)oy * H / OH), ix = (int)((int64_t)ox * W / OW);
         const uint4 v = *reinterpret_cast<const uint4*>(
             x + n * x_nstride + ((int64_t)iy * W + ix) * x_cstride + cc * 8);
         *reinterpret_cast<uint4*>(y + n * y_nstride + (int64_t)pp * y_cstride + cc * 8) = v;
-        if (G) atomicMax(&ls[cc >> 1], f2u(max8_abs(v)));
+        if (G) gm.add(cc >> 1, max8_abs(v), ls);
     }
+    if (G) gm.flush(ls);
     if (G) slots_flush(ls, G, y_slots);
 }
 
@@ -263,13 +303,14 @@ __global__ __launch_bounds__(kThreads) void add_nhwc_kernel(
     __shared__ uint32_t ls[kMaxSlots];
     const int G = y_slots ? C / 16 : 0;
     slots_init(ls, G);
+    GroupMax gm;
     const int CC = C / 8;
     const int64_t step = (int64_t)gridDim.x * blockDim.x;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
-        const int64_t pix = e / CC;
-        const int cc = (int)(e - pix * CC);
-        const int64_t n = pix / HW;
-        const int64_t pp = pix - n * HW;
+        const int pix = (int)e / CC;
+        const int cc = (int)e - pix * CC;
+        const int n = pix / HW;
+        const int pp = pix - n * HW;
         const uint4 va = *reinterpret_cast<const uint4*>(a + n * a_nstride + pp * a_cstride + cc * 8);
         const uint4 vb = *reinterpret_cast<const uint4*>(b + n * b_nstride + pp * b_cstride + cc * 8);
         const __half2* ha = reinterpret_cast<const __half2*>(&va);
@@ -282,8 +323,9 @@ __global__ __launch_bounds__(kThreads) void add_nhwc_kernel(
             ho[i] = __floats2half2_rn(fa.x + fb.x, fa.y + fb.y);
         }
         *reinterpret_cast<uint4*>(y + n * y_nstride + pp * y_cstride + cc * 8) = o;
-        if (G) atomicMax(&ls[cc >> 1], f2u(max8_abs(o)));
+        if (G) gm.add(cc >> 1, max8_abs(o), ls);
     }
+    if (G) gm.flush(ls);
     if (G) slots_flush(ls, G, y_slots);
 }
 
@@ -305,6 +347,30 @@ __global__ __launch_bounds__(kThreads) void nchw_f32_to_nhwc_f16_kernel(
         if (G) atomicMax(&ls[c >> 4], f2u(fabsf(__half2float(h))));
     }
     if (G) slots_flush(ls, G, y_slots);
+}
+
+// One thread per (pixel, 8-channel group): reads up to 8 fp32 planes
+// (coalesced across the pixels of a wave) and writes one 16-byte fp16 chunk,
+// zero-filling the channels past C.
+__global__ __launch_bounds__(kThreads) void nchw_f32_to_nhwc8_kernel(const float* x, __half* y, int C, int Cp,
+                                                                    int HW, int total) {
+    const int G = Cp / 8;
+    const int step = gridDim.x * blockDim.x;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += step) {
+        const int pix = i / G;
+        const int g = i - pix * G;
+        const int n = pix / HW;
+        const int pos = pix - n * HW;
+        const float* src = x + ((int64_t)n * C + g * 8) * HW + pos;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (g * 8 + e < C) ? src[(int64_t)e * HW] : 0.0f;
+        uint4 o;
+        __half2* oh = reinterpret_cast<__half2*>(&o);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) oh[e] = __floats2half2_rn(v[2 * e], v[2 * e + 1]);
+        *reinterpret_cast<uint4*>(y + (int64_t)pix * Cp + g * 8) = o;
+    }
 }
 
 template <typename T>
@@ -331,7 +397,7 @@ hipError_t launch_amax_slots_nhwc(const __half* x, int64_t nstride, int32_t cstr
                                   uint32_t* slots, hipStream_t stream) {
     if (C % 16 != 0 || C / 16 > kMaxSlots) return hipErrorInvalidValue;
     const int64_t chunks = (int64_t)N * HW * (C / 8);
-    hipLaunchKernelGGL(amax_slots_nhwc_kernel, dim3(grid_for(chunks)), dim3(kThreads), 0, stream, x,
+    hipLaunchKernelGGL(amax_slots_nhwc_kernel, dim3(grid_cols(chunks, C)), dim3(kThreads), 0, stream, x,
                        nstride, cstride, HW, C, chunks, slots);
     return hipGetLastError();
 }
@@ -355,7 +421,7 @@ hipError_t launch_quantize_nhwc(const __half* x, int64_t nstride, int32_t cstrid
                                 const uint32_t* slots, int nslots, int8_t* q, hipStream_t stream) {
     if (C % 8 != 0) return hipErrorInvalidValue;
     const int64_t chunks = (int64_t)N * HW * (C / 8);
-    hipLaunchKernelGGL(quantize_nhwc_kernel, dim3(grid_for(chunks)), dim3(kThreads), 0, stream, x, nstride,
+    hipLaunchKernelGGL(quantize_nhwc_kernel, dim3(grid_cols(chunks, C)), dim3(kThreads), 0, stream, x, nstride,
                        cstride, HW, C, chunks, slots, nslots, q);
     return hipGetLastError();
 }
@@ -385,7 +451,7 @@ hipError_t launch_copy_nhwc(const __half* src, int64_t s_nstride, int32_t s_cstr
                             hipStream_t stream) {
     if (C % 8 != 0 || (dst_slots && (C % 16 != 0 || C / 16 > kMaxSlots))) return hipErrorInvalidValue;
     const int64_t chunks = (int64_t)N * HW * (C / 8);
-    hipLaunchKernelGGL(copy_nhwc_kernel, dim3(grid_for(chunks)), dim3(kThreads), 0, stream, src, s_nstride,
+    hipLaunchKernelGGL(copy_nhwc_kernel, dim3(grid_cols(chunks, C)), dim3(kThreads), 0, stream, src, s_nstride,
                        s_cstride, dst, d_nstride, d_cstride, HW, C, chunks, dst_slots);
     return hipGetLastError();
 }
@@ -395,7 +461,7 @@ hipError_t launch_maxpool_nhwc(const __half* x, int64_t x_nstride, int32_t x_cst
                                int OW, int k, int s, int pad, uint32_t* y_slots, hipStream_t stream) {
     if (C % 8 != 0 || (y_slots && (C % 16 != 0 || C / 16 > kMaxSlots))) return hipErrorInvalidValue;
     const int64_t chunks = (int64_t)N * OH * OW * (C / 8);
-    hipLaunchKernelGGL(maxpool_nhwc_kernel, dim3(grid_for(chunks)), dim3(kThreads), 0, stream, x, x_nstride,
+    hipLaunchKernelGGL(maxpool_nhwc_kernel, dim3(grid_cols(chunks, C)), dim3(kThreads), 0, stream, x, x_nstride,
                        x_cstride, y, y_nstride, y_cstride, H, W, C, OH, OW, k, s, pad, chunks, y_slots);
     return hipGetLastError();
 }
@@ -405,7 +471,7 @@ hipError_t launch_resize_nearest_nhwc(const __half* x, int64_t x_nstride, int32_
                                       int OH, int OW, uint32_t* y_slots, hipStream_t stream) {
     if (C % 8 != 0 || (y_slots && (C % 16 != 0 || C / 16 > kMaxSlots))) return hipErrorInvalidValue;
     const int64_t chunks = (int64_t)N * OH * OW * (C / 8);
-    hipLaunchKernelGGL(resize_nearest_nhwc_kernel, dim3(grid_for(chunks)), dim3(kThreads), 0, stream, x,
+    hipLaunchKernelGGL(resize_nearest_nhwc_kernel, dim3(grid_cols(chunks, C)), dim3(kThreads), 0, stream, x,
                        x_nstride, x_cstride, y, y_nstride, y_cstride, H, W, C, OH, OW, chunks, y_slots);
     return hipGetLastError();
 }
@@ -415,7 +481,7 @@ hipError_t launch_add_nhwc(const __half* a, int64_t a_nstride, int32_t a_cstride
                            int N, int HW, int C, uint32_t* y_slots, hipStream_t stream) {
     if (C % 8 != 0 || (y_slots && (C % 16 != 0 || C / 16 > kMaxSlots))) return hipErrorInvalidValue;
     const int64_t chunks = (int64_t)N * HW * (C / 8);
-    hipLaunchKernelGGL(add_nhwc_kernel, dim3(grid_for(chunks)), dim3(kThreads), 0, stream, a, a_nstride,
+    hipLaunchKernelGGL(add_nhwc_kernel, dim3(grid_cols(chunks, C)), dim3(kThreads), 0, stream, a, a_nstride,
                        a_cstride, b, b_nstride, b_cstride, y, y_nstride, y_cstride, HW, C, chunks, y_slots);
     return hipGetLastError();
 }
@@ -426,6 +492,15 @@ hipError_t launch_nchw_f32_to_nhwc_f16(const float* x, __half* y, int64_t y_nstr
     const int64_t total = (int64_t)N * C * HW;
     hipLaunchKernelGGL(nchw_f32_to_nhwc_f16_kernel, dim3(grid_for(total)), dim3(kThreads), 0, stream, x, y,
                        y_nstride, y_cstride, C, HW, total, y_slots);
+    return hipGetLastError();
+}
+
+hipError_t launch_nchw_f32_to_nhwc8(const float* x, __half* y, int N, int C, int HW, hipStream_t stream) {
+    const int Cp = (C + 7) / 8 * 8;
+    const int64_t total = (int64_t)N * HW * (Cp / 8);
+    if (total >= INT32_MAX) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(nchw_f32_to_nhwc8_kernel, dim3(grid_for(total)), dim3(kThreads), 0, stream, x, y, C, Cp, HW,
+                       (int)total);
     return hipGetLastError();
 }
 

@@ -57,6 +57,7 @@ struct ValueInfo {
     std::vector<int> consumers;
     Placement pl;
     int redirect = -1;   // conv output fused into this value (residual add output)
+    int cpad = 0;        // physical channels when zero-padded (network input)
 };
 
 struct Root {
@@ -123,6 +124,10 @@ struct AexrtYoloModel {
     uint8_t* arena = nullptr;
     uint32_t* slots = nullptr;
     int nslots = 0;
+    void* splitk_ws = nullptr;          // shared by the split-K convs (they run in order)
+    uint32_t* splitk_counters = nullptr;
+    size_t splitk_ws_bytes = 0;
+    int splitk_tiles = 0;
     float* input_dev = nullptr;
     float* input_host = nullptr;
     bool input_needs_nhwc = false;
@@ -337,20 +342,21 @@ bool is_fused_add(AexrtYoloModel* m, size_t ci) {
 // ---- placement ------------------------------------------------------------------------
 int new_root(AexrtYoloModel* m, int v, bool f32) {
     ValueInfo& x = m->vals[v];
+    const int C = x.cpad > x.C ? x.cpad : x.C;
     Root r;
-    r.elements = int64_t(x.N) * x.H * x.W * x.C;
+    r.elements = int64_t(x.N) * x.H * x.W * C;
     r.f32 = f32;
-    r.C = x.C;
-    if (!f32 && x.C % 16 == 0 && x.C / 16 <= 128) {
+    r.C = C;
+    if (!f32 && C % 16 == 0 && C / 16 <= 128) {
         r.slot_base = m->nslots;
-        m->nslots += x.C / 16;
+        m->nslots += C / 16;
     }
     m->roots.push_back(r);
     x.pl.valid = true;
     x.pl.root = (int)m->roots.size() - 1;
     x.pl.offset = 0;
-    x.pl.cstride = x.C;
-    x.pl.nstride = int64_t(x.H) * x.W * x.C;
+    x.pl.cstride = C;
+    x.pl.nstride = int64_t(x.H) * x.W * C;
     x.pl.slot = r.slot_base;
     return x.pl.root;
 }
@@ -461,17 +467,12 @@ bool plan_memory(AexrtYoloModel* m, std::vector<CopyJob>& copies) {
         if (o.redirect >= 0) continue;  // fused conv output: never stored
         if (!o.pl.valid) new_root(m, (int)c.output, false);
     }
-    // the network input: fp32 NCHW buffer; an NHWC fp16 copy only if a
-    // consumer cannot read NCHW fp32 directly (only fp16 convs can)
+    // the network input arrives as fp32 NCHW; every kernel reads fp16 NHWC,
+    // so a staging step writes an NHWC copy, channels zero-padded to 8
     const uint32_t in_v = e.manifest.input_value;
-    for (int ci : V[in_v].consumers) {
-        const EngineCommand& c = e.commands[ci];
-        const bool conv = c.kind == kCmdConv || c.kind == kCmdConvSilu;
-        if (!conv || is_int8_algorithm(m->convs[ci].algorithm) || is_winograd_algorithm(m->convs[ci].algorithm))
-            m->input_needs_nhwc = true;
-    }
-    if (m->input_needs_nhwc) {
-        if (V[in_v].C % 8) return fail(m, "network input channels must be a multiple of 8 for an NHWC consumer");
+    if (!V[in_v].consumers.empty()) {
+        m->input_needs_nhwc = true;
+        if (V[in_v].C % 8) V[in_v].cpad = (V[in_v].C + 7) / 8 * 8;
         new_root(m, (int)in_v, false);
     }
     return true;
@@ -501,6 +502,16 @@ AexrtConv2DDesc desc_of(const EngineCommand& c) {
     return d;
 }
 
+// Descriptor of a conv as launched: a zero-padded input (network input with
+// C % 8 != 0) is convolved at its padded channel count.
+AexrtConv2DDesc conv_desc_padded(AexrtYoloModel* m, size_t ci) {
+    const EngineCommand& c = m->eng.commands[ci];
+    AexrtConv2DDesc d = desc_of(c);
+    const ValueInfo& x = m->vals[c.inputs[0]];
+    if (x.cpad > x.C) d.in_channels = (uint32_t)x.cpad;
+    return d;
+}
+
 uint32_t resolve_algorithm(AexrtYoloModel* m, size_t ci, uint32_t wanted) {
     const EngineCommand& c = m->eng.commands[ci];
     const AexrtConv2DDesc d = desc_of(c);
@@ -524,7 +535,8 @@ uint32_t resolve_algorithm(AexrtYoloModel* m, size_t ci, uint32_t wanted) {
 bool prepare_conv_weights(AexrtYoloModel* m, size_t ci) {
     const EngineCommand& c = m->eng.commands[ci];
     ConvState& cs = m->convs[ci];
-    const AexrtConv2DDesc d = desc_of(c);
+    const AexrtConv2DDesc d = conv_desc_padded(m, ci);
+    const uint32_t real_c = c.params[1];
     const uint32_t wid = c.inputs[1], bid = c.inputs[2];
     const EnginePacked& pk = m->eng.packed[wid];
     uint32_t layout = AEXRT_HIP_SRC_RAW_F32;
@@ -546,7 +558,21 @@ bool prepare_conv_weights(AexrtYoloModel* m, size_t ci) {
     } else if (!is_int8_algorithm(a) && !is_winograd_algorithm(a) && pk_ok(2) && kk == 9) {
         layout = AEXRT_HIP_SRC_LAYOUT_OC4_F16;
     }
-    if (layout != AEXRT_HIP_SRC_RAW_F32) {
+    std::vector<float> padded;
+    if (d.in_channels != real_c) {
+        // zero-pad the input channels of the weight: [oc][real_c][kk] -> [oc][C][kk]
+        std::vector<float> w;
+        if (!constant_f32(m, wid, w) || w.size() != uint64_t(d.out_channels) * real_c * kk)
+            return fail(m, "command " + std::to_string(ci) + ": conv weight is not a constant");
+        padded.assign(uint64_t(d.out_channels) * d.in_channels * kk, 0.0f);
+        for (uint32_t o = 0; o < d.out_channels; ++o)
+            for (uint32_t ch = 0; ch < real_c; ++ch)
+                for (uint32_t k = 0; k < kk; ++k)
+                    padded[(uint64_t(o) * d.in_channels + ch) * kk + k] = w[(uint64_t(o) * real_c + ch) * kk + k];
+        layout = AEXRT_HIP_SRC_RAW_F32;
+        src = padded.data();
+        src_bytes = padded.size() * 4;
+    } else if (layout != AEXRT_HIP_SRC_RAW_F32) {
         src = pk.data.data();
         src_bytes = pk.data.size();
     } else {
@@ -605,6 +631,31 @@ AexrtHipTensorView view_of_pl(AexrtYoloModel* m, const Placement& pl) {
 
 bool is_f32(AexrtYoloModel* m, int v) { return m->roots[m->vals[v].pl.root].f32; }
 
+// Split-K factor of an igemm conv: when its output tiles cannot fill the
+// chip (small spatial maps at small batch), the K chunks are spread over up
+// to ~384 blocks in total.
+int choose_ksplit(AexrtYoloModel* m, size_t ci, int* tiles_out) {
+    const ConvState& cs = m->convs[ci];
+    if (is_winograd_algorithm(cs.algorithm)) return 1;
+    const AexrtConv2DDesc d = conv_desc_padded(m, ci);
+    const bool int8 = is_int8_algorithm(cs.algorithm);
+    const bool f32 = is_f32(m, cs.out_value);
+    const int M = (int)(d.batch * d.out_h * d.out_w);
+    const int bn = conv_block_n((int)d.out_channels, f32);
+    const int tiles = ((M + conv_block_m() - 1) / conv_block_m()) * (((int)d.out_channels + bn - 1) / bn);
+    const WeightGeom g = weight_geom(d, cs.algorithm);
+    const int kch = conv_chunk_k(int8, (int)d.out_channels, f32);
+    const int nchunks = (int)((g.kp + kch - 1) / kch);
+    if (tiles_out) *tiles_out = tiles;
+    if (tiles >= 192 || nchunks < 2) return 1;
+    int ks = (384 + tiles - 1) / tiles;
+    if (ks > nchunks) ks = nchunks;
+    // equal chunk counts per split, so no split is left empty
+    const int cps = (nchunks + ks - 1) / ks;
+    ks = (nchunks + cps - 1) / cps;
+    return ks;
+}
+
 std::string conv_label(const EngineCommand& c, size_t ci, uint32_t alg) {
     char buf[192];
     std::snprintf(buf, sizeof(buf), "cmd#%zu %s %ux%ux%u -> %ux%ux%u k%u s%u alg=%s", ci, kind_name(c.kind), c.params[1],
@@ -630,10 +681,17 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
         AexrtHipTensorView y = view_of(m, (int)in_v);
         const float* src = m->input_dev;
         const int N = x.N, C = x.C, HW = x.H * x.W;
-        m->steps.push_back(Step{-1, "input nchw->nhwc", [=](hipStream_t s) {
-                                    return launch_nchw_f32_to_nhwc_f16(src, static_cast<__half*>(y.data), y.n_stride,
-                                                                       y.c_stride, N, C, HW, y.amax_slots, s);
-                                }});
+        if (x.cpad > x.C) {
+            m->steps.push_back(Step{-1, "input nchw->nhwc8", [=](hipStream_t s) {
+                                        return launch_nchw_f32_to_nhwc8(src, static_cast<__half*>(y.data), N, C, HW, s);
+                                    }});
+        } else {
+            m->steps.push_back(Step{-1, "input nchw->nhwc", [=](hipStream_t s) {
+                                        return launch_nchw_f32_to_nhwc_f16(src, static_cast<__half*>(y.data),
+                                                                           y.n_stride, y.c_stride, N, C, HW,
+                                                                           y.amax_slots, s);
+                                    }});
+        }
     }
     for (size_t ci = 0; ci < e.commands.size(); ++ci) {
         const EngineCommand& c = e.commands[ci];
@@ -641,18 +699,10 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
             case kCmdConv:
             case kCmdConvSilu: {
                 ConvState& cs = m->convs[ci];
-                const AexrtConv2DDesc d = desc_of(c);
                 const int xv = (int)c.inputs[0];
+                const AexrtConv2DDesc d = conv_desc_padded(m, ci);
                 uint32_t flags = c.kind == kCmdConvSilu ? AEXRT_HIP_CONV_SILU : 0u;
-                AexrtHipTensorView xvw{};
-                if (V[xv].is_input && !m->input_needs_nhwc) {
-                    flags |= AEXRT_HIP_CONV_IN_NCHW_F32;
-                    xvw.data = m->input_dev;
-                    xvw.n_stride = int64_t(d.in_channels) * d.in_h * d.in_w;
-                    xvw.c_stride = 1;
-                } else {
-                    xvw = view_of(m, xv);
-                }
+                const AexrtHipTensorView xvw = view_of(m, xv);
                 const int yv = cs.out_value;
                 AexrtHipTensorView yvw = view_of(m, yv);
                 if (is_f32(m, yv)) flags |= AEXRT_HIP_CONV_OUT_F32;
@@ -666,6 +716,18 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                 if (!build_conv_params(d, cs.algorithm, flags, xvw, cs.w, cs.scale, cs.bias,
                                        cs.fused_residual ? &rvw : nullptr, yvw, nullptr, p, why))
                     return fail(m, "command " + std::to_string(ci) + ": " + why);
+                int tiles = 0;
+                p.ksplit = choose_ksplit(m, ci, &tiles);
+                if (p.ksplit > 1) {
+                    const int bn = conv_block_n(p.OC, (flags & AEXRT_HIP_CONV_OUT_F32) != 0);
+                    const size_t need = size_t(p.ksplit) * tiles * conv_block_m() * bn * 4;
+                    if (need > m->splitk_ws_bytes || tiles > m->splitk_tiles) {
+                        p.ksplit = 1;  // e.g. after an override: run unsplit
+                    } else {
+                        p.ws = m->splitk_ws;
+                        p.counters = m->splitk_counters;
+                    }
+                }
                 const uint32_t alg = cs.algorithm;
                 m->steps.push_back(Step{(int)ci, conv_label(c, ci, alg), [p, alg](hipStream_t s) {
                                             if (is_winograd_algorithm(alg)) return launch_winograd_f2x2(p, s);
@@ -835,6 +897,25 @@ bool build_model(AexrtYoloModel* m) {
         m->input_host = nullptr;
     for (size_t ci = 0; ci < e.commands.size(); ++ci)
         if (m->convs[ci].is_conv && !prepare_conv_weights(m, ci)) return false;
+    // split-K workspace sized for the largest split conv (convs run in order)
+    for (size_t ci = 0; ci < e.commands.size(); ++ci) {
+        if (!m->convs[ci].is_conv) continue;
+        int tiles = 0;
+        const int ks = choose_ksplit(m, ci, &tiles);
+        if (ks <= 1) continue;
+        const AexrtConv2DDesc d = conv_desc_padded(m, ci);
+        const int bn = conv_block_n((int)d.out_channels, is_f32(m, m->convs[ci].out_value));
+        const size_t bytes = size_t(ks) * tiles * conv_block_m() * bn * 4;
+        if (bytes > m->splitk_ws_bytes) m->splitk_ws_bytes = bytes;
+        if (tiles > m->splitk_tiles) m->splitk_tiles = tiles;
+    }
+    if (m->splitk_ws_bytes) {
+        m->splitk_ws = dev_alloc(m, m->splitk_ws_bytes);
+        m->splitk_counters = static_cast<uint32_t*>(dev_alloc(m, size_t(m->splitk_tiles) * 4));
+        if (!m->splitk_ws || !m->splitk_counters ||
+            !check_hip(hipMemset(m->splitk_counters, 0, size_t(m->splitk_tiles) * 4), "split-K counters"))
+            return fail(m, "out of device memory for the split-K workspace");
+    }
     if (!build_steps(m, m->copies)) return false;
     if (!check_hip(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking), "stream create"))
         return fail(m, last_error());

@@ -167,7 +167,7 @@ __global__ __launch_bounds__(256) void winograd_f2x2_kernel(ConvParams p) {
     if (p.y_slots) {
         gmax = wave_max(gmax);
         const int g = (n0 + wn * 16) / 16;
-        if (lane == 0 && n0 + wn * 16 < p.OC) atomicMax(p.y_slots + g, f2u(gmax));
+        if (lane == 0 && n0 + wn * 16 < p.OC) slot_max(p.y_slots + g, gmax);
     }
 }
 

@@ -168,14 +168,21 @@ def test_fp16_conv_parity(cuda, case):
     wt = he_weight(rng, oc, ic, k)
     b = packing.fp16_round(rng.uniform(-0.1, 0.1, oc).astype(np.float32))
     desc = O.conv_desc(n, ic, h, w, oc, k, s, k // 2)
-    pc = K.prepare_conv(desc, 5, K.SRC_RAW_F32, wt, b, device=cuda)
     _, _, oh, ow = O.out_shape(desc)
     y = torch.empty((n, oh, ow, oc), dtype=torch.float16, device=cuda)
     if nchw_in:
-        xd = torch.from_numpy(x).to(cuda)
-        K.conv2d(pc, xd, y, flags=K.SILU | K.IN_NCHW_F32)
+        # network input: fp32 NCHW staged to fp16 NHWC with channels padded to 8
+        cp = (ic + 7) // 8 * 8
+        xd = torch.zeros((n, h, w, cp), dtype=torch.float16, device=cuda)
+        K.nchw_f32_to_nhwc(torch.from_numpy(x).to(cuda), xd[..., :ic])
+        wpad = np.zeros((oc, cp, k, k), np.float32)
+        wpad[:, :ic] = wt
+        dpad = O.conv_desc(n, cp, h, w, oc, k, s, k // 2)
+        pc = K.prepare_conv(dpad, 5, K.SRC_RAW_F32, wpad, b, device=cuda)
+        K.conv2d(pc, xd, y, flags=K.SILU)
         x_ref = O.round_f16(x)
     else:
+        pc = K.prepare_conv(desc, 5, K.SRC_RAW_F32, wt, b, device=cuda)
         x_ref = O.round_f16(x)
         xd = _dev_nhwc(x_ref, cuda)
         K.conv2d(pc, xd, y, flags=K.SILU)
