@@ -172,6 +172,14 @@ int aexrt_hip_can_use_conv_int8(const AexrtConv2DDesc* desc, uint32_t kernel_ele
     return desc && can_use_int8(*desc, kernel_elems) ? 1 : 0;
 }
 
+int aexrt_hip_set_conv_tile(int32_t jn, int32_t pw, int32_t ksw) {
+    if (!set_conv_tile_override(jn, pw, ksw)) {
+        set_error("set_conv_tile: no kernel instance for this tile");
+        return 0;
+    }
+    return 1;
+}
+
 int aexrt_hip_conv_weight_bytes(const AexrtConv2DDesc* desc, uint32_t algorithm, uint64_t* out_nbytes) {
     if (!desc || !out_nbytes) {
         set_error("conv_weight_bytes: null argument");

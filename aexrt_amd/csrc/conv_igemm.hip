@@ -2,33 +2,35 @@
 // (reference kernels 51/52/53) and the fp16 convolution it falls back to
 // (reference kernels 5/43/45 and the fp16 stem/head convs).
 //
-// GEMM view: M = N*OH*OW output positions (batch folded into M), N = output
-// channels, K = KH*KW*C ordered (ky, kx, c) with c fastest, so that NHWC
-// activations give contiguous K runs.  Weights are repacked at load to
-// [OCp][Kp] (OCp = OC rounded up to 16, Kp = K rounded up to 64, zero padded),
-// one K-contiguous row per output channel.
+// GEMM view: out[oc][m] = sum_k W[oc][k] * A[k][m], m = (n, oh, ow) over the
+// batch-folded output positions, k = (ky, kx, c) with c fastest so that NHWC
+// activations give contiguous k runs.  Weights are repacked at load to
+// [OCp][Kp] (OCp = OC rounded up to 16, Kp = K rounded up to 64, zero padded).
 //
-// int8: the activation tile is quantized while it is staged into LDS
-// (q = rne(x * 127/amax) & 0xFF, the reference's pack pass RT:3314-3346, done
-// by the consumer instead of a separate dispatch), the contraction runs on
-// v_mfma_i32_16x16x64_i8 with exact int32 accumulation, and the epilogue
+// The weights are the MFMA's A operand (16 output channels per 16x16 tile)
+// and the activations its B operand (16 output positions per tile), so every
+// lane ends up holding 4 consecutive output channels of one position: one
+// 8-byte NHWC store per lane and tile, no LDS transpose.  Operands go from
+// memory straight into MFMA registers: a lane loads the 16 consecutive k of
+// its operand row with two 16-byte buffer loads (8 channels of one input
+// pixel each); taps that fall into the zero padding get an out-of-range
+// buffer offset and read as zero.  There is no LDS staging and no barrier in
+// the main loop; each wave owns a 16*PW position x 16*JN channel tile.  For
+// maps too small to fill the GPU, the four waves of a block instead split the
+// k steps of one tile (KSW) and add their partial tiles through LDS.
+//
+// int8: the activation fragment is quantized in registers right after its
+// load (q = rne(x * 127/amax) & 0xFF, the reference's pack pass RT:3314-3346,
+// done by the consumer instead of a separate dispatch), the contraction runs
+// on v_mfma_i32_16x16x64_i8 with exact int32 accumulation, and the epilogue
 // dequantizes as float(acc) * (amax/127) * w_scale[oc] + bias[oc]
 // (RT:4669-4674) before SiLU.  fp16: v_mfma_f32_16x16x32_f16, fp32
-// accumulation, + bias, SiLU.
-//
-// Pipeline per block: a whole K chunk (128-256 elements) of the A and B tiles
-// is fetched with every load of the chunk in flight at once, quantized /
-// staged into LDS, and consumed by 2-8 MFMA k-steps per wave; the next
-// chunk's loads are issued before the current chunk's MFMAs.  The epilogue
-// goes register -> LDS -> 16-byte coalesced stores, adds the residual there
-// (a bottleneck's "x + cv2(cv1(x))", RT's BINARY add fused) and folds max|y|
-// of each 16-channel group into the output tensor's amax slots.
-//
-// Split-K (small M, e.g. 10x10 layers at batch 1): blocks of one output tile
-// split the K chunks, write exact int32 (fp32 for fp16) partial tiles to a
-// workspace, and the last block to arrive sums the partials in split order
-// and runs the epilogue; it also re-arms the tile's arrival counter, so the
-// workspace needs no clearing between runs (graph replays included).
+// accumulation, + bias, SiLU.  The epilogue adds the residual of a fused
+// bottleneck add (RT's BINARY add) and folds max|y| of each 16-channel group
+// into the output tensor's amax slots.
+#include <algorithm>
+#include <atomic>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -36,420 +38,565 @@ namespace aexrt {
 
 namespace {
 
-template <bool INT8>
-struct Elem;
-template <>
-struct Elem<true> { static constexpr int bytes = 1; };
-template <>
-struct Elem<false> { static constexpr int bytes = 2; };
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// Offset for loads that must read zero: beyond every buffer's num_records
+// (<= kMaxViewBytes) even after the compiler folds a small immediate into it.
+constexpr uint32_t kOob = 0x80000000u;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    // raw buffer, stride 0, range-checked against num_records (gfx9 dword3)
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ v4i bload16(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
 
 // XCD-aware tile order: workgroups are dealt round-robin over the 8 XCDs, so
 // block b runs on XCD b % 8.  Give each XCD a contiguous run of tiles so the
-// input rows of neighbouring tiles are fetched into one L2.
+// input rows of neighbouring tiles (3x3 halos, the oc tiles of one position
+// tile) are fetched into one L2.
 __device__ __forceinline__ int xcd_remap(int b, int nb) {
     const int full = (nb / 8) * 8;
     if (b >= full) return b;
     return (b % 8) * (nb / 8) + b / 8;
 }
 
-template <bool INT8, int BM, int BN, int WM, int WN, int KCH>
-__global__ __launch_bounds__(256) void conv_igemm_kernel(ConvParams p) {
-    constexpr int NT = 256;
-    static_assert(WM * WN == 4, "4 waves");
-    constexpr int ESZ = Elem<INT8>::bytes;
-    constexpr int ROWB = KCH * ESZ + 16;  // padded LDS row (bytes)
-    constexpr int TM = BM / WM, TN = BN / WN;
-    constexpr int SI = TM / 16, SJ = TN / 16;
-    constexpr int KCC = KCH / 8;          // 8-element A chunks per row
-    static_assert(NT % KCC == 0 && BM % (NT / KCC) == 0, "A tile split");
-    constexpr int CA = BM / (NT / KCC);   // A chunks (rows) per thread
-    constexpr int BCPR = KCH * ESZ / 16;  // 16-byte B chunks per row
-    constexpr int BCH = BN * BCPR;
-    constexpr int CB = (BCH + NT - 1) / NT;
-    constexpr int AB_BYTES = (BM + BN) * ROWB;
-    // epilogue staging reuses the A/B LDS: fp16 always fits, fp32 only for
-    // tiles the host launches with fp32 output (F32_OK)
-    constexpr int OUT_ROW16 = BN * 2 + 16;
-    constexpr int OUT_ROW32 = BN * 4 + 16;
-    constexpr int LDS_BYTES = AB_BYTES > BM * OUT_ROW16 ? AB_BYTES : BM * OUT_ROW16;
-    constexpr bool F32_OK = BM * OUT_ROW32 <= LDS_BYTES;
+// 8 fp16 -> 8 int8 of the reference quantizer.  x * s is rounded to fp32 and
+// then to an integer by adding 1.5 * 2^23: for |x * s| < 2^22 the sum's low
+// mantissa bits are exactly rne(x * s) in two's complement, so its low byte
+// is the reference's q & 0xFF.  |x| <= amax bounds |x * s| by 127 (+1 ulp);
+// NaN keeps a zero low byte, as the saturating float->int cast gives 0.
+// Contraction stays off: one fma would round x * s + 1.5 * 2^23 once and
+// change the ties.
+__device__ __forceinline__ v2i quant8(v4i raw, float s) {
+#pragma clang fp contract(off)
+    _Float16 h[8];
+    __builtin_memcpy(h, &raw, 16);
+    uint32_t b[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b[i] = __float_as_uint(((float)h[i] * s) + 12582912.0f);
+    v2i o;
+    o[0] = (int)((b[0] & 0xFFu) | ((b[1] & 0xFFu) << 8) | ((b[2] & 0xFFu) << 16) | (b[3] << 24));
+    o[1] = (int)((b[4] & 0xFFu) | ((b[5] & 0xFFu) << 8) | ((b[6] & 0xFFu) << 16) | (b[7] << 24));
+    return o;
+}
 
-    __shared__ __attribute__((aligned(16))) uint8_t smem[LDS_BYTES];
-    __shared__ uint32_t lslots[BN / 16];
-    __shared__ int last_flag;
+template <bool INT8>
+struct Frag;
+template <>
+struct Frag<true> {
+    static constexpr int wq = 1;  // 16-byte weight pieces per lane and k step
+    static constexpr int esz = 1;
+};
+template <>
+struct Frag<false> {
+    static constexpr int wq = 2;
+    static constexpr int esz = 2;
+};
+
+// k steps (64 k each) per weight chunk staged in LDS: 16 KB per buffer, at
+// least 4 steps when the 4 waves split the steps of a chunk.
+template <bool INT8, int JN, bool KSW>
+constexpr int chunk_steps() {
+    constexpr int kc = 16384 / (JN * 16 * 64 * Frag<INT8>::esz);
+    constexpr int k1 = kc < 1 ? 1 : kc;
+    return KSW ? (k1 < 4 ? 4 : k1) : k1;
+}
+
+template <bool INT8, int JN, int PW, bool KSW>
+__global__ __launch_bounds__(256) void conv_mfma_kernel(ConvParams p) {
+    constexpr int WQ = Frag<INT8>::wq;
+    constexpr int ESZ = Frag<INT8>::esz;
+    constexpr int R = JN * 16;                       // weight rows of the block
+    constexpr int KC = chunk_steps<INT8, JN, KSW>();
+    constexpr int CH_BYTES = KC * WQ * R * 64;       // one staged weight chunk
+    constexpr int ST = CH_BYTES / (256 * 16);        // 16-byte pieces per thread
+    static_assert(ST >= 1 && CH_BYTES % (256 * 16) == 0, "chunk split");
+    constexpr int RED_BYTES = KSW ? 4 * JN * PW * 4 * 64 * 4 : 0;
+    constexpr int LDS_BYTES = 2 * CH_BYTES > RED_BYTES ? 2 * CH_BYTES : RED_BYTES;
+    typedef typename std::conditional<INT8, v4i, v4f>::type acc_t;
+
+    // weight chunks: [buf][ks][h][row][64 B]; after the k loop the KSW
+    // partial tiles reuse the same memory
+    __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
+    __shared__ float l_bias[R], l_scale[R];
+    __shared__ uint32_t l_amax, l_slots[JN];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int wm = wave / WN, wn = wave % WN;
-    const int lr = lane & 15, lg = lane >> 4;
+    const int col = lane & 15;  // position within a 16-position subtile
+    const int grp = lane >> 4;  // k group (16 k each) / output channel quad
 
-    const int ntn = (p.OC + BN - 1) / BN;
-    const int ntiles = gridDim.x;
-    const int tile = xcd_remap(blockIdx.x, ntiles);
-    const int m0 = (tile / ntn) * BM;
-    const int n0 = (tile % ntn) * BN;
-    const int split = blockIdx.y;
+    const int tile = xcd_remap(blockIdx.x, gridDim.x);
+    const int mt = (int)fdiv((uint32_t)tile, p.fd_ntn);
+    const int n0 = (tile - mt * p.ntn) * R;
+    const int pb = KSW ? mt * (16 * PW) : (mt * 4 + wave) * (16 * PW);
+    // 16-channel subtiles of this tile that hold real (padded) channels
+    const int jmax = min(JN, (p.OCp - n0) >> 4);
 
-    // K chunks of this block
-    const int nchunks = (p.Kp + KCH - 1) / KCH;
-    const int cps = (nchunks + p.ksplit - 1) / p.ksplit;
-    const int c_begin = split * cps;
-    const int c_end = min(nchunks, c_begin + cps);
+    const rsrc_t rx = make_rsrc(p.x, p.x_bytes);
+    const rsrc_t rw = make_rsrc(p.w, (uint32_t)p.OCp * (uint32_t)p.Kp * ESZ);
 
-    float s_q = 0.0f, in_scale = 0.0f;
+    // ---- block set-up: per-channel constants, input amax, slot partials ----
+    if (tid < R) {
+        const int oc = n0 + tid;
+        l_bias[tid] = oc < p.OC ? p.bias[oc] : 0.0f;
+        if constexpr (INT8) l_scale[tid] = oc < p.OC ? p.w_scale[oc] : 0.0f;
+    }
+    if (tid < JN) l_slots[tid] = 0u;
     if constexpr (INT8) {
-        uint32_t am = 0;
-        for (int i = 0; i < p.x_nslots; ++i) am = max(am, p.x_slots[i]);
-        const float a = u2f(am);
-        if (a > 0.0f) {
-            s_q = 127.0f / a;
-            in_scale = a / 127.0f;
-        }
-    }
-
-    // Per-thread A rows: fixed chunk column kc, rows tid/KCC + i*(NT/KCC).
-    const int kc = tid % KCC;
-    const int OHW = p.OH * p.OW;
-    int rowpix[CA];       // pixel index of (n, oh*S-P, ow*S-P)
-    uint32_t rowhw[CA];   // (ih0 + 32768) << 16 | (iw0 + 32768)
-#pragma unroll
-    for (int i = 0; i < CA; ++i) {
-        const int m = m0 + tid / KCC + i * (NT / KCC);
-        if (m < p.M) {
-            const int n = m / OHW;
-            const int rem = m - n * OHW;
-            const int oh = rem / p.OW;
-            const int ow = rem - oh * p.OW;
-            const int ih0 = oh * p.S - p.P, iw0 = ow * p.S - p.P;
-            rowpix[i] = (n * p.H + ih0) * p.W + iw0;
-            rowhw[i] = ((uint32_t)(ih0 + 32768) << 16) | (uint32_t)(iw0 + 32768);
-        } else {
-            rowpix[i] = 0;
-            rowhw[i] = 0u;  // ih0 = -32768: never in bounds
-        }
-    }
-
-    uint4 areg[CA];
-    uint4 breg[CB];
-    const __half* xb = reinterpret_cast<const __half*>(p.x);
-    const uint8_t* wb = reinterpret_cast<const uint8_t*>(p.w);
-
-    auto load_chunk = [&](int ch) {
-        const int k = ch * KCH + kc * 8;
-#pragma unroll
-        for (int i = 0; i < CA; ++i) areg[i] = make_uint4(0, 0, 0, 0);
-        if (k < p.K) {
-            const int tap = k / p.C;
-            const int c = k - tap * p.C;
-            const int ky = tap / p.KW;
-            const int kx = tap - ky * p.KW;
-            const int koff = ky * p.W + kx;
-#pragma unroll
-            for (int i = 0; i < CA; ++i) {
-                const int ih = (int)(rowhw[i] >> 16) - 32768 + ky;
-                const int iw = (int)(rowhw[i] & 0xffffu) - 32768 + kx;
-                if ((unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.W)
-                    areg[i] = *reinterpret_cast<const uint4*>(xb + (int64_t)(rowpix[i] + koff) * p.x_cstride + c);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < CB; ++j) {
-            const int cidx = tid + j * NT;
-            breg[j] = make_uint4(0, 0, 0, 0);
-            if (cidx < BCH) {
-                const int r = n0 + cidx / BCPR;
-                const int kel = ch * KCH + (cidx % BCPR) * (16 / ESZ);
-                if (r < p.OCp && kel < p.Kp)
-                    breg[j] = *reinterpret_cast<const uint4*>(wb + ((int64_t)r * p.Kp + kel) * ESZ);
-            }
-        }
-    };
-
-    auto store_chunk = [&]() {
-        uint8_t* sa = smem;
-        uint8_t* sb = smem + BM * ROWB;
-#pragma unroll
-        for (int i = 0; i < CA; ++i) {
-            const int r = tid / KCC + i * (NT / KCC);
-            if constexpr (INT8) {
-                const __half2* h = reinterpret_cast<const __half2*>(&areg[i]);
-                const float2 f0 = __half22float2(h[0]), f1 = __half22float2(h[1]);
-                const float2 f2 = __half22float2(h[2]), f3 = __half22float2(h[3]);
-                uint2 q;
-                q.x = pack4_q(f0.x, f0.y, f1.x, f1.y, s_q);
-                q.y = pack4_q(f2.x, f2.y, f3.x, f3.y, s_q);
-                *reinterpret_cast<uint2*>(sa + r * ROWB + kc * 8) = q;
-            } else {
-                *reinterpret_cast<uint4*>(sa + r * ROWB + kc * 16) = areg[i];
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < CB; ++j) {
-            const int cidx = tid + j * NT;
-            if (cidx < BCH)
-                *reinterpret_cast<uint4*>(sb + (cidx / BCPR) * ROWB + (cidx % BCPR) * 16) = breg[j];
-        }
-    };
-
-    typedef typename std::conditional<INT8, v4i, v4f>::type acc_t;
-    acc_t acc[SI][SJ];
-#pragma unroll
-    for (int i = 0; i < SI; ++i)
-#pragma unroll
-        for (int j = 0; j < SJ; ++j) acc[i][j] = acc_t{0, 0, 0, 0};
-
-    if (c_begin < c_end) {
-        load_chunk(c_begin);
-        store_chunk();
+        if (tid == 0) l_amax = 0u;
         __syncthreads();
+        uint32_t am = 0;
+        for (int i = tid; i < p.x_nslots; i += 256) am = max(am, p.x_slots[i]);
+        if (am) atomicMax(&l_amax, am);
     }
-    for (int ch = c_begin; ch < c_end; ++ch) {
-        const bool more = ch + 1 < c_end;
-        if (more) load_chunk(ch + 1);
-        const uint8_t* sa = smem;
-        const uint8_t* sb = smem + BM * ROWB;
-        const int ksteps = (min(KCH, p.Kp - ch * KCH) + 63) / 64;
-        for (int kk = 0; kk < ksteps; ++kk) {
-            if constexpr (INT8) {
-                v4i a[SI], b[SJ];
+
+    // ---- weight chunk staging: global -> registers -> LDS ----
+    const int nks = p.Kp >> 6;
+    const int nch = (nks + KC - 1) / KC;
+    v4i wst[ST];
+    auto stage_load = [&](int c) {
 #pragma unroll
-                for (int i = 0; i < SI; ++i)
-                    a[i] = *reinterpret_cast<const v4i*>(sa + (wm * TM + i * 16 + lr) * ROWB + kk * 64 + lg * 16);
+        for (int i = 0; i < ST; ++i) {
+            const int e = tid + i * 256;  // 16-byte piece of the chunk
+            const int g = e & 3;
+            const int row = (e >> 2) % R;
+            const int kh = (e >> 2) / R;  // ks * WQ + h
+            const int ks = kh / WQ, h = kh % WQ;
+            const int s = c * KC + ks;
+            const int oc = n0 + row;
+            if (s < nks && oc < p.OCp)
+                wst[i] = bload16(rw, (uint32_t)(oc * p.Kp + s * 64) * ESZ + g * 16 * ESZ + h * 16);
+            else
+                wst[i] = v4i{0, 0, 0, 0};
+        }
+    };
+    auto stage_store = [&](int buf) {
 #pragma unroll
-                for (int j = 0; j < SJ; ++j)
-                    b[j] = *reinterpret_cast<const v4i*>(sb + (wn * TN + j * 16 + lr) * ROWB + kk * 64 + lg * 16);
+        for (int i = 0; i < ST; ++i)
+            *reinterpret_cast<v4i*>(lds + buf * CH_BYTES + (tid + i * 256) * 16) = wst[i];
+    };
+
+    // ---- activation fragments: direct to registers ----
+    int xo[PW], ih0[PW], iw0[PW];
 #pragma unroll
-                for (int i = 0; i < SI; ++i)
+    for (int q = 0; q < PW; ++q) {
+        const int m = pb + q * 16 + col;
+        if (m < p.M) {
+            const int n = (int)fdiv((uint32_t)m, p.fd_ohw);
+            const int rem = m - n * p.OH * p.OW;
+            const int oh = (int)fdiv((uint32_t)rem, p.fd_ow);
+            const int ow = rem - oh * p.OW;
+            ih0[q] = oh * p.S - p.P;
+            iw0[q] = ow * p.S - p.P;
+            xo[q] = n * (int)p.x_nstride + (ih0[q] * p.W + iw0[q]) * p.x_cstride;
+        } else {
+            ih0[q] = -0x40000000;  // every tap out of range
+            iw0[q] = 0;
+            xo[q] = 0;
+        }
+    }
+    // a[q][h] = 8 channels (16 B fp16) of position subtile q at
+    // k = s*64 + grp*16 + h*8; taps in the zero padding read as zero
+    auto load_act = [&](int s, v4i (&a)[PW][2]) {
+        const int kb = s * 64 + grp * 16;
 #pragma unroll
-                    for (int j = 0; j < SJ; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], acc[i][j], 0, 0, 0);
-            } else {
+        for (int h = 0; h < 2; ++h) {
+            const int k = kb + h * 8;
+            const int tap = (int)fdiv((uint32_t)k, p.fd_c);
+            const int c = k - tap * p.C;
+            const int ky = (int)fdiv((uint32_t)tap, p.fd_kw);
+            const int kx = tap - ky * p.KW;
+            const bool kok = k < p.K;
+            const int toff = (ky * p.W + kx) * p.x_cstride + c;
+#pragma unroll
+            for (int q = 0; q < PW; ++q) {
+                const int ih = ih0[q] + ky, iw = iw0[q] + kx;
+                const bool ok = kok && (unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.W;
+                a[q][h] = bload16(rx, ok ? (uint32_t)(xo[q] + toff) * 2u : kOob);
+            }
+        }
+    };
+
+    acc_t acc[JN][PW];
+#pragma unroll
+    for (int j = 0; j < JN; ++j)
+#pragma unroll
+        for (int q = 0; q < PW; ++q) acc[j][q] = acc_t{0, 0, 0, 0};
+
+    float s_q = 0.0f;
+    auto mma_step = [&](const v4i (&a)[PW][2], const uint8_t* wl) {
+        // wl: this k step's [h][row][64 B] weights in LDS
+        if constexpr (INT8) {
+            v4i b[PW];
+#pragma unroll
+            for (int q = 0; q < PW; ++q) {
+                const v2i lo = quant8(a[q][0], s_q), hi = quant8(a[q][1], s_q);
+                b[q] = v4i{lo[0], lo[1], hi[0], hi[1]};
+            }
+#pragma unroll
+            for (int j = 0; j < JN; ++j) {
+                if (j >= jmax) continue;
+                const v4i w = *reinterpret_cast<const v4i*>(wl + (j * 16 + col) * 64 + grp * 16);
+#pragma unroll
+                for (int q = 0; q < PW; ++q)
+                    acc[j][q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w, b[q], acc[j][q], 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < JN; ++j) {
+                if (j >= jmax) continue;
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
-                    v8h a[SI], b[SJ];
-                    const int off = kk * 128 + h * 64 + lg * 16;
+                    const v8h w = *reinterpret_cast<const v8h*>(wl + (h * R + j * 16 + col) * 64 + grp * 16);
 #pragma unroll
-                    for (int i = 0; i < SI; ++i)
-                        a[i] = *reinterpret_cast<const v8h*>(sa + (wm * TM + i * 16 + lr) * ROWB + off);
-#pragma unroll
-                    for (int j = 0; j < SJ; ++j)
-                        b[j] = *reinterpret_cast<const v8h*>(sb + (wn * TN + j * 16 + lr) * ROWB + off);
-#pragma unroll
-                    for (int i = 0; i < SI; ++i)
-#pragma unroll
-                        for (int j = 0; j < SJ; ++j)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+                    for (int q = 0; q < PW; ++q) {
+                        v8h xb;
+                        __builtin_memcpy(&xb, &a[q][h], 16);
+                        acc[j][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, xb, acc[j][q], 0, 0, 0);
+                    }
                 }
             }
         }
-        __syncthreads();
-        if (more) {
-            store_chunk();
+    };
+
+    // ---- main loop over weight chunks, act fragments one step ahead ----
+    const int sstep = KSW ? 4 : 1;
+    int s = KSW ? wave : 0;
+    v4i a_cur[PW][2];
+    stage_load(0);
+    if (s < nks) load_act(s, a_cur);
+    stage_store(0);
+    __syncthreads();
+    if constexpr (INT8) {
+        const float am = u2f(l_amax);
+        if (am > 0.0f) s_q = 127.0f / am;
+    }
+    for (int c = 0; c < nch; ++c) {
+        const bool more_w = c + 1 < nch;
+        if (more_w) stage_load(c + 1);
+        const int s_end = min(nks, (c + 1) * KC);
+        const uint8_t* wbuf = lds + (c & 1) * CH_BYTES;
+        for (; s < s_end; s += sstep) {
+            v4i a_nxt[PW][2];
+            const bool more_a = s + sstep < nks;
+            if (more_a) load_act(s + sstep, a_nxt);
+            mma_step(a_cur, wbuf + (s - c * KC) * WQ * R * 64);
+            if (more_a) {
+#pragma unroll
+                for (int q = 0; q < PW; ++q) {
+                    a_cur[q][0] = a_nxt[q][0];
+                    a_cur[q][1] = a_nxt[q][1];
+                }
+            }
+        }
+        if (more_w) {
+            stage_store((c + 1) & 1);
             __syncthreads();
         }
     }
 
-    // ---- split-K: exchange partial tiles through the workspace ----------
-    if (p.ksplit > 1) {
-        int32_t* ws = reinterpret_cast<int32_t*>(p.ws);
-        const int64_t slice = (int64_t)ntiles * BM * BN;
-        int32_t* mine = ws + (int64_t)split * slice + (int64_t)tile * BM * BN;
+    if constexpr (KSW) {
+        // partial tiles of the 4 waves -> LDS; wave w finishes subtiles j % 4 == w
+        int32_t* red = reinterpret_cast<int32_t*>(lds);
+        __syncthreads();  // every wave is done reading the weight chunks
 #pragma unroll
-        for (int i = 0; i < SI; ++i)
+        for (int j = 0; j < JN; ++j)
 #pragma unroll
-            for (int j = 0; j < SJ; ++j)
+            for (int q = 0; q < PW; ++q)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int row = wm * TM + i * 16 + lg * 4 + r;
-                    const int col = wn * TN + j * 16 + lr;
                     int32_t v;
-                    if constexpr (INT8) v = acc[i][j][r];
-                    else v = __float_as_int(acc[i][j][r]);
-                    mine[row * BN + col] = v;
+                    if constexpr (INT8) v = acc[j][q][r];
+                    else v = __float_as_int(acc[j][q][r]);
+                    red[((wave * JN + j) * PW * 4 + q * 4 + r) * 64 + lane] = v;
                 }
-        __threadfence();
         __syncthreads();
-        if (tid == 0) {
-            const uint32_t prev = atomicAdd(p.counters + tile, 1u);
-            last_flag = prev == (uint32_t)(p.ksplit - 1);
-        }
-        __syncthreads();
-        if (!last_flag) return;
-        __threadfence();
-        if (tid == 0) p.counters[tile] = 0u;  // re-arm for the next run
 #pragma unroll
-        for (int i = 0; i < SI; ++i)
+        for (int j = 0; j < JN; ++j) {
+            if ((j & 3) != wave) continue;
 #pragma unroll
-            for (int j = 0; j < SJ; ++j) acc[i][j] = acc_t{0, 0, 0, 0};
-        for (int s = 0; s < p.ksplit; ++s) {
-            const int32_t* part = ws + (int64_t)s * slice + (int64_t)tile * BM * BN;
+            for (int q = 0; q < PW; ++q)
 #pragma unroll
-            for (int i = 0; i < SI; ++i)
+                for (int r = 0; r < 4; ++r) {
+                    if constexpr (INT8) {
+                        int32_t t = 0;
 #pragma unroll
-                for (int j = 0; j < SJ; ++j)
+                        for (int w = 0; w < 4; ++w) t += red[((w * JN + j) * PW * 4 + q * 4 + r) * 64 + lane];
+                        acc[j][q][r] = t;
+                    } else {
+                        float t = 0.0f;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int row = wm * TM + i * 16 + lg * 4 + r;
-                        const int col = wn * TN + j * 16 + lr;
-                        const int32_t v = part[row * BN + col];
-                        if constexpr (INT8) acc[i][j][r] += v;
-                        else acc[i][j][r] += __int_as_float(v);
+                        for (int w = 0; w < 4; ++w)
+                            t += __int_as_float(red[((w * JN + j) * PW * 4 + q * 4 + r) * 64 + lane]);
+                        acc[j][q][r] = t;
                     }
+                }
         }
     }
 
-    // ---- epilogue: registers -> LDS (dequant, bias, activation, rounding) ----
+    // ---- epilogue: dequant, bias, activation, residual, store, amax ----
+    float in_scale = 0.0f;
+    if constexpr (INT8) {
+        const float am = u2f(l_amax);
+        if (am > 0.0f) in_scale = am / 127.0f;
+    }
     const bool do_silu = p.flags & kConvSilu;
     const bool do_res = p.flags & kConvResidual;
-    const bool out_f32 = F32_OK && (p.flags & kConvOutF32);
-    const int OUT_ROW = out_f32 ? OUT_ROW32 : OUT_ROW16;
-    uint8_t* stage = smem;
+    const bool out_f32 = p.flags & kConvOutF32;
+    const rsrc_t ry = make_rsrc(p.y, p.y_bytes);
+    const rsrc_t rr = make_rsrc(p.res, p.r_bytes);
+    int yo[PW], ro[PW];
 #pragma unroll
-    for (int j = 0; j < SJ; ++j) {
-        const int lcol = wn * TN + j * 16 + lr;
-        const int col = n0 + lcol;
-        const bool col_ok = col < p.OC;
-        float ws = 0.0f, bs = 0.0f;
-        if (col_ok) {
-            bs = p.bias[col];
-            if constexpr (INT8) ws = p.w_scale[col];
+    for (int q = 0; q < PW; ++q) {
+        const int m = pb + q * 16 + col;
+        if (m < p.M) {
+            const int n = (int)fdiv((uint32_t)m, p.fd_ohw);
+            const int pos = m - n * p.OH * p.OW;
+            yo[q] = n * (int)p.y_nstride + pos * p.y_cstride;
+            ro[q] = n * (int)p.r_nstride + pos * p.r_cstride;
+        } else {
+            yo[q] = -1;
+            ro[q] = 0;
         }
+    }
 #pragma unroll
-        for (int i = 0; i < SI; ++i) {
+    for (int j = 0; j < JN; ++j) {
+        if (j >= jmax) continue;
+        if (KSW && (j & 3) != wave) continue;
+        const int lc = j * 16 + grp * 4;  // block-local channel of this lane's quad
+        const int oc0 = n0 + lc;
+        const bool oc_ok = oc0 < p.OC;  // OC % 4 == 0: the quad is all in or all out
+        // residual fragments first, so their latency overlaps the arithmetic
+        v2i rv[PW];
+#pragma unroll
+        for (int q = 0; q < PW; ++q)
+            rv[q] = do_res ? __builtin_amdgcn_raw_buffer_load_b64(
+                                 rr, oc_ok && yo[q] >= 0 ? (uint32_t)(ro[q] + oc0) * 2u : kOob, 0, 0)
+                           : v2i{0, 0};
+        float bv[4], wv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            bv[r] = l_bias[lc + r];
+            wv[r] = INT8 ? l_scale[lc + r] : 0.0f;
+        }
+        float gmax = 0.0f;
+#pragma unroll
+        for (int q = 0; q < PW; ++q) {
+            if (!oc_ok || yo[q] < 0) continue;
+            float v[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int lrow = wm * TM + i * 16 + lg * 4 + r;
-                float v;
+#pragma clang fp contract(off)
+                float t;
                 if constexpr (INT8) {
-                    const int32_t a = acc[i][j][r];
-                    if (p.acc_out && col_ok && m0 + lrow < p.M) p.acc_out[(int64_t)(m0 + lrow) * p.OC + col] = a;
-                    v = (float)a * in_scale;
-                    v = v * ws;
-                    v = v + bs;
+                    t = (float)acc[j][q][r] * in_scale;
+                    t = t * wv[r];
+                    t = t + bv[r];
                 } else {
-                    v = acc[i][j][r] + bs;
+                    t = acc[j][q][r] + bv[r];
                 }
-                if (do_silu) v = silu(v);
-                if (out_f32) *reinterpret_cast<float*>(stage + lrow * OUT_ROW + lcol * 4) = v;
-                else *reinterpret_cast<__half*>(stage + lrow * OUT_ROW + lcol * 2) = __float2half(v);
+                if (do_silu) t = silu(t);
+                v[r] = t;
             }
+            if constexpr (INT8) {
+                if (p.acc_out)
+                    *reinterpret_cast<int4*>(p.acc_out + (int64_t)(pb + q * 16 + col) * p.OC + oc0) =
+                        make_int4(acc[j][q][0], acc[j][q][1], acc[j][q][2], acc[j][q][3]);
+            }
+            __half2 rh[2];
+            __builtin_memcpy(rh, &rv[q], 8);
+            if (out_f32) {
+                if (do_res) {
+                    const float2 r0 = __half22float2(rh[0]), r1 = __half22float2(rh[1]);
+                    v[0] += r0.x; v[1] += r0.y; v[2] += r1.x; v[3] += r1.y;
+                }
+                v4i o;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    o[r] = __float_as_int(v[r]);
+                    gmax = fmaxf(gmax, fabsf(v[r]));
+                }
+                __builtin_amdgcn_raw_buffer_store_b128(o, ry, (uint32_t)(yo[q] + oc0) * 4u, 0, 0);
+            } else {
+                __half2 oh[2] = {__floats2half2_rn(v[0], v[1]), __floats2half2_rn(v[2], v[3])};
+                if (do_res) {
+                    // fp16 conv output + fp16 residual, added in fp32 and
+                    // rounded again: the reference's separate BINARY add
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const float2 a = __half22float2(oh[e]), b = __half22float2(rh[e]);
+                        oh[e] = __floats2half2_rn(a.x + b.x, a.y + b.y);
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const float2 f = __half22float2(oh[e]);
+                    gmax = fmaxf(gmax, fmaxf(fabsf(f.x), fabsf(f.y)));
+                }
+                v2i o;
+                __builtin_memcpy(&o, oh, 8);
+                __builtin_amdgcn_raw_buffer_store_b64(o, ry, (uint32_t)(yo[q] + oc0) * 2u, 0, 0);
+            }
+        }
+        if (p.y_slots) {
+            gmax = wave_max(gmax);
+            if (lane == 0 && gmax > 0.0f) atomicMax(&l_slots[j], f2u(gmax));
         }
     }
-    if (tid < BN / 16) lslots[tid] = 0u;
-    __syncthreads();
-
-    // ---- LDS -> global, 8 channels (16 B of fp16 / 32 B of fp32) per item ----
-    constexpr int QPR = BN / 8;           // 8-channel items per row
-    for (int it = tid; it < BM * QPR; it += NT) {
-        const int lrow = it / QPR;
-        const int q = it - lrow * QPR;
-        const int col0 = n0 + q * 8;
-        const int m = m0 + lrow;
-        if (m >= p.M || col0 >= p.OC) continue;
-        float gmax = 0.0f;
-        const int n = m / OHW;
-        const int pos = m - n * OHW;
-        const int64_t yo = (int64_t)n * p.y_nstride + (int64_t)pos * p.y_cstride + col0;
-        float v[8];
-        if (out_f32) {
-            const float4* s4 = reinterpret_cast<const float4*>(stage + lrow * OUT_ROW + q * 32);
-            const float4 a = s4[0], b = s4[1];
-            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-        } else {
-            const uint4 u = *reinterpret_cast<const uint4*>(stage + lrow * OUT_ROW + q * 16);
-            const __half2* h = reinterpret_cast<const __half2*>(&u);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float2 f = __half22float2(h[e]);
-                v[2 * e] = f.x;
-                v[2 * e + 1] = f.y;
-            }
-        }
-        if (do_res) {
-            const uint4 ru = *reinterpret_cast<const uint4*>(p.res + (int64_t)n * p.r_nstride +
-                                                             (int64_t)pos * p.r_cstride + col0);
-            const __half2* rh = reinterpret_cast<const __half2*>(&ru);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float2 f = __half22float2(rh[e]);
-                v[2 * e] += f.x;
-                v[2 * e + 1] += f.y;
-            }
-        }
-        if (out_f32) {
-            float4* y4 = reinterpret_cast<float4*>(reinterpret_cast<float*>(p.y) + yo);
-            y4[0] = make_float4(v[0], v[1], v[2], v[3]);
-            y4[1] = make_float4(v[4], v[5], v[6], v[7]);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) gmax = fmaxf(gmax, fabsf(v[e]));
-        } else {
-            uint4 o;
-            __half2* oh = reinterpret_cast<__half2*>(&o);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                oh[e] = __floats2half2_rn(v[2 * e], v[2 * e + 1]);
-                const float2 f = __half22float2(oh[e]);
-                gmax = fmaxf(gmax, fmaxf(fabsf(f.x), fabsf(f.y)));
-            }
-            *reinterpret_cast<uint4*>(reinterpret_cast<__half*>(p.y) + yo) = o;
-        }
-        if (p.y_slots) atomicMax(&lslots[q >> 1], f2u(gmax));
-    }
+    // one global amax update per 16-channel group and block
     if (p.y_slots) {
         __syncthreads();
-        if (tid < BN / 16 && n0 + tid * 16 < p.OC && lslots[tid]) slot_max(p.y_slots + (n0 / 16) + tid, u2f(lslots[tid]));
+        if (tid < jmax && n0 + tid * 16 < p.OC && l_slots[tid]) slot_max(p.y_slots + (n0 >> 4) + tid, u2f(l_slots[tid]));
     }
 }
 
-template <bool INT8, int BM, int BN, int WM, int WN, int KCH>
-hipError_t launch_cfg(const ConvParams& p, hipStream_t stream) {
-    const int tiles = ((p.M + BM - 1) / BM) * ((p.OC + BN - 1) / BN);
-    hipLaunchKernelGGL((conv_igemm_kernel<INT8, BM, BN, WM, WN, KCH>), dim3(tiles, p.ksplit), dim3(256), 0, stream,
-                       p);
+template <bool INT8, int JN, int PW, bool KSW>
+hipError_t launch_cfg(const ConvParams& p, int blocks, hipStream_t stream) {
+    hipLaunchKernelGGL((conv_mfma_kernel<INT8, JN, PW, KSW>), dim3(blocks), dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 
-// Tile configs by output channels.  BN covers all channels up to 128 so the
-// input tile is read once per output position; K chunks are as large as the
-// 64 KB LDS budget and the 16-rows-per-thread staging allow.
 template <bool INT8>
-hipError_t launch_any(const ConvParams& p, hipStream_t stream) {
-    constexpr int K1 = INT8 ? 256 : 128;  // BM + BN <= 224
-    constexpr int K2 = INT8 ? 128 : 64;   // BM + BN = 256
-    switch (conv_block_n(p.OC, (p.flags & kConvOutF32) != 0)) {
-        case 16: return launch_cfg<INT8, 128, 16, 4, 1, K1>(p, stream);
-        case 32: return launch_cfg<INT8, 128, 32, 4, 1, K1>(p, stream);
-        case 64: return launch_cfg<INT8, 128, 64, 2, 2, K1>(p, stream);
-        case 80: return launch_cfg<INT8, 128, 80, 4, 1, K1>(p, stream);
-        default: return launch_cfg<INT8, 128, 128, 2, 2, K2>(p, stream);
+hipError_t launch_any(const ConvParams& p, const ConvTile& t, int blocks, hipStream_t stream) {
+    if (t.ksw) {
+        switch (t.jn) {
+            case 1: return launch_cfg<INT8, 1, 1, true>(p, blocks, stream);
+            case 2: return launch_cfg<INT8, 2, 1, true>(p, blocks, stream);
+            case 4: return launch_cfg<INT8, 4, 1, true>(p, blocks, stream);
+            case 8: return launch_cfg<INT8, 8, 1, true>(p, blocks, stream);
+        }
+        return hipErrorInvalidValue;
     }
+    switch (t.jn * 8 + t.pw) {
+        case 1 * 8 + 1: return launch_cfg<INT8, 1, 1, false>(p, blocks, stream);
+        case 1 * 8 + 2: return launch_cfg<INT8, 1, 2, false>(p, blocks, stream);
+        case 1 * 8 + 4: return launch_cfg<INT8, 1, 4, false>(p, blocks, stream);
+        case 2 * 8 + 1: return launch_cfg<INT8, 2, 1, false>(p, blocks, stream);
+        case 2 * 8 + 2: return launch_cfg<INT8, 2, 2, false>(p, blocks, stream);
+        case 2 * 8 + 4: return launch_cfg<INT8, 2, 4, false>(p, blocks, stream);
+        case 4 * 8 + 1: return launch_cfg<INT8, 4, 1, false>(p, blocks, stream);
+        case 4 * 8 + 2: return launch_cfg<INT8, 4, 2, false>(p, blocks, stream);
+        case 4 * 8 + 4: return launch_cfg<INT8, 4, 4, false>(p, blocks, stream);
+        case 8 * 8 + 1: return launch_cfg<INT8, 8, 1, false>(p, blocks, stream);
+        case 8 * 8 + 2: return launch_cfg<INT8, 8, 2, false>(p, blocks, stream);
+    }
+    return hipErrorInvalidValue;
+}
+
+int pow2_at_least(int v, int cap) {
+    int r = 1;
+    while (r < v && r < cap) r <<= 1;
+    return r;
+}
+
+// Byte span of an NHWC view of N images (0 when absent).
+uint64_t view_span(int N, int64_t nstride, int32_t cstride, int HW, int C, int esz) {
+    if (N <= 0) return 0;
+    return (uint64_t)(((int64_t)(N - 1) * nstride + (int64_t)(HW - 1) * cstride + C) * esz);
 }
 
 }  // namespace
 
-int conv_block_m() { return 128; }
+namespace {
+// jn * 100 + pw * 10 + ksw + 1, 0 = no override
+std::atomic<int> g_tile_override{0};
 
-// Output channels per block: all of them up to 80, else 128 (64 for fp32
-// output, whose staging would not fit a 128-wide tile).
-int conv_block_n(int oc, bool out_f32) {
-    if (oc <= 16) return 16;
-    if (oc <= 32) return 32;
-    if (oc <= 64) return 64;
-    if (oc <= 80) return 80;
-    return out_f32 ? 64 : 128;
+bool tile_instantiated(const ConvTile& t) {
+    if (t.ksw) return t.pw == 1 && (t.jn == 1 || t.jn == 2 || t.jn == 4 || t.jn == 8);
+    switch (t.jn * 8 + t.pw) {
+        case 9: case 10: case 12: case 17: case 18: case 20: case 33: case 34: case 36: case 65: case 66:
+            return true;
+    }
+    return false;
+}
+}  // namespace
+
+bool set_conv_tile_override(int jn, int pw, int ksw) {
+    if (jn == 0 && pw == 0 && ksw == 0) {
+        g_tile_override.store(0);
+        return true;
+    }
+    const ConvTile t{jn, pw, ksw != 0};
+    if (!tile_instantiated(t)) return false;
+    g_tile_override.store(jn * 100 + pw * 10 + (ksw ? 1 : 0) + 1);
+    return true;
 }
 
-int conv_chunk_k(bool int8, int oc, bool out_f32) {
-    const bool big = conv_block_n(oc, out_f32) == 128;
-    return int8 ? (big ? 128 : 256) : (big ? 64 : 128);
+// Tile choice.  A block is 4 waves x pw 16-position subtiles by jn
+// 16-channel subtiles; its weight chunks are staged once in LDS for all 4
+// waves, each wave streams its own positions.  Cover all output channels (up
+// to 128) so activations are read once, take the most positions per wave that
+// still gives >= 2 blocks per CU, and for maps too small for that shrink the
+// channel tile, then let the 4 waves of a block split k (one position subtile
+// per block).
+ConvTile choose_conv_tile(int M, int OC, int Kp) {
+    const int ov = g_tile_override.load(std::memory_order_relaxed);
+    if (ov) return ConvTile{(ov - 1) / 100, ((ov - 1) / 10) % 10, ((ov - 1) % 10) != 0};
+    const int ocj = (OC + 15) / 16;
+    const int nks = Kp / 64;
+    const int64_t want = 512;
+    auto blocks = [&](int jn, int pw, bool ksw) {
+        return (int64_t)((M + (ksw ? 16 : 64) * pw - 1) / ((ksw ? 16 : 64) * pw)) * ((ocj + jn - 1) / jn);
+    };
+    const int jn0 = pow2_at_least(ocj, 8);
+    for (int pw = 4; pw >= 1; pw >>= 1) {
+        const ConvTile t{jn0, pw, false};
+        if (tile_instantiated(t) && blocks(jn0, pw, false) >= want) return t;
+    }
+    int jn = jn0;
+    while (jn > 1 && blocks(jn, 1, false) < want) jn >>= 1;
+    if (blocks(jn, 1, false) >= want / 2 || nks < 4) return ConvTile{jn, 1, false};
+    // small map: one position subtile per block, k split over the 4 waves
+    jn = jn0;
+    while (jn > 1 && blocks(jn, 1, true) < want) jn >>= 1;
+    return ConvTile{jn, 1, true};
 }
 
-hipError_t launch_conv_igemm(const ConvParams& p, bool int8, hipStream_t stream) {
-    if (p.loader != kLoaderNhwc || p.ksplit < 1 || (p.ksplit > 1 && (!p.ws || !p.counters)))
-        return hipErrorInvalidValue;
-    if (int8) return launch_any<true>(p, stream);
-    return launch_any<false>(p, stream);
+hipError_t launch_conv_igemm(const ConvParams& p0, bool int8, hipStream_t stream) {
+    if (p0.loader != kLoaderNhwc || p0.OC % 4 || p0.C % 8 || p0.Kp % 64 || p0.OCp % 16) return hipErrorInvalidValue;
+    const ConvTile t = choose_conv_tile(p0.M, p0.OC, p0.Kp);
+    const bool out_f32 = (p0.flags & kConvOutF32) != 0;
+    const int HWi = p0.H * p0.W, HWo = p0.OH * p0.OW;
+    // Images per launch: every view a launch touches must stay inside
+    // kMaxViewBytes so the kernel can address it with 32-bit offsets.
+    const uint64_t per_img = std::max({(uint64_t)p0.x_nstride * 2, (uint64_t)p0.y_nstride * (out_f32 ? 4 : 2),
+                                       p0.res ? (uint64_t)p0.r_nstride * 2 : 0,
+                                       p0.acc_out ? (uint64_t)HWo * p0.OC * 4 : 0,
+                                       (uint64_t)HWi * p0.x_cstride * 2});
+    if ((uint64_t)p0.OCp * p0.Kp * 2 > kMaxViewBytes || per_img == 0) return hipErrorInvalidValue;
+    const int per_launch = (int)std::min<uint64_t>((uint64_t)p0.N, kMaxViewBytes / per_img);
+    if (per_launch < 1) return hipErrorInvalidValue;
+    for (int nb = 0; nb < p0.N; nb += per_launch) {
+        ConvParams p = p0;
+        p.N = std::min(per_launch, p0.N - nb);
+        p.M = p.N * HWo;
+        p.x = static_cast<const __half*>(p0.x) + (int64_t)nb * p0.x_nstride;
+        p.y = static_cast<char*>(p0.y) + (int64_t)nb * p0.y_nstride * (out_f32 ? 4 : 2);
+        if (p0.res) p.res = p0.res + (int64_t)nb * p0.r_nstride;
+        if (p0.acc_out) p.acc_out = p0.acc_out + (int64_t)nb * HWo * p0.OC;
+        p.x_bytes = (uint32_t)view_span(p.N, p.x_nstride, p.x_cstride, HWi, p.C, 2);
+        p.y_bytes = (uint32_t)view_span(p.N, p.y_nstride, p.y_cstride, HWo, p.OC, out_f32 ? 4 : 2);
+        p.r_bytes = p.res ? (uint32_t)view_span(p.N, p.r_nstride, p.r_cstride, HWo, p.OC, 2) : 0u;
+        p.ntn = (p.OCp / 16 + t.jn - 1) / t.jn;
+        const int mtile = (t.ksw ? 16 : 64) * t.pw;
+        const int mtiles = (p.M + mtile - 1) / mtile;
+        p.fd_ntn = make_fastdiv((uint32_t)p.ntn);
+        p.fd_ohw = make_fastdiv((uint32_t)HWo);
+        p.fd_ow = make_fastdiv((uint32_t)p.OW);
+        p.fd_c = make_fastdiv((uint32_t)p.C);
+        p.fd_kw = make_fastdiv((uint32_t)p.KW);
+        const int64_t blocks = (int64_t)mtiles * p.ntn;
+        if (blocks > INT32_MAX) return hipErrorInvalidValue;
+        const hipError_t e = int8 ? launch_any<true>(p, t, (int)blocks, stream)
+                                  : launch_any<false>(p, t, (int)blocks, stream);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 }  // namespace aexrt

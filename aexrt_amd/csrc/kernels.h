@@ -6,6 +6,25 @@
 
 namespace aexrt {
 
+// Exact unsigned division by a launch constant d for n < 2^31: q = (umulhi(n,
+// mul) + n) >> shift with l = ceil(log2 d), mul = 2^32 (2^l - d) / d + 1.
+struct FastDiv {
+    uint32_t mul;
+    uint32_t shift;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+    uint32_t l = 0;
+    while ((1ull << l) < d) ++l;
+    const uint64_t mul = ((1ull << 32) * ((1ull << l) - d)) / d + 1;
+    return FastDiv{(uint32_t)mul, l};
+}
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, FastDiv f) { return (__umulhi(n, f.mul) + n) >> f.shift; }
+
+// Largest byte span of one tensor view inside a conv launch: views are
+// addressed with 32-bit buffer offsets; bigger batches are split into several
+// launches by the host.
+constexpr uint64_t kMaxViewBytes = 0x7FF00000ull;
+
 enum ConvFlags : int {
     kConvSilu = 1,      // SiLU after bias
     kConvResidual = 2,  // + residual tensor after the activation
@@ -40,19 +59,28 @@ struct ConvParams {
     int N, H, W, C, OH, OW, OC, KH, KW, S, P;
     int K, M;
     int flags;
-    // split-K: ksplit blocks per output tile exchange partial tiles through
-    // ws (ksplit * tiles * BM * BN int32) and per-tile arrival counters
-    // (zero between runs; the last block re-arms them)
-    int ksplit = 1;
-    void* ws = nullptr;
-    uint32_t* counters = nullptr;
+    // filled in by the igemm launcher
+    uint32_t x_bytes = 0, y_bytes = 0, r_bytes = 0;  // byte spans of the views
+    int ntn = 1;                                     // output-channel tiles
+    FastDiv fd_ntn{}, fd_ohw{}, fd_ow{}, fd_c{}, fd_kw{};
 };
 
+// Per-wave tile of the igemm kernel: jn 16-channel subtiles x pw 16-position
+// subtiles; ksw = the 4 waves of a block split the k steps of one tile.
+struct ConvTile {
+    int jn;
+    int pw;
+    bool ksw;
+};
+ConvTile choose_conv_tile(int M, int OC, int Kp);
+// Forces every following igemm launch onto one tile shape (tuning and tests);
+// (0, 0, 0) restores the automatic choice.  False for a shape that has no
+// kernel instance.
+bool set_conv_tile_override(int jn, int pw, int ksw);
+
+// Implicit-GEMM conv (int8 or fp16 MFMA).  Requires C % 8 == 0, OC % 4 == 0,
+// Kp % 64 == 0, OCp % 16 == 0 and 16-byte aligned views.
 hipError_t launch_conv_igemm(const ConvParams& p, bool int8, hipStream_t stream);
-// Tile geometry of the igemm kernel (for split-K workspace sizing).
-int conv_block_m();
-int conv_block_n(int oc, bool out_f32);
-int conv_chunk_k(bool int8, int oc, bool out_f32);
 // Input staging of the network's first conv: fp32 NCHW -> fp16 NHWC with the
 // channels zero-padded to a multiple of 8 (one 16-byte store per pixel and
 // 8 channels).  y has c_stride Cp = C rounded up to 8, dense.

@@ -124,10 +124,6 @@ struct AexrtYoloModel {
     uint8_t* arena = nullptr;
     uint32_t* slots = nullptr;
     int nslots = 0;
-    void* splitk_ws = nullptr;          // shared by the split-K convs (they run in order)
-    uint32_t* splitk_counters = nullptr;
-    size_t splitk_ws_bytes = 0;
-    int splitk_tiles = 0;
     float* input_dev = nullptr;
     float* input_host = nullptr;
     bool input_needs_nhwc = false;
@@ -631,31 +627,6 @@ AexrtHipTensorView view_of_pl(AexrtYoloModel* m, const Placement& pl) {
 
 bool is_f32(AexrtYoloModel* m, int v) { return m->roots[m->vals[v].pl.root].f32; }
 
-// Split-K factor of an igemm conv: when its output tiles cannot fill the
-// chip (small spatial maps at small batch), the K chunks are spread over up
-// to ~384 blocks in total.
-int choose_ksplit(AexrtYoloModel* m, size_t ci, int* tiles_out) {
-    const ConvState& cs = m->convs[ci];
-    if (is_winograd_algorithm(cs.algorithm)) return 1;
-    const AexrtConv2DDesc d = conv_desc_padded(m, ci);
-    const bool int8 = is_int8_algorithm(cs.algorithm);
-    const bool f32 = is_f32(m, cs.out_value);
-    const int M = (int)(d.batch * d.out_h * d.out_w);
-    const int bn = conv_block_n((int)d.out_channels, f32);
-    const int tiles = ((M + conv_block_m() - 1) / conv_block_m()) * (((int)d.out_channels + bn - 1) / bn);
-    const WeightGeom g = weight_geom(d, cs.algorithm);
-    const int kch = conv_chunk_k(int8, (int)d.out_channels, f32);
-    const int nchunks = (int)((g.kp + kch - 1) / kch);
-    if (tiles_out) *tiles_out = tiles;
-    if (tiles >= 192 || nchunks < 2) return 1;
-    int ks = (384 + tiles - 1) / tiles;
-    if (ks > nchunks) ks = nchunks;
-    // equal chunk counts per split, so no split is left empty
-    const int cps = (nchunks + ks - 1) / ks;
-    ks = (nchunks + cps - 1) / cps;
-    return ks;
-}
-
 std::string conv_label(const EngineCommand& c, size_t ci, uint32_t alg) {
     char buf[192];
     std::snprintf(buf, sizeof(buf), "cmd#%zu %s %ux%ux%u -> %ux%ux%u k%u s%u alg=%s", ci, kind_name(c.kind), c.params[1],
@@ -716,18 +687,6 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                 if (!build_conv_params(d, cs.algorithm, flags, xvw, cs.w, cs.scale, cs.bias,
                                        cs.fused_residual ? &rvw : nullptr, yvw, nullptr, p, why))
                     return fail(m, "command " + std::to_string(ci) + ": " + why);
-                int tiles = 0;
-                p.ksplit = choose_ksplit(m, ci, &tiles);
-                if (p.ksplit > 1) {
-                    const int bn = conv_block_n(p.OC, (flags & AEXRT_HIP_CONV_OUT_F32) != 0);
-                    const size_t need = size_t(p.ksplit) * tiles * conv_block_m() * bn * 4;
-                    if (need > m->splitk_ws_bytes || tiles > m->splitk_tiles) {
-                        p.ksplit = 1;  // e.g. after an override: run unsplit
-                    } else {
-                        p.ws = m->splitk_ws;
-                        p.counters = m->splitk_counters;
-                    }
-                }
                 const uint32_t alg = cs.algorithm;
                 m->steps.push_back(Step{(int)ci, conv_label(c, ci, alg), [p, alg](hipStream_t s) {
                                             if (is_winograd_algorithm(alg)) return launch_winograd_f2x2(p, s);
@@ -806,8 +765,8 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
 }
 
 void drop_graph(AexrtYoloModel* m) {
-    if (m->graph_exec) hipGraphExecDestroy(m->graph_exec);
-    if (m->graph) hipGraphDestroy(m->graph);
+    if (m->graph_exec) (void)hipGraphExecDestroy(m->graph_exec);
+    if (m->graph) (void)hipGraphDestroy(m->graph);
     m->graph_exec = nullptr;
     m->graph = nullptr;
     m->graph_valid = false;
@@ -823,25 +782,30 @@ bool launch_steps(AexrtYoloModel* m, hipStream_t s) {
 
 bool run_network(AexrtYoloModel* m, hipStream_t s) {
     if (m->profile) {
-        std::vector<hipEvent_t> ev(m->steps.size() + 1);
-        for (auto& e : ev) hipEventCreate(&e);
-        hipEventRecord(ev[0], s);
+        std::vector<hipEvent_t> ev(m->steps.size() + 1, nullptr);
         bool ok = true;
+        for (auto& e : ev) ok = ok && check_hip(hipEventCreate(&e), "profile event create");
+        if (ok) ok = check_hip(hipEventRecord(ev[0], s), "profile event record");
+        if (!ok) fail(m, last_error());
         for (size_t i = 0; i < m->steps.size() && ok; ++i) {
             hipError_t e = m->steps[i].launch(s);
             if (e != hipSuccess) ok = fail(m, m->steps[i].label + ": " + hipGetErrorString(e));
-            hipEventRecord(ev[i + 1], s);
+            else if (!check_hip(hipEventRecord(ev[i + 1], s), "profile event record")) ok = fail(m, last_error());
         }
-        hipEventSynchronize(ev.back());
+        if (ok && !check_hip(hipEventSynchronize(ev.back()), "profile sync")) ok = fail(m, last_error());
         m->prof_labels.clear();
         m->prof_ms.clear();
         for (size_t i = 0; ok && i < m->steps.size(); ++i) {
             float ms = 0.f;
-            hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
+            if (!check_hip(hipEventElapsedTime(&ms, ev[i], ev[i + 1]), "profile elapsed")) {
+                ok = fail(m, last_error());
+                break;
+            }
             m->prof_labels.push_back(m->steps[i].label);
             m->prof_ms.push_back(ms);
         }
-        for (auto& e : ev) hipEventDestroy(e);
+        for (auto& e : ev)
+            if (e) (void)hipEventDestroy(e);
         return ok;
     }
     if (!m->use_graph) return launch_steps(m, s);
@@ -853,7 +817,7 @@ bool run_network(AexrtYoloModel* m, hipStream_t s) {
         hipGraph_t g = nullptr;
         const hipError_t ec = hipStreamEndCapture(s, &g);
         if (!ok) {
-            if (g) hipGraphDestroy(g);
+            if (g) (void)hipGraphDestroy(g);
             return false;
         }
         if (ec != hipSuccess) return fail(m, std::string("graph capture end: ") + hipGetErrorString(ec));
@@ -897,25 +861,6 @@ bool build_model(AexrtYoloModel* m) {
         m->input_host = nullptr;
     for (size_t ci = 0; ci < e.commands.size(); ++ci)
         if (m->convs[ci].is_conv && !prepare_conv_weights(m, ci)) return false;
-    // split-K workspace sized for the largest split conv (convs run in order)
-    for (size_t ci = 0; ci < e.commands.size(); ++ci) {
-        if (!m->convs[ci].is_conv) continue;
-        int tiles = 0;
-        const int ks = choose_ksplit(m, ci, &tiles);
-        if (ks <= 1) continue;
-        const AexrtConv2DDesc d = conv_desc_padded(m, ci);
-        const int bn = conv_block_n((int)d.out_channels, is_f32(m, m->convs[ci].out_value));
-        const size_t bytes = size_t(ks) * tiles * conv_block_m() * bn * 4;
-        if (bytes > m->splitk_ws_bytes) m->splitk_ws_bytes = bytes;
-        if (tiles > m->splitk_tiles) m->splitk_tiles = tiles;
-    }
-    if (m->splitk_ws_bytes) {
-        m->splitk_ws = dev_alloc(m, m->splitk_ws_bytes);
-        m->splitk_counters = static_cast<uint32_t*>(dev_alloc(m, size_t(m->splitk_tiles) * 4));
-        if (!m->splitk_ws || !m->splitk_counters ||
-            !check_hip(hipMemset(m->splitk_counters, 0, size_t(m->splitk_tiles) * 4), "split-K counters"))
-            return fail(m, "out of device memory for the split-K workspace");
-    }
     if (!build_steps(m, m->copies)) return false;
     if (!check_hip(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking), "stream create"))
         return fail(m, last_error());
@@ -927,11 +872,12 @@ bool build_model(AexrtYoloModel* m) {
 
 void free_model(AexrtYoloModel* m) {
     if (!m) return;
-    if (m->stream) hipStreamSynchronize(m->stream);
+    // teardown: errors are not actionable here, every resource is released anyway
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
     drop_graph(m);
-    for (void* p : m->allocations) hipFree(p);
-    if (m->input_host) hipHostFree(m->input_host);
-    if (m->stream) hipStreamDestroy(m->stream);
+    for (void* p : m->allocations) (void)hipFree(p);
+    if (m->input_host) (void)hipHostFree(m->input_host);
+    if (m->stream) (void)hipStreamDestroy(m->stream);
     delete m;
 }
 
@@ -973,7 +919,8 @@ bool copy_value_to_host(AexrtYoloModel* m, int v, float* out, uint64_t elements)
                                            x.H * x.W, m->stream);
     if (e == hipSuccess) e = hipMemcpyAsync(out, tmp, n * 4, hipMemcpyDeviceToHost, m->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
-    hipFree(tmp);
+    const hipError_t ef = hipFree(tmp);
+    if (e == hipSuccess) e = ef;
     if (e != hipSuccess) return fail(m, std::string("readback: ") + hipGetErrorString(e));
     return true;
 }
@@ -1170,14 +1117,14 @@ int aexrt_yolo_run(AexrtDevice* device, AexrtYoloModel* m, const float* input, u
 int aexrt_yolo_debug_output(AexrtYoloModel* m, float* out, uint64_t elements) {
     if (!m || !out) return 0;
     std::lock_guard<std::mutex> lock(m->mutex);
-    hipStreamSynchronize(m->stream);
+    if (!check_hip(hipStreamSynchronize(m->stream), "debug output sync")) return fail(m, last_error()) ? 1 : 0;
     return copy_value_to_host(m, (int)m->eng.manifest.output_value, out, elements) ? 1 : 0;
 }
 
 int aexrt_yolo_debug_value(AexrtYoloModel* m, uint32_t value_id, float* out, uint64_t elements) {
     if (!m || !out || value_id >= m->vals.size()) return 0;
     std::lock_guard<std::mutex> lock(m->mutex);
-    hipStreamSynchronize(m->stream);
+    if (!check_hip(hipStreamSynchronize(m->stream), "debug value sync")) return fail(m, last_error()) ? 1 : 0;
     int v = (int)value_id;
     if (m->vals[v].redirect >= 0) return fail(m, "value was fused into a residual add and is never stored") ? 1 : 0;
     if (m->vals[v].is_input) {
@@ -1273,7 +1220,7 @@ int aexrt_yolo_override_conv_algorithm(AexrtYoloModel* m, uint32_t command_index
         ok = true;
     }
     if (!ok) return fail(m, "override: algorithm not applicable to this command") ? 1 : 0;
-    hipStreamSynchronize(m->stream);
+    if (!check_hip(hipStreamSynchronize(m->stream), "override sync")) return fail(m, last_error()) ? 1 : 0;
     const uint32_t previous = m->convs[command_index].algorithm;
     m->convs[command_index].algorithm = kernel;
     if (!prepare_conv_weights(m, command_index)) {

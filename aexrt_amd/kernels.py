@@ -108,6 +108,11 @@ def can_use_conv_int8(params: Sequence[int], kernel_elems: int) -> bool:
     return bool(_lib.lib().aexrt_hip_can_use_conv_int8(ctypes.byref(d), kernel_elems))
 
 
+def set_conv_tile(jn: int = 0, pw: int = 0, ksw: bool = False) -> None:
+    """Force the igemm conv kernel's per-wave tile for later launches ((0, 0) = automatic)."""
+    check(_lib.lib().aexrt_hip_set_conv_tile(jn, pw, 1 if ksw else 0), "set_conv_tile")
+
+
 def conv_weight_bytes(params: Sequence[int], algorithm: int) -> int:
     d = ConvDesc.from_params(params)
     n = ctypes.c_uint64()

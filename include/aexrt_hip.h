@@ -163,6 +163,13 @@ int aexrt_hip_conv2d(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t f
  * requirement in_channels % 16 == 0 (amax is kept per 16 channels). */
 int aexrt_hip_can_use_conv_int8(const AexrtConv2DDesc* desc, uint32_t kernel_elems);
 
+/* Tuning/test hook with no counterpart in the reference: forces the
+ * implicit-GEMM conv kernel onto one per-wave tile (jn 16-channel x pw
+ * 16-position subtiles; ksw = the 4 waves of a block split k, pw must be 1)
+ * for every following launch in the process; (0, 0, 0) restores the
+ * automatic choice.  Returns 0 for a tile without a kernel instance. */
+int aexrt_hip_set_conv_tile(int32_t jn, int32_t pw, int32_t ksw);
+
 /* Glue ops of the replay stream on NHWC fp16 views. */
 int aexrt_hip_fill_u32(uint32_t* dst, uint64_t count, uint32_t value, void* stream);
 int aexrt_hip_nchw_f32_to_nhwc(const float* x, uint32_t batch, uint32_t channels, uint32_t plane,

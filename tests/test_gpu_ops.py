@@ -220,6 +220,64 @@ def test_fp16_conv_residual_into_channel_slice(cuda):
         assert s[g] == np.float32(np.abs(got[:, g * 16:(g + 1) * 16]).max()).view(np.uint32)
 
 
+def _run_fp16_residual(cuda, n, c, h, w, seed, *, tail=(32, 64), width=96):
+    """silu(conv3x3(x)) + r written into channels [tail) of a wider NHWC tensor."""
+    import torch
+
+    rng = np.random.default_rng(seed)
+    x = O.round_f16(rng.standard_normal((n, c, h, w)).astype(np.float32))
+    r = O.round_f16(rng.standard_normal((n, c, h, w)).astype(np.float32))
+    wt = he_weight(rng, c, c, 3)
+    b = packing.fp16_round(rng.uniform(-0.1, 0.1, c).astype(np.float32))
+    desc = O.conv_desc(n, c, h, w, c, 3, 1, 1)
+    pc = K.prepare_conv(desc, 5, K.SRC_RAW_F32, wt, b, device=cuda)
+    big = torch.zeros((n, h, w, width), dtype=torch.float16, device=cuda)
+    slots = K.new_slots(width, cuda)
+    lo, hi = tail
+    K.conv2d(pc, _dev_nhwc(x, cuda), big[..., lo:hi], flags=K.SILU | K.RESIDUAL, residual=_dev_nhwc(r, cuda),
+             y_slots=slots[lo // 16:(hi + 15) // 16])
+    torch.cuda.synchronize()
+    y_ref = O.cpu_conv2d(x, O.round_f16(wt), b, desc, silu=True) + r
+    return y_ref, nhwc_to_nchw(big.float().cpu().numpy()), _u32(slots)
+
+
+# Every per-wave tile the igemm kernel is instantiated for: (jn, pw, ksw).
+TILES = [(1, 1, False), (1, 2, False), (1, 4, False), (2, 1, False), (2, 2, False), (2, 4, False),
+         (4, 1, False), (4, 2, False), (4, 4, False), (8, 1, False), (8, 2, False),
+         (1, 1, True), (2, 1, True), (4, 1, True), (8, 1, True)]
+
+
+@pytest.mark.parametrize("jn,pw,ksw", TILES, ids=[f"jn{t[0]}_pw{t[1]}{'_ksw' if t[2] else ''}" for t in TILES])
+def test_conv_every_tile(cuda, jn, pw, ksw):
+    """Each kernel instance on shapes with partial channel tiles, ragged
+    position tails, k steps that straddle taps, fp32 output and a residual."""
+    K.set_conv_tile(jn, pw, ksw)
+    try:
+        # int8 3x3 s1: OC 80 = 5 channel subtiles, M = 286, C = 48 (taps straddle k steps)
+        r = _run_int8(cuda, 2, 48, 11, 13, 80, 3, 1, 71)
+        np.testing.assert_array_equal(r["acc"], r["acc_ref"])
+        err, allowed = tol_range(r["y_ref"], r["y"], FP16_TOL)
+        assert err <= allowed, (err, allowed)
+        want = np.array([np.float32(np.abs(r["y"][:, g * 16:(g + 1) * 16]).max()).view(np.uint32)
+                         for g in range(5)], dtype=np.uint32)
+        np.testing.assert_array_equal(r["slots"], want)
+        # int8 3x3 s2, fp32 output without activation
+        r = _run_int8(cuda, 1, 32, 17, 15, 32, 3, 2, 72, silu=False, out_f32=True)
+        np.testing.assert_array_equal(r["acc"], r["acc_ref"])
+        err, allowed = tol_range(r["y_ref"], r["y"], FP32_TOL)
+        assert err <= allowed, (err, allowed)
+        # int8 1x1 with a long k (K = 384, 6 steps)
+        r = _run_int8(cuda, 1, 384, 6, 5, 64, 1, 1, 73)
+        np.testing.assert_array_equal(r["acc"], r["acc_ref"])
+        # fp16 3x3, C = 24 (8-channel halves cross taps), residual into a channel slice
+        y_ref, got, slots = _run_fp16_residual(cuda, 2, 24, 9, 7, 74, tail=(48, 72), width=96)
+        err, allowed = tol_range(y_ref, got[:, 48:72], FP16_TOL)
+        assert err <= allowed, (err, allowed)
+        assert not got[:, :48].any() and not got[:, 72:].any()
+    finally:
+        K.set_conv_tile(0, 0, False)
+
+
 WINO_CASES = [
     ("64_64_20", 1, 64, 20, 20, 64),
     ("96_64_20x18", 1, 96, 20, 18, 64),

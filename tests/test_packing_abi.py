@@ -155,3 +155,35 @@ def test_int8_eligibility_follows_reference_plus_c16():
     ]
     for d, kk in bad:
         assert not K.can_use_conv_int8(d, kk)
+
+
+def test_conv_tile_override_accepts_only_instantiated_tiles():
+    for jn, pw, ksw in [(1, 1, False), (2, 4, False), (8, 1, False), (4, 1, True), (8, 1, True)]:
+        K.set_conv_tile(jn, pw, ksw)
+    try:
+        for jn, pw, ksw in [(3, 1, False), (8, 4, False), (1, 8, False), (2, 2, True), (16, 1, False)]:
+            with pytest.raises(RuntimeError, match="no kernel instance"):
+                K.set_conv_tile(jn, pw, ksw)
+    finally:
+        K.set_conv_tile(0, 0, False)
+
+
+def _fastdiv(n: np.ndarray, d: int) -> np.ndarray:
+    """The kernels' launch-constant division (kernels.h FastDiv) in uint64 arithmetic."""
+    l = 0
+    while (1 << l) < d:
+        l += 1
+    mul = ((1 << 32) * ((1 << l) - d)) // d + 1
+    hi = (n.astype(np.uint64) * np.uint64(mul)) >> np.uint64(32)
+    return (hi + n.astype(np.uint64)) >> np.uint64(l)
+
+
+def test_fastdiv_is_exact_division_below_2_31():
+    rng = np.random.default_rng(5)
+    divisors = [1, 2, 3, 5, 7, 10, 20, 40, 80, 100, 160, 400, 1600, 6400, 25600, 102400, 2100, 144]
+    divisors += [int(v) for v in rng.integers(1, 1 << 20, 40)]
+    for d in divisors:
+        n = np.concatenate([rng.integers(0, 1 << 31, 20000, dtype=np.int64),
+                            np.arange(0, 4096, dtype=np.int64) * d + (d - 1),
+                            np.arange((1 << 31) - 4096, 1 << 31, dtype=np.int64)])
+        np.testing.assert_array_equal(_fastdiv(n, d), n // d)
