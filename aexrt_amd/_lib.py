@@ -44,8 +44,9 @@ class TensorView(Structure):
         ("data", c_void_p),
         ("n_stride", c_int64),
         ("c_stride", c_int32),
-        ("reserved", c_uint32),
+        ("amax_stripes", c_uint32),
         ("amax_slots", c_void_p),
+        ("amax_stripe_stride", c_uint64),
     ]
 
 

@@ -164,7 +164,7 @@ using namespace aexrt;
 
 extern "C" {
 
-uint32_t aexrt_hip_abi_version(void) { return 1u; }
+uint32_t aexrt_hip_abi_version(void) { return 2u; }
 
 const char* aexrt_hip_get_last_error(void) { return last_error(); }
 
@@ -305,12 +305,13 @@ int aexrt_hip_conv2d(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t f
 
 int aexrt_hip_amax_slots(const AexrtHipTensorView* x, uint32_t batch, uint32_t height, uint32_t width,
                          uint32_t channels, void* stream) {
-    if (!x || !x->data || !x->amax_slots || channels % 16 || x->c_stride % 8 || x->n_stride % 8) {
+    if (!x || !x->data || !x->amax_slots || channels % 16 || x->c_stride % 8 || x->n_stride % 8 ||
+        !slot_ref_ok(*x)) {
         set_error("amax_slots: bad view (need slots, C % 16 == 0, 8-element strides)");
         return 0;
     }
     return check_hip(launch_amax_slots_nhwc(static_cast<const __half*>(x->data), x->n_stride, x->c_stride,
-                                            (int)batch, (int)(height * width), (int)channels, x->amax_slots,
+                                            (int)batch, (int)(height * width), (int)channels, slot_ref(x),
                                             static_cast<hipStream_t>(stream)),
                      "amax_slots")
                ? 1
@@ -333,12 +334,13 @@ int aexrt_hip_amax_nchw(const void* x, uint32_t is_f16, uint32_t batch, uint32_t
 
 int aexrt_hip_quantize(const AexrtHipTensorView* x, uint32_t batch, uint32_t height, uint32_t width,
                        uint32_t channels, int8_t* q, void* stream) {
-    if (!x || !x->data || !x->amax_slots || !q || channels % 16 || x->c_stride % 8 || x->n_stride % 8) {
+    if (!x || !x->data || !x->amax_slots || !q || channels % 16 || x->c_stride % 8 || x->n_stride % 8 ||
+        !slot_ref_ok(*x)) {
         set_error("quantize: bad view (need slots, C % 16 == 0, 8-element strides)");
         return 0;
     }
     return check_hip(launch_quantize_nhwc(static_cast<const __half*>(x->data), x->n_stride, x->c_stride,
-                                          (int)batch, (int)(height * width), (int)channels, x->amax_slots,
+                                          (int)batch, (int)(height * width), (int)channels, slot_ref(x),
                                           (int)(channels / 16), q, static_cast<hipStream_t>(stream)),
                      "quantize")
                ? 1
@@ -370,12 +372,12 @@ int aexrt_hip_fill_u32(uint32_t* dst, uint64_t count, uint32_t value, void* stre
 
 int aexrt_hip_nchw_f32_to_nhwc(const float* x, uint32_t batch, uint32_t channels, uint32_t plane,
                                const AexrtHipTensorView* y, void* stream) {
-    if (!x || !y || !y->data) {
-        set_error("nchw_f32_to_nhwc: null argument");
+    if (!x || !y || !y->data || !slot_ref_ok(*y)) {
+        set_error("nchw_f32_to_nhwc: null argument or bad slot stripes");
         return 0;
     }
     return check_hip(launch_nchw_f32_to_nhwc_f16(x, static_cast<__half*>(y->data), y->n_stride, y->c_stride,
-                                                 (int)batch, (int)channels, (int)plane, y->amax_slots,
+                                                 (int)batch, (int)channels, (int)plane, slot_ref(y),
                                                  static_cast<hipStream_t>(stream)),
                      "nchw_f32_to_nhwc")
                ? 1
@@ -397,7 +399,7 @@ int aexrt_hip_nhwc_to_nchw_f32(const AexrtHipTensorView* x, uint32_t is_f16, uin
 
 static bool vec_view_ok(const AexrtHipTensorView* v) {
     return v && v->data && (reinterpret_cast<uintptr_t>(v->data) % 16) == 0 && v->c_stride % 8 == 0 &&
-           v->n_stride % 8 == 0;
+           v->n_stride % 8 == 0 && slot_ref_ok(*v);
 }
 
 int aexrt_hip_copy(const AexrtHipTensorView* src, const AexrtHipTensorView* dst, uint32_t batch, uint32_t plane,
@@ -408,7 +410,7 @@ int aexrt_hip_copy(const AexrtHipTensorView* src, const AexrtHipTensorView* dst,
     }
     return check_hip(launch_copy_nhwc(static_cast<const __half*>(src->data), src->n_stride, src->c_stride,
                                       static_cast<__half*>(dst->data), dst->n_stride, dst->c_stride, (int)batch,
-                                      (int)plane, (int)channels, dst->amax_slots, static_cast<hipStream_t>(stream)),
+                                      (int)plane, (int)channels, slot_ref(dst), static_cast<hipStream_t>(stream)),
                      "copy")
                ? 1
                : 0;
@@ -424,7 +426,7 @@ int aexrt_hip_maxpool(const AexrtHipTensorView* x, const AexrtHipTensorView* y, 
     return check_hip(launch_maxpool_nhwc(static_cast<const __half*>(x->data), x->n_stride, x->c_stride,
                                          static_cast<__half*>(y->data), y->n_stride, y->c_stride, (int)batch,
                                          (int)in_h, (int)in_w, (int)channels, (int)out_h, (int)out_w, (int)kernel,
-                                         (int)stride, (int)pad, y->amax_slots, static_cast<hipStream_t>(stream)),
+                                         (int)stride, (int)pad, slot_ref(y), static_cast<hipStream_t>(stream)),
                      "maxpool")
                ? 1
                : 0;
@@ -440,7 +442,7 @@ int aexrt_hip_resize_nearest(const AexrtHipTensorView* x, const AexrtHipTensorVi
     return check_hip(launch_resize_nearest_nhwc(static_cast<const __half*>(x->data), x->n_stride, x->c_stride,
                                                 static_cast<__half*>(y->data), y->n_stride, y->c_stride,
                                                 (int)batch, (int)in_h, (int)in_w, (int)channels, (int)out_h,
-                                                (int)out_w, y->amax_slots, static_cast<hipStream_t>(stream)),
+                                                (int)out_w, slot_ref(y), static_cast<hipStream_t>(stream)),
                      "resize")
                ? 1
                : 0;
@@ -455,7 +457,7 @@ int aexrt_hip_add(const AexrtHipTensorView* a, const AexrtHipTensorView* b, cons
     return check_hip(launch_add_nhwc(static_cast<const __half*>(a->data), a->n_stride, a->c_stride,
                                      static_cast<const __half*>(b->data), b->n_stride, b->c_stride,
                                      static_cast<__half*>(y->data), y->n_stride, y->c_stride, (int)batch,
-                                     (int)plane, (int)channels, y->amax_slots, static_cast<hipStream_t>(stream)),
+                                     (int)plane, (int)channels, slot_ref(y), static_cast<hipStream_t>(stream)),
                      "add")
                ? 1
                : 0;

@@ -4,6 +4,8 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include "kernels.h"
+
 namespace aexrt {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -19,12 +21,25 @@ constexpr int kWave = 64;
 // of its slots; the per-tensor amax is the max over all slots.
 constexpr int kAmaxGroup = 16;
 
+// The slot copy a workgroup's maxima go to.
+__device__ __forceinline__ uint32_t* slot_copy(const SlotRef& r, uint32_t block) {
+    return r.p + (block % r.stripes) * r.stride;
+}
+
 __device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
 __device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+// Max of the slot bit patterns over a wave: slots order as unsigned integers
+// (a NaN pattern wins over every finite value, as in the atomicMax producers).
+__device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, off, kWave));
     return v;
 }
 
@@ -44,7 +59,10 @@ __device__ __forceinline__ uint32_t pack4_q(float a, float b, float c, float d, 
            (((uint32_t)quant_int(c, s) & 0xFFu) << 16) | (((uint32_t)quant_int(d, s) & 0xFFu) << 24);
 }
 
-__device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
+// SiLU v * sigmoid(v) = v / (1 + e^-v) with the hardware exp2 and reciprocal
+// (1 ulp each); the reference's HLSL division is itself a 2.5-ulp operation,
+// and both round to the same fp16 except at rare ties.
+__device__ __forceinline__ float silu(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
 
 // Folds a non-negative value into an amax slot.  Slots only grow during a
 // run, so a value that does not exceed what is already visible cannot change

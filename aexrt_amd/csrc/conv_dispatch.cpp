@@ -74,6 +74,10 @@ bool build_conv_params(const AexrtConv2DDesc& d, uint32_t algorithm, uint32_t fl
             return false;
         }
     }
+    if (!slot_ref_ok(x) || !slot_ref_ok(y)) {
+        why = "striped amax slots need a stride with stripes * stride < 2^31";
+        return false;
+    }
     if ((uint32_t)x.c_stride < d.in_channels) {
         why = "input c_stride smaller than in_channels";
         return false;
@@ -96,7 +100,7 @@ bool build_conv_params(const AexrtConv2DDesc& d, uint32_t algorithm, uint32_t fl
     p.x_nstride = x.n_stride;
     p.x_cstride = x.c_stride;
     p.loader = kLoaderNhwc;
-    p.x_slots = x.amax_slots;
+    p.x_slots = slot_ref(x);
     p.x_nslots = (int)(d.in_channels / 16);
     p.w = weight;
     p.Kp = (int)g.kp;
@@ -106,7 +110,7 @@ bool build_conv_params(const AexrtConv2DDesc& d, uint32_t algorithm, uint32_t fl
     p.y = y.data;
     p.y_nstride = y.n_stride;
     p.y_cstride = y.c_stride;
-    p.y_slots = y.amax_slots;
+    p.y_slots = slot_ref(y);
     if (residual && (flags & AEXRT_HIP_CONV_RESIDUAL)) {
         p.res = static_cast<const __half*>(residual->data);
         p.r_nstride = residual->n_stride;

@@ -1,0 +1,10 @@
+// Implicit-GEMM conv kernel instances: int8, weights staged chunk by chunk, SiLU plus residual to fp16.
+#include "conv_igemm.h"
+
+namespace aexrt {
+namespace igemm {
+
+AEXRT_IGEMM_INSTANCE(true, true, 2)
+
+}  // namespace igemm
+}  // namespace aexrt

@@ -20,6 +20,18 @@ bool can_use_int8(const AexrtConv2DDesc& d, uint32_t kernel_elems);
 bool winograd_shape_ok(const AexrtConv2DDesc& d);
 bool generic_shape_ok(const AexrtConv2DDesc& d);
 
+// The (possibly striped) slot array of a view; p == nullptr when it has none.
+inline SlotRef slot_ref(const AexrtHipTensorView& v) {
+    const uint32_t stripes = v.amax_stripes ? v.amax_stripes : 1u;
+    return SlotRef{v.amax_slots, stripes, stripes > 1 ? (uint32_t)v.amax_stripe_stride : 0u};
+}
+inline SlotRef slot_ref(const AexrtHipTensorView* v) { return v ? slot_ref(*v) : SlotRef{nullptr, 1u, 0u}; }
+// A striped view needs a stride that fits the kernels' 32-bit slot arithmetic.
+inline bool slot_ref_ok(const AexrtHipTensorView& v) {
+    return v.amax_stripes <= 1 || (v.amax_stripe_stride > 0 && v.amax_stripe_stride <= 0x7FFFFFFFull &&
+                                   (uint64_t)v.amax_stripes * v.amax_stripe_stride <= 0x7FFFFFFFull);
+}
+
 // Geometry of a repacked conv weight.
 struct WeightGeom {
     uint32_t ocp;        // output channels rounded up to 16

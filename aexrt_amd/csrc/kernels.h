@@ -25,6 +25,15 @@ __device__ __forceinline__ uint32_t fdiv(uint32_t n, FastDiv f) { return (__umul
 // launches by the host.
 constexpr uint64_t kMaxViewBytes = 0x7FF00000ull;
 
+// A (possibly striped) amax slot array: copy s of slot g at p[s * stride + g].
+// Producers fold each workgroup's maxima into one copy, readers take the max
+// over all copies.  p == nullptr: no slots.
+struct SlotRef {
+    uint32_t* p;
+    uint32_t stripes;  // >= 1
+    uint32_t stride;   // uint32 elements between copies
+};
+
 enum ConvFlags : int {
     kConvSilu = 1,      // SiLU after bias
     kConvResidual = 2,  // + residual tensor after the activation
@@ -42,7 +51,7 @@ struct ConvParams {
     int64_t x_nstride;
     int32_t x_cstride;
     int32_t loader;
-    const uint32_t* x_slots;  // amax slots of the input channel range (int8 only)
+    SlotRef x_slots;          // amax slots of the input channel range (int8 only)
     int32_t x_nslots;
     const void* w;            // [OCp][Kp], int8 or fp16
     int32_t Kp, OCp;
@@ -51,7 +60,7 @@ struct ConvParams {
     void* y;
     int64_t y_nstride;
     int32_t y_cstride;
-    uint32_t* y_slots;        // amax slots of the output channels, may be null
+    SlotRef y_slots;          // amax slots of the output channels, p may be null
     const __half* res;        // residual view, same geometry as y
     int64_t r_nstride;
     int32_t r_cstride;
@@ -61,8 +70,11 @@ struct ConvParams {
     int flags;
     // filled in by the igemm launcher
     uint32_t x_bytes = 0, y_bytes = 0, r_bytes = 0;  // byte spans of the views
+    uint32_t x_slot_bytes = 0;                       // byte span of the input slots
     int ntn = 1;                                     // output-channel tiles
-    FastDiv fd_ntn{}, fd_ohw{}, fd_ow{}, fd_c{}, fd_kw{};
+    int npt = 1;                                     // position tiles
+    int per = 1;                                     // position tiles per block
+    FastDiv fd_ntn{}, fd_ohw{}, fd_ow{}, fd_c{}, fd_kw{}, fd_nit{}, fd_ns{};
 };
 
 // Per-wave tile of the igemm kernel: jn 16-channel subtiles x pw 16-position
@@ -95,14 +107,14 @@ hipError_t launch_winograd_f2x2(const ConvParams& p, hipStream_t stream);
 // amax slots of an NHWC fp16 view: slots[g] |= max|x| over channels 16g..16g+15
 // (atomicMax, caller clears).  C % 16 == 0.
 hipError_t launch_amax_slots_nhwc(const __half* x, int64_t nstride, int32_t cstride, int N, int HW,
-                                  int C, uint32_t* slots, hipStream_t stream);
+                                  int C, SlotRef slots, hipStream_t stream);
 // The reference's amax buffer over an NCHW tensor (fp16 or fp32): slot 0 =
 // whole tensor, slot 1+g = memory strip [g*16*N*HW, (g+1)*16*N*HW).
 hipError_t launch_amax_strips_nchw(const void* x, bool f16, int N, int C, int HW, uint32_t* slots,
                                    hipStream_t stream);
 // int8 NHWC (dense) from an fp16 NHWC view with the per-tensor amax of nslots slots.
 hipError_t launch_quantize_nhwc(const __half* x, int64_t nstride, int32_t cstride, int N, int HW, int C,
-                                const uint32_t* slots, int nslots, int8_t* q, hipStream_t stream);
+                                SlotRef slots, int nslots, int8_t* q, hipStream_t stream);
 // The reference's NC/4HW4 pack (per-tensor slot 0, or per_group slots 1+icg/4).
 hipError_t launch_quant_pack_nchw(const void* x, bool f16, int N, int C, int HW, const uint32_t* slots,
                                   bool per_group, uint32_t* packed, hipStream_t stream);
@@ -112,20 +124,20 @@ hipError_t launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t strea
 // dst view (channels [0,C)) = src view; amax slots of dst updated when non-null.
 hipError_t launch_copy_nhwc(const __half* src, int64_t s_nstride, int32_t s_cstride, __half* dst,
                             int64_t d_nstride, int32_t d_cstride, int N, int HW, int C,
-                            uint32_t* dst_slots, hipStream_t stream);
+                            SlotRef dst_slots, hipStream_t stream);
 hipError_t launch_maxpool_nhwc(const __half* x, int64_t x_nstride, int32_t x_cstride, __half* y,
                                int64_t y_nstride, int32_t y_cstride, int N, int H, int W, int C,
-                               int OH, int OW, int k, int s, int pad, uint32_t* y_slots,
+                               int OH, int OW, int k, int s, int pad, SlotRef y_slots,
                                hipStream_t stream);
 hipError_t launch_resize_nearest_nhwc(const __half* x, int64_t x_nstride, int32_t x_cstride, __half* y,
                                       int64_t y_nstride, int32_t y_cstride, int N, int H, int W, int C,
-                                      int OH, int OW, uint32_t* y_slots, hipStream_t stream);
+                                      int OH, int OW, SlotRef y_slots, hipStream_t stream);
 hipError_t launch_add_nhwc(const __half* a, int64_t a_nstride, int32_t a_cstride, const __half* b,
                            int64_t b_nstride, int32_t b_cstride, __half* y, int64_t y_nstride,
-                           int32_t y_cstride, int N, int HW, int C, uint32_t* y_slots, hipStream_t stream);
+                           int32_t y_cstride, int N, int HW, int C, SlotRef y_slots, hipStream_t stream);
 // fp32 NCHW <-> fp16 NHWC views.
 hipError_t launch_nchw_f32_to_nhwc_f16(const float* x, __half* y, int64_t y_nstride, int32_t y_cstride,
-                                       int N, int C, int HW, uint32_t* y_slots, hipStream_t stream);
+                                       int N, int C, int HW, SlotRef y_slots, hipStream_t stream);
 hipError_t launch_nhwc_to_nchw_f32(const void* x, bool f16, int64_t x_nstride, int32_t x_cstride, float* y,
                                    int N, int C, int HW, hipStream_t stream);
 

@@ -16,10 +16,10 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kMaxSlots = 128;  // up to 2048 channels per view
 
-inline int grid_for(int64_t work, int per_block = kThreads) {
-    int64_t g = (work + per_block - 1) / per_block;
+inline int grid_for(int64_t work, int max_blocks = 256 * 16) {
+    int64_t g = (work + kThreads - 1) / kThreads;
     if (g < 1) g = 1;
-    if (g > 256 * 16) g = 256 * 16;  // 16 waves-of-blocks per CU is plenty
+    if (g > max_blocks) g = max_blocks;
     return (int)g;
 }
 
@@ -35,7 +35,9 @@ inline int grid_cols(int64_t chunks, int C) {
         b = t;
     }
     const int r = cc / a;
-    int g = grid_for(chunks);
+    // 4 blocks per CU: enough to keep HBM busy with the grid-stride loops,
+    // and few enough that the blocks' slot updates (one per group) stay cheap
+    int g = grid_for(chunks, 256 * 4);
     g = (g + r - 1) / r * r;
     return g;
 }
@@ -45,8 +47,10 @@ __device__ __forceinline__ void slots_init(uint32_t* s, int n) {
     __syncthreads();
 }
 
-__device__ __forceinline__ void slots_flush(const uint32_t* s, int n, uint32_t* g) {
+// Block maxima -> this block's copy of the slot array.
+__device__ __forceinline__ void slots_flush(const uint32_t* s, int n, const SlotRef& ref) {
     __syncthreads();
+    uint32_t* g = slot_copy(ref, blockIdx.x);
     for (int i = threadIdx.x; i < n; i += blockDim.x)
         if (s[i]) slot_max(g + i, u2f(s[i]));
 }
@@ -73,6 +77,28 @@ struct GroupMax {
     }
 };
 
+// Element e of a chunk loop over (n, pos, 8-channel chunk) NHWC views:
+// e = (n * HW + pos) * CC + cc.  The divisions are by launch constants.
+struct ChunkDivs {
+    FastDiv cc;   // C / 8
+    FastDiv hw;   // pixels per image
+    FastDiv ow;   // output row width (maxpool / resize)
+    FastDiv oh;   // output rows (resize)
+};
+
+inline ChunkDivs chunk_divs(int C, int HW, int OW = 1, int OH = 1) {
+    return ChunkDivs{make_fastdiv((uint32_t)(C / 8)), make_fastdiv((uint32_t)HW), make_fastdiv((uint32_t)OW),
+                     make_fastdiv((uint32_t)OH)};
+}
+
+__device__ __forceinline__ void chunk_split(uint32_t e, int CC, int HW, const ChunkDivs& d, int& n, int& pp,
+                                            int& cc) {
+    const uint32_t pix = fdiv(e, d.cc);
+    cc = (int)(e - pix * (uint32_t)CC);
+    n = (int)fdiv(pix, d.hw);
+    pp = (int)(pix - (uint32_t)n * (uint32_t)HW);
+}
+
 __device__ __forceinline__ float max8_abs(const uint4& v) {
     const __half2* h = reinterpret_cast<const __half2*>(&v);
     float m = 0.0f;
@@ -87,19 +113,17 @@ __device__ __forceinline__ float max8_abs(const uint4& v) {
 // ---- amax --------------------------------------------------------------------
 
 __global__ __launch_bounds__(kThreads) void amax_slots_nhwc_kernel(
-    const __half* x, int64_t nstride, int32_t cstride, int HW, int C, int64_t chunks,
-    uint32_t* slots) {
+    const __half* x, int64_t nstride, int32_t cstride, int HW, int C, int chunks, ChunkDivs dv,
+    SlotRef slots) {
     __shared__ uint32_t ls[kMaxSlots];
     const int CC = C / 8;
     const int G = C / 16;
     slots_init(ls, G);
     GroupMax gm;
-    const int64_t step = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
-        const int pix = (int)e / CC;
-        const int cc = (int)e - pix * CC;
-        const int n = pix / HW;
-        const int pp = pix - n * HW;
+    const int step = gridDim.x * blockDim.x;
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
+        int n, pp, cc;
+        chunk_split((uint32_t)e, CC, HW, dv, n, pp, cc);
         const uint4 v = *reinterpret_cast<const uint4*>(x + n * nstride + (int64_t)pp * cstride + cc * 8);
         gm.add(cc >> 1, max8_abs(v), ls);
     }
@@ -128,30 +152,30 @@ __global__ __launch_bounds__(kThreads) void amax_strips_kernel(const T* x, int64
     }
     gm.flush(ls);
     if (G > 0) atomicMax(&ls[0], f2u(all));
-    slots_flush(ls, G + 1, slots);
+    slots_flush(ls, G + 1, SlotRef{slots, 1u, 0u});
 }
 
-__device__ __forceinline__ float slots_amax(const uint32_t* slots, int n) {
+__device__ __forceinline__ float slots_amax(const SlotRef& r, int n) {
     uint32_t am = 0;
-    for (int i = 0; i < n; ++i) am = max(am, slots[i]);
+    for (uint32_t c = 0; c < r.stripes; ++c)
+        for (int i = 0; i < n; ++i) am = max(am, r.p[c * r.stride + i]);
     return u2f(am);
 }
 
 // ---- quantize -----------------------------------------------------------------
 
 __global__ __launch_bounds__(kThreads) void quantize_nhwc_kernel(
-    const __half* x, int64_t nstride, int32_t cstride, int HW, int C, int64_t chunks,
-    const uint32_t* slots, int nslots, int8_t* q) {
+    const __half* x, int64_t nstride, int32_t cstride, int HW, int C, int chunks, ChunkDivs dv,
+    SlotRef slots, int nslots, int8_t* q) {
     const float a = slots_amax(slots, nslots);
     const float s = a > 0.0f ? 127.0f / a : 0.0f;
     const int CC = C / 8;
-    const int64_t step = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
-        const int pix = (int)e / CC;
-        const int cc = (int)e - pix * CC;
-        const int n = pix / HW;
-        const int pp = pix - n * HW;
-        const uint4 v = *reinterpret_cast<const uint4*>(x + n * nstride + pp * cstride + cc * 8);
+    const int step = gridDim.x * blockDim.x;
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
+        int n, pp, cc;
+        chunk_split((uint32_t)e, CC, HW, dv, n, pp, cc);
+        const int pix = n * HW + pp;
+        const uint4 v = *reinterpret_cast<const uint4*>(x + n * nstride + (int64_t)pp * cstride + cc * 8);
         uint2 o = make_uint2(0u, 0u);
         if (a > 0.0f) {
             const __half2* h = reinterpret_cast<const __half2*>(&v);
@@ -160,7 +184,7 @@ __global__ __launch_bounds__(kThreads) void quantize_nhwc_kernel(
             o.x = pack4_q(f0.x, f0.y, f1.x, f1.y, s);
             o.y = pack4_q(f2.x, f2.y, f3.x, f3.y, s);
         }
-        *reinterpret_cast<uint2*>(q + pix * C + cc * 8) = o;
+        *reinterpret_cast<uint2*>(q + (int64_t)pix * C + cc * 8) = o;
     }
 }
 
@@ -202,62 +226,66 @@ __global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t v) {
 
 __global__ __launch_bounds__(kThreads) void copy_nhwc_kernel(
     const __half* src, int64_t s_nstride, int32_t s_cstride, __half* dst, int64_t d_nstride,
-    int32_t d_cstride, int HW, int C, int64_t chunks, uint32_t* dst_slots) {
+    int32_t d_cstride, int HW, int C, int chunks, ChunkDivs dv, SlotRef dst_slots) {
     __shared__ uint32_t ls[kMaxSlots];
-    const int G = dst_slots ? C / 16 : 0;
+    const int G = dst_slots.p ? C / 16 : 0;
     slots_init(ls, G);
     GroupMax gm;
     const int CC = C / 8;
-    const int64_t step = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
-        const int pix = (int)e / CC;
-        const int cc = (int)e - pix * CC;
-        const int n = pix / HW;
-        const int pp = pix - n * HW;
-        const uint4 v = *reinterpret_cast<const uint4*>(src + n * s_nstride + pp * s_cstride + cc * 8);
-        *reinterpret_cast<uint4*>(dst + n * d_nstride + pp * d_cstride + cc * 8) = v;
+    const int step = gridDim.x * blockDim.x;
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
+        int n, pp, cc;
+        chunk_split((uint32_t)e, CC, HW, dv, n, pp, cc);
+        const uint4 v = *reinterpret_cast<const uint4*>(src + n * s_nstride + (int64_t)pp * s_cstride + cc * 8);
+        *reinterpret_cast<uint4*>(dst + n * d_nstride + (int64_t)pp * d_cstride + cc * 8) = v;
         if (G) gm.add(cc >> 1, max8_abs(v), ls);
     }
     if (G) gm.flush(ls);
     if (G) slots_flush(ls, G, dst_slots);
 }
 
+// KS > 0: window size fixed at compile time (every tap load in flight at
+// once); KS == 0: runtime k.
+template <int KS>
 __global__ __launch_bounds__(kThreads) void maxpool_nhwc_kernel(
     const __half* x, int64_t x_nstride, int32_t x_cstride, __half* y, int64_t y_nstride,
-    int32_t y_cstride, int H, int W, int C, int OH, int OW, int k, int s, int pad, int64_t chunks,
-    uint32_t* y_slots) {
+    int32_t y_cstride, int H, int W, int C, int OH, int OW, int kr, int s, int pad, int chunks, ChunkDivs dv,
+    SlotRef y_slots) {
     __shared__ uint32_t ls[kMaxSlots];
-    const int G = y_slots ? C / 16 : 0;
+    const int G = y_slots.p ? C / 16 : 0;
     slots_init(ls, G);
     GroupMax gm;
     const int CC = C / 8;
     const int OHW = OH * OW;
-    const int64_t step = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
-        const int pix = (int)e / CC;
-        const int cc = (int)e - pix * CC;
-        const int n = pix / OHW;
-        const int pp = pix - n * OHW;
-        const int oy = pp / OW, ox = pp - (pp / OW) * OW;
+    const int step = gridDim.x * blockDim.x;
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
+        int n, pp, cc;
+        chunk_split((uint32_t)e, CC, OHW, dv, n, pp, cc);
+        const int oy = (int)fdiv((uint32_t)pp, dv.ow), ox = pp - oy * OW;
+        const __half* xb = x + n * x_nstride + cc * 8;
         float m[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) m[i] = -INFINITY;
-        for (int ky = 0; ky < k; ++ky) {
-            const int iy = oy * s + ky - pad;
-            if ((unsigned)iy >= (unsigned)H) continue;
-            for (int kx = 0; kx < k; ++kx) {
-                const int ix = ox * s + kx - pad;
-                if ((unsigned)ix >= (unsigned)W) continue;
-                const uint4 v = *reinterpret_cast<const uint4*>(
-                    x + n * x_nstride + ((int64_t)iy * W + ix) * x_cstride + cc * 8);
-                const __half2* h = reinterpret_cast<const __half2*>(&v);
+        auto tap = [&](int ry, int rx) {
+            const int iy = oy * s + ry - pad, ix = ox * s + rx - pad;
+            if ((unsigned)iy >= (unsigned)H || (unsigned)ix >= (unsigned)W) return;
+            const uint4 v = *reinterpret_cast<const uint4*>(xb + ((int64_t)iy * W + ix) * x_cstride);
+            const __half2* h = reinterpret_cast<const __half2*>(&v);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float2 f = __half22float2(h[i]);
-                    m[2 * i] = fmaxf(m[2 * i], f.x);
-                    m[2 * i + 1] = fmaxf(m[2 * i + 1], f.y);
-                }
+            for (int i = 0; i < 4; ++i) {
+                const float2 f = __half22float2(h[i]);
+                m[2 * i] = fmaxf(m[2 * i], f.x);
+                m[2 * i + 1] = fmaxf(m[2 * i + 1], f.y);
             }
+        };
+        if constexpr (KS > 0) {
+#pragma unroll
+            for (int ry = 0; ry < KS; ++ry)
+#pragma unroll
+                for (int rx = 0; rx < KS; ++rx) tap(ry, rx);
+        } else {
+            for (int ry = 0; ry < kr; ++ry)
+                for (int rx = 0; rx < kr; ++rx) tap(ry, rx);
         }
         uint4 o;
         __half2* oh = reinterpret_cast<__half2*>(&o);
@@ -272,21 +300,20 @@ __global__ __launch_bounds__(kThreads) void maxpool_nhwc_kernel(
 
 __global__ __launch_bounds__(kThreads) void resize_nearest_nhwc_kernel(
     const __half* x, int64_t x_nstride, int32_t x_cstride, __half* y, int64_t y_nstride,
-    int32_t y_cstride, int H, int W, int C, int OH, int OW, int64_t chunks, uint32_t* y_slots) {
+    int32_t y_cstride, int H, int W, int C, int OH, int OW, int chunks, ChunkDivs dv, SlotRef y_slots) {
     __shared__ uint32_t ls[kMaxSlots];
-    const int G = y_slots ? C / 16 : 0;
+    const int G = y_slots.p ? C / 16 : 0;
     slots_init(ls, G);
     GroupMax gm;
     const int CC = C / 8;
     const int OHW = OH * OW;
-    const int64_t step = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
-        const int pix = (int)e / CC;
-        const int cc = (int)e - pix * CC;
-        const int n = pix / OHW;
-        const int pp = pix - n * OHW;
-        const int oy = pp / OW, ox = pp - (pp / OW) * OW;
-        const int iy = (int)((int64_t)oy * H / OH), ix = (int)((int64_t)ox * W / OW);
+    const int step = gridDim.x * blockDim.x;
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
+        int n, pp, cc;
+        chunk_split((uint32_t)e, CC, OHW, dv, n, pp, cc);
+        const int oy = (int)fdiv((uint32_t)pp, dv.ow), ox = pp - oy * OW;
+        // floor(o * in / out), as the reference's nearest resize
+        const int iy = (int)fdiv((uint32_t)(oy * H), dv.oh), ix = (int)fdiv((uint32_t)(ox * W), dv.ow);
         const uint4 v = *reinterpret_cast<const uint4*>(
             x + n * x_nstride + ((int64_t)iy * W + ix) * x_cstride + cc * 8);
         *reinterpret_cast<uint4*>(y + n * y_nstride + (int64_t)pp * y_cstride + cc * 8) = v;
@@ -298,21 +325,19 @@ __global__ __launch_bounds__(kThreads) void resize_nearest_nhwc_kernel(
 
 __global__ __launch_bounds__(kThreads) void add_nhwc_kernel(
     const __half* a, int64_t a_nstride, int32_t a_cstride, const __half* b, int64_t b_nstride,
-    int32_t b_cstride, __half* y, int64_t y_nstride, int32_t y_cstride, int HW, int C, int64_t chunks,
-    uint32_t* y_slots) {
+    int32_t b_cstride, __half* y, int64_t y_nstride, int32_t y_cstride, int HW, int C, int chunks,
+    ChunkDivs dv, SlotRef y_slots) {
     __shared__ uint32_t ls[kMaxSlots];
-    const int G = y_slots ? C / 16 : 0;
+    const int G = y_slots.p ? C / 16 : 0;
     slots_init(ls, G);
     GroupMax gm;
     const int CC = C / 8;
-    const int64_t step = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
-        const int pix = (int)e / CC;
-        const int cc = (int)e - pix * CC;
-        const int n = pix / HW;
-        const int pp = pix - n * HW;
-        const uint4 va = *reinterpret_cast<const uint4*>(a + n * a_nstride + pp * a_cstride + cc * 8);
-        const uint4 vb = *reinterpret_cast<const uint4*>(b + n * b_nstride + pp * b_cstride + cc * 8);
+    const int step = gridDim.x * blockDim.x;
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < chunks; e += step) {
+        int n, pp, cc;
+        chunk_split((uint32_t)e, CC, HW, dv, n, pp, cc);
+        const uint4 va = *reinterpret_cast<const uint4*>(a + n * a_nstride + (int64_t)pp * a_cstride + cc * 8);
+        const uint4 vb = *reinterpret_cast<const uint4*>(b + n * b_nstride + (int64_t)pp * b_cstride + cc * 8);
         const __half2* ha = reinterpret_cast<const __half2*>(&va);
         const __half2* hb = reinterpret_cast<const __half2*>(&vb);
         uint4 o;
@@ -322,7 +347,7 @@ __global__ __launch_bounds__(kThreads) void add_nhwc_kernel(
             const float2 fa = __half22float2(ha[i]), fb = __half22float2(hb[i]);
             ho[i] = __floats2half2_rn(fa.x + fb.x, fa.y + fb.y);
         }
-        *reinterpret_cast<uint4*>(y + n * y_nstride + pp * y_cstride + cc * 8) = o;
+        *reinterpret_cast<uint4*>(y + n * y_nstride + (int64_t)pp * y_cstride + cc * 8) = o;
         if (G) gm.add(cc >> 1, max8_abs(o), ls);
     }
     if (G) gm.flush(ls);
@@ -331,9 +356,9 @@ __global__ __launch_bounds__(kThreads) void add_nhwc_kernel(
 
 __global__ __launch_bounds__(kThreads) void nchw_f32_to_nhwc_f16_kernel(
     const float* x, __half* y, int64_t y_nstride, int32_t y_cstride, int C, int HW, int64_t total,
-    uint32_t* y_slots) {
+    SlotRef y_slots) {
     __shared__ uint32_t ls[kMaxSlots];
-    const int G = y_slots ? C / 16 : 0;
+    const int G = y_slots.p ? C / 16 : 0;
     slots_init(ls, G);
     const int64_t step = (int64_t)gridDim.x * blockDim.x;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += step) {
@@ -394,11 +419,12 @@ __global__ __launch_bounds__(kThreads) void nhwc_to_nchw_f32_kernel(const T* x, 
 }  // namespace
 
 hipError_t launch_amax_slots_nhwc(const __half* x, int64_t nstride, int32_t cstride, int N, int HW, int C,
-                                  uint32_t* slots, hipStream_t stream) {
+                                  SlotRef slots, hipStream_t stream) {
     if (C % 16 != 0 || C / 16 > kMaxSlots) return hipErrorInvalidValue;
     const int64_t chunks = (int64_t)N * HW * (C / 8);
+    if (chunks >= INT32_MAX) return hipErrorInvalidValue;
     hipLaunchKernelGGL(amax_slots_nhwc_kernel, dim3(grid_cols(chunks, C)), dim3(kThreads), 0, stream, x,
-                       nstride, cstride, HW, C, chunks, slots);
+                       nstride, cstride, HW, C, (int)chunks, chunk_divs(C, HW), slots);
     return hipGetLastError();
 }
 
@@ -418,11 +444,12 @@ hipError_t launch_amax_strips_nchw(const void* x, bool f16, int N, int C, int HW
 }
 
 hipError_t launch_quantize_nhwc(const __half* x, int64_t nstride, int32_t cstride, int N, int HW, int C,
-                                const uint32_t* slots, int nslots, int8_t* q, hipStream_t stream) {
+                                SlotRef slots, int nslots, int8_t* q, hipStream_t stream) {
     if (C % 8 != 0) return hipErrorInvalidValue;
     const int64_t chunks = (int64_t)N * HW * (C / 8);
+    if (chunks >= INT32_MAX) return hipErrorInvalidValue;
     hipLaunchKernelGGL(quantize_nhwc_kernel, dim3(grid_cols(chunks, C)), dim3(kThreads), 0, stream, x, nstride,
-                       cstride, HW, C, chunks, slots, nslots, q);
+                       cstride, HW, C, (int)chunks, chunk_divs(C, HW), slots, nslots, q);
     return hipGetLastError();
 }
 
@@ -447,48 +474,62 @@ hipError_t launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t strea
 }
 
 hipError_t launch_copy_nhwc(const __half* src, int64_t s_nstride, int32_t s_cstride, __half* dst,
-                            int64_t d_nstride, int32_t d_cstride, int N, int HW, int C, uint32_t* dst_slots,
+                            int64_t d_nstride, int32_t d_cstride, int N, int HW, int C, SlotRef dst_slots,
                             hipStream_t stream) {
-    if (C % 8 != 0 || (dst_slots && (C % 16 != 0 || C / 16 > kMaxSlots))) return hipErrorInvalidValue;
+    if (C % 8 != 0 || (dst_slots.p && (C % 16 != 0 || C / 16 > kMaxSlots))) return hipErrorInvalidValue;
     const int64_t chunks = (int64_t)N * HW * (C / 8);
+    if (chunks >= INT32_MAX) return hipErrorInvalidValue;
     hipLaunchKernelGGL(copy_nhwc_kernel, dim3(grid_cols(chunks, C)), dim3(kThreads), 0, stream, src, s_nstride,
-                       s_cstride, dst, d_nstride, d_cstride, HW, C, chunks, dst_slots);
+                       s_cstride, dst, d_nstride, d_cstride, HW, C, (int)chunks, chunk_divs(C, HW), dst_slots);
     return hipGetLastError();
 }
 
 hipError_t launch_maxpool_nhwc(const __half* x, int64_t x_nstride, int32_t x_cstride, __half* y,
                                int64_t y_nstride, int32_t y_cstride, int N, int H, int W, int C, int OH,
-                               int OW, int k, int s, int pad, uint32_t* y_slots, hipStream_t stream) {
-    if (C % 8 != 0 || (y_slots && (C % 16 != 0 || C / 16 > kMaxSlots))) return hipErrorInvalidValue;
+                               int OW, int k, int s, int pad, SlotRef y_slots, hipStream_t stream) {
+    if (C % 8 != 0 || (y_slots.p && (C % 16 != 0 || C / 16 > kMaxSlots))) return hipErrorInvalidValue;
     const int64_t chunks = (int64_t)N * OH * OW * (C / 8);
-    hipLaunchKernelGGL(maxpool_nhwc_kernel, dim3(grid_cols(chunks, C)), dim3(kThreads), 0, stream, x, x_nstride,
-                       x_cstride, y, y_nstride, y_cstride, H, W, C, OH, OW, k, s, pad, chunks, y_slots);
+    if (chunks >= INT32_MAX) return hipErrorInvalidValue;
+    const ChunkDivs dv = chunk_divs(C, OH * OW, OW);
+    if (k == 5)
+        hipLaunchKernelGGL(maxpool_nhwc_kernel<5>, dim3(grid_cols(chunks, C)), dim3(kThreads), 0, stream, x,
+                           x_nstride, x_cstride, y, y_nstride, y_cstride, H, W, C, OH, OW, k, s, pad, (int)chunks,
+                           dv, y_slots);
+    else
+        hipLaunchKernelGGL(maxpool_nhwc_kernel<0>, dim3(grid_cols(chunks, C)), dim3(kThreads), 0, stream, x,
+                           x_nstride, x_cstride, y, y_nstride, y_cstride, H, W, C, OH, OW, k, s, pad, (int)chunks,
+                           dv, y_slots);
     return hipGetLastError();
 }
 
 hipError_t launch_resize_nearest_nhwc(const __half* x, int64_t x_nstride, int32_t x_cstride, __half* y,
                                       int64_t y_nstride, int32_t y_cstride, int N, int H, int W, int C,
-                                      int OH, int OW, uint32_t* y_slots, hipStream_t stream) {
-    if (C % 8 != 0 || (y_slots && (C % 16 != 0 || C / 16 > kMaxSlots))) return hipErrorInvalidValue;
+                                      int OH, int OW, SlotRef y_slots, hipStream_t stream) {
+    if (C % 8 != 0 || (y_slots.p && (C % 16 != 0 || C / 16 > kMaxSlots))) return hipErrorInvalidValue;
     const int64_t chunks = (int64_t)N * OH * OW * (C / 8);
+    if (chunks >= INT32_MAX || (int64_t)OH * H >= INT32_MAX || (int64_t)OW * W >= INT32_MAX)
+        return hipErrorInvalidValue;
     hipLaunchKernelGGL(resize_nearest_nhwc_kernel, dim3(grid_cols(chunks, C)), dim3(kThreads), 0, stream, x,
-                       x_nstride, x_cstride, y, y_nstride, y_cstride, H, W, C, OH, OW, chunks, y_slots);
+                       x_nstride, x_cstride, y, y_nstride, y_cstride, H, W, C, OH, OW, (int)chunks,
+                       chunk_divs(C, OH * OW, OW, OH), y_slots);
     return hipGetLastError();
 }
 
 hipError_t launch_add_nhwc(const __half* a, int64_t a_nstride, int32_t a_cstride, const __half* b,
                            int64_t b_nstride, int32_t b_cstride, __half* y, int64_t y_nstride, int32_t y_cstride,
-                           int N, int HW, int C, uint32_t* y_slots, hipStream_t stream) {
-    if (C % 8 != 0 || (y_slots && (C % 16 != 0 || C / 16 > kMaxSlots))) return hipErrorInvalidValue;
+                           int N, int HW, int C, SlotRef y_slots, hipStream_t stream) {
+    if (C % 8 != 0 || (y_slots.p && (C % 16 != 0 || C / 16 > kMaxSlots))) return hipErrorInvalidValue;
     const int64_t chunks = (int64_t)N * HW * (C / 8);
+    if (chunks >= INT32_MAX) return hipErrorInvalidValue;
     hipLaunchKernelGGL(add_nhwc_kernel, dim3(grid_cols(chunks, C)), dim3(kThreads), 0, stream, a, a_nstride,
-                       a_cstride, b, b_nstride, b_cstride, y, y_nstride, y_cstride, HW, C, chunks, y_slots);
+                       a_cstride, b, b_nstride, b_cstride, y, y_nstride, y_cstride, HW, C, (int)chunks,
+                       chunk_divs(C, HW), y_slots);
     return hipGetLastError();
 }
 
 hipError_t launch_nchw_f32_to_nhwc_f16(const float* x, __half* y, int64_t y_nstride, int32_t y_cstride, int N,
-                                       int C, int HW, uint32_t* y_slots, hipStream_t stream) {
-    if (y_slots && (C % 16 != 0 || C / 16 > kMaxSlots)) return hipErrorInvalidValue;
+                                       int C, int HW, SlotRef y_slots, hipStream_t stream) {
+    if (y_slots.p && (C % 16 != 0 || C / 16 > kMaxSlots)) return hipErrorInvalidValue;
     const int64_t total = (int64_t)N * C * HW;
     hipLaunchKernelGGL(nchw_f32_to_nhwc_f16_kernel, dim3(grid_for(total)), dim3(kThreads), 0, stream, x, y,
                        y_nstride, y_cstride, C, HW, total, y_slots);

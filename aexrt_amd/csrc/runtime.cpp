@@ -40,6 +40,10 @@ struct AexrtDevice {
 namespace aexrt {
 namespace {
 
+// Copies of the model's amax slot array: the workgroups of a layer spread
+// their slot updates over this many cache lines (4 KB apart).
+constexpr uint32_t kSlotStripes = 8;
+
 struct Placement {
     bool valid = false;
     int root = -1;
@@ -124,6 +128,7 @@ struct AexrtYoloModel {
     uint8_t* arena = nullptr;
     uint32_t* slots = nullptr;
     int nslots = 0;
+    uint32_t slot_stride = 0;  // uint32 elements between the slot copies
     float* input_dev = nullptr;
     float* input_host = nullptr;
     bool input_needs_nhwc = false;
@@ -612,6 +617,8 @@ AexrtHipTensorView view_of(AexrtYoloModel* m, int v) {
     tv.n_stride = x.pl.nstride;
     tv.c_stride = x.pl.cstride;
     tv.amax_slots = x.pl.slot >= 0 ? m->slots + x.pl.slot : nullptr;
+    tv.amax_stripes = tv.amax_slots ? kSlotStripes : 0u;
+    tv.amax_stripe_stride = m->slot_stride;
     return tv;
 }
 
@@ -622,6 +629,8 @@ AexrtHipTensorView view_of_pl(AexrtYoloModel* m, const Placement& pl) {
     tv.n_stride = pl.nstride;
     tv.c_stride = pl.cstride;
     tv.amax_slots = pl.slot >= 0 ? m->slots + pl.slot : nullptr;
+    tv.amax_stripes = tv.amax_slots ? kSlotStripes : 0u;
+    tv.amax_stripe_stride = m->slot_stride;
     return tv;
 }
 
@@ -641,7 +650,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
     m->steps.clear();
     {
         uint32_t* slots = m->slots;
-        const int n = m->nslots;
+        const int64_t n = int64_t(kSlotStripes) * m->slot_stride;
         m->steps.push_back(Step{-1, "amax slots clear", [slots, n](hipStream_t s) {
                                     return launch_fill_u32(slots, n, 0u, s);
                                 }});
@@ -660,7 +669,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
             m->steps.push_back(Step{-1, "input nchw->nhwc", [=](hipStream_t s) {
                                         return launch_nchw_f32_to_nhwc_f16(src, static_cast<__half*>(y.data),
                                                                            y.n_stride, y.c_stride, N, C, HW,
-                                                                           y.amax_slots, s);
+                                                                           slot_ref(y), s);
                                     }});
         }
     }
@@ -707,7 +716,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                                                 return launch_copy_nhwc(static_cast<const __half*>(s.data), s.n_stride,
                                                                         s.c_stride, static_cast<__half*>(dv.data),
                                                                         dv.n_stride, dv.c_stride, N, HW, C,
-                                                                        dv.amax_slots, st);
+                                                                        slot_ref(dv), st);
                                             }});
                 }
                 break;
@@ -723,7 +732,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                                             return launch_maxpool_nhwc(static_cast<const __half*>(xv.data), xv.n_stride,
                                                                        xv.c_stride, static_cast<__half*>(yv.data),
                                                                        yv.n_stride, yv.c_stride, N, H, W, C, OH, OW, k,
-                                                                       st, pad, yv.amax_slots, s);
+                                                                       st, pad, slot_ref(yv), s);
                                         }});
                 break;
             }
@@ -737,7 +746,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                                             return launch_resize_nearest_nhwc(
                                                 static_cast<const __half*>(xv.data), xv.n_stride, xv.c_stride,
                                                 static_cast<__half*>(yv.data), yv.n_stride, yv.c_stride, N, H, W, C, OH,
-                                                OW, yv.amax_slots, s);
+                                                OW, slot_ref(yv), s);
                                         }});
                 break;
             }
@@ -753,7 +762,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                                                                    av.c_stride, static_cast<const __half*>(bv.data),
                                                                    bv.n_stride, bv.c_stride,
                                                                    static_cast<__half*>(yv.data), yv.n_stride,
-                                                                   yv.c_stride, N, HW, C, yv.amax_slots, s);
+                                                                   yv.c_stride, N, HW, C, slot_ref(yv), s);
                                         }});
                 break;
             }
@@ -852,7 +861,9 @@ bool build_model(AexrtYoloModel* m) {
         total += (size_t(r.elements) * (r.f32 ? 4 : 2) + 255) & ~size_t(255);
     }
     m->arena = static_cast<uint8_t*>(dev_alloc(m, total));
-    m->slots = static_cast<uint32_t*>(dev_alloc(m, size_t(m->nslots + 1) * 4));
+    // kSlotStripes copies of the slot array, 4 KB apart
+    m->slot_stride = (uint32_t)((m->nslots + 1 + 1023) & ~1023);
+    m->slots = static_cast<uint32_t*>(dev_alloc(m, size_t(kSlotStripes) * m->slot_stride * 4));
     const ValueInfo& in = m->vals[e.manifest.input_value];
     const size_t in_elems = size_t(in.N) * in.C * in.H * in.W;
     m->input_dev = static_cast<float*>(dev_alloc(m, in_elems * 4));

@@ -48,19 +48,35 @@ def view(t, slots=None) -> TensorView:
         raise ValueError("activation views are 4-D NHWC")
     if t.stride(3) != 1 or t.stride(1) != t.shape[2] * t.stride(2):
         raise ValueError("view must be NHWC with contiguous pixels (channel slices allowed)")
-    return TensorView(data=t.data_ptr(), n_stride=t.stride(0), c_stride=t.stride(2), reserved=0,
-                      amax_slots=_ptr(slots))
+    stripes, stride = 0, 0
+    if slots is not None and slots.dim() == 2:
+        # striped slot array [stripes, groups]: producers spread their updates
+        # over the rows, readers take the max over the rows
+        if slots.stride(1) != 1:
+            raise ValueError("slot rows must be contiguous")
+        stripes, stride = slots.shape[0], slots.stride(0)
+    return TensorView(data=t.data_ptr(), n_stride=t.stride(0), c_stride=t.stride(2), amax_stripes=stripes,
+                      amax_slots=_ptr(slots), amax_stripe_stride=stride)
 
 
-def new_slots(channels: int, device="cuda"):
+def new_slots(channels: int, device="cuda", stripes: int = 1):
+    """Zeroed amax slots of a ``channels``-wide tensor: [groups], or [stripes, groups] when striped."""
     import torch
 
-    return torch.zeros((channels + 15) // 16, dtype=torch.int32, device=device)
+    g = (channels + 15) // 16
+    shape = (g,) if stripes == 1 else (stripes, g)
+    return torch.zeros(shape, dtype=torch.int32, device=device)
+
+
+def slots_max(slots) -> np.ndarray:
+    """Per-group slot bit patterns, max over the stripes of a striped slot array (host read)."""
+    a = slots.detach().cpu().numpy().astype(np.int32).view(np.uint32)
+    return a.max(axis=0) if a.ndim == 2 else a
 
 
 def slots_amax(slots) -> float:
     """Per-tensor amax from a slot tensor (host read)."""
-    a = slots.detach().cpu().numpy().astype(np.int32).view(np.uint32)
+    a = slots_max(slots)
     return float(np.uint32(a.max() if a.size else 0).view(np.float32))
 
 
@@ -161,7 +177,8 @@ def conv2d(pc: PreparedConv, x, y, *, flags: int = SILU, x_slots=None, y_slots=N
     """Runs one conv: x and y are NHWC views (x may be dense fp32 NCHW with IN_NCHW_F32)."""
     d = ConvDesc.from_params(pc.params)
     if flags & IN_NCHW_F32:
-        xv = TensorView(data=x.data_ptr(), n_stride=x.stride(0), c_stride=1, reserved=0, amax_slots=None)
+        xv = TensorView(data=x.data_ptr(), n_stride=x.stride(0), c_stride=1, amax_stripes=0, amax_slots=None,
+                        amax_stripe_stride=0)
     else:
         xv = view(x, x_slots)
     yv = view(y, y_slots)

@@ -64,14 +64,19 @@ typedef struct AexrtYoloDetection {
  * data[n * n_stride + (h * W + w) * c_stride + c] (elements of the view's
  * dtype).  amax_slots, when non-NULL, holds one uint32 per 16 channels of
  * the view: the bit pattern of max|x| over that channel group (all n, h, w).
- * A channel slice of a larger tensor is a view with a shifted data pointer
- * and the larger tensor's c_stride. */
+ * The slot array may be striped: amax_stripes copies (0 counts as 1), copy s
+ * at amax_slots + s * amax_stripe_stride.  Producers fold each workgroup's
+ * maxima into one copy (spreading the atomics of thousands of workgroups
+ * over several cache lines); readers take the max over all copies.  A channel
+ * slice of a larger tensor is a view with a shifted data pointer and the
+ * larger tensor's c_stride (and a slot pointer shifted by c0 / 16). */
 typedef struct AexrtHipTensorView {
     void* data;
     int64_t n_stride;
     int32_t c_stride;
-    uint32_t reserved;
+    uint32_t amax_stripes;
     uint32_t* amax_slots;
+    uint64_t amax_stripe_stride;
 } AexrtHipTensorView;
 
 /* Conv flags (aexrt_hip_conv2d). */

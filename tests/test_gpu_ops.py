@@ -141,6 +141,52 @@ def test_int8_conv_fp32_output_and_linear(cuda):
     assert err <= allowed, (err, allowed)
 
 
+def test_striped_slots_producer_and_consumer(cuda):
+    """Striped amax slots: producers spread over the copies, readers take the max over them."""
+    import torch
+
+    n, ic, h, w, oc = 2, 64, 12, 10, 48
+    rng = np.random.default_rng(81)
+    x = rng.standard_normal((n, ic, h, w)).astype(np.float16).astype(np.float32)
+    wt = group16_weight(rng, oc, ic, 3)
+    b = packing.fp16_round(rng.uniform(-0.1, 0.1, oc).astype(np.float32))
+    desc = O.conv_desc(n, ic, h, w, oc, 3, 1, 1)
+    pc = K.prepare_conv(desc, 52, K.SRC_LAYOUT_INT8, packing.pack_conv_int8(wt, fp16_engine=True), b, device=cuda)
+    xd = _dev_nhwc(x, cuda)
+    # producer: amax over the input into 5 stripes
+    xs = K.new_slots(ic, cuda, stripes=5)
+    K.amax_slots(xd, xs)
+    torch.cuda.synchronize()
+    want = np.array([np.float32(np.abs(x[:, g * 16:(g + 1) * 16]).max()).view(np.uint32) for g in range(ic // 16)])
+    np.testing.assert_array_equal(K.slots_max(xs), want)
+    # consumer: each group's max sits in a different stripe, the rest hold smaller values
+    striped = np.zeros((4, ic // 16), np.uint32)
+    for g in range(ic // 16):
+        striped[:, g] = (want[g].view(np.float32) * np.float32(0.5)).view(np.uint32)
+        striped[g % 4, g] = want[g]
+    xs4 = torch.from_numpy(striped.view(np.int32)).to(cuda)
+    y = torch.empty((n, h, w, oc), dtype=torch.float16, device=cuda)
+    ys = K.new_slots(oc, cuda, stripes=3)
+    acc = torch.empty((n * h * w, oc), dtype=torch.int32, device=cuda)
+    K.conv2d(pc, xd, y, flags=K.SILU, x_slots=xs4, y_slots=ys, acc_out=acc)
+    torch.cuda.synchronize()
+    _, _, _, _, acc_ref, y_ref = O.w8a8_conv(x, wt, b, desc, silu=True, fp16_engine=True)
+    np.testing.assert_array_equal(nhwc_to_nchw(acc.cpu().numpy().reshape(n, h, w, oc)), acc_ref)
+    got = nhwc_to_nchw(y.float().cpu().numpy())
+    err, allowed = tol_range(y_ref, got, FP16_TOL)
+    assert err <= allowed, (err, allowed)
+    np.testing.assert_array_equal(
+        K.slots_max(ys), [np.float32(np.abs(got[:, g * 16:(g + 1) * 16]).max()).view(np.uint32) for g in range(3)])
+    # glue producer into a striped slice of a wider tensor's slots
+    big = torch.zeros((n, h, w, 96), dtype=torch.float16, device=cuda)
+    bs = K.new_slots(96, cuda, stripes=4)
+    K.copy(xd, big[..., 32:96], dst_slots=bs[:, 2:6])
+    torch.cuda.synchronize()
+    m = K.slots_max(bs)
+    assert m[0] == 0 and m[1] == 0
+    np.testing.assert_array_equal(m[2:6], want)
+
+
 def test_int8_conv_all_zero_input(cuda):
     """amax == 0 packs zeros: output is bias (then SiLU), accumulators zero."""
     x = np.zeros((1, 32, 8, 8), np.float32)

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_library_loads_and_reports_abi():
-    assert _lib.lib().aexrt_hip_abi_version() >= 1
+    assert _lib.lib().aexrt_hip_abi_version() == 2
 
 
 @pytest.mark.parametrize("fp16_engine", [True, False])
@@ -187,3 +187,17 @@ def test_fastdiv_is_exact_division_below_2_31():
                             np.arange(0, 4096, dtype=np.int64) * d + (d - 1),
                             np.arange((1 << 31) - 4096, 1 << 31, dtype=np.int64)])
         np.testing.assert_array_equal(_fastdiv(n, d), n // d)
+
+
+def test_tensor_view_layout_matches_header():
+    """AexrtHipTensorView: data, n_stride, c_stride, amax_stripes, amax_slots, amax_stripe_stride."""
+    tv = _lib.TensorView
+    assert ctypes.sizeof(tv) == 40
+    offs = {name: getattr(tv, name).offset for name, _ in tv._fields_}
+    assert offs == {"data": 0, "n_stride": 8, "c_stride": 16, "amax_stripes": 20, "amax_slots": 24,
+                    "amax_stripe_stride": 32}
+    hdr = (Path(__file__).resolve().parents[1] / "include" / "aexrt_hip.h").read_text()
+    body = hdr[hdr.index("typedef struct AexrtHipTensorView"):]
+    body = body[:body.index("} AexrtHipTensorView;")]
+    names = re.findall(r"\b(\w+);", body)
+    assert names == ["data", "n_stride", "c_stride", "amax_stripes", "amax_slots", "amax_stripe_stride"]
