@@ -212,7 +212,8 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8 (W8A8 backbone+neck, int32 acc) / fp16 (stem, head)",
+        "dtype": "int8",
+        "dtype_detail": "int8 MFMA with int32 accumulation on the 44 W8A8 convs; fp16 stem and head",
         "data": "synthetic U(0,1) images, seeded random He-init weights",
         "config": {"workload": f"YOLOv8n-320 W8A8 forward, batch {args.batch}", "global_batch": args.batch,
                    "imgsz": 320, "int8_convs": 44, "fp16_convs": 19, "parallelism": "single GPU"},
