@@ -180,6 +180,14 @@ int aexrt_hip_set_conv_tile(int32_t jn, int32_t pw, int32_t ksw) {
     return 1;
 }
 
+int aexrt_hip_set_conv3x3_halo(int32_t mode, int32_t jn, int32_t pw, int32_t tr, int32_t tc, int32_t cc) {
+    if (!set_conv3x3_halo(mode, jn, pw, tr, tc, cc)) {
+        set_error("set_conv3x3_halo: bad mode or no kernel instance for this tile");
+        return 0;
+    }
+    return 1;
+}
+
 int aexrt_hip_conv_weight_bytes(const AexrtConv2DDesc* desc, uint32_t algorithm, uint64_t* out_nbytes) {
     if (!desc || !out_nbytes) {
         set_error("conv_weight_bytes: null argument");

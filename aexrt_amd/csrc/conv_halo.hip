@@ -1,0 +1,191 @@
+// Host side of the halo-tile 3x3 conv (kernel in conv_halo.h): applicability,
+// tile choice, launch geometry.
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+
+#include "conv_halo.h"
+
+namespace aexrt {
+
+namespace halo {
+AEXRT_HALO_FAMILIES(AEXRT_HALO_EXTERN)
+}  // namespace halo
+
+namespace {
+
+// 0: automatic; 1: never (implicit GEMM only); 2: forced tile (g_force).
+std::atomic<int> g_halo_mode{0};
+std::atomic<uint64_t> g_force{0};  // jn | pw << 8 | tr << 16 | tc << 32 | cc << 48 (8/8/16/16/16 bits)
+
+constexpr int kLdsBudget = 65536 - 2048;  // dynamic LDS of one block (static tables aside)
+
+struct HaloTile {
+    int jn, pw, np, TR, TC, CC;
+};
+
+int pow2_at_least(int v, int cap) {
+    int r = 1;
+    while (r < v && r < cap) r <<= 1;
+    return r;
+}
+
+// Fills the geometry of tile t into h; false when it does not fit the kernel.
+bool halo_geometry(HaloParams& h, const HaloTile& t, bool int8) {
+    const ConvParams& p = h.c;
+    const int esz = int8 ? 1 : 2;
+    const int wq = int8 ? 1 : 2;
+    if (t.CC < 16 || t.CC % 16 || p.C % t.CC || t.TR < 1 || t.TC < 1) return false;
+    if (t.TR * t.TC > 64 * t.pw) return false;
+    h.TR = t.TR;
+    h.TC = t.TC;
+    h.IR = (t.TR - 1) * p.S + 3;
+    h.ICOL = (t.TC - 1) * p.S + 3;
+    h.CC = t.CC;
+    h.nch = p.C / t.CC;
+    h.spc = (9 * t.CC + 63) / 64;
+    if (h.spc > kHaloMaxSpc) return false;
+    h.npieces = h.IR * h.ICOL * t.CC / 8;
+    if (h.npieces > 256 * t.np) return false;
+    h.ntc = (p.OW + t.TC - 1) / t.TC;
+    h.tpi = ((p.OH + t.TR - 1) / t.TR) * h.ntc;
+    const int64_t ntile = (int64_t)p.N * h.tpi;
+    if (ntile > INT32_MAX / 2) return false;
+    h.ntile = (int)ntile;
+    h.wbytes = h.nch * h.spc * wq * t.jn * 16 * 64;
+    h.tbytes = (h.npieces * 8 * esz + 15) & ~15;
+    if (h.wbytes + 2 * h.tbytes > kLdsBudget || h.wbytes > 256 * kHaloWeightRounds * 16) return false;
+    h.c.ntn = (p.OCp / 16 + t.jn - 1) / t.jn;
+    h.fd_cc8 = make_fastdiv((uint32_t)(t.CC / 8));
+    h.fd_icol = make_fastdiv((uint32_t)h.ICOL);
+    h.fd_tc = make_fastdiv((uint32_t)t.TC);
+    h.fd_ntc = make_fastdiv((uint32_t)h.ntc);
+    h.fd_tpi = make_fastdiv((uint32_t)h.tpi);
+    h.fd_cg = make_fastdiv((uint32_t)(t.CC / 16));
+    h.fd_spc = make_fastdiv((uint32_t)h.spc);
+    h.c.fd_ntn = make_fastdiv((uint32_t)h.c.ntn);
+    return true;
+}
+
+// Estimated duration (GPU clocks) of a launch with tile t.  Per tile and
+// block: MFMA issue of one wave, LDS operand reads of the 4 waves, window
+// staging (loads + int8 quantization), a fixed part per chunk (barrier,
+// latency) and per tile (epilogue).  Blocks spread over 256 CUs; the input
+// window traffic (with its halo, once per oc tile) and the output bound from
+// below.
+double halo_cost(const HaloParams& h, const HaloTile& t, bool int8) {
+    const ConvParams& p = h.c;
+    const int wq = int8 ? 1 : 2;
+    const double steps = (double)h.nch * h.spc;
+    const double t_mfma = steps * t.jn * t.pw * wq * 16.0;
+    const double t_lds = steps * (t.jn + t.pw) * wq * 4 * 8.0;
+    const double t_stage = h.nch * std::ceil(h.npieces / 256.0) * (int8 ? 110.0 : 24.0);
+    const double t_tile = std::max(t_mfma, t_lds) + t_stage + h.nch * 350.0 + t.jn * t.pw * (int8 ? 160.0 : 120.0);
+    const double blocks = (double)h.ntile * h.c.ntn;
+    const double waves_of_blocks = std::ceil(blocks / 512.0);  // ~2 blocks per CU overlap
+    const double compute = waves_of_blocks * t_tile;
+    const double bytes = blocks * h.nch * h.npieces * 16.0 + (double)p.M * p.OC * 2.0;
+    return std::max(compute, bytes / 2500.0) + 1500.0;
+}
+
+bool halo_shape_ok(const ConvParams& p) {
+    return p.KH == 3 && p.KW == 3 && p.P == 1 && (p.S == 1 || p.S == 2) && p.C % 16 == 0 && p.x_cstride % 8 == 0 &&
+           p.OH == (p.H - 1) / p.S + 1 && p.OW == (p.W - 1) / p.S + 1 && p.H < 8192 && p.W < 8192 &&
+           p.loader == kLoaderNhwc;
+}
+
+// Lowest-cost tile of the instantiated shapes.
+bool choose_halo_tile(HaloParams& h, bool int8, HaloTile& best) {
+    const ConvParams& p = h.c;
+    double best_cost = 0.0;
+    bool found = false;
+    const int ocj = (p.OCp + 15) / 16;
+    for (int div = 1; div <= 8; div <<= 1) {
+        if (p.C % div) break;
+        const int CC = p.C / div;
+        if (CC % 16 || CC > (int8 ? 128 : 64)) continue;
+        for (int jn = 1; jn <= std::min(4, pow2_at_least(ocj, 4)); jn <<= 1) {
+            for (int pw = 1; pw <= 4; pw <<= 1) {
+                int tcs[6] = {p.OW, 16, 32, 48, 64, 80};
+                for (int tc : tcs) {
+                    if (tc > p.OW || (tc != p.OW && tc > 64 * pw)) continue;
+                    const int TR = std::min(p.OH, 64 * pw / tc);
+                    if (TR < 1) continue;
+                    for (int np : {4, 8}) {
+                        const HaloTile t{jn, pw, np, TR, tc, CC};
+                        HaloParams hh = h;
+                        if (!halo_geometry(hh, t, int8)) continue;
+                        if (np == 8 && hh.npieces <= 4 * 256) continue;
+                        const double c = halo_cost(hh, t, int8);
+                        if (!found || c < best_cost) {
+                            best_cost = c;
+                            best = t;
+                            found = true;
+                        }
+                    }
+                }
+            }
+        }
+    }
+    return found;
+}
+
+hipError_t halo_launch(const HaloParams& h, bool int8, int epi, const HaloTile& t, hipStream_t s) {
+    using halo::halo_launch_family;
+    if (int8) {
+        if (epi == 1) return halo_launch_family<true, 1>(h, t.jn, t.pw, t.np, s);
+        if (epi == 2) return halo_launch_family<true, 2>(h, t.jn, t.pw, t.np, s);
+        return halo_launch_family<true, 0>(h, t.jn, t.pw, t.np, s);
+    }
+    if (epi == 1) return halo_launch_family<false, 1>(h, t.jn, t.pw, t.np, s);
+    return halo_launch_family<false, 0>(h, t.jn, t.pw, t.np, s);
+}
+
+}  // namespace
+
+bool set_conv3x3_halo(int mode, int jn, int pw, int tr, int tc, int cc) {
+    if (mode == 0 || mode == 1) {
+        g_halo_mode.store(mode);
+        return true;
+    }
+    if (mode != 2 || !(jn == 1 || jn == 2 || jn == 4) || !(pw == 1 || pw == 2 || pw == 4) || tr < 1 ||
+        tr > 0xFFFF || tc < 1 || tc > 0xFFFF || cc < 16 || cc > 0xFFFF)
+        return false;
+    g_force.store((uint64_t)jn | ((uint64_t)pw << 8) | ((uint64_t)tr << 16) | ((uint64_t)tc << 32) |
+                  ((uint64_t)cc << 48));
+    g_halo_mode.store(2);
+    return true;
+}
+
+// One batch slice of a conv (views already inside 32-bit spans).
+// hipErrorNotSupported: the shape is not a halo-tile conv (the caller uses
+// the implicit-GEMM kernel).
+hipError_t launch_conv_halo(const ConvParams& p, bool int8, int epi, hipStream_t stream) {
+    const int mode = g_halo_mode.load(std::memory_order_relaxed);
+    if (mode == 1 || !halo_shape_ok(p)) return hipErrorNotSupported;
+    HaloParams h{};
+    h.c = p;
+    HaloTile t{};
+    if (mode == 2) {
+        const uint64_t f = g_force.load(std::memory_order_relaxed);
+        t.jn = (int)(f & 0xFF);
+        t.pw = (int)((f >> 8) & 0xFF);
+        t.TR = (int)((f >> 16) & 0xFFFF);
+        t.TC = (int)((f >> 32) & 0xFFFF);
+        t.CC = (int)((f >> 48) & 0xFFFF);
+        // a forced tile that does not fit this conv is an error, not a
+        // silent fallback (tests rely on the tile being used)
+        t.np = 4;
+        if (!halo_geometry(h, t, int8)) {
+            t.np = 8;
+            HaloParams h8 = h;
+            if (!halo_geometry(h8, t, int8)) return hipErrorInvalidValue;
+        }
+    } else if (!choose_halo_tile(h, int8, t)) {
+        return hipErrorNotSupported;
+    }
+    if (!halo_geometry(h, t, int8)) return hipErrorNotSupported;
+    return halo_launch(h, int8, epi, t, stream);
+}
+
+}  // namespace aexrt

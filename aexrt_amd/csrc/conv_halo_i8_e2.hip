@@ -1,0 +1,8 @@
+// int8 halo-tile 3x3 conv instances, epilogue variant 2.
+#include "conv_halo.h"
+
+namespace aexrt {
+namespace halo {
+AEXRT_HALO_INSTANCE(true, 2)
+}  // namespace halo
+}  // namespace aexrt

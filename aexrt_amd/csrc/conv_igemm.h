@@ -129,13 +129,204 @@ constexpr int chunk_steps() {
     return KSW ? (k1 < 4 ? 4 : k1) : k1;
 }
 
-// Epilogue variants: the common ones are compiled without the runtime flag
-// tests.
+// ---- input scale of an int8 conv -------------------------------------------
+// The stripes x slots of the input view are spread over the lanes of each
+// wave (8 loads per lane, issued early), then reduced: amax = max over all
+// copies and groups, the reference's per-tensor activation scale.
+__device__ __forceinline__ void in_slot_loads(const ConvParams& p, int lane, uint32_t (&raw)[kMaxSlotReads / 64]) {
+    const rsrc_t rs = make_rsrc(p.x_slots.p, p.x_slot_bytes);
+    const int ns = p.x_nslots;
+    const int tot = (int)p.x_slots.stripes * ns;
+#pragma unroll
+    for (int r = 0; r < kMaxSlotReads / 64; ++r) {
+        const int e = lane + r * 64;
+        const int c = (int)fdiv((uint32_t)e, p.fd_ns);
+        raw[r] = __builtin_amdgcn_raw_buffer_load_b32(
+            rs, e < tot ? ((uint32_t)c * p.x_slots.stride + (uint32_t)(e - c * ns)) * 4u : kOob, 0, 0);
+    }
+}
+// s_q = 127 / amax (quantizer), in_scale = amax / 127 (dequant); both 0 for
+// an all-zero input, whose quantized values are then all 0.
+__device__ __forceinline__ void in_slot_scale(const uint32_t (&raw)[kMaxSlotReads / 64], float& s_q,
+                                              float& in_scale) {
+    uint32_t am = 0;
+#pragma unroll
+    for (int r = 0; r < kMaxSlotReads / 64; ++r) am = max(am, raw[r]);
+    const float a_max = u2f(wave_umax(am));
+    s_q = 0.0f;
+    in_scale = 0.0f;
+    if (a_max > 0.0f) {
+        s_q = 127.0f / a_max;
+        in_scale = a_max / 127.0f;
+    }
+}
+
+// ---- output side of a tile, shared by the conv kernels ---------------------
+// A lane holds, for each 16-channel subtile j and 16-position subtile q,
+// acc[j][q][r] = channel n0 + 16j + 4*grp + r of one output position; yo[q]
+// is that position's element offset in the output view (-1: none), ro[q] in
+// the residual view, mo[q] its row in acc_out.  jmask: subtiles this wave
+// stores.  Every lane issues every load/store (invalid ones at the
+// out-of-range offset, which the hardware drops), so the number of memory
+// operations in flight is the same on all paths.
+
 enum Epi : int {
     kEpiAny = 0,      // flags read at run time (fp32 output, no SiLU, ...)
     kEpiSilu = 1,     // SiLU, fp16 output
     kEpiSiluRes = 2,  // SiLU, + residual, fp16 output
 };
+
+template <int EPI>
+__device__ __forceinline__ bool epi_res(const ConvParams& p) {
+    return EPI == kEpiSiluRes || (EPI == kEpiAny && (p.flags & kConvResidual));
+}
+
+template <int JN, int PW, int EPI>
+__device__ __forceinline__ void tile_residual(const ConvParams& p, const rsrc_t& rr, const int (&yo)[PW],
+                                              const int (&ro)[PW], int n0, int jmax, int grp, uint32_t jmask,
+                                              v2i (&rv)[JN][PW]) {
+    if (!epi_res<EPI>(p)) return;
+#pragma unroll
+    for (int j = 0; j < JN; ++j)
+#pragma unroll
+        for (int q = 0; q < PW; ++q) {
+            const int oc0 = n0 + j * 16 + grp * 4;
+            const bool ok = j < jmax && ((jmask >> j) & 1u) && oc0 < p.OC && yo[q] >= 0;
+            rv[j][q] = __builtin_amdgcn_raw_buffer_load_b64(rr, ok ? (uint32_t)(ro[q] + oc0) * 2u : kOob, 0, 0);
+        }
+}
+
+// Output values of one lane's 4 channels: dequant (int8), bias, SiLU and the
+// residual (fp16 conv output + fp16 residual added in fp32, the reference's
+// separate BINARY add; with fp32 output the residual is added unrounded).
+template <bool INT8, int EPI, typename AccT>
+__device__ __forceinline__ void epi_values(const ConvParams& p, const AccT& acc, const float (&bv)[4],
+                                           const float (&wv)[4], const v2i& rv, float (&v)[4]) {
+    const bool do_silu = EPI != kEpiAny || (p.flags & kConvSilu);
+    const bool do_res = epi_res<EPI>(p);
+    const bool out_f32 = EPI == kEpiAny && (p.flags & kConvOutF32);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        float t;
+        if constexpr (INT8) t = __builtin_fmaf((float)acc[r], wv[r], bv[r]);
+        else t = acc[r] + bv[r];
+        if (do_silu) t = silu(t);
+        v[r] = t;
+    }
+    if (do_res) {
+        __half2 rh[2];
+        __builtin_memcpy(rh, &rv, 8);
+        const float2 r0 = __half22float2(rh[0]), r1 = __half22float2(rh[1]);
+        if (out_f32) {
+            v[0] += r0.x; v[1] += r0.y; v[2] += r1.x; v[3] += r1.y;
+        } else {
+            v[0] = __half2float(__float2half(v[0])) + r0.x;
+            v[1] = __half2float(__float2half(v[1])) + r0.y;
+            v[2] = __half2float(__float2half(v[2])) + r1.x;
+            v[3] = __half2float(__float2half(v[3])) + r1.y;
+        }
+    }
+}
+
+// Dequant (int8: one fma with the factor amax/127 * w_scale[oc] in l_scale),
+// bias, SiLU, residual, store, and the running max|y| per channel subtile
+// (fp32 before rounding: fp16 rounding is monotone, so it commutes with max).
+template <bool INT8, int JN, int PW, int EPI, typename AccT>
+__device__ __forceinline__ void tile_store(const ConvParams& p, const AccT (&acc)[JN][PW], const int (&yo)[PW],
+                                           const int (&mo)[PW], const v2i (&rv)[JN][PW], int n0, int jmax,
+                                           int grp, uint32_t jmask, const float* l_bias, const float* l_scale,
+                                           float (&gmax)[JN], const rsrc_t& ry, const rsrc_t& racc) {
+    const bool do_silu = EPI != kEpiAny || (p.flags & kConvSilu);
+    const bool do_res = epi_res<EPI>(p);
+    const bool out_f32 = EPI == kEpiAny && (p.flags & kConvOutF32);
+#pragma unroll
+    for (int j = 0; j < JN; ++j) {
+        if (j >= jmax || !((jmask >> j) & 1u)) continue;
+        const int lc = j * 16 + grp * 4;  // block-local channel of this lane's quad
+        const int oc0 = n0 + lc;
+        const bool oc_ok = oc0 < p.OC;  // OC % 4 == 0: the quad is all in or all out
+        float bv[4], wv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            bv[r] = l_bias[lc + r];
+            wv[r] = INT8 ? l_scale[lc + r] : 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < PW; ++q) {
+            const bool ok = oc_ok && yo[q] >= 0;
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float t;
+                if constexpr (INT8) t = __builtin_fmaf((float)acc[j][q][r], wv[r], bv[r]);
+                else t = acc[j][q][r] + bv[r];
+                if (do_silu) t = silu(t);
+                v[r] = t;
+            }
+            if constexpr (INT8) {
+                if (p.acc_out) {
+                    const v4i av{acc[j][q][0], acc[j][q][1], acc[j][q][2], acc[j][q][3]};
+                    __builtin_amdgcn_raw_buffer_store_b128(av, racc, ok ? (uint32_t)(mo[q] * p.OC + oc0) * 4u : kOob,
+                                                           0, 0);
+                }
+            }
+            __half2 rh[2];
+            __builtin_memcpy(rh, &rv[j][q], 8);
+            if (out_f32) {
+                if (do_res) {
+                    const float2 r0 = __half22float2(rh[0]), r1 = __half22float2(rh[1]);
+                    v[0] += r0.x; v[1] += r0.y; v[2] += r1.x; v[3] += r1.y;
+                }
+                v4i o;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) o[r] = __float_as_int(v[r]);
+                const float m4 = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+                gmax[j] = fmaxf(gmax[j], ok ? m4 : 0.0f);
+                __builtin_amdgcn_raw_buffer_store_b128(o, ry, ok ? (uint32_t)(yo[q] + oc0) * 4u : kOob, 0, 0);
+            } else {
+                __half2 oh[2] = {__floats2half2_rn(v[0], v[1]), __floats2half2_rn(v[2], v[3])};
+                if (do_res) {
+                    // fp16 conv output + fp16 residual, added in fp32 and
+                    // rounded again: the reference's separate BINARY add
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const float2 fa = __half22float2(oh[e]), fb = __half22float2(rh[e]);
+                        v[2 * e] = fa.x + fb.x;
+                        v[2 * e + 1] = fa.y + fb.y;
+                        oh[e] = __floats2half2_rn(v[2 * e], v[2 * e + 1]);
+                    }
+                }
+                const float m4 = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+                gmax[j] = fmaxf(gmax[j], ok ? m4 : 0.0f);
+                v2i o;
+                __builtin_memcpy(&o, oh, 8);
+                __builtin_amdgcn_raw_buffer_store_b64(o, ry, ok ? (uint32_t)(yo[q] + oc0) * 2u : kOob, 0, 0);
+            }
+        }
+    }
+}
+
+// Block-wide end of a conv launch: one atomic per 16-channel group into this
+// block's copy of the output slots (no read first: with the copies striped
+// over the blocks the atomics hardly contend, and one without a return value
+// ends the block without waiting for its round trip).
+template <int JN>
+__device__ __forceinline__ void flush_slots(const ConvParams& p, float (&gmax)[JN], int n0, int jmax, uint32_t jmask,
+                                            bool out_f32, uint32_t* l_slots) {
+    if (!p.y_slots.p) return;
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < JN; ++j) {
+        if (j >= jmax || !((jmask >> j) & 1u)) continue;
+        // the stored values are fp16 (fp32 for fp32 output)
+        const float g = wave_max(out_f32 ? gmax[j] : __half2float(__float2half(gmax[j])));
+        if (lane == 0 && g > 0.0f) atomicMax(&l_slots[j], f2u(g));
+    }
+    __syncthreads();
+    const int tid = threadIdx.x;
+    if (tid < jmax && n0 + tid * 16 < p.OC && l_slots[tid])
+        atomicMax(slot_copy(p.y_slots, blockIdx.x) + (n0 >> 4) + tid, l_slots[tid]);
+}
 
 // MC: the weights span more than one chunk (staged chunk by chunk, double
 // buffered); otherwise they are staged once for all tiles of the block.
@@ -268,20 +459,8 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvParams p) {
     // ---- prologue: every independent load goes out first (slots, per-channel
     // constants, weights, the first activations), then the waits, in issue
     // order, so the block pays one memory latency before its first MFMA ----
-    uint32_t slot_raw[INT8 ? kMaxSlotReads / 64 : 1];
-    if constexpr (INT8) {
-        // stripes x slots of the input view spread over the lanes
-        const rsrc_t rs = make_rsrc(p.x_slots.p, p.x_slot_bytes);
-        const int ns = p.x_nslots;
-        const int tot = (int)p.x_slots.stripes * ns;
-#pragma unroll
-        for (int r = 0; r < kMaxSlotReads / 64; ++r) {
-            const int e = lane + r * 64;
-            const int c = (int)fdiv((uint32_t)e, p.fd_ns);
-            slot_raw[r] = __builtin_amdgcn_raw_buffer_load_b32(
-                rs, e < tot ? ((uint32_t)c * p.x_slots.stride + (uint32_t)(e - c * ns)) * 4u : kOob, 0, 0);
-        }
-    }
+    uint32_t slot_raw[kMaxSlotReads / 64];
+    if constexpr (INT8) in_slot_loads(p, lane, slot_raw);
     const rsrc_t rb = make_rsrc(p.bias, (uint32_t)p.OC * 4u);
     const rsrc_t rsc = make_rsrc(p.w_scale, INT8 ? (uint32_t)p.OC * 4u : 0u);
     const uint32_t cofs = tid < R && n0 + tid < p.OC ? (uint32_t)(n0 + tid) * 4u : kOob;
@@ -305,16 +484,7 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvParams p) {
     }
     if (tid < JN) l_slots[tid] = 0u;
     float s_q = 0.0f, in_scale = 0.0f;
-    if constexpr (INT8) {
-        uint32_t am = 0;
-#pragma unroll
-        for (int r = 0; r < kMaxSlotReads / 64; ++r) am = max(am, slot_raw[r]);
-        const float a_max = u2f(wave_umax(am));
-        if (a_max > 0.0f) {
-            s_q = 127.0f / a_max;
-            in_scale = a_max / 127.0f;
-        }
-    }
+    if constexpr (INT8) in_slot_scale(slot_raw, s_q, in_scale);
     if (tid < R) {
         l_bias[tid] = bias_v;
         // dequant factor amax/127 * w_scale[oc], applied as one fma (the
@@ -367,18 +537,17 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvParams p) {
         }
     };
 
-    // ---- epilogue of one tile: dequant, bias, activation, residual, store ----
-    const bool do_silu = EPI != kEpiAny || (p.flags & kConvSilu);
-    const bool do_res = EPI == kEpiSiluRes || (EPI == kEpiAny && (p.flags & kConvResidual));
+    // ---- epilogue of one tile ------------------------------------------------
     const bool out_f32 = EPI == kEpiAny && (p.flags & kConvOutF32);
     const rsrc_t ry = make_rsrc(p.y, p.y_bytes);
     const rsrc_t rr = make_rsrc(p.res, p.r_bytes);
-    // running max|y| of each channel subtile over the block's tiles (fp32
-    // before rounding: fp16 rounding is monotone, so it commutes with max)
+    const rsrc_t racc = make_rsrc(p.acc_out, p.acc_out ? (uint32_t)p.M * (uint32_t)p.OC * 4u : 0u);
+    // KSW: wave w finishes channel subtiles j % 4 == w
+    const uint32_t jmask = KSW ? (0x11111111u << wave) : 0xFFFFFFFFu;
     float gmax[JN];
 #pragma unroll
     for (int j = 0; j < JN; ++j) gmax[j] = 0.0f;
-    int yo[PW], ro[PW];
+    int yo[PW], ro[PW], mo[PW];
     v2i rv[JN][PW];
     // output offsets and residual fragments of tile tl; issued before the
     // next tile's activation loads so that waiting for them leaves those in
@@ -392,90 +561,12 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvParams p) {
             const int pos = m - n * p.OH * p.OW;
             yo[q] = m < p.M ? n * (int)p.y_nstride + pos * p.y_cstride : -1;
             ro[q] = n * (int)p.r_nstride + pos * p.r_cstride;
+            mo[q] = m;
         }
-        if (do_res) {
-#pragma unroll
-            for (int j = 0; j < JN; ++j)
-#pragma unroll
-                for (int q = 0; q < PW; ++q) {
-                    const int oc0 = n0 + j * 16 + grp * 4;
-                    const bool ok = j < jmax && (!KSW || (j & 3) == wave) && oc0 < p.OC && yo[q] >= 0;
-                    rv[j][q] = __builtin_amdgcn_raw_buffer_load_b64(rr, ok ? (uint32_t)(ro[q] + oc0) * 2u : kOob, 0, 0);
-                }
-        }
+        tile_residual<JN, PW, EPI>(p, rr, yo, ro, n0, jmax, grp, jmask, rv);
     };
-    const rsrc_t racc = make_rsrc(p.acc_out, p.acc_out ? (uint32_t)p.M * (uint32_t)p.OC * 4u : 0u);
-    // Every lane issues every store of the tile (invalid ones at the
-    // out-of-range offset, which the hardware drops), so the number of memory
-    // operations in flight stays the same on all paths.
-    auto epilogue = [&](int tl) {
-        const int pb = (pt0 + tl) * TPOS + (KSW ? 0 : wave * 16 * PW);
-#pragma unroll
-        for (int j = 0; j < JN; ++j) {
-            if (j >= jmax) continue;
-            if (KSW && (j & 3) != wave) continue;
-            const int lc = j * 16 + grp * 4;  // block-local channel of this lane's quad
-            const int oc0 = n0 + lc;
-            const bool oc_ok = oc0 < p.OC;  // OC % 4 == 0: the quad is all in or all out
-            float bv[4], wv[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                bv[r] = l_bias[lc + r];
-                wv[r] = INT8 ? l_scale[lc + r] : 0.0f;
-            }
-#pragma unroll
-            for (int q = 0; q < PW; ++q) {
-                const bool ok = oc_ok && yo[q] >= 0;
-                float v[4];
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    float t;
-                    if constexpr (INT8) t = __builtin_fmaf((float)acc[j][q][r], wv[r], bv[r]);
-                    else t = acc[j][q][r] + bv[r];
-                    if (do_silu) t = silu(t);
-                    v[r] = t;
-                }
-                if constexpr (INT8) {
-                    if (p.acc_out) {
-                        const v4i av{acc[j][q][0], acc[j][q][1], acc[j][q][2], acc[j][q][3]};
-                        __builtin_amdgcn_raw_buffer_store_b128(
-                            av, racc, ok ? (uint32_t)((pb + q * 16 + col) * p.OC + oc0) * 4u : kOob, 0, 0);
-                    }
-                }
-                __half2 rh[2];
-                __builtin_memcpy(rh, &rv[j][q], 8);
-                if (out_f32) {
-                    if (do_res) {
-                        const float2 r0 = __half22float2(rh[0]), r1 = __half22float2(rh[1]);
-                        v[0] += r0.x; v[1] += r0.y; v[2] += r1.x; v[3] += r1.y;
-                    }
-                    v4i o;
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) o[r] = __float_as_int(v[r]);
-                    const float m4 = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-                    gmax[j] = fmaxf(gmax[j], ok ? m4 : 0.0f);
-                    __builtin_amdgcn_raw_buffer_store_b128(o, ry, ok ? (uint32_t)(yo[q] + oc0) * 4u : kOob, 0, 0);
-                } else {
-                    __half2 oh[2] = {__floats2half2_rn(v[0], v[1]), __floats2half2_rn(v[2], v[3])};
-                    if (do_res) {
-                        // fp16 conv output + fp16 residual, added in fp32 and
-                        // rounded again: the reference's separate BINARY add
-#pragma unroll
-                        for (int e = 0; e < 2; ++e) {
-                            const float2 fa = __half22float2(oh[e]), fb = __half22float2(rh[e]);
-                            v[2 * e] = fa.x + fb.x;
-                            v[2 * e + 1] = fa.y + fb.y;
-                            oh[e] = __floats2half2_rn(v[2 * e], v[2 * e + 1]);
-                        }
-                    }
-                    const float m4 = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-                    gmax[j] = fmaxf(gmax[j], ok ? m4 : 0.0f);
-                    v2i o;
-                    __builtin_memcpy(&o, oh, 8);
-                    __builtin_amdgcn_raw_buffer_store_b64(o, ry, ok ? (uint32_t)(yo[q] + oc0) * 2u : kOob, 0, 0);
-                }
-            }
-        }
+    auto epilogue = [&](int) {
+        tile_store<INT8, JN, PW, EPI>(p, acc, yo, mo, rv, n0, jmax, grp, jmask, l_bias, l_scale, gmax, ry, racc);
     };
 
     // ---- main loop ----------------------------------------------------------
@@ -565,23 +656,7 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvParams p) {
         }
     }
 
-    // one global amax update per 16-channel group and block
-    if (p.y_slots.p) {
-#pragma unroll
-        for (int j = 0; j < JN; ++j) {
-            if (j >= jmax) continue;
-            if (KSW && (j & 3) != wave) continue;
-            // the stored values are fp16 (fp32 for fp32 output)
-            const float g = wave_max(out_f32 ? gmax[j] : __half2float(__float2half(gmax[j])));
-            if (lane == 0 && g > 0.0f) atomicMax(&l_slots[j], f2u(g));
-        }
-        __syncthreads();
-        // no read-before-write here: with the copies striped over the blocks
-        // the atomics hardly contend, and one without a return value ends the
-        // block without waiting for its round trip
-        if (tid < jmax && n0 + tid * 16 < p.OC && l_slots[tid])
-            atomicMax(slot_copy(p.y_slots, blockIdx.x) + (n0 >> 4) + tid, l_slots[tid]);
-    }
+    flush_slots<JN>(p, gmax, n0, jmax, jmask, out_f32, l_slots);
 }
 
 // Blocks of one kernel instance the GPU holds at once (occupancy x CUs),

@@ -115,8 +115,11 @@ hipError_t launch_conv_igemm(const ConvParams& p0, bool int8, hipStream_t stream
         return hipErrorInvalidValue;
     const bool mc = nks > igemm::chunk_steps_of(int8, t.jn, t.ksw);
     const int f = p0.flags & (kConvSilu | kConvResidual | kConvOutF32);
-    const int epi = f == kConvSilu ? igemm::kEpiSilu
-                                   : (int8 && f == (kConvSilu | kConvResidual) ? igemm::kEpiSiluRes : igemm::kEpiAny);
+    // the int32 accumulator output (acc_out) is written by the run-time
+    // flag variant only
+    const int epi = p0.acc_out ? igemm::kEpiAny
+                    : f == kConvSilu ? igemm::kEpiSilu
+                    : (int8 && f == (kConvSilu | kConvResidual) ? igemm::kEpiSiluRes : igemm::kEpiAny);
     for (int nb = 0; nb < p0.N; nb += per_launch) {
         ConvParams p = p0;
         p.N = std::min(per_launch, p0.N - nb);
@@ -140,7 +143,8 @@ hipError_t launch_conv_igemm(const ConvParams& p0, bool int8, hipStream_t stream
         p.fd_ow = make_fastdiv((uint32_t)p.OW);
         p.fd_c = make_fastdiv((uint32_t)p.C);
         p.fd_kw = make_fastdiv((uint32_t)p.KW);
-        const hipError_t e = launch_variant(int8, mc, epi, p, t, stream);
+        hipError_t e = launch_conv_halo(p, int8, epi, stream);
+        if (e == hipErrorNotSupported) e = launch_variant(int8, mc, epi, p, t, stream);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

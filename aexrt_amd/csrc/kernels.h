@@ -93,6 +93,16 @@ bool set_conv_tile_override(int jn, int pw, int ksw);
 // Implicit-GEMM conv (int8 or fp16 MFMA).  Requires C % 8 == 0, OC % 4 == 0,
 // Kp % 64 == 0, OCp % 16 == 0 and 16-byte aligned views.
 hipError_t launch_conv_igemm(const ConvParams& p, bool int8, hipStream_t stream);
+// Halo-tile 3x3 conv (pad 1, stride 1/2, C % 16 == 0) on one batch slice whose
+// views fit 32-bit offsets: the input window of each position tile is staged
+// (and quantized) once in LDS.  epi: 0 any flags, 1 SiLU -> fp16, 2 int8
+// SiLU + residual -> fp16.  hipErrorNotSupported for other shapes.
+hipError_t launch_conv_halo(const ConvParams& p, bool int8, int epi, hipStream_t stream);
+// Halo kernel selection for 3x3 convs: mode 0 automatic, 1 never (implicit
+// GEMM only), 2 forced tile (jn oc subtiles, pw position subtiles per wave,
+// tr x tc output positions per tile, cc channels per chunk; a 3x3 conv the
+// tile does not fit then fails).  False for a tile without a kernel instance.
+bool set_conv3x3_halo(int mode, int jn, int pw, int tr, int tc, int cc);
 // Input staging of the network's first conv: fp32 NCHW -> fp16 NHWC with the
 // channels zero-padded to a multiple of 8 (one 16-byte store per pixel and
 // 8 channels).  y has c_stride Cp = C rounded up to 8, dense.

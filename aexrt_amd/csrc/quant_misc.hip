@@ -266,16 +266,20 @@ __global__ __launch_bounds__(kThreads) void maxpool_nhwc_kernel(
         float m[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) m[i] = -INFINITY;
+        // Every tap loads (from a clamped in-image pixel) and padding taps
+        // become -inf by a select: no load sits under a branch, so all of
+        // them are in flight at once instead of one latency per tap.
         auto tap = [&](int ry, int rx) {
             const int iy = oy * s + ry - pad, ix = ox * s + rx - pad;
-            if ((unsigned)iy >= (unsigned)H || (unsigned)ix >= (unsigned)W) return;
-            const uint4 v = *reinterpret_cast<const uint4*>(xb + ((int64_t)iy * W + ix) * x_cstride);
+            const bool ok = (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W;
+            const int cy = min(max(iy, 0), H - 1), cx = min(max(ix, 0), W - 1);
+            const uint4 v = *reinterpret_cast<const uint4*>(xb + ((int64_t)cy * W + cx) * x_cstride);
             const __half2* h = reinterpret_cast<const __half2*>(&v);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float2 f = __half22float2(h[i]);
-                m[2 * i] = fmaxf(m[2 * i], f.x);
-                m[2 * i + 1] = fmaxf(m[2 * i + 1], f.y);
+                m[2 * i] = fmaxf(m[2 * i], ok ? f.x : -INFINITY);
+                m[2 * i + 1] = fmaxf(m[2 * i + 1], ok ? f.y : -INFINITY);
             }
         };
         if constexpr (KS > 0) {

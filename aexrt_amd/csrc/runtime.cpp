@@ -527,6 +527,13 @@ uint32_t resolve_algorithm(AexrtYoloModel* m, size_t ci, uint32_t wanted) {
         return 5;  // fail-closed fallback to the generic kernel
     }
     if (is_winograd_algorithm(wanted)) {
+        // The reference plans Winograd F(2x2,3x3) for fp16 3x3 convs where its
+        // autotuner measured it fastest.  On gfx950 the direct fp16 kernel
+        // (halo-tile 3x3) beats the Winograd one on every such layer of the
+        // network, so it runs them from the raw weights; the result is the same
+        // conv within fp16 rounding.  aexrt_yolo_override_conv_algorithm(.., 40)
+        // still selects the Winograd kernel.
+        if (d.in_channels % 16 == 0 && d.out_channels % 8 == 0 && nhwc_input) return 5;
         if (winograd_shape_ok(d) && c.kind == kCmdConvSilu && nhwc_input) return wanted;
         return 5;
     }

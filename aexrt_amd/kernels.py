@@ -129,6 +129,14 @@ def set_conv_tile(jn: int = 0, pw: int = 0, ksw: bool = False) -> None:
     check(_lib.lib().aexrt_hip_set_conv_tile(jn, pw, 1 if ksw else 0), "set_conv_tile")
 
 
+HALO_AUTO, HALO_OFF, HALO_FORCE = 0, 1, 2
+
+
+def set_conv3x3_halo(mode: int = HALO_AUTO, jn: int = 0, pw: int = 0, tr: int = 0, tc: int = 0, cc: int = 0) -> None:
+    """Select the halo-tile kernel for 3x3 convs: automatic, off (implicit GEMM), or a forced tile."""
+    check(_lib.lib().aexrt_hip_set_conv3x3_halo(mode, jn, pw, tr, tc, cc), "set_conv3x3_halo")
+
+
 def conv_weight_bytes(params: Sequence[int], algorithm: int) -> int:
     d = ConvDesc.from_params(params)
     n = ctypes.c_uint64()

@@ -92,12 +92,13 @@ INT8_CASES = [
 ]
 
 
-def _run_int8(cuda, n, ic, h, w, oc, k, s, seed, *, silu=True, out_f32=False, x=None):
+def _run_int8(cuda, n, ic, h, w, oc, k, s, seed, *, silu=True, out_f32=False, x=None, residual=False):
     import torch
 
     rng = np.random.default_rng(seed)
     if x is None:
         x = rng.standard_normal((n, ic, h, w)).astype(np.float16).astype(np.float32)
+    r = None
     wt = group16_weight(rng, oc, ic, k)
     b = packing.fp16_round(rng.uniform(-0.1, 0.1, oc).astype(np.float32))
     desc = O.conv_desc(n, ic, h, w, oc, k, s, k // 2)
@@ -112,9 +113,16 @@ def _run_int8(cuda, n, ic, h, w, oc, k, s, seed, *, silu=True, out_f32=False, x=
     ys = K.new_slots(oc, cuda)
     acc = torch.empty((n * oh * ow, oc), dtype=torch.int32, device=cuda)
     flags = (K.SILU if silu else 0) | (K.OUT_F32 if out_f32 else 0)
-    K.conv2d(pc, xd, y, flags=flags, x_slots=xs, y_slots=ys, acc_out=acc)
+    rd = None
+    if residual:
+        r = O.round_f16(rng.standard_normal((n, oc, oh, ow)).astype(np.float32))
+        rd = _dev_nhwc(r, cuda)
+        flags |= K.RESIDUAL
+    K.conv2d(pc, xd, y, flags=flags, x_slots=xs, y_slots=ys, acc_out=acc, residual=rd)
     torch.cuda.synchronize()
     a, qa, qw, ws, acc_ref, y_ref = O.w8a8_conv(x, wt, b, desc, silu=silu, fp16_engine=True)
+    if residual:
+        y_ref = y_ref + r
     got_acc = nhwc_to_nchw(acc.cpu().numpy().reshape(n, oh, ow, oc))
     return dict(acc=got_acc, acc_ref=acc_ref, y=nhwc_to_nchw(y.float().cpu().numpy()), y_ref=y_ref,
                 slots=_u32(ys), y_raw=y, qa=qa, a=a)
@@ -298,6 +306,7 @@ def test_conv_every_tile(cuda, jn, pw, ksw):
     """Each kernel instance on shapes with partial channel tiles, ragged
     position tails, k steps that straddle taps, fp32 output and a residual."""
     K.set_conv_tile(jn, pw, ksw)
+    K.set_conv3x3_halo(K.HALO_OFF)  # the 3x3 cases below run on the implicit GEMM too
     try:
         # int8 3x3 s1: OC 80 = 5 channel subtiles, M = 286, C = 48 (taps straddle k steps)
         r = _run_int8(cuda, 2, 48, 11, 13, 80, 3, 1, 71)
@@ -322,6 +331,87 @@ def test_conv_every_tile(cuda, jn, pw, ksw):
         assert not got[:, :48].any() and not got[:, 72:].any()
     finally:
         K.set_conv_tile(0, 0, False)
+        K.set_conv3x3_halo(K.HALO_AUTO)
+
+
+def _halo_fits(c, h, w, s, jn, pw, tr, tc, cc, int8):
+    """Whether a forced halo tile fits a conv: the kernel's LDS holds the
+    block's weights (C/cc chunks of ceil(9cc/64) 64-k steps, jn*16 channels)
+    and two input windows ((tr-1)s+3 x (tc-1)s+3 pixels x cc channels)."""
+    esz = 1 if int8 else 2
+    if cc % 16 or c % cc or tr * tc > 64 * pw:
+        return False
+    spc = (9 * cc + 63) // 64
+    npieces = ((tr - 1) * s + 3) * ((tc - 1) * s + 3) * cc // 8
+    wbytes = (c // cc) * spc * esz * jn * 16 * 64
+    tbytes = (npieces * 8 * esz + 15) // 16 * 16
+    return npieces <= 8 * 256 and wbytes + 2 * tbytes <= 65536 - 2048
+
+
+# Halo-tile kernel tiles: (jn, pw, tile columns (0 = whole output row), channel chunk divisor)
+HALO_TILES = [(1, 1, 16, 1), (1, 2, 0, 1), (1, 4, 16, 2), (2, 1, 0, 2), (2, 2, 16, 1), (2, 4, 0, 2),
+              (4, 1, 16, 1), (4, 2, 0, 2), (4, 4, 16, 2), (4, 4, 0, 1)]
+
+
+@pytest.mark.parametrize("jn,pw,tc,ccd", HALO_TILES, ids=[f"jn{t[0]}_pw{t[1]}_tc{t[2]}_cc{t[3]}" for t in HALO_TILES])
+def test_halo_every_tile(cuda, jn, pw, tc, ccd):
+    """The halo-tile 3x3 kernel on forced tiles: ragged row/column tiles,
+    several channel chunks, stride 2, fp32 output, SiLU + residual, fp16."""
+    ran = 0
+
+    def force(c, h, w, s, int8):
+        nonlocal ran
+        oh, ow = (h - 1) // s + 1, (w - 1) // s + 1
+        cols = ow if tc == 0 else tc
+        rows = max(1, min(oh, 64 * pw // cols))
+        cc = c // ccd
+        K.set_conv3x3_halo(K.HALO_FORCE, jn, pw, rows, cols, max(cc, 16))
+        fits = cc >= 16 and _halo_fits(c, h, w, s, jn, pw, rows, cols, cc, int8)
+        ran += fits
+        return fits
+
+    try:
+        # int8 s1: OC 80 = 5 channel subtiles, 11 x 13 map
+        if force(64, 11, 13, 1, True):
+            r = _run_int8(cuda, 2, 64, 11, 13, 80, 3, 1, 91)
+            np.testing.assert_array_equal(r["acc"], r["acc_ref"])
+            err, allowed = tol_range(r["y_ref"], r["y"], FP16_TOL)
+            assert err <= allowed, (err, allowed)
+            want = np.array([np.float32(np.abs(r["y"][:, g * 16:(g + 1) * 16]).max()).view(np.uint32)
+                             for g in range(5)], dtype=np.uint32)
+            np.testing.assert_array_equal(r["slots"], want)
+        # int8 s2, fp32 output without activation
+        if force(32, 17, 15, 2, True):
+            r = _run_int8(cuda, 1, 32, 17, 15, 32, 3, 2, 92, silu=False, out_f32=True)
+            np.testing.assert_array_equal(r["acc"], r["acc_ref"])
+            err, allowed = tol_range(r["y_ref"], r["y"], FP32_TOL)
+            assert err <= allowed, (err, allowed)
+        # int8 SiLU + residual (the bottleneck's fused add)
+        if force(16, 20, 20, 1, True):
+            r = _run_int8(cuda, 2, 16, 20, 20, 16, 3, 1, 93, residual=True)
+            np.testing.assert_array_equal(r["acc"], r["acc_ref"])
+            err, allowed = tol_range(r["y_ref"], r["y"], FP16_TOL)
+            assert err <= allowed, (err, allowed)
+        # fp16, residual into a channel slice of a wider tensor
+        if force(32, 9, 7, 1, False):
+            y_ref, got, slots = _run_fp16_residual(cuda, 2, 32, 9, 7, 94, tail=(48, 80), width=96)
+            err, allowed = tol_range(y_ref, got[:, 48:80], FP16_TOL)
+            assert err <= allowed, (err, allowed)
+            assert not got[:, :48].any() and not got[:, 80:].any()
+    finally:
+        K.set_conv3x3_halo(K.HALO_AUTO)
+    assert ran >= 3
+
+
+def test_halo_forced_tile_that_does_not_fit_fails(cuda):
+    K.set_conv3x3_halo(K.HALO_FORCE, 1, 1, 4, 16, 48)  # C = 64 is not a multiple of 48
+    try:
+        with pytest.raises(RuntimeError):
+            _run_int8(cuda, 1, 64, 8, 8, 16, 3, 1, 95)
+    finally:
+        K.set_conv3x3_halo(K.HALO_AUTO)
+    r = _run_int8(cuda, 1, 64, 8, 8, 16, 3, 1, 95)
+    np.testing.assert_array_equal(r["acc"], r["acc_ref"])
 
 
 WINO_CASES = [
