@@ -25,11 +25,24 @@ bool build_conv_params(const AexrtConv2DDesc& d, uint32_t algorithm, uint32_t fl
     }
     const bool int8 = is_int8_algorithm(algorithm);
     const bool wino = is_winograd_algorithm(algorithm);
-    if (flags & AEXRT_HIP_CONV_IN_NCHW_F32) {
-        why = "convert fp32 NCHW input with aexrt_hip_nchw_f32_to_nhwc first (channels padded to 8)";
-        return false;
-    }
     const bool out_f32 = (flags & AEXRT_HIP_CONV_OUT_F32) != 0;
+    // fp32 NCHW input read by the conv itself: x->n_stride = c_real * H * W
+    // elements per image, c_real <= 4 channels read as in_channels = 8 (the
+    // weights are packed for 8 channels, the missing ones zero)
+    const bool nchw = (flags & AEXRT_HIP_CONV_IN_NCHW_F32) != 0;
+    int c_real = 0;
+    if (nchw) {
+        const int64_t plane = int64_t(d.in_h) * d.in_w;
+        c_real = plane > 0 ? (int)(x.n_stride / plane) : 0;
+        if (int8 || wino || d.in_channels != 8 || d.kernel_h != 3 || d.kernel_w != 3 || d.pad_top != 1 ||
+            (d.stride_h != 1 && d.stride_h != 2) || c_real < 1 || c_real > 4 || x.n_stride != c_real * plane ||
+            reinterpret_cast<uintptr_t>(x.data) % 4 || !(flags & AEXRT_HIP_CONV_SILU) ||
+            (flags & (AEXRT_HIP_CONV_RESIDUAL | AEXRT_HIP_CONV_OUT_F32))) {
+            why = "fp32 NCHW input: fp16 3x3 pad-1 SiLU conv with in_channels 8, n_stride = c*H*W (c <= 4), "
+                  "fp16 output, no residual";
+            return false;
+        }
+    }
     if (int8) {
         if (!can_use_int8(d, int8_kernel_elems(algorithm))) {
             why = "descriptor is not eligible for the planned int8 kernel";
@@ -58,8 +71,8 @@ bool build_conv_params(const AexrtConv2DDesc& d, uint32_t algorithm, uint32_t fl
             return false;
         }
     } else {
-        if (d.in_channels % 8 || !aligned16(x.data) || x.c_stride % 8 ||
-            x.n_stride != int64_t(d.in_h) * d.in_w * x.c_stride) {
+        if (!nchw && (d.in_channels % 8 || !aligned16(x.data) || x.c_stride % 8 ||
+                      x.n_stride != int64_t(d.in_h) * d.in_w * x.c_stride)) {
             why = "NHWC input view must be 16-byte aligned, C % 8 == 0, c_stride % 8 == 0 and n_stride == H*W*c_stride";
             return false;
         }
@@ -78,7 +91,7 @@ bool build_conv_params(const AexrtConv2DDesc& d, uint32_t algorithm, uint32_t fl
         why = "striped amax slots need a stride with stripes * stride < 2^31";
         return false;
     }
-    if ((uint32_t)x.c_stride < d.in_channels) {
+    if (!nchw && (uint32_t)x.c_stride < d.in_channels) {
         why = "input c_stride smaller than in_channels";
         return false;
     }
@@ -98,8 +111,9 @@ bool build_conv_params(const AexrtConv2DDesc& d, uint32_t algorithm, uint32_t fl
     p = ConvParams{};
     p.x = x.data;
     p.x_nstride = x.n_stride;
-    p.x_cstride = x.c_stride;
-    p.loader = kLoaderNhwc;
+    p.x_cstride = nchw ? 8 : x.c_stride;
+    p.loader = nchw ? kLoaderNchwF32 : kLoaderNhwc;
+    p.c_real = c_real;
     p.x_slots = slot_ref(x);
     p.x_nslots = (int)(d.in_channels / 16);
     p.w = weight;

@@ -20,6 +20,14 @@
 // the position tile (PW 16-position subtiles each).  The input of the next
 // (tile, chunk) is loaded into registers while the current one is computed;
 // two LDS tile buffers need one barrier per chunk.
+//
+// NCHW: the window is read from the fp32 NCHW network input (c_real <= 4
+// channels) in 16-byte quads of 4 columns of one channel row, rounded to
+// fp16 and scattered into the 8-channel zero-padded pixels of the LDS window,
+// so the first conv runs without a separate layout-conversion pass (fp16
+// only, CC = 8).  Quads start at columns that are multiples of 4 (TC * S % 4
+// == 0 keeps that the same for every tile), so a quad is either wholly left
+// of the image or starts inside it.
 #pragma once
 #include "conv_igemm.h"
 
@@ -39,7 +47,9 @@ struct HaloParams {
     int ntile;       // N * tpi
     int wbytes;      // LDS bytes of the resident weights
     int tbytes;      // LDS bytes of one window buffer
-    FastDiv fd_cc8, fd_icol, fd_tc, fd_ntc, fd_tpi, fd_cg, fd_spc;
+    FastDiv fd_cc8, fd_icol, fd_tc, fd_ntc, fd_tpi, fd_cc, fd_spc;
+    int icol4;                // NCHW: column quads of a window row: (ICOL + 3 + 3) / 4
+    FastDiv fd_icol4, fd_rq;  // NCHW: / icol4, / (IR * icol4)
 };
 
 // Largest k-step count of one chunk (table of tap offsets).
@@ -59,7 +69,7 @@ using igemm::rsrc_t;
 using igemm::v2i;
 using igemm::xcd_remap;
 
-template <bool INT8, int JN, int PW, int NP, int EPI>
+template <bool INT8, int JN, int PW, int NP, int EPI, bool NCHW = false>
 __global__ __launch_bounds__(256) void conv3x3_halo_kernel(HaloParams h) {
     const ConvParams& p = h.c;
     constexpr int WQ = Frag<INT8>::wq;   // MFMAs (and weight pieces) per 64-k step
@@ -68,13 +78,14 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(HaloParams h) {
     constexpr int LOG2R = JN == 1 ? 4 : (JN == 2 ? 5 : (JN == 4 ? 6 : 7));
     constexpr int PIECE = 8 * ESZ;       // LDS bytes of one 8-channel input piece
     static_assert((1 << LOG2R) == R, "JN must be 1, 2, 4 or 8");
+    static_assert(!(NCHW && INT8), "the NCHW input loader is fp16 only");
     typedef typename std::conditional<INT8, v4i, v4f>::type acc_t;
 
     // [weights: wbytes][window buffer 0: tbytes][window buffer 1: tbytes]
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    // (k step, k group) -> byte offset of the tap and channel group inside
+    // (k step, k group, half) -> byte offset of the tap and channels inside
     // the window, relative to the output position's (0, 0) tap
-    __shared__ int l_toff[kHaloMaxSpc * 4];
+    __shared__ int l_toff[kHaloMaxSpc * 4 * WQ];
     __shared__ float l_bias[R], l_scale[R];
     __shared__ uint32_t l_slots[JN];
 
@@ -93,6 +104,7 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(HaloParams h) {
     const int S = p.S;
 
     const rsrc_t rx = make_rsrc(p.x, p.x_bytes);
+    const int plane = p.H * p.W;  // NCHW: elements of one channel plane
     const rsrc_t rw = make_rsrc(p.w, (uint32_t)p.OCp * (uint32_t)p.Kp * ESZ);
 
     // ---- prologue loads: input scale, per-channel constants ----------------
@@ -106,21 +118,20 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(HaloParams h) {
     if constexpr (INT8) scale_v = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsc, cofs, 0, 0));
 
     // ---- weights: [chunk * spc + s][h][row][grp * 16 B], gathered ----------
-    // 16-byte piece e: grp = e & 3, row = (e >> 2) % R, (gs, h) from the rest.
-    // At most 64 KB: one round of kHaloWeightRounds pieces per thread.
+    // 16-byte piece e: grp = e & 3, row = (e >> 2) % R, (gs, h) from the rest;
+    // chunk-local k = g * 16 + h * 8 = tap * CC + c.  At most 64 KB: one
+    // round of kHaloWeightRounds pieces per thread.
     const int wpieces = h.wbytes >> 4;
-    const int ng = 9 * (h.CC >> 4);  // 16-k groups of a chunk
     auto wload = [&](int e) {
         const int g4 = e & 3;
         const int row = (e >> 2) & (R - 1);
         const int gsh = e >> (2 + LOG2R);
         const int gs = gsh / WQ, hh = gsh - (gsh / WQ) * WQ;
         const int ch = (int)fdiv((uint32_t)gs, h.fd_spc);
-        const int g = (gs - ch * h.spc) * 4 + g4;
-        const int tap = (int)fdiv((uint32_t)g, h.fd_cg);
-        const int cg = g - tap * (h.CC >> 4);
-        const int k = tap * p.C + ch * h.CC + cg * 16 + hh * 8;
-        const bool ok = e < wpieces && g < ng && n0 + row < p.OCp;
+        const int kk = ((gs - ch * h.spc) * 4 + g4) * 16 + hh * 8;
+        const int tap = (int)fdiv((uint32_t)kk, h.fd_cc);
+        const int k = tap * p.C + ch * h.CC + (kk - tap * h.CC);
+        const bool ok = e < wpieces && tap < 9 && n0 + row < p.OCp;
         return bload16(rw, ok ? (uint32_t)((n0 + row) * p.Kp + k) * ESZ : kOob);
     };
     v4i wst[kHaloWeightRounds];
@@ -131,17 +142,30 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(HaloParams h) {
     // Piece k of this thread: e = tid + k * 256 -> window pixel (ir, ic) and
     // 8-channel group; the LDS place is e * PIECE.  Pieces past the window get
     // a row that fails every bounds test.
+    // NCHW pieces: e -> channel c, window row ir, column quad q4 (columns
+    // 4 q4 - 3 .. 4 q4 relative to the window's first column), packed as
+    // ir | q4 << 12 | c << 24 in prc.
     int prc[NP], prel[NP];
 #pragma unroll
     for (int k = 0; k < NP; ++k) {
         const int e = tid + k * 256;
-        const int pix = (int)fdiv((uint32_t)e, h.fd_cc8);
-        const int cp = e - pix * (h.CC >> 3);
-        const int ir = (int)fdiv((uint32_t)pix, h.fd_icol);
-        const int ic = pix - ir * h.ICOL;
-        prc[k] = e < h.npieces ? (ir | (ic << 16)) : 0x7FFF;
-        prel[k] = (ir * p.W + ic) * p.x_cstride + cp * 8;
+        if constexpr (NCHW) {
+            const int c = (int)fdiv((uint32_t)e, h.fd_rq);
+            const int rem = e - c * h.IR * h.icol4;
+            const int ir = (int)fdiv((uint32_t)rem, h.fd_icol4);
+            const int q4 = rem - ir * h.icol4;
+            prc[k] = e < h.npieces ? (ir | (q4 << 12) | (c << 24)) : 0xFFF;
+            prel[k] = c * plane + ir * p.W + 4 * q4;
+        } else {
+            const int pix = (int)fdiv((uint32_t)e, h.fd_cc8);
+            const int cp = e - pix * (h.CC >> 3);
+            const int ir = (int)fdiv((uint32_t)pix, h.fd_icol);
+            const int ic = pix - ir * h.ICOL;
+            prc[k] = e < h.npieces ? (ir | (ic << 16)) : 0x7FFF;
+            prel[k] = (ir * p.W + ic) * p.x_cstride + cp * 8;
+        }
     }
+    int pvalid[NCHW ? NP : 1];  // NCHW: columns of the quad inside the image (0..4)
     // tile tl of this block -> image, first output row and column
     auto tile_pos = [&](int tl, int& n, int& oh0, int& ow0) {
         const int ti = pt0 + tl;
@@ -159,12 +183,25 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(HaloParams h) {
         tile_pos(tl, n, oh0, ow0);
         const int ihb = live ? oh0 * S - 1 : -0x40000000;
         const int iwb = ow0 * S - 1;
-        const int gbase = n * (int)p.x_nstride + ((oh0 * S - 1) * p.W + iwb) * p.x_cstride + ch * h.CC;
+        if constexpr (NCHW) {
+            // quads start at column ow0 * S - 4 + 4 q4 (a multiple of 4)
+            const int ws = ow0 * S - 4;
+            const int gbase = n * (int)p.x_nstride + (oh0 * S - 1) * p.W + ws;
 #pragma unroll
-        for (int k = 0; k < NP; ++k) {
-            const int ih = ihb + (prc[k] & 0xFFFF), iw = iwb + (prc[k] >> 16);
-            const bool ok = (unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.W;
-            pf[k] = bload16(rx, ok ? (uint32_t)(gbase + prel[k]) * 2u : kOob);
+            for (int k = 0; k < NP; ++k) {
+                const int ih = ihb + (prc[k] & 0xFFF), c0 = ws + 4 * ((prc[k] >> 12) & 0xFFF);
+                const bool ok = (unsigned)ih < (unsigned)p.H && c0 >= 0 && c0 < p.W;
+                pvalid[k] = ok ? min(4, p.W - c0) : 0;
+                pf[k] = bload16(rx, ok ? (uint32_t)(gbase + prel[k]) * 4u : kOob);
+            }
+        } else {
+            const int gbase = n * (int)p.x_nstride + ((oh0 * S - 1) * p.W + iwb) * p.x_cstride + ch * h.CC;
+#pragma unroll
+            for (int k = 0; k < NP; ++k) {
+                const int ih = ihb + (prc[k] & 0xFFFF), iw = iwb + (prc[k] >> 16);
+                const bool ok = (unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.W;
+                pf[k] = bload16(rx, ok ? (uint32_t)(gbase + prel[k]) * 2u : kOob);
+            }
         }
     };
     window_loads(0, 0, true);
@@ -186,14 +223,14 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(HaloParams h) {
         __builtin_amdgcn_raw_buffer_store_b64(v2i{0, 0}, ry, kOob, 0, 0);
 
     // ---- tables (ALU only while the loads are in flight) -------------------
-    for (int e = tid; e < h.spc * 4; e += 256) {
-        const int g = e;  // (s, grp) -> 16-k group s * 4 + grp of the chunk
-        int off = 0;      // padding group: any in-window address, zero weights
-        if (g < ng) {
-            const int tap = (int)fdiv((uint32_t)g, h.fd_cg);
-            const int cg = g - tap * (h.CC >> 4);
+    for (int e = tid; e < h.spc * 4 * WQ; e += 256) {
+        // e = (s * 4 + grp) * WQ + hh -> chunk-local k = (s * 4 + grp) * 16 + hh * 8
+        const int kk = (e / WQ) * 16 + (e - (e / WQ) * WQ) * 8;
+        const int tap = (int)fdiv((uint32_t)kk, h.fd_cc);
+        int off = 0;  // padding k: any in-window address, zero weights
+        if (tap < 9) {
             const int ky = tap / 3, kx = tap - (tap / 3) * 3;
-            off = ((ky * h.ICOL + kx) * h.CC + cg * 16) * ESZ;
+            off = ((ky * h.ICOL + kx) * h.CC + (kk - tap * h.CC)) * ESZ;
         }
         l_toff[e] = off;
     }
@@ -221,6 +258,12 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(HaloParams h) {
     for (int r = 0; r < kHaloWeightRounds; ++r) {
         const int e = tid + r * 256;
         if (e < wpieces) *reinterpret_cast<v4i*>(lds + e * 16) = wst[r];
+    }
+    if constexpr (NCHW) {
+        // the padding channels of the window pixels are never written
+        for (int e = tid; e < (2 * h.tbytes) >> 4; e += 256)
+            *reinterpret_cast<v4i*>(lds + h.wbytes + e * 16) = v4i{0, 0, 0, 0};
+        __syncthreads();  // zeros land before any thread's first window stores
     }
 
     float gmax[JN];
@@ -262,8 +305,23 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(HaloParams h) {
         for (int k = 0; k < NP; ++k) {
             const int e = tid + k * 256;
             if (e < h.npieces) {
-                if constexpr (INT8) *reinterpret_cast<v2i*>(tb + e * PIECE) = quant8(pf[k], s_q);
-                else *reinterpret_cast<v4i*>(tb + e * PIECE) = pf[k];
+                if constexpr (INT8) {
+                    *reinterpret_cast<v2i*>(tb + e * PIECE) = quant8(pf[k], s_q);
+                } else if constexpr (NCHW) {
+                    // channel c of window pixels 4 q4 - 3 + j (those inside
+                    // the window; columns past the image are zero)
+                    const int ir = prc[k] & 0xFFF, q4 = (prc[k] >> 12) & 0xFFF, c = prc[k] >> 24;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int ic = 4 * q4 - 3 + j;
+                        if (ic >= 0 && ic < h.ICOL) {
+                            const __half v = __float2half(j < pvalid[k] ? __int_as_float(pf[k][j]) : 0.0f);
+                            *reinterpret_cast<__half*>(tb + ((ir * h.ICOL + ic) * 8 + c) * 2) = v;
+                        }
+                    }
+                } else {
+                    *reinterpret_cast<v4i*>(tb + e * PIECE) = pf[k];
+                }
             }
         }
         const bool tile_end = ch == h.nch - 1;
@@ -293,14 +351,14 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(HaloParams h) {
         // the compiler from sinking the reads next to their MFMAs)
         const uint8_t* const wb = lds + ch * h.spc * wstep;
         auto fetch = [&](int s, v4i (&A)[WQ][JN], v4i (&B)[WQ][PW]) {
-            const int toff = l_toff[s * 4 + grp];
 #pragma unroll
             for (int hh = 0; hh < WQ; ++hh) {
+                const int toff = l_toff[(s * 4 + grp) * WQ + hh];
 #pragma unroll
                 for (int j = 0; j < JN; ++j)
                     A[hh][j] = *reinterpret_cast<const v4i*>(wb + s * wstep + (hh * R + j * 16 + col) * 64 + grp * 16);
 #pragma unroll
-                for (int q = 0; q < PW; ++q) B[hh][q] = *reinterpret_cast<const v4i*>(tb + bofs[q] + toff + hh * 16);
+                for (int q = 0; q < PW; ++q) B[hh][q] = *reinterpret_cast<const v4i*>(tb + bofs[q] + toff);
             }
         };
         auto mma = [&](const v4i (&A)[WQ][JN], const v4i (&B)[WQ][PW]) {
@@ -399,11 +457,11 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(HaloParams h) {
 }
 
 // Blocks of one instance the GPU holds at once with lds_bytes of dynamic LDS.
-template <bool INT8, int JN, int PW, int NP, int EPI>
+template <bool INT8, int JN, int PW, int NP, int EPI, bool NCHW>
 int halo_resident_blocks(int lds_bytes) {
     int per_cu = 0, cus = 0, dev = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv3x3_halo_kernel<INT8, JN, PW, NP, EPI>, 256,
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv3x3_halo_kernel<INT8, JN, PW, NP, EPI, NCHW>, 256,
                                                      (size_t)lds_bytes) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu < 1 ||
         cus < 1)
@@ -413,17 +471,17 @@ int halo_resident_blocks(int lds_bytes) {
 
 // Persistent grid: every resident block slot gets one contiguous run of
 // position tiles of one oc tile.
-template <bool INT8, int JN, int PW, int NP, int EPI>
+template <bool INT8, int JN, int PW, int NP, int EPI, bool NCHW = false>
 hipError_t halo_launch_cfg(HaloParams h, hipStream_t stream) {
     const int lds_bytes = h.wbytes + 2 * h.tbytes;
-    const int cap = halo_resident_blocks<INT8, JN, PW, NP, EPI>(lds_bytes);
+    const int cap = halo_resident_blocks<INT8, JN, PW, NP, EPI, NCHW>(lds_bytes);
     int groups = h.ntile;
     if ((int64_t)h.ntile * h.c.ntn > cap) groups = std::max(1, cap / h.c.ntn);
     h.c.per = (h.ntile + groups - 1) / groups;
     groups = (h.ntile + h.c.per - 1) / h.c.per;
     const int64_t blocks = (int64_t)groups * h.c.ntn;
     if (blocks > INT32_MAX) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((conv3x3_halo_kernel<INT8, JN, PW, NP, EPI>), dim3((unsigned)blocks), dim3(256),
+    hipLaunchKernelGGL((conv3x3_halo_kernel<INT8, JN, PW, NP, EPI, NCHW>), dim3((unsigned)blocks), dim3(256),
                        (size_t)lds_bytes, stream, h);
     return hipGetLastError();
 }
@@ -442,6 +500,9 @@ hipError_t halo_launch_family(const HaloParams& h, int jn, int pw, int np, hipSt
 #undef AEXRT_HALO_CASE
     return hipErrorInvalidValue;
 }
+
+// The first conv on the fp32 NCHW input (fp16, SiLU).
+hipError_t halo_launch_nchw(const HaloParams& h, int jn, int pw, int np, hipStream_t stream);
 
 #define AEXRT_HALO_FAMILIES(X) X(true, 0) X(true, 1) X(true, 2) X(false, 0) X(false, 1)
 #define AEXRT_HALO_EXTERN(I, E) \

@@ -35,7 +35,9 @@ bool halo_geometry(HaloParams& h, const HaloTile& t, bool int8) {
     const ConvParams& p = h.c;
     const int esz = int8 ? 1 : 2;
     const int wq = int8 ? 1 : 2;
-    if (t.CC < 16 || t.CC % 16 || p.C % t.CC || t.TR < 1 || t.TC < 1) return false;
+    // int8: a 16-k MFMA operand piece is 16 channels of one tap; fp16: 8
+    if (t.CC < (int8 ? 16 : 8) || t.CC % (int8 ? 16 : 8) || p.C % t.CC || t.TR < 1 || t.TC < 1) return false;
+    if (p.loader == kLoaderNchwF32 && t.CC != p.C) return false;
     if (t.TR * t.TC > 64 * t.pw) return false;
     h.TR = t.TR;
     h.TC = t.TC;
@@ -46,6 +48,15 @@ bool halo_geometry(HaloParams& h, const HaloTile& t, bool int8) {
     h.spc = (9 * t.CC + 63) / 64;
     if (h.spc > kHaloMaxSpc) return false;
     h.npieces = h.IR * h.ICOL * t.CC / 8;
+    if (p.loader == kLoaderNchwF32) {
+        // 16-byte quads of one channel row; every tile's first quad starts
+        // at a multiple of 4 columns
+        if ((t.TC * p.S) % 4) return false;
+        h.icol4 = (h.ICOL + 3 + 3) / 4;
+        h.npieces = p.c_real * h.IR * h.icol4;
+        h.fd_icol4 = make_fastdiv((uint32_t)h.icol4);
+        h.fd_rq = make_fastdiv((uint32_t)(h.IR * h.icol4));
+    }
     if (h.npieces > 256 * t.np) return false;
     h.ntc = (p.OW + t.TC - 1) / t.TC;
     h.tpi = ((p.OH + t.TR - 1) / t.TR) * h.ntc;
@@ -53,7 +64,7 @@ bool halo_geometry(HaloParams& h, const HaloTile& t, bool int8) {
     if (ntile > INT32_MAX / 2) return false;
     h.ntile = (int)ntile;
     h.wbytes = h.nch * h.spc * wq * t.jn * 16 * 64;
-    h.tbytes = (h.npieces * 8 * esz + 15) & ~15;
+    h.tbytes = ((p.loader == kLoaderNchwF32 ? h.IR * h.ICOL : h.npieces) * 8 * esz + 15) & ~15;
     if (h.wbytes + 2 * h.tbytes > kLdsBudget || h.wbytes > 256 * kHaloWeightRounds * 16) return false;
     h.c.ntn = (p.OCp / 16 + t.jn - 1) / t.jn;
     h.fd_cc8 = make_fastdiv((uint32_t)(t.CC / 8));
@@ -61,7 +72,7 @@ bool halo_geometry(HaloParams& h, const HaloTile& t, bool int8) {
     h.fd_tc = make_fastdiv((uint32_t)t.TC);
     h.fd_ntc = make_fastdiv((uint32_t)h.ntc);
     h.fd_tpi = make_fastdiv((uint32_t)h.tpi);
-    h.fd_cg = make_fastdiv((uint32_t)(t.CC / 16));
+    h.fd_cc = make_fastdiv((uint32_t)t.CC);
     h.fd_spc = make_fastdiv((uint32_t)h.spc);
     h.c.fd_ntn = make_fastdiv((uint32_t)h.c.ntn);
     return true;
@@ -88,10 +99,13 @@ double halo_cost(const HaloParams& h, const HaloTile& t, bool int8) {
     return std::max(compute, bytes / 2500.0) + 1500.0;
 }
 
-bool halo_shape_ok(const ConvParams& p) {
-    return p.KH == 3 && p.KW == 3 && p.P == 1 && (p.S == 1 || p.S == 2) && p.C % 16 == 0 && p.x_cstride % 8 == 0 &&
-           p.OH == (p.H - 1) / p.S + 1 && p.OW == (p.W - 1) / p.S + 1 && p.H < 8192 && p.W < 8192 &&
-           p.loader == kLoaderNhwc;
+bool halo_shape_ok(const ConvParams& p, bool int8) {
+    if (!(p.KH == 3 && p.KW == 3 && p.P == 1 && (p.S == 1 || p.S == 2) && p.OH == (p.H - 1) / p.S + 1 &&
+          p.OW == (p.W - 1) / p.S + 1 && p.H < 8192 && p.W < 8192))
+        return false;
+    if (p.loader == kLoaderNchwF32)
+        return !int8 && p.C == 8 && p.c_real >= 1 && p.c_real <= 4 && p.flags == kConvSilu;
+    return p.loader == kLoaderNhwc && p.C % (int8 ? 16 : 8) == 0 && p.x_cstride % 8 == 0;
 }
 
 // Lowest-cost tile of the instantiated shapes.
@@ -100,15 +114,19 @@ bool choose_halo_tile(HaloParams& h, bool int8, HaloTile& best) {
     double best_cost = 0.0;
     bool found = false;
     const int ocj = (p.OCp + 15) / 16;
+    const bool nchw = p.loader == kLoaderNchwF32;
     for (int div = 1; div <= 8; div <<= 1) {
         if (p.C % div) break;
         const int CC = p.C / div;
-        if (CC % 16 || CC > (int8 ? 128 : 64)) continue;
+        if (CC % (int8 ? 16 : 8) || CC > (int8 ? 128 : 64)) continue;
         for (int jn = 1; jn <= std::min(4, pow2_at_least(ocj, 4)); jn <<= 1) {
-            for (int pw = 1; pw <= 4; pw <<= 1) {
-                int tcs[6] = {p.OW, 16, 32, 48, 64, 80};
+            for (int pw = nchw ? 2 : 1; pw <= 4; pw <<= 1) {
+                // the whole row, or its width rounded up to 4 (the NCHW
+                // loader needs TC * S % 4 == 0), or multiples of 16
+                const int ow4 = (p.OW + 3) / 4 * 4;
+                int tcs[7] = {p.OW, ow4, 16, 32, 48, 64, 80};
                 for (int tc : tcs) {
-                    if (tc > p.OW || (tc != p.OW && tc > 64 * pw)) continue;
+                    if (tc > ow4 || (tc > p.OW && tc != ow4) || (tc < p.OW && tc > 64 * pw)) continue;
                     const int TR = std::min(p.OH, 64 * pw / tc);
                     if (TR < 1) continue;
                     for (int np : {4, 8}) {
@@ -132,6 +150,7 @@ bool choose_halo_tile(HaloParams& h, bool int8, HaloTile& best) {
 
 hipError_t halo_launch(const HaloParams& h, bool int8, int epi, const HaloTile& t, hipStream_t s) {
     using halo::halo_launch_family;
+    if (h.c.loader == kLoaderNchwF32) return halo::halo_launch_nchw(h, t.jn, t.pw, t.np, s);
     if (int8) {
         if (epi == 1) return halo_launch_family<true, 1>(h, t.jn, t.pw, t.np, s);
         if (epi == 2) return halo_launch_family<true, 2>(h, t.jn, t.pw, t.np, s);
@@ -161,8 +180,10 @@ bool set_conv3x3_halo(int mode, int jn, int pw, int tr, int tc, int cc) {
 // hipErrorNotSupported: the shape is not a halo-tile conv (the caller uses
 // the implicit-GEMM kernel).
 hipError_t launch_conv_halo(const ConvParams& p, bool int8, int epi, hipStream_t stream) {
-    const int mode = g_halo_mode.load(std::memory_order_relaxed);
-    if (mode == 1 || !halo_shape_ok(p)) return hipErrorNotSupported;
+    if (!halo_shape_ok(p, int8)) return hipErrorNotSupported;
+    // the NCHW input has no other kernel; the tile modes apply to NHWC convs
+    const int mode = p.loader == kLoaderNchwF32 ? 0 : g_halo_mode.load(std::memory_order_relaxed);
+    if (mode == 1) return hipErrorNotSupported;
     HaloParams h{};
     h.c = p;
     HaloTile t{};

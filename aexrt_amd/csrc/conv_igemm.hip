@@ -95,16 +95,21 @@ ConvTile choose_conv_tile(int M, int OC, int Kp) {
 }
 
 hipError_t launch_conv_igemm(const ConvParams& p0, bool int8, hipStream_t stream) {
-    if (p0.loader != kLoaderNhwc || p0.OC % 4 || p0.C % 8 || p0.Kp % 64 || p0.OCp % 16) return hipErrorInvalidValue;
+    const bool nchw = p0.loader == kLoaderNchwF32;
+    if ((p0.loader != kLoaderNhwc && !nchw) || p0.OC % 4 || p0.C % 8 || p0.Kp % 64 || p0.OCp % 16)
+        return hipErrorInvalidValue;
+    if (nchw && (int8 || p0.c_real < 1 || p0.c_real > 4 || p0.x_nstride != (int64_t)p0.c_real * p0.H * p0.W))
+        return hipErrorInvalidValue;
     const ConvTile t = choose_conv_tile(p0.M, p0.OC, p0.Kp);
     const bool out_f32 = (p0.flags & kConvOutF32) != 0;
     const int HWi = p0.H * p0.W, HWo = p0.OH * p0.OW;
     // Images per launch: every view a launch touches must stay inside
     // kMaxViewBytes so the kernel can address it with 32-bit offsets.
-    const uint64_t per_img = std::max({(uint64_t)p0.x_nstride * 2, (uint64_t)p0.y_nstride * (out_f32 ? 4 : 2),
+    const uint64_t x_img = nchw ? (uint64_t)p0.x_nstride * 4
+                                : std::max((uint64_t)p0.x_nstride * 2, (uint64_t)HWi * p0.x_cstride * 2);
+    const uint64_t per_img = std::max({x_img, (uint64_t)p0.y_nstride * (out_f32 ? 4 : 2),
                                        p0.res ? (uint64_t)p0.r_nstride * 2 : 0,
-                                       p0.acc_out ? (uint64_t)HWo * p0.OC * 4 : 0,
-                                       (uint64_t)HWi * p0.x_cstride * 2});
+                                       p0.acc_out ? (uint64_t)HWo * p0.OC * 4 : 0});
     if ((uint64_t)p0.OCp * p0.Kp * 2 > kMaxViewBytes || per_img == 0) return hipErrorInvalidValue;
     const int per_launch = (int)std::min<uint64_t>((uint64_t)p0.N, kMaxViewBytes / per_img);
     if (per_launch < 1) return hipErrorInvalidValue;
@@ -124,11 +129,13 @@ hipError_t launch_conv_igemm(const ConvParams& p0, bool int8, hipStream_t stream
         ConvParams p = p0;
         p.N = std::min(per_launch, p0.N - nb);
         p.M = p.N * HWo;
-        p.x = static_cast<const __half*>(p0.x) + (int64_t)nb * p0.x_nstride;
+        p.x = nchw ? static_cast<const void*>(static_cast<const float*>(p0.x) + (int64_t)nb * p0.x_nstride)
+                   : static_cast<const void*>(static_cast<const __half*>(p0.x) + (int64_t)nb * p0.x_nstride);
         p.y = static_cast<char*>(p0.y) + (int64_t)nb * p0.y_nstride * (out_f32 ? 4 : 2);
         if (p0.res) p.res = p0.res + (int64_t)nb * p0.r_nstride;
         if (p0.acc_out) p.acc_out = p0.acc_out + (int64_t)nb * HWo * p0.OC;
-        p.x_bytes = (uint32_t)view_span(p.N, p.x_nstride, p.x_cstride, HWi, p.C, 2);
+        p.x_bytes = nchw ? (uint32_t)((uint64_t)p.N * p.x_nstride * 4)
+                         : (uint32_t)view_span(p.N, p.x_nstride, p.x_cstride, HWi, p.C, 2);
         p.y_bytes = (uint32_t)view_span(p.N, p.y_nstride, p.y_cstride, HWo, p.OC, out_f32 ? 4 : 2);
         p.r_bytes = p.res ? (uint32_t)view_span(p.N, p.r_nstride, p.r_cstride, HWo, p.OC, 2) : 0u;
         p.ntn = (p.OCp / 16 + t.jn - 1) / t.jn;
@@ -144,7 +151,7 @@ hipError_t launch_conv_igemm(const ConvParams& p0, bool int8, hipStream_t stream
         p.fd_c = make_fastdiv((uint32_t)p.C);
         p.fd_kw = make_fastdiv((uint32_t)p.KW);
         hipError_t e = launch_conv_halo(p, int8, epi, stream);
-        if (e == hipErrorNotSupported) e = launch_variant(int8, mc, epi, p, t, stream);
+        if (e == hipErrorNotSupported && !nchw) e = launch_variant(int8, mc, epi, p, t, stream);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

@@ -42,6 +42,7 @@ enum ConvFlags : int {
 
 enum Loader : int {
     kLoaderNhwc = 0,     // fp16 NHWC activation view, C % 8 == 0
+    kLoaderNchwF32 = 1,  // fp32 NCHW network input, c_real <= 4 channels read as C = 8 (zero padded)
 };
 
 // One convolution launch.  Activation views address element (n, h, w, c) at
@@ -66,6 +67,7 @@ struct ConvParams {
     int32_t r_cstride;
     int32_t* acc_out;         // optional int32 accumulators [M][OC] (int8)
     int N, H, W, C, OH, OW, OC, KH, KW, S, P;
+    int c_real = 0;           // kLoaderNchwF32: channels present in memory (x_nstride = c_real*H*W)
     int K, M;
     int flags;
     // filled in by the igemm launcher

@@ -132,6 +132,7 @@ struct AexrtYoloModel {
     float* input_dev = nullptr;
     float* input_host = nullptr;
     bool input_needs_nhwc = false;
+    bool input_nchw_direct = false;  // the input's convs read the fp32 NCHW tensor themselves
     hipStream_t stream = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
@@ -387,6 +388,8 @@ bool try_place(AexrtYoloModel* m, int t, const Placement& pl) {
     return true;
 }
 
+AexrtConv2DDesc desc_of(const EngineCommand& c);
+
 bool plan_memory(AexrtYoloModel* m, std::vector<CopyJob>& copies) {
     Engine& e = m->eng;
     auto& V = m->vals;
@@ -468,13 +471,24 @@ bool plan_memory(AexrtYoloModel* m, std::vector<CopyJob>& copies) {
         if (o.redirect >= 0) continue;  // fused conv output: never stored
         if (!o.pl.valid) new_root(m, (int)c.output, false);
     }
-    // the network input arrives as fp32 NCHW; every kernel reads fp16 NHWC,
-    // so a staging step writes an NHWC copy, channels zero-padded to 8
+    // The network input arrives as fp32 NCHW.  When every consumer is a 3x3
+    // pad-1 SiLU conv on at most 4 channels (the stem), those convs read it
+    // directly (fp32 NCHW loader, channels zero-padded to 8); otherwise a
+    // staging step writes an fp16 NHWC copy, channels zero-padded to 8.
     const uint32_t in_v = e.manifest.input_value;
     if (!V[in_v].consumers.empty()) {
-        m->input_needs_nhwc = true;
         if (V[in_v].C % 8) V[in_v].cpad = (V[in_v].C + 7) / 8 * 8;
-        new_root(m, (int)in_v, false);
+        bool direct = V[in_v].C <= 4 && V[in_v].rank == 4;
+        for (int ci : V[in_v].consumers) {
+            const EngineCommand& c = e.commands[ci];
+            const AexrtConv2DDesc d = desc_of(c);
+            direct = direct && c.kind == kCmdConvSilu && c.inputs[0] == in_v && d.kernel_h == 3 && d.kernel_w == 3 &&
+                     d.pad_top == 1 && (d.stride_h == 1 || d.stride_h == 2) && !m->convs[ci].fused_residual &&
+                     c.output != e.manifest.output_value;
+        }
+        m->input_nchw_direct = direct;
+        m->input_needs_nhwc = !direct;
+        if (!direct) new_root(m, (int)in_v, false);
     }
     return true;
 }
@@ -689,7 +703,16 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                 const int xv = (int)c.inputs[0];
                 const AexrtConv2DDesc d = conv_desc_padded(m, ci);
                 uint32_t flags = c.kind == kCmdConvSilu ? AEXRT_HIP_CONV_SILU : 0u;
-                const AexrtHipTensorView xvw = view_of(m, xv);
+                AexrtHipTensorView xvw{};
+                if (m->vals[xv].is_input && m->input_nchw_direct) {
+                    const ValueInfo& xi = m->vals[xv];
+                    xvw.data = m->input_dev;
+                    xvw.n_stride = int64_t(xi.C) * xi.H * xi.W;
+                    xvw.c_stride = xi.C;
+                    flags |= AEXRT_HIP_CONV_IN_NCHW_F32;
+                } else {
+                    xvw = view_of(m, xv);
+                }
                 const int yv = cs.out_value;
                 AexrtHipTensorView yvw = view_of(m, yv);
                 if (is_f32(m, yv)) flags |= AEXRT_HIP_CONV_OUT_F32;

@@ -84,7 +84,10 @@ typedef struct AexrtHipTensorView {
 #define AEXRT_HIP_CONV_RESIDUAL 2u /* + residual view after the activation        */
 #define AEXRT_HIP_CONV_OUT_F32 4u  /* fp32 output view instead of fp16             */
 #define AEXRT_HIP_CONV_IN_NCHW_F32 8u /* x->data is a dense fp32 NCHW tensor (network
-                                       * input of the stem conv; fp16 algorithms only) */
+                                       * input of the stem conv): c = x->n_stride / (H*W)
+                                       * <= 4 channels, read as in_channels = 8 (weights
+                                       * packed for 8, zero past c); fp16 3x3 pad-1 SiLU
+                                       * convs with fp16 output only */
 
 /* Weight source layouts accepted by aexrt_hip_pack_conv_weight: the
  * reference's packed layouts (src/aexrt/engine.py:59-71) plus raw constants. */

@@ -246,6 +246,58 @@ def test_fp16_conv_parity(cuda, case):
     assert err <= allowed, (err, allowed)
 
 
+@pytest.mark.parametrize("n,h,w,oc,s", [(2, 64, 64, 16, 2), (1, 37, 29, 32, 2), (3, 20, 18, 24, 1),
+                                         (1, 160, 160, 16, 2)])
+def test_stem_conv_reads_fp32_nchw_input(cuda, n, h, w, oc, s):
+    """The first conv reading the fp32 NCHW network input itself equals the
+    staged path (fp16 NHWC copy, channels padded to 8) bit for bit."""
+    import torch
+
+    rng = np.random.default_rng(61 + h)
+    ic, cp = 3, 8
+    x = rng.standard_normal((n, ic, h, w)).astype(np.float32)
+    wt = he_weight(rng, oc, ic, 3)
+    b = packing.fp16_round(rng.uniform(-0.1, 0.1, oc).astype(np.float32))
+    wpad = np.zeros((oc, cp, 3, 3), np.float32)
+    wpad[:, :ic] = wt
+    dpad = O.conv_desc(n, cp, h, w, oc, 3, s, 1)
+    pc = K.prepare_conv(dpad, 5, K.SRC_RAW_F32, wpad, b, device=cuda)
+    _, _, oh, ow = O.out_shape(dpad)
+    xf = torch.from_numpy(x).to(cuda)
+    staged = torch.zeros((n, h, w, cp), dtype=torch.float16, device=cuda)
+    K.nchw_f32_to_nhwc(xf, staged[..., :ic])
+    y0 = torch.empty((n, oh, ow, oc), dtype=torch.float16, device=cuda)
+    y1 = torch.empty_like(y0)
+    s0, s1 = K.new_slots(oc, cuda), K.new_slots(oc, cuda)
+    K.conv2d(pc, staged, y0, flags=K.SILU, y_slots=s0)
+    K.conv2d(pc, xf, y1, flags=K.SILU | K.IN_NCHW_F32, y_slots=s1)
+    torch.cuda.synchronize()
+    assert torch.equal(y0, y1)
+    np.testing.assert_array_equal(_u32(s0), _u32(s1))
+    desc = O.conv_desc(n, ic, h, w, oc, 3, s, 1)
+    y_ref = O.cpu_conv2d(O.round_f16(x), O.round_f16(wt), b, desc, silu=True)
+    err, allowed = tol_range(y_ref, nhwc_to_nchw(y1.float().cpu().numpy()), FP16_TOL)
+    assert err <= allowed, (err, allowed)
+
+
+def test_stem_conv_nchw_input_rejects_unsupported(cuda):
+    import torch
+
+    rng = np.random.default_rng(62)
+    wpad = np.zeros((16, 8, 3, 3), np.float32)
+    wpad[:, :3] = he_weight(rng, 16, 3, 3)
+    b = np.zeros(16, np.float32)
+    dpad = O.conv_desc(1, 8, 16, 16, 16, 3, 2, 1)
+    pc = K.prepare_conv(dpad, 5, K.SRC_RAW_F32, wpad, b, device=cuda)
+    xf = torch.zeros((1, 3, 16, 16), dtype=torch.float32, device=cuda)
+    y = torch.empty((1, 8, 8, 16), dtype=torch.float16, device=cuda)
+    with pytest.raises(RuntimeError, match="NCHW"):
+        K.conv2d(pc, xf, y, flags=K.IN_NCHW_F32)  # no SiLU
+    x5 = torch.zeros((1, 5, 16, 16), dtype=torch.float32, device=cuda)
+    with pytest.raises(RuntimeError, match="NCHW"):
+        K.conv2d(pc, x5, y, flags=K.SILU | K.IN_NCHW_F32)  # more than 4 channels
+
+
 def test_fp16_conv_residual_into_channel_slice(cuda):
     """Bottleneck tail: y[..., 32:64] = silu(conv(x)) + r, written into a wider tensor."""
     import torch
