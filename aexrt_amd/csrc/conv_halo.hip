@@ -162,6 +162,48 @@ hipError_t halo_launch(const HaloParams& h, bool int8, int epi, const HaloTile& 
 
 }  // namespace
 
+int enumerate_halo_choices(const ConvParams& p, bool int8, ConvChoice* out, int cap) {
+    if (!halo_shape_ok(p, int8)) return 0;
+    const bool nchw = p.loader == kLoaderNchwF32;
+    const int ocj = (p.OCp + 15) / 16;
+    const int ow4 = (p.OW + 3) / 4 * 4;
+    int n = 0;
+    for (int div = 1; div <= 8 && n < cap; div <<= 1) {
+        if (p.C % div) break;
+        const int CC = p.C / div;
+        if (CC % (int8 ? 16 : 8) || CC > (int8 ? 128 : 64)) continue;
+        for (int jn = 1; jn <= std::min(4, pow2_at_least(ocj, 4)) && n < cap; jn <<= 1) {
+            for (int pw = nchw ? 2 : 1; pw <= 4 && n < cap; pw <<= 1) {
+                const int tcs[7] = {p.OW, ow4, 16, 32, 48, 64, 80};
+                for (int i = 0; i < 7 && n < cap; ++i) {
+                    const int tc = tcs[i];
+                    bool dup = false;
+                    for (int k = 0; k < i; ++k) dup = dup || tcs[k] == tc;
+                    if (dup || tc > ow4 || (tc > p.OW && tc != ow4) || (tc < p.OW && tc > 64 * pw)) continue;
+                    const int TR = std::min(p.OH, 64 * pw / tc);
+                    if (TR < 1) continue;
+                    HaloParams hh{};
+                    hh.c = p;
+                    HaloTile t{jn, pw, 4, TR, tc, CC};
+                    if (!halo_geometry(hh, t, int8)) {
+                        t.np = 8;
+                        if (!halo_geometry(hh, t, int8)) continue;
+                    }
+                    ConvChoice c;
+                    c.kind = 2;
+                    c.jn = jn;
+                    c.pw = pw;
+                    c.tr = TR;
+                    c.tc = tc;
+                    c.cc = CC;
+                    out[n++] = c;
+                }
+            }
+        }
+    }
+    return n;
+}
+
 bool set_conv3x3_halo(int mode, int jn, int pw, int tr, int tc, int cc) {
     if (mode == 0 || mode == 1) {
         g_halo_mode.store(mode);
@@ -183,17 +225,25 @@ hipError_t launch_conv_halo(const ConvParams& p, bool int8, int epi, hipStream_t
     if (!halo_shape_ok(p, int8)) return hipErrorNotSupported;
     // the NCHW input has no other kernel; the tile modes apply to NHWC convs
     const int mode = p.loader == kLoaderNchwF32 ? 0 : g_halo_mode.load(std::memory_order_relaxed);
-    if (mode == 1) return hipErrorNotSupported;
+    if (mode == 1 && p.choice.kind != 2) return hipErrorNotSupported;
     HaloParams h{};
     h.c = p;
     HaloTile t{};
-    if (mode == 2) {
-        const uint64_t f = g_force.load(std::memory_order_relaxed);
-        t.jn = (int)(f & 0xFF);
-        t.pw = (int)((f >> 8) & 0xFF);
-        t.TR = (int)((f >> 16) & 0xFFFF);
-        t.TC = (int)((f >> 32) & 0xFFFF);
-        t.CC = (int)((f >> 48) & 0xFFFF);
+    if (mode == 2 || p.choice.kind == 2) {
+        if (p.choice.kind == 2) {
+            t.jn = p.choice.jn;
+            t.pw = p.choice.pw;
+            t.TR = p.choice.tr;
+            t.TC = p.choice.tc;
+            t.CC = p.choice.cc;
+        } else {
+            const uint64_t f = g_force.load(std::memory_order_relaxed);
+            t.jn = (int)(f & 0xFF);
+            t.pw = (int)((f >> 8) & 0xFF);
+            t.TR = (int)((f >> 16) & 0xFFFF);
+            t.TC = (int)((f >> 32) & 0xFFFF);
+            t.CC = (int)((f >> 48) & 0xFFFF);
+        }
         // a forced tile that does not fit this conv is an error, not a
         // silent fallback (tests rely on the tile being used)
         t.np = 4;

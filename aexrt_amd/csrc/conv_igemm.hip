@@ -94,13 +94,39 @@ ConvTile choose_conv_tile(int M, int OC, int Kp) {
     return ConvTile{jn, 1, true};
 }
 
+int enumerate_conv_choices(const ConvParams& p, bool int8, ConvChoice* out, int cap) {
+    int n = 0;
+    const bool nchw = p.loader == kLoaderNchwF32;
+    if (!nchw && p.Kp / 64 <= igemm::kMaxSteps) {
+        static const ConvTile tiles[] = {{1, 1, false}, {1, 2, false}, {1, 4, false}, {2, 1, false}, {2, 2, false},
+                                         {2, 4, false}, {4, 1, false}, {4, 2, false}, {4, 4, false}, {8, 1, false},
+                                         {8, 2, false}, {1, 1, true},  {2, 1, true},  {4, 1, true},  {8, 1, true}};
+        const int ocj = (p.OCp + 15) / 16;
+        for (const ConvTile& t : tiles) {
+            if (n >= cap) break;
+            if (t.jn > 1 && t.jn / 2 >= ocj) continue;  // a channel tile past every channel
+            if (t.ksw && p.Kp / 64 < 4) continue;
+            ConvChoice c;
+            c.kind = 1;
+            c.jn = t.jn;
+            c.pw = t.pw;
+            c.ksw = t.ksw ? 1 : 0;
+            out[n++] = c;
+        }
+    }
+    if (n < cap) n += enumerate_halo_choices(p, int8, out + n, cap - n);
+    return n;
+}
+
 hipError_t launch_conv_igemm(const ConvParams& p0, bool int8, hipStream_t stream) {
     const bool nchw = p0.loader == kLoaderNchwF32;
     if ((p0.loader != kLoaderNhwc && !nchw) || p0.OC % 4 || p0.C % 8 || p0.Kp % 64 || p0.OCp % 16)
         return hipErrorInvalidValue;
     if (nchw && (int8 || p0.c_real < 1 || p0.c_real > 4 || p0.x_nstride != (int64_t)p0.c_real * p0.H * p0.W))
         return hipErrorInvalidValue;
-    const ConvTile t = choose_conv_tile(p0.M, p0.OC, p0.Kp);
+    const ConvTile t = p0.choice.kind == 1 ? ConvTile{p0.choice.jn, p0.choice.pw, p0.choice.ksw != 0}
+                                           : choose_conv_tile(p0.M, p0.OC, p0.Kp);
+    if (p0.choice.kind == 1 && !tile_instantiated(t)) return hipErrorInvalidValue;
     const bool out_f32 = (p0.flags & kConvOutF32) != 0;
     const int HWi = p0.H * p0.W, HWo = p0.OH * p0.OW;
     // Images per launch: every view a launch touches must stay inside
@@ -150,8 +176,8 @@ hipError_t launch_conv_igemm(const ConvParams& p0, bool int8, hipStream_t stream
         p.fd_ow = make_fastdiv((uint32_t)p.OW);
         p.fd_c = make_fastdiv((uint32_t)p.C);
         p.fd_kw = make_fastdiv((uint32_t)p.KW);
-        hipError_t e = launch_conv_halo(p, int8, epi, stream);
-        if (e == hipErrorNotSupported && !nchw) e = launch_variant(int8, mc, epi, p, t, stream);
+        hipError_t e = p.choice.kind == 1 ? hipErrorNotSupported : launch_conv_halo(p, int8, epi, stream);
+        if (e == hipErrorNotSupported && !nchw && p.choice.kind != 2) e = launch_variant(int8, mc, epi, p, t, stream);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

@@ -45,6 +45,15 @@ enum Loader : int {
     kLoaderNchwF32 = 1,  // fp32 NCHW network input, c_real <= 4 channels read as C = 8 (zero padded)
 };
 
+// Kernel and tile of one conv launch.  kind 0: chosen by the heuristics;
+// 1: implicit GEMM with tile (jn, pw, ksw); 2: halo-tile 3x3 with (jn, pw)
+// and tr x tc positions, cc channels per chunk.
+struct ConvChoice {
+    int kind = 0;
+    int jn = 0, pw = 0, ksw = 0;
+    int tr = 0, tc = 0, cc = 0;
+};
+
 // One convolution launch.  Activation views address element (n, h, w, c) at
 // n*nstride + (h*W + w)*cstride + c relative to their data pointer.
 struct ConvParams {
@@ -68,6 +77,7 @@ struct ConvParams {
     int32_t* acc_out;         // optional int32 accumulators [M][OC] (int8)
     int N, H, W, C, OH, OW, OC, KH, KW, S, P;
     int c_real = 0;           // kLoaderNchwF32: channels present in memory (x_nstride = c_real*H*W)
+    ConvChoice choice{};      // kernel / tile (kind 0: heuristics)
     int K, M;
     int flags;
     // filled in by the igemm launcher
@@ -95,6 +105,10 @@ bool set_conv_tile_override(int jn, int pw, int ksw);
 // Implicit-GEMM conv (int8 or fp16 MFMA).  Requires C % 8 == 0, OC % 4 == 0,
 // Kp % 64 == 0, OCp % 16 == 0 and 16-byte aligned views.
 hipError_t launch_conv_igemm(const ConvParams& p, bool int8, hipStream_t stream);
+// Every kernel/tile choice that can run conv p (implicit-GEMM tiles, and
+// halo tiles for 3x3 convs), at most cap; returns the count.
+int enumerate_conv_choices(const ConvParams& p, bool int8, ConvChoice* out, int cap);
+int enumerate_halo_choices(const ConvParams& p, bool int8, ConvChoice* out, int cap);
 // Halo-tile 3x3 conv (pad 1, stride 1/2, C % 16 == 0) on one batch slice whose
 // views fit 32-bit offsets: the input window of each position tile is staged
 // (and quantized) once in LDS.  epi: 0 any flags, 1 SiLU -> fp16, 2 int8

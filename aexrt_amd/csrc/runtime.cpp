@@ -25,6 +25,7 @@
 #include <cstring>
 #include <fstream>
 #include <functional>
+#include <map>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -133,6 +134,8 @@ struct AexrtYoloModel {
     float* input_host = nullptr;
     bool input_needs_nhwc = false;
     bool input_nchw_direct = false;  // the input's convs read the fp32 NCHW tensor themselves
+    bool autotune = true;            // measure every conv's kernel/tile choices at load
+    std::map<std::string, ConvChoice> tuned;  // conv shape -> measured choice
     hipStream_t stream = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
@@ -665,6 +668,65 @@ std::string conv_label(const EngineCommand& c, size_t ci, uint32_t alg) {
     return buf;
 }
 
+// ---- plan-time kernel choice ---------------------------------------------------
+// The reference's kernel plan records, per conv, the kernel its autotuner
+// measured fastest on the reference's GPU.  Here every conv gets the
+// implicit-GEMM or halo tile measured fastest on this one: each candidate runs
+// once to warm up, then kTuneReps times between two events on the model stream,
+// on the conv's own buffers (the first real run overwrites what they leave,
+// and clears the amax slots at its start).  Convs of one shape share the
+// result.  AEXRT_HIP_AUTOTUNE=0 keeps the heuristic choice.
+constexpr int kTuneReps = 4;
+
+std::string tune_key(const ConvParams& p, bool int8) {
+    char buf[256];
+    std::snprintf(buf, sizeof(buf), "%d|%d|%d|%d,%d,%d,%d|%d,%d,%d,%d,%d|%d,%d|%lld,%d,%lld,%d|%d,%d|%u", int8 ? 1 : 0,
+                  p.flags, p.loader, p.N, p.H, p.W, p.C, p.OC, p.KH, p.KW, p.S, p.P, p.OH, p.OW,
+                  (long long)p.x_nstride, p.x_cstride, (long long)p.y_nstride, p.y_cstride, p.res ? 1 : 0,
+                  p.acc_out ? 1 : 0, p.x_slots.stripes);
+    return buf;
+}
+
+bool tune_conv(AexrtYoloModel* m, ConvParams& p, bool int8) {
+    const std::string key = tune_key(p, int8);
+    auto it = m->tuned.find(key);
+    if (it != m->tuned.end()) {
+        p.choice = it->second;
+        return true;
+    }
+    ConvChoice cand[128];
+    const int n = enumerate_conv_choices(p, int8, cand, 128);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (!check_hip(hipEventCreate(&e0), "tune event") || !check_hip(hipEventCreate(&e1), "tune event")) {
+        if (e0) (void)hipEventDestroy(e0);
+        return fail(m, last_error());
+    }
+    ConvChoice best{};
+    float best_ms = 0.0f;
+    bool ok = true;
+    for (int i = 0; i < n && ok; ++i) {
+        ConvParams q = p;
+        q.choice = cand[i];
+        if (launch_conv_igemm(q, int8, m->stream) != hipSuccess) continue;  // rejected on the host
+        ok = check_hip(hipEventRecord(e0, m->stream), "tune record");
+        for (int r = 0; r < kTuneReps && ok; ++r) ok = check_hip(launch_conv_igemm(q, int8, m->stream), "tune launch");
+        ok = ok && check_hip(hipEventRecord(e1, m->stream), "tune record") &&
+             check_hip(hipEventSynchronize(e1), "tune sync");
+        float ms = 0.0f;
+        ok = ok && check_hip(hipEventElapsedTime(&ms, e0, e1), "tune elapsed");
+        if (ok && (best.kind == 0 || ms < best_ms)) {
+            best = cand[i];
+            best_ms = ms;
+        }
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (!ok) return fail(m, last_error());
+    m->tuned[key] = best;
+    p.choice = best;
+    return true;
+}
+
 bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
     Engine& e = m->eng;
     auto& V = m->vals;
@@ -727,6 +789,8 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                                        cs.fused_residual ? &rvw : nullptr, yvw, nullptr, p, why))
                     return fail(m, "command " + std::to_string(ci) + ": " + why);
                 const uint32_t alg = cs.algorithm;
+                if (m->autotune && !is_winograd_algorithm(alg) && !tune_conv(m, p, is_int8_algorithm(alg)))
+                    return false;
                 m->steps.push_back(Step{(int)ci, conv_label(c, ci, alg), [p, alg](hipStream_t s) {
                                             if (is_winograd_algorithm(alg)) return launch_winograd_f2x2(p, s);
                                             return launch_conv_igemm(p, is_int8_algorithm(alg), s);
@@ -902,9 +966,11 @@ bool build_model(AexrtYoloModel* m) {
         m->input_host = nullptr;
     for (size_t ci = 0; ci < e.commands.size(); ++ci)
         if (m->convs[ci].is_conv && !prepare_conv_weights(m, ci)) return false;
-    if (!build_steps(m, m->copies)) return false;
     if (!check_hip(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking), "stream create"))
         return fail(m, last_error());
+    const char* tune = std::getenv("AEXRT_HIP_AUTOTUNE");
+    m->autotune = !(tune && tune[0] == '0');
+    if (!build_steps(m, m->copies)) return false;
     const char* prof = std::getenv("AEXRT_HIP_PROFILE");
     m->profile = prof && prof[0] == '1';
     m->executable = true;
