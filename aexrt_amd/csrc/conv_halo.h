@@ -16,7 +16,8 @@
 // whole 64-k steps with zero weights; the block's weights for all chunks
 // are gathered from the [OCp][Kp] (k = tap * C + c) layout into LDS once
 // and stay resident while the block walks its run of position tiles.  The
-// 4 waves of a block share the oc tile (JN 16-channel subtiles) and split
+// NW (4 or 8) waves of a block share the oc tile (JN 16-channel subtiles) and
+// its weights in LDS (8 waves halve the LDS per wave for more waves per CU), and split
 // the position tile (PW 16-position subtiles each).  The input of the next
 // (tile, chunk) is loaded into registers while the current one is computed;
 // two LDS tile buffers need one barrier per chunk.
@@ -55,7 +56,7 @@ struct HaloParams {
 // Largest k-step count of one chunk (table of tap offsets).
 constexpr int kHaloMaxSpc = 32;
 // 16-byte weight pieces per thread: the block's weights are at most
-// 256 * kHaloWeightRounds * 16 bytes (64 KB).
+// 256 * kHaloWeightRounds * 16 bytes (64 KB) with 4 waves.
 constexpr int kHaloWeightRounds = 16;
 
 namespace halo {
@@ -69,8 +70,9 @@ using igemm::rsrc_t;
 using igemm::v2i;
 using igemm::xcd_remap;
 
-template <bool INT8, int JN, int PW, int NP, int EPI, bool NCHW = false>
-__global__ __launch_bounds__(256) void conv3x3_halo_kernel(HaloParams h) {
+template <bool INT8, int JN, int PW, int NP, int EPI, bool NCHW = false, int NW = 4>
+__global__ __launch_bounds__(NW * 64) void conv3x3_halo_kernel(HaloParams h) {
+    constexpr int NT = NW * 64;  // threads of the block
     const ConvParams& p = h.c;
     constexpr int WQ = Frag<INT8>::wq;   // MFMAs (and weight pieces) per 64-k step
     constexpr int ESZ = Frag<INT8>::esz;
@@ -136,10 +138,10 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(HaloParams h) {
     };
     v4i wst[kHaloWeightRounds];
 #pragma unroll
-    for (int r = 0; r < kHaloWeightRounds; ++r) wst[r] = wload(tid + r * 256);
+    for (int r = 0; r < kHaloWeightRounds; ++r) wst[r] = wload(tid + r * NT);
 
     // ---- input windows -----------------------------------------------------
-    // Piece k of this thread: e = tid + k * 256 -> window pixel (ir, ic) and
+    // Piece k of this thread: e = tid + k * NT -> window pixel (ir, ic) and
     // 8-channel group; the LDS place is e * PIECE.  Pieces past the window get
     // a row that fails every bounds test.
     // NCHW pieces: e -> channel c, window row ir, column quad q4 (columns
@@ -148,7 +150,7 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(HaloParams h) {
     int prc[NP], prel[NP];
 #pragma unroll
     for (int k = 0; k < NP; ++k) {
-        const int e = tid + k * 256;
+        const int e = tid + k * NT;
         if constexpr (NCHW) {
             const int c = (int)fdiv((uint32_t)e, h.fd_rq);
             const int rem = e - c * h.IR * h.icol4;
@@ -223,7 +225,7 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(HaloParams h) {
         __builtin_amdgcn_raw_buffer_store_b64(v2i{0, 0}, ry, kOob, 0, 0);
 
     // ---- tables (ALU only while the loads are in flight) -------------------
-    for (int e = tid; e < h.spc * 4 * WQ; e += 256) {
+    for (int e = tid; e < h.spc * 4 * WQ; e += NT) {
         // e = (s * 4 + grp) * WQ + hh -> chunk-local k = (s * 4 + grp) * 16 + hh * 8
         const int kk = (e / WQ) * 16 + (e - (e / WQ) * WQ) * 8;
         const int tap = (int)fdiv((uint32_t)kk, h.fd_cc);
@@ -256,12 +258,12 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(HaloParams h) {
     }
 #pragma unroll
     for (int r = 0; r < kHaloWeightRounds; ++r) {
-        const int e = tid + r * 256;
+        const int e = tid + r * NT;
         if (e < wpieces) *reinterpret_cast<v4i*>(lds + e * 16) = wst[r];
     }
     if constexpr (NCHW) {
         // the padding channels of the window pixels are never written
-        for (int e = tid; e < (2 * h.tbytes) >> 4; e += 256)
+        for (int e = tid; e < (2 * h.tbytes) >> 4; e += NT)
             *reinterpret_cast<v4i*>(lds + h.wbytes + e * 16) = v4i{0, 0, 0, 0};
         __syncthreads();  // zeros land before any thread's first window stores
     }
@@ -303,7 +305,7 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(HaloParams h) {
         // this iteration's window -> LDS (int8: quantized once here)
 #pragma unroll
         for (int k = 0; k < NP; ++k) {
-            const int e = tid + k * 256;
+            const int e = tid + k * NT;
             if (e < h.npieces) {
                 if constexpr (INT8) {
                     *reinterpret_cast<v2i*>(tb + e * PIECE) = quant8(pf[k], s_q);
@@ -457,11 +459,11 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(HaloParams h) {
 }
 
 // Blocks of one instance the GPU holds at once with lds_bytes of dynamic LDS.
-template <bool INT8, int JN, int PW, int NP, int EPI, bool NCHW>
+template <bool INT8, int JN, int PW, int NP, int EPI, bool NCHW, int NW>
 int halo_resident_blocks(int lds_bytes) {
     int per_cu = 0, cus = 0, dev = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv3x3_halo_kernel<INT8, JN, PW, NP, EPI, NCHW>, 256,
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv3x3_halo_kernel<INT8, JN, PW, NP, EPI, NCHW, NW>, NW * 64,
                                                      (size_t)lds_bytes) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu < 1 ||
         cus < 1)
@@ -471,26 +473,26 @@ int halo_resident_blocks(int lds_bytes) {
 
 // Persistent grid: every resident block slot gets one contiguous run of
 // position tiles of one oc tile.
-template <bool INT8, int JN, int PW, int NP, int EPI, bool NCHW = false>
+template <bool INT8, int JN, int PW, int NP, int EPI, bool NCHW = false, int NW = 4>
 hipError_t halo_launch_cfg(HaloParams h, hipStream_t stream) {
     const int lds_bytes = h.wbytes + 2 * h.tbytes;
-    const int cap = halo_resident_blocks<INT8, JN, PW, NP, EPI, NCHW>(lds_bytes);
+    const int cap = halo_resident_blocks<INT8, JN, PW, NP, EPI, NCHW, NW>(lds_bytes);
     int groups = h.ntile;
     if ((int64_t)h.ntile * h.c.ntn > cap) groups = std::max(1, cap / h.c.ntn);
     h.c.per = (h.ntile + groups - 1) / groups;
     groups = (h.ntile + h.c.per - 1) / h.c.per;
     const int64_t blocks = (int64_t)groups * h.c.ntn;
     if (blocks > INT32_MAX) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((conv3x3_halo_kernel<INT8, JN, PW, NP, EPI, NCHW>), dim3((unsigned)blocks), dim3(256),
+    hipLaunchKernelGGL((conv3x3_halo_kernel<INT8, JN, PW, NP, EPI, NCHW, NW>), dim3((unsigned)blocks), dim3(NW * 64),
                        (size_t)lds_bytes, stream, h);
     return hipGetLastError();
 }
 
-// Every (JN, PW, NP) of one (INT8, EPI) family.
+// Every (JN, PW, NP, NW) of one (INT8, EPI) family.
 template <bool INT8, int EPI>
-hipError_t halo_launch_family(const HaloParams& h, int jn, int pw, int np, hipStream_t stream) {
+hipError_t halo_launch_family(const HaloParams& h, int jn, int pw, int np, int nw, hipStream_t stream) {
 #define AEXRT_HALO_CASE(J, P, N) \
-    if (jn == J && pw == P && np == N) return halo_launch_cfg<INT8, J, P, N, EPI>(h, stream);
+    if (nw == 4 && jn == J && pw == P && np == N) return halo_launch_cfg<INT8, J, P, N, EPI, false, 4>(h, stream);
     AEXRT_HALO_CASE(1, 1, 4) AEXRT_HALO_CASE(1, 2, 4) AEXRT_HALO_CASE(1, 4, 4)
     AEXRT_HALO_CASE(2, 1, 4) AEXRT_HALO_CASE(2, 2, 4) AEXRT_HALO_CASE(2, 4, 4)
     AEXRT_HALO_CASE(4, 1, 4) AEXRT_HALO_CASE(4, 2, 4) AEXRT_HALO_CASE(4, 4, 4)
@@ -498,6 +500,13 @@ hipError_t halo_launch_family(const HaloParams& h, int jn, int pw, int np, hipSt
     AEXRT_HALO_CASE(2, 1, 8) AEXRT_HALO_CASE(2, 2, 8) AEXRT_HALO_CASE(2, 4, 8)
     AEXRT_HALO_CASE(4, 1, 8) AEXRT_HALO_CASE(4, 2, 8) AEXRT_HALO_CASE(4, 4, 8)
 #undef AEXRT_HALO_CASE
+    // 8 waves: the block's weights shared by twice the positions
+#define AEXRT_HALO_CASE8(J, P, N) \
+    if (nw == 8 && jn == J && pw == P && np == N) return halo_launch_cfg<INT8, J, P, N, EPI, false, 8>(h, stream);
+    AEXRT_HALO_CASE8(1, 1, 4) AEXRT_HALO_CASE8(1, 2, 4) AEXRT_HALO_CASE8(2, 1, 4) AEXRT_HALO_CASE8(2, 2, 4)
+    AEXRT_HALO_CASE8(4, 1, 4) AEXRT_HALO_CASE8(4, 2, 4) AEXRT_HALO_CASE8(1, 1, 8) AEXRT_HALO_CASE8(1, 2, 8)
+    AEXRT_HALO_CASE8(2, 1, 8) AEXRT_HALO_CASE8(2, 2, 8) AEXRT_HALO_CASE8(4, 1, 8) AEXRT_HALO_CASE8(4, 2, 8)
+#undef AEXRT_HALO_CASE8
     return hipErrorInvalidValue;
 }
 
@@ -506,9 +515,9 @@ hipError_t halo_launch_nchw(const HaloParams& h, int jn, int pw, int np, hipStre
 
 #define AEXRT_HALO_FAMILIES(X) X(true, 0) X(true, 1) X(true, 2) X(false, 0) X(false, 1)
 #define AEXRT_HALO_EXTERN(I, E) \
-    extern template hipError_t halo_launch_family<I, E>(const HaloParams&, int, int, int, hipStream_t);
+    extern template hipError_t halo_launch_family<I, E>(const HaloParams&, int, int, int, int, hipStream_t);
 #define AEXRT_HALO_INSTANCE(I, E) \
-    template hipError_t halo_launch_family<I, E>(const HaloParams&, int, int, int, hipStream_t);
+    template hipError_t halo_launch_family<I, E>(const HaloParams&, int, int, int, int, hipStream_t);
 
 }  // namespace halo
 }  // namespace aexrt

@@ -17,11 +17,14 @@ namespace {
 // 0: automatic; 1: never (implicit GEMM only); 2: forced tile (g_force).
 std::atomic<int> g_halo_mode{0};
 std::atomic<uint64_t> g_force{0};  // jn | pw << 8 | tr << 16 | tc << 32 | cc << 48 (8/8/16/16/16 bits)
+std::atomic<int> g_force_nw{4};     // waves per block of the forced tile
 
-constexpr int kLdsBudget = 65536 - 2048;  // dynamic LDS of one block (static tables aside)
+// dynamic LDS of one block (static tables aside): two blocks fit a CU's 160 KB
+constexpr int kLdsBudget = 80 * 1024 - 2048;
 
 struct HaloTile {
     int jn, pw, np, TR, TC, CC;
+    int nw = 4;  // waves per block
 };
 
 int pow2_at_least(int v, int cap) {
@@ -38,7 +41,7 @@ bool halo_geometry(HaloParams& h, const HaloTile& t, bool int8) {
     // int8: a 16-k MFMA operand piece is 16 channels of one tap; fp16: 8
     if (t.CC < (int8 ? 16 : 8) || t.CC % (int8 ? 16 : 8) || p.C % t.CC || t.TR < 1 || t.TC < 1) return false;
     if (p.loader == kLoaderNchwF32 && t.CC != p.C) return false;
-    if (t.TR * t.TC > 64 * t.pw) return false;
+    if (t.TR * t.TC > 16 * t.nw * t.pw) return false;
     h.TR = t.TR;
     h.TC = t.TC;
     h.IR = (t.TR - 1) * p.S + 3;
@@ -57,7 +60,7 @@ bool halo_geometry(HaloParams& h, const HaloTile& t, bool int8) {
         h.fd_icol4 = make_fastdiv((uint32_t)h.icol4);
         h.fd_rq = make_fastdiv((uint32_t)(h.IR * h.icol4));
     }
-    if (h.npieces > 256 * t.np) return false;
+    if (h.npieces > 64 * t.nw * t.np) return false;
     h.ntc = (p.OW + t.TC - 1) / t.TC;
     h.tpi = ((p.OH + t.TR - 1) / t.TR) * h.ntc;
     const int64_t ntile = (int64_t)p.N * h.tpi;
@@ -65,7 +68,7 @@ bool halo_geometry(HaloParams& h, const HaloTile& t, bool int8) {
     h.ntile = (int)ntile;
     h.wbytes = h.nch * h.spc * wq * t.jn * 16 * 64;
     h.tbytes = ((p.loader == kLoaderNchwF32 ? h.IR * h.ICOL : h.npieces) * 8 * esz + 15) & ~15;
-    if (h.wbytes + 2 * h.tbytes > kLdsBudget || h.wbytes > 256 * kHaloWeightRounds * 16) return false;
+    if (h.wbytes + 2 * h.tbytes > kLdsBudget || h.wbytes > 64 * t.nw * kHaloWeightRounds * 16) return false;
     h.c.ntn = (p.OCp / 16 + t.jn - 1) / t.jn;
     h.fd_cc8 = make_fastdiv((uint32_t)(t.CC / 8));
     h.fd_icol = make_fastdiv((uint32_t)h.ICOL);
@@ -133,7 +136,7 @@ bool choose_halo_tile(HaloParams& h, bool int8, HaloTile& best) {
                         const HaloTile t{jn, pw, np, TR, tc, CC};
                         HaloParams hh = h;
                         if (!halo_geometry(hh, t, int8)) continue;
-                        if (np == 8 && hh.npieces <= 4 * 256) continue;
+                        if (np == 8 && hh.npieces <= 4 * 64 * t.nw) continue;
                         const double c = halo_cost(hh, t, int8);
                         if (!found || c < best_cost) {
                             best_cost = c;
@@ -152,12 +155,12 @@ hipError_t halo_launch(const HaloParams& h, bool int8, int epi, const HaloTile& 
     using halo::halo_launch_family;
     if (h.c.loader == kLoaderNchwF32) return halo::halo_launch_nchw(h, t.jn, t.pw, t.np, s);
     if (int8) {
-        if (epi == 1) return halo_launch_family<true, 1>(h, t.jn, t.pw, t.np, s);
-        if (epi == 2) return halo_launch_family<true, 2>(h, t.jn, t.pw, t.np, s);
-        return halo_launch_family<true, 0>(h, t.jn, t.pw, t.np, s);
+        if (epi == 1) return halo_launch_family<true, 1>(h, t.jn, t.pw, t.np, t.nw, s);
+        if (epi == 2) return halo_launch_family<true, 2>(h, t.jn, t.pw, t.np, t.nw, s);
+        return halo_launch_family<true, 0>(h, t.jn, t.pw, t.np, t.nw, s);
     }
-    if (epi == 1) return halo_launch_family<false, 1>(h, t.jn, t.pw, t.np, s);
-    return halo_launch_family<false, 0>(h, t.jn, t.pw, t.np, s);
+    if (epi == 1) return halo_launch_family<false, 1>(h, t.jn, t.pw, t.np, t.nw, s);
+    return halo_launch_family<false, 0>(h, t.jn, t.pw, t.np, t.nw, s);
 }
 
 }  // namespace
@@ -172,19 +175,21 @@ int enumerate_halo_choices(const ConvParams& p, bool int8, ConvChoice* out, int 
         if (p.C % div) break;
         const int CC = p.C / div;
         if (CC % (int8 ? 16 : 8) || CC > (int8 ? 128 : 64)) continue;
+        for (int nw = 4; nw <= (nchw ? 4 : 8) && n < cap; nw <<= 1)
         for (int jn = 1; jn <= std::min(4, pow2_at_least(ocj, 4)) && n < cap; jn <<= 1) {
-            for (int pw = nchw ? 2 : 1; pw <= 4 && n < cap; pw <<= 1) {
+            for (int pw = nchw ? 2 : 1; pw <= (nw == 8 ? 2 : 4) && n < cap; pw <<= 1) {
+                const int npos = 16 * nw * pw;  // positions of a tile
                 const int tcs[7] = {p.OW, ow4, 16, 32, 48, 64, 80};
                 for (int i = 0; i < 7 && n < cap; ++i) {
                     const int tc = tcs[i];
                     bool dup = false;
                     for (int k = 0; k < i; ++k) dup = dup || tcs[k] == tc;
-                    if (dup || tc > ow4 || (tc > p.OW && tc != ow4) || (tc < p.OW && tc > 64 * pw)) continue;
-                    const int TR = std::min(p.OH, 64 * pw / tc);
+                    if (dup || tc > ow4 || (tc > p.OW && tc != ow4) || (tc < p.OW && tc > npos)) continue;
+                    const int TR = std::min(p.OH, npos / tc);
                     if (TR < 1) continue;
                     HaloParams hh{};
                     hh.c = p;
-                    HaloTile t{jn, pw, 4, TR, tc, CC};
+                    HaloTile t{jn, pw, 4, TR, tc, CC, nw};
                     if (!halo_geometry(hh, t, int8)) {
                         t.np = 8;
                         if (!halo_geometry(hh, t, int8)) continue;
@@ -196,6 +201,7 @@ int enumerate_halo_choices(const ConvParams& p, bool int8, ConvChoice* out, int 
                     c.tr = TR;
                     c.tc = tc;
                     c.cc = CC;
+                    c.nw = nw;
                     out[n++] = c;
                 }
             }
@@ -209,11 +215,13 @@ bool set_conv3x3_halo(int mode, int jn, int pw, int tr, int tc, int cc) {
         g_halo_mode.store(mode);
         return true;
     }
-    if (mode != 2 || !(jn == 1 || jn == 2 || jn == 4) || !(pw == 1 || pw == 2 || pw == 4) || tr < 1 ||
-        tr > 0xFFFF || tc < 1 || tc > 0xFFFF || cc < 16 || cc > 0xFFFF)
+    // mode 2: 4 waves per block, mode 3: 8 waves (pw 1 or 2)
+    if ((mode != 2 && mode != 3) || !(jn == 1 || jn == 2 || jn == 4) || !(pw == 1 || pw == 2 || pw == 4) ||
+        (mode == 3 && pw == 4) || tr < 1 || tr > 0xFFFF || tc < 1 || tc > 0xFFFF || cc < 8 || cc > 0xFFFF)
         return false;
     g_force.store((uint64_t)jn | ((uint64_t)pw << 8) | ((uint64_t)tr << 16) | ((uint64_t)tc << 32) |
                   ((uint64_t)cc << 48));
+    g_force_nw.store(mode == 3 ? 8 : 4);
     g_halo_mode.store(2);
     return true;
 }
@@ -236,6 +244,7 @@ hipError_t launch_conv_halo(const ConvParams& p, bool int8, int epi, hipStream_t
             t.TR = p.choice.tr;
             t.TC = p.choice.tc;
             t.CC = p.choice.cc;
+            t.nw = p.choice.nw;
         } else {
             const uint64_t f = g_force.load(std::memory_order_relaxed);
             t.jn = (int)(f & 0xFF);
@@ -243,6 +252,7 @@ hipError_t launch_conv_halo(const ConvParams& p, bool int8, int epi, hipStream_t
             t.TR = (int)((f >> 16) & 0xFFFF);
             t.TC = (int)((f >> 32) & 0xFFFF);
             t.CC = (int)((f >> 48) & 0xFFFF);
+            t.nw = g_force_nw.load(std::memory_order_relaxed);
         }
         // a forced tile that does not fit this conv is an error, not a
         // silent fallback (tests rely on the tile being used)

@@ -46,12 +46,13 @@ enum Loader : int {
 };
 
 // Kernel and tile of one conv launch.  kind 0: chosen by the heuristics;
-// 1: implicit GEMM with tile (jn, pw, ksw); 2: halo-tile 3x3 with (jn, pw)
-// and tr x tc positions, cc channels per chunk.
+// 1: implicit GEMM with tile (jn, pw, ksw); 2: halo-tile 3x3 with (jn, pw),
+// tr x tc positions, cc channels per chunk and nw waves per block.
 struct ConvChoice {
     int kind = 0;
     int jn = 0, pw = 0, ksw = 0;
     int tr = 0, tc = 0, cc = 0;
+    int nw = 4;  // halo: waves per block (4 or 8)
 };
 
 // One convolution launch.  Activation views address element (n, h, w, c) at

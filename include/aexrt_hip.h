@@ -180,10 +180,12 @@ int aexrt_hip_set_conv_tile(int32_t jn, int32_t pw, int32_t ksw);
 /* Tuning/test hook, no reference counterpart: 3x3 pad-1 convs with C % 16 == 0
  * run on the halo-tile kernel (input window staged and quantized once in LDS).
  * mode 0 = automatic tile, 1 = never (implicit GEMM for every conv), 2 = force
- * the tile: jn 16-channel subtiles (1/2/4), pw 16-position subtiles per wave
- * (1/2/4), tr x tc output positions (tr * tc <= 64 * pw), cc input channels per
- * LDS chunk (C % cc == 0, cc % 16 == 0); a 3x3 conv that the forced tile
- * does not fit (LDS, channel chunk) then fails.  Returns 0 for a bad request. */
+ * the tile with 4 waves per block, 3 = with 8 waves (pw 1 or 2): jn 16-channel
+ * subtiles (1/2/4), pw 16-position subtiles per wave (1/2/4), tr x tc output
+ * positions (tr * tc <= 16 * waves * pw), cc input channels per LDS chunk
+ * (C % cc == 0; cc % 16 == 0 for int8, % 8 for fp16); a 3x3 conv that the
+ * forced tile does not fit (LDS, channel chunk) then fails.  Returns 0 for a
+ * bad request. */
 int aexrt_hip_set_conv3x3_halo(int32_t mode, int32_t jn, int32_t pw, int32_t tr, int32_t tc, int32_t cc);
 
 /* Glue ops of the replay stream on NHWC fp16 views. */

@@ -386,27 +386,29 @@ def test_conv_every_tile(cuda, jn, pw, ksw):
         K.set_conv3x3_halo(K.HALO_AUTO)
 
 
-def _halo_fits(c, h, w, s, jn, pw, tr, tc, cc, int8):
+def _halo_fits(c, h, w, s, jn, pw, tr, tc, cc, int8, nw=4):
     """Whether a forced halo tile fits a conv: the kernel's LDS holds the
     block's weights (C/cc chunks of ceil(9cc/64) 64-k steps, jn*16 channels)
     and two input windows ((tr-1)s+3 x (tc-1)s+3 pixels x cc channels)."""
     esz = 1 if int8 else 2
-    if cc % 16 or c % cc or tr * tc > 64 * pw:
+    if cc % (16 if int8 else 8) or c % cc or tr * tc > 16 * nw * pw:
         return False
     spc = (9 * cc + 63) // 64
     npieces = ((tr - 1) * s + 3) * ((tc - 1) * s + 3) * cc // 8
     wbytes = (c // cc) * spc * esz * jn * 16 * 64
     tbytes = (npieces * 8 * esz + 15) // 16 * 16
-    return npieces <= 8 * 256 and wbytes + 2 * tbytes <= 65536 - 2048
+    return npieces <= 8 * 64 * nw and wbytes + 2 * tbytes <= 80 * 1024 - 2048
 
 
-# Halo-tile kernel tiles: (jn, pw, tile columns (0 = whole output row), channel chunk divisor)
-HALO_TILES = [(1, 1, 16, 1), (1, 2, 0, 1), (1, 4, 16, 2), (2, 1, 0, 2), (2, 2, 16, 1), (2, 4, 0, 2),
-              (4, 1, 16, 1), (4, 2, 0, 2), (4, 4, 16, 2), (4, 4, 0, 1)]
+# Halo-tile kernel tiles: (jn, pw, tile columns (0 = whole output row), channel chunk divisor, waves)
+HALO_TILES = [(1, 1, 16, 1, 4), (1, 2, 0, 1, 4), (1, 4, 16, 2, 4), (2, 1, 0, 2, 4), (2, 2, 16, 1, 4),
+              (2, 4, 0, 2, 4), (4, 1, 16, 1, 4), (4, 2, 0, 2, 4), (4, 4, 16, 2, 4), (4, 4, 0, 1, 4),
+              (1, 1, 16, 1, 8), (2, 2, 0, 2, 8), (4, 1, 0, 1, 8), (4, 2, 16, 2, 8)]
 
 
-@pytest.mark.parametrize("jn,pw,tc,ccd", HALO_TILES, ids=[f"jn{t[0]}_pw{t[1]}_tc{t[2]}_cc{t[3]}" for t in HALO_TILES])
-def test_halo_every_tile(cuda, jn, pw, tc, ccd):
+@pytest.mark.parametrize("jn,pw,tc,ccd,nw", HALO_TILES,
+                         ids=[f"jn{t[0]}_pw{t[1]}_tc{t[2]}_cc{t[3]}_w{t[4]}" for t in HALO_TILES])
+def test_halo_every_tile(cuda, jn, pw, tc, ccd, nw):
     """The halo-tile 3x3 kernel on forced tiles: ragged row/column tiles,
     several channel chunks, stride 2, fp32 output, SiLU + residual, fp16."""
     ran = 0
@@ -415,10 +417,10 @@ def test_halo_every_tile(cuda, jn, pw, tc, ccd):
         nonlocal ran
         oh, ow = (h - 1) // s + 1, (w - 1) // s + 1
         cols = ow if tc == 0 else tc
-        rows = max(1, min(oh, 64 * pw // cols))
+        rows = max(1, min(oh, 16 * nw * pw // cols))
         cc = c // ccd
-        K.set_conv3x3_halo(K.HALO_FORCE, jn, pw, rows, cols, max(cc, 16))
-        fits = cc >= 16 and _halo_fits(c, h, w, s, jn, pw, rows, cols, cc, int8)
+        K.set_conv3x3_halo(K.HALO_FORCE if nw == 4 else K.HALO_FORCE8, jn, pw, rows, cols, max(cc, 16))
+        fits = cc >= 16 and _halo_fits(c, h, w, s, jn, pw, rows, cols, cc, int8, nw)
         ran += fits
         return fits
 
