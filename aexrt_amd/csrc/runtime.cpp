@@ -135,6 +135,7 @@ struct AexrtYoloModel {
     bool input_needs_nhwc = false;
     bool input_nchw_direct = false;  // the input's convs read the fp32 NCHW tensor themselves
     bool autotune = true;            // measure every conv's kernel/tile choices at load
+    bool tune_log = false;           // print each measured choice (AEXRT_HIP_TUNE_LOG=1)
     std::map<std::string, ConvChoice> tuned;  // conv shape -> measured choice
     hipStream_t stream = nullptr;
     hipGraph_t graph = nullptr;
@@ -724,6 +725,10 @@ bool tune_conv(AexrtYoloModel* m, ConvParams& p, bool int8) {
     if (!ok) return fail(m, last_error());
     m->tuned[key] = best;
     p.choice = best;
+    if (m->tune_log)
+        std::fprintf(stderr, "aexrt tune %s: kind %d jn %d pw %d ksw %d tr %d tc %d cc %d nw %d  %.2f us (%d candidates)\n",
+                     key.c_str(), best.kind, best.jn, best.pw, best.ksw, best.tr, best.tc, best.cc, best.nw,
+                     best_ms * 1000.0f / kTuneReps, n);
     return true;
 }
 
@@ -970,6 +975,8 @@ bool build_model(AexrtYoloModel* m) {
         return fail(m, last_error());
     const char* tune = std::getenv("AEXRT_HIP_AUTOTUNE");
     m->autotune = !(tune && tune[0] == '0');
+    const char* tlog = std::getenv("AEXRT_HIP_TUNE_LOG");
+    m->tune_log = tlog && tlog[0] == '1';
     if (!build_steps(m, m->copies)) return false;
     const char* prof = std::getenv("AEXRT_HIP_PROFILE");
     m->profile = prof && prof[0] == '1';
