@@ -89,7 +89,17 @@ struct Step {
     int cmd = -1;
     std::string label;
     std::function<hipError_t(hipStream_t)> launch;
+    // memory roots the step reads / writes (all: every root and the slots)
+    std::vector<int> reads, writes;
+    bool all = false;
+    // schedule: earlier steps it must follow, and its stream lane
+    std::vector<int> deps;
+    int lane = 0;
+    bool signal = false;  // a later step on another lane waits for this one
 };
+
+// Streams a captured graph spreads independent steps over.
+constexpr int kLanes = 4;
 
 // A CONCAT input that could not be placed inside its concat: copied there.
 struct CopyJob {
@@ -137,6 +147,10 @@ struct AexrtYoloModel {
     bool autotune = true;            // measure every conv's kernel/tile choices at load
     bool tune_log = false;           // print each measured choice (AEXRT_HIP_TUNE_LOG=1)
     std::map<std::string, ConvChoice> tuned;  // conv shape -> measured choice
+    hipStream_t lane_stream[kLanes] = {};      // capture-time streams of lanes 1..kLanes-1
+    int n_lanes = 1;                           // lanes the schedule uses (measured at load)
+    std::vector<hipEvent_t> step_events;      // per step, recorded when a step signals
+    std::vector<hipEvent_t> lane_events;      // fork / join events of the captures
     hipStream_t stream = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
@@ -732,6 +746,57 @@ bool tune_conv(AexrtYoloModel* m, ConvParams& p, bool int8) {
     return true;
 }
 
+// ---- multi-stream schedule ---------------------------------------------------------
+// Every value lives in its own region of a root (concat inputs in disjoint channel
+// slices of the concat's root) and is written once per run, so the only ordering a
+// step needs is after the earlier steps that write a root it reads (read after
+// write), and everything after the slot clear.  Two producers of slices of one root
+// touch disjoint bytes and disjoint amax slot groups, so they may run concurrently.
+// Lanes: a step continues the lane of its latest dependency when that lane has not
+// moved on, else takes an idle lane (else the least recently used one, which then
+// orders it after that lane's last step too); dependencies on other lanes become
+// event waits.  The captured graph thus has parallel branches (the head's box and
+// class chains, the finest head level beside the rest of the neck).
+void schedule_steps(AexrtYoloModel* m) {
+    auto& st = m->steps;
+    const int nl = std::max(1, std::min(kLanes, m->n_lanes));
+    const int n = (int)st.size();
+    for (int i = 0; i < n; ++i) {
+        st[i].deps.clear();
+        st[i].signal = false;
+        for (int j = i - 1; j >= 0; --j) {
+            bool dep = st[i].all || st[j].all;
+            for (int r : st[i].reads)
+                for (int w : st[j].writes) dep = dep || r == w;
+            if (dep) st[i].deps.push_back(j);
+        }
+    }
+    int last[kLanes];
+    for (int l = 0; l < kLanes; ++l) last[l] = -1;
+    for (int i = 0; i < n; ++i) {
+        int lane = -1, best = -1;
+        for (int l = 0; l < nl; ++l)
+            for (int d : st[i].deps)
+                if (last[l] == d && d > best) {
+                    best = d;
+                    lane = l;
+                }
+        if (lane < 0) {
+            for (int l = 0; l < nl && lane < 0; ++l)
+                if (last[l] < 0) lane = l;
+            if (lane < 0) {
+                lane = 0;
+                for (int l = 1; l < nl; ++l)
+                    if (last[l] < last[lane]) lane = l;
+            }
+        }
+        st[i].lane = lane;
+        for (int d : st[i].deps)
+            if (st[d].lane != lane) st[d].signal = true;
+        last[lane] = i;
+    }
+}
+
 bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
     Engine& e = m->eng;
     auto& V = m->vals;
@@ -742,6 +807,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
         m->steps.push_back(Step{-1, "amax slots clear", [slots, n](hipStream_t s) {
                                     return launch_fill_u32(slots, n, 0u, s);
                                 }});
+        m->steps.back().all = true;
     }
     const uint32_t in_v = e.manifest.input_value;
     if (m->input_needs_nhwc) {
@@ -753,12 +819,14 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
             m->steps.push_back(Step{-1, "input nchw->nhwc8", [=](hipStream_t s) {
                                         return launch_nchw_f32_to_nhwc8(src, static_cast<__half*>(y.data), N, C, HW, s);
                                     }});
+            m->steps.back().writes = {V[in_v].pl.root};
         } else {
             m->steps.push_back(Step{-1, "input nchw->nhwc", [=](hipStream_t s) {
                                         return launch_nchw_f32_to_nhwc_f16(src, static_cast<__half*>(y.data),
                                                                            y.n_stride, y.c_stride, N, C, HW,
                                                                            slot_ref(y), s);
                                     }});
+            m->steps.back().writes = {V[in_v].pl.root};
         }
     }
     for (size_t ci = 0; ci < e.commands.size(); ++ci) {
@@ -800,6 +868,9 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                                             if (is_winograd_algorithm(alg)) return launch_winograd_f2x2(p, s);
                                             return launch_conv_igemm(p, is_int8_algorithm(alg), s);
                                         }});
+                if (!(m->vals[xv].is_input && m->input_nchw_direct)) m->steps.back().reads.push_back(V[xv].pl.root);
+                if (cs.fused_residual) m->steps.back().reads.push_back(V[cs.residual_value].pl.root);
+                m->steps.back().writes = {V[yv].pl.root};
                 break;
             }
             case kCmdConcat: {
@@ -817,6 +888,8 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                                                                         dv.n_stride, dv.c_stride, N, HW, C,
                                                                         slot_ref(dv), st);
                                             }});
+                    m->steps.back().reads = {V[j.src].pl.root};
+                    m->steps.back().writes = {j.dst.root};
                 }
                 break;
             }
@@ -833,6 +906,8 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                                                                        yv.n_stride, yv.c_stride, N, H, W, C, OH, OW, k,
                                                                        st, pad, slot_ref(yv), s);
                                         }});
+                m->steps.back().reads = {V[c.inputs[0]].pl.root};
+                m->steps.back().writes = {V[c.output].pl.root};
                 break;
             }
             case kCmdResize: {
@@ -847,6 +922,8 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                                                 static_cast<__half*>(yv.data), yv.n_stride, yv.c_stride, N, H, W, C, OH,
                                                 OW, slot_ref(yv), s);
                                         }});
+                m->steps.back().reads = {V[c.inputs[0]].pl.root};
+                m->steps.back().writes = {V[c.output].pl.root};
                 break;
             }
             case kCmdBinary: {
@@ -863,12 +940,15 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                                                                    static_cast<__half*>(yv.data), yv.n_stride,
                                                                    yv.c_stride, N, HW, C, slot_ref(yv), s);
                                         }});
+                m->steps.back().reads = {V[c.inputs[0]].pl.root, V[c.inputs[1]].pl.root};
+                m->steps.back().writes = {V[c.output].pl.root};
                 break;
             }
             default:
                 break;  // VIEW / ALIAS: placement only
         }
     }
+    schedule_steps(m);
     return true;
 }
 
@@ -884,6 +964,55 @@ bool launch_steps(AexrtYoloModel* m, hipStream_t s) {
     for (const Step& st : m->steps) {
         hipError_t e = st.launch(s);
         if (e != hipSuccess) return fail(m, st.label + ": " + hipGetErrorString(e));
+    }
+    return true;
+}
+
+// Issues the steps over the lanes (lane 0 = s) inside a stream capture: the
+// other lanes fork from s before the first step, wait on the events of their
+// cross-lane dependencies, and s joins them all at the end.
+bool launch_steps_lanes(AexrtYoloModel* m, hipStream_t s) {
+    auto& st = m->steps;
+    if (m->step_events.size() < st.size()) {
+        size_t k = m->step_events.size();
+        m->step_events.resize(st.size(), nullptr);
+        for (; k < st.size(); ++k)
+            if (!check_hip(hipEventCreateWithFlags(&m->step_events[k], hipEventDisableTiming), "step event"))
+                return fail(m, last_error());
+    }
+    auto new_event = [&](hipEvent_t& e) {
+        e = nullptr;
+        if (!check_hip(hipEventCreateWithFlags(&e, hipEventDisableTiming), "lane event")) return false;
+        m->lane_events.push_back(e);
+        return true;
+    };
+    hipStream_t lanes[kLanes];
+    lanes[0] = s;
+    bool used[kLanes] = {};
+    for (int l = 1; l < kLanes; ++l) lanes[l] = m->lane_stream[l];
+    for (const Step& x : st) used[x.lane] = true;
+    bool any = false;
+    for (int l = 1; l < kLanes; ++l) any = any || used[l];
+    hipEvent_t fork = nullptr;
+    if (any && (!new_event(fork) || !check_hip(hipEventRecord(fork, s), "fork record"))) return fail(m, last_error());
+    for (int l = 1; l < kLanes; ++l)
+        if (used[l] && !check_hip(hipStreamWaitEvent(lanes[l], fork, 0), "fork wait")) return fail(m, last_error());
+    for (size_t i = 0; i < st.size(); ++i) {
+        const int l = st[i].lane;
+        for (int d : st[i].deps)
+            if (st[d].lane != l && !check_hip(hipStreamWaitEvent(lanes[l], m->step_events[d], 0), "step wait"))
+                return fail(m, last_error());
+        const hipError_t e = st[i].launch(lanes[l]);
+        if (e != hipSuccess) return fail(m, st[i].label + ": " + hipGetErrorString(e));
+        if (st[i].signal && !check_hip(hipEventRecord(m->step_events[i], lanes[l]), "step record"))
+            return fail(m, last_error());
+    }
+    for (int l = 1; l < kLanes; ++l) {
+        if (!used[l]) continue;
+        hipEvent_t join = nullptr;
+        if (!new_event(join) || !check_hip(hipEventRecord(join, lanes[l]), "join record") ||
+            !check_hip(hipStreamWaitEvent(s, join, 0), "join wait"))
+            return fail(m, last_error());
     }
     return true;
 }
@@ -921,7 +1050,7 @@ bool run_network(AexrtYoloModel* m, hipStream_t s) {
         drop_graph(m);
         if (!check_hip(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "graph capture begin"))
             return fail(m, last_error());
-        const bool ok = launch_steps(m, s);
+        const bool ok = launch_steps_lanes(m, s);
         hipGraph_t g = nullptr;
         const hipError_t ec = hipStreamEndCapture(s, &g);
         if (!ok) {
@@ -935,6 +1064,46 @@ bool run_network(AexrtYoloModel* m, hipStream_t s) {
         m->graph_valid = true;
     }
     return check_hip(hipGraphLaunch(m->graph_exec, s), "graph launch") ? true : fail(m, last_error());
+}
+
+// Spreading independent steps over streams pays when kernels are long enough to
+// overlap (large batch) and costs cross-queue synchronization when they are not
+// (batch 1): both schedules are captured and timed at load, the faster one kept.
+bool choose_lanes(AexrtYoloModel* m) {
+    if (!m->use_graph) return true;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (!check_hip(hipEventCreate(&e0), "lanes event") || !check_hip(hipEventCreate(&e1), "lanes event")) {
+        if (e0) (void)hipEventDestroy(e0);
+        return fail(m, last_error());
+    }
+    const int options[2] = {kLanes, 1};
+    float best_ms = 0.0f;
+    int best = 1;
+    bool ok = true;
+    for (int k = 0; k < 2 && ok; ++k) {
+        m->n_lanes = options[k];
+        schedule_steps(m);
+        drop_graph(m);
+        for (int r = 0; r < 3 && ok; ++r) ok = run_network(m, m->stream);  // capture + warm-up
+        ok = ok && check_hip(hipEventRecord(e0, m->stream), "lanes record");
+        for (int r = 0; r < 10 && ok; ++r) ok = run_network(m, m->stream);
+        ok = ok && check_hip(hipEventRecord(e1, m->stream), "lanes record") &&
+             check_hip(hipEventSynchronize(e1), "lanes sync");
+        float ms = 0.0f;
+        ok = ok && check_hip(hipEventElapsedTime(&ms, e0, e1), "lanes elapsed");
+        if (ok && (k == 0 || ms < best_ms)) {
+            best_ms = ms;
+            best = options[k];
+        }
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (!ok) return false;
+    m->n_lanes = best;
+    schedule_steps(m);
+    drop_graph(m);
+    if (m->tune_log) std::fprintf(stderr, "aexrt lanes: %d (%.1f us per run)\n", best, best_ms * 100.0f);
+    return true;
 }
 
 bool build_model(AexrtYoloModel* m) {
@@ -973,11 +1142,16 @@ bool build_model(AexrtYoloModel* m) {
         if (m->convs[ci].is_conv && !prepare_conv_weights(m, ci)) return false;
     if (!check_hip(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking), "stream create"))
         return fail(m, last_error());
+    for (int l = 1; l < kLanes; ++l)
+        if (!check_hip(hipStreamCreateWithFlags(&m->lane_stream[l], hipStreamNonBlocking), "lane stream create"))
+            return fail(m, last_error());
     const char* tune = std::getenv("AEXRT_HIP_AUTOTUNE");
     m->autotune = !(tune && tune[0] == '0');
     const char* tlog = std::getenv("AEXRT_HIP_TUNE_LOG");
     m->tune_log = tlog && tlog[0] == '1';
+    m->n_lanes = 1;
     if (!build_steps(m, m->copies)) return false;
+    if (m->autotune && !choose_lanes(m)) return false;
     const char* prof = std::getenv("AEXRT_HIP_PROFILE");
     m->profile = prof && prof[0] == '1';
     m->executable = true;
@@ -992,6 +1166,12 @@ void free_model(AexrtYoloModel* m) {
     for (void* p : m->allocations) (void)hipFree(p);
     if (m->input_host) (void)hipHostFree(m->input_host);
     if (m->stream) (void)hipStreamDestroy(m->stream);
+    for (int l = 1; l < kLanes; ++l)
+        if (m->lane_stream[l]) (void)hipStreamDestroy(m->lane_stream[l]);
+    for (hipEvent_t e : m->step_events)
+        if (e) (void)hipEventDestroy(e);
+    for (hipEvent_t e : m->lane_events)
+        if (e) (void)hipEventDestroy(e);
     delete m;
 }
 
