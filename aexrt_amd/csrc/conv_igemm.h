@@ -385,13 +385,20 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvParams p) {
         for (int q = 0; q < PW; ++q) {
             const int m = pb + q * 16 + col;
             const bool mok = m < p.M;
-            const int n = (int)fdiv((uint32_t)m, p.fd_ohw);
-            const int rem = m - n * p.OH * p.OW;
-            const int oh = (int)fdiv((uint32_t)rem, p.fd_ow);
-            const int ow = rem - oh * p.OW;
-            ih0[q] = mok ? oh * p.S - p.P : -0x40000000;  // out of range for every tap
-            iw0[q] = ow * p.S - p.P;
-            xo[q] = n * (int)p.x_nstride + ((oh * p.S - p.P) * p.W + iw0[q]) * p.x_cstride;
+            if (p.lin & kLinX) {
+                // 1x1 s1 on a dense view: input pixel m, no padding taps
+                ih0[q] = mok ? 0 : -0x40000000;
+                iw0[q] = 0;
+                xo[q] = (int)__umul24((uint32_t)m, (uint32_t)p.x_cstride);
+            } else {
+                const int n = (int)fdiv((uint32_t)m, p.fd_ohw);
+                const int rem = m - n * p.OH * p.OW;
+                const int oh = (int)fdiv((uint32_t)rem, p.fd_ow);
+                const int ow = rem - oh * p.OW;
+                ih0[q] = mok ? oh * p.S - p.P : -0x40000000;  // out of range for every tap
+                iw0[q] = ow * p.S - p.P;
+                xo[q] = n * (int)p.x_nstride + ((oh * p.S - p.P) * p.W + iw0[q]) * p.x_cstride;
+            }
         }
         pos_tl = tl;
     };
@@ -557,10 +564,16 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvParams p) {
 #pragma unroll
         for (int q = 0; q < PW; ++q) {
             const int m = pb + q * 16 + col;
-            const int n = (int)fdiv((uint32_t)m, p.fd_ohw);
-            const int pos = m - n * p.OH * p.OW;
-            yo[q] = m < p.M ? n * (int)p.y_nstride + pos * p.y_cstride : -1;
-            ro[q] = n * (int)p.r_nstride + pos * p.r_cstride;
+            if (p.lin & kLinY) {
+                // dense output (and residual) views: position m
+                yo[q] = m < p.M ? (int)__umul24((uint32_t)m, (uint32_t)p.y_cstride) : -1;
+                ro[q] = (int)__umul24((uint32_t)m, (uint32_t)p.r_cstride);
+            } else {
+                const int n = (int)fdiv((uint32_t)m, p.fd_ohw);
+                const int pos = m - n * p.OH * p.OW;
+                yo[q] = m < p.M ? n * (int)p.y_nstride + pos * p.y_cstride : -1;
+                ro[q] = n * (int)p.r_nstride + pos * p.r_cstride;
+            }
             mo[q] = m;
         }
         tile_residual<JN, PW, EPI>(p, rr, yo, ro, n0, jmax, grp, jmask, rv);

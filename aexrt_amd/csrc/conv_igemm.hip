@@ -172,6 +172,15 @@ hipError_t launch_conv_igemm(const ConvParams& p0, bool int8, hipStream_t stream
             p.x_slot_bytes = ((p.x_slots.stripes - 1) * p.x_slots.stride + (uint32_t)p.x_nslots) * 4u;
             p.fd_ns = make_fastdiv((uint32_t)std::max(p.x_nslots, 1));
         }
+        p.lin = 0;
+        if (p.M < (1 << 24)) {
+            if (!nchw && p.KH == 1 && p.KW == 1 && p.S == 1 && p.P == 0 && p.x_nstride == (int64_t)HWi * p.x_cstride &&
+                p.x_cstride < (1 << 24))
+                p.lin |= kLinX;
+            if (p.y_nstride == (int64_t)HWo * p.y_cstride && p.y_cstride < (1 << 24) &&
+                (!p.res || (p.r_nstride == (int64_t)HWo * p.r_cstride && p.r_cstride < (1 << 24))))
+                p.lin |= kLinY;
+        }
         p.fd_ohw = make_fastdiv((uint32_t)HWo);
         p.fd_ow = make_fastdiv((uint32_t)p.OW);
         p.fd_c = make_fastdiv((uint32_t)p.C);

@@ -40,6 +40,15 @@ enum ConvFlags : int {
     kConvOutF32 = 4,    // store fp32 instead of fp16
 };
 
+// Views whose element (position m, channel c) sits at m * c_stride + c: the
+// image stride is H*W*c_stride (every full-image view of an NHWC root) and,
+// for kLinX, the conv is 1x1 stride 1 without padding.  Offsets then need
+// no division; positions and strides must stay below 2^24 (24-bit multiply).
+enum LinearViews : int {
+    kLinX = 1,  // input pixel of position m at m * x_cstride
+    kLinY = 2,  // output (and residual) of position m at m * y_cstride (r_cstride)
+};
+
 enum Loader : int {
     kLoaderNhwc = 0,     // fp16 NHWC activation view, C % 8 == 0
     kLoaderNchwF32 = 1,  // fp32 NCHW network input, c_real <= 4 channels read as C = 8 (zero padded)
@@ -78,6 +87,7 @@ struct ConvParams {
     int32_t* acc_out;         // optional int32 accumulators [M][OC] (int8)
     int N, H, W, C, OH, OW, OC, KH, KW, S, P;
     int c_real = 0;           // kLoaderNchwF32: channels present in memory (x_nstride = c_real*H*W)
+    int lin = 0;              // kLinX / kLinY: view offsets linear in the position (set by the launcher)
     ConvChoice choice{};      // kernel / tile (kind 0: heuristics)
     int K, M;
     int flags;
