@@ -48,6 +48,7 @@ struct HaloParams {
     int ntile;       // N * tpi
     int wbytes;      // LDS bytes of the resident weights
     int tbytes;      // LDS bytes of one window buffer
+    int pstride;     // LDS bytes per window pixel (CC * element size)
     FastDiv fd_cc8, fd_icol, fd_tc, fd_ntc, fd_tpi, fd_cc, fd_spc;
     int icol4;                // NCHW: column quads of a window row: (ICOL + 3 + 3) / 4
     FastDiv fd_icol4, fd_rq;  // NCHW: / icol4, / (IR * icol4)
@@ -142,12 +143,12 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_halo_kernel(HaloParams h) {
 
     // ---- input windows -----------------------------------------------------
     // Piece k of this thread: e = tid + k * NT -> window pixel (ir, ic) and
-    // 8-channel group; the LDS place is e * PIECE.  Pieces past the window get
-    // a row that fails every bounds test.
+    // 8-channel group; its LDS place is plds[k] = pixel * pstride + group * PIECE.
+    // Pieces past the window get a row that fails every bounds test.
     // NCHW pieces: e -> channel c, window row ir, column quad q4 (columns
     // 4 q4 - 3 .. 4 q4 relative to the window's first column), packed as
     // ir | q4 << 12 | c << 24 in prc.
-    int prc[NP], prel[NP];
+    int prc[NP], prel[NP], plds[NCHW ? 1 : NP];
 #pragma unroll
     for (int k = 0; k < NP; ++k) {
         const int e = tid + k * NT;
@@ -165,6 +166,7 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_halo_kernel(HaloParams h) {
             const int ic = pix - ir * h.ICOL;
             prc[k] = e < h.npieces ? (ir | (ic << 16)) : 0x7FFF;
             prel[k] = (ir * p.W + ic) * p.x_cstride + cp * 8;
+            plds[k] = pix * h.pstride + cp * PIECE;
         }
     }
     int pvalid[NCHW ? NP : 1];  // NCHW: columns of the quad inside the image (0..4)
@@ -232,7 +234,7 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_halo_kernel(HaloParams h) {
         int off = 0;  // padding k: any in-window address, zero weights
         if (tap < 9) {
             const int ky = tap / 3, kx = tap - (tap / 3) * 3;
-            off = ((ky * h.ICOL + kx) * h.CC + (kk - tap * h.CC)) * ESZ;
+            off = (ky * h.ICOL + kx) * h.pstride + (kk - tap * h.CC) * ESZ;
         }
         l_toff[e] = off;
     }
@@ -246,7 +248,7 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_halo_kernel(HaloParams h) {
         const int pc = min(pl, tpos - 1);
         const int r = (int)fdiv((uint32_t)pc, h.fd_tc);
         const int c = pc - r * h.TC;
-        bofs[q] = ((r * S) * h.ICOL + c * S) * h.CC * ESZ;
+        bofs[q] = ((r * S) * h.ICOL + c * S) * h.pstride;
         prc_out[q] = pl < tpos ? (r | (c << 16)) : -1;
     }
     if (tid < JN) l_slots[tid] = 0u;
@@ -308,7 +310,7 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_halo_kernel(HaloParams h) {
             const int e = tid + k * NT;
             if (e < h.npieces) {
                 if constexpr (INT8) {
-                    *reinterpret_cast<v2i*>(tb + e * PIECE) = quant8(pf[k], s_q);
+                    *reinterpret_cast<v2i*>(tb + plds[k]) = quant8(pf[k], s_q);
                 } else if constexpr (NCHW) {
                     // channel c of window pixels 4 q4 - 3 + j (those inside
                     // the window; columns past the image are zero)
@@ -318,11 +320,11 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_halo_kernel(HaloParams h) {
                         const int ic = 4 * q4 - 3 + j;
                         if (ic >= 0 && ic < h.ICOL) {
                             const __half v = __float2half(j < pvalid[k] ? __int_as_float(pf[k][j]) : 0.0f);
-                            *reinterpret_cast<__half*>(tb + ((ir * h.ICOL + ic) * 8 + c) * 2) = v;
+                            *reinterpret_cast<__half*>(tb + (ir * h.ICOL + ic) * h.pstride + c * 2) = v;
                         }
                     }
                 } else {
-                    *reinterpret_cast<v4i*>(tb + e * PIECE) = pf[k];
+                    *reinterpret_cast<v4i*>(tb + plds[k]) = pf[k];
                 }
             }
         }

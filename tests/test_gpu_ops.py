@@ -394,9 +394,10 @@ def _halo_fits(c, h, w, s, jn, pw, tr, tc, cc, int8, nw=4):
     if cc % (16 if int8 else 8) or c % cc or tr * tc > 16 * nw * pw:
         return False
     spc = (9 * cc + 63) // 64
-    npieces = ((tr - 1) * s + 3) * ((tc - 1) * s + 3) * cc // 8
+    pixels = ((tr - 1) * s + 3) * ((tc - 1) * s + 3)
+    npieces = pixels * cc // 8
     wbytes = (c // cc) * spc * esz * jn * 16 * 64
-    tbytes = (npieces * 8 * esz + 15) // 16 * 16
+    tbytes = (pixels * cc * esz + 15) // 16 * 16
     return npieces <= 8 * 64 * nw and wbytes + 2 * tbytes <= 80 * 1024 - 2048
 
 
