@@ -122,6 +122,8 @@ _SIGS = {
     "aexrt_hip_copy": (c_int, [POINTER(TensorView), POINTER(TensorView), c_uint32, c_uint32, c_uint32, _vp]),
     "aexrt_hip_maxpool": (c_int, [POINTER(TensorView), POINTER(TensorView), c_uint32, c_uint32, c_uint32,
                                   c_uint32, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32, _vp]),
+    "aexrt_hip_sppf_maxpool": (c_int, [POINTER(TensorView), POINTER(TensorView), POINTER(TensorView),
+                                       POINTER(TensorView), c_uint32, c_uint32, c_uint32, c_uint32, _vp]),
     "aexrt_hip_resize_nearest": (c_int, [POINTER(TensorView), POINTER(TensorView), c_uint32, c_uint32,
                                          c_uint32, c_uint32, c_uint32, c_uint32, _vp]),
     "aexrt_hip_add": (c_int, [POINTER(TensorView), POINTER(TensorView), POINTER(TensorView), c_uint32,

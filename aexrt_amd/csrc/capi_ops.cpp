@@ -440,6 +440,25 @@ int aexrt_hip_maxpool(const AexrtHipTensorView* x, const AexrtHipTensorView* y, 
                : 0;
 }
 
+int aexrt_hip_sppf_maxpool(const AexrtHipTensorView* x, const AexrtHipTensorView* y1, const AexrtHipTensorView* y2,
+                           const AexrtHipTensorView* y3, uint32_t batch, uint32_t channels, uint32_t h, uint32_t w,
+                           void* stream) {
+    if (!vec_view_ok(x) || !vec_view_ok(y1) || !vec_view_ok(y2) || !vec_view_ok(y3) || channels % 8 ||
+        y1->n_stride != y2->n_stride || y1->n_stride != y3->n_stride || y1->c_stride != y2->c_stride ||
+        y1->c_stride != y3->c_stride || !sppf_fits((int)h, (int)w)) {
+        set_error("sppf_maxpool: 16-byte aligned views, C % 8 == 0, outputs with one geometry, plane fits LDS");
+        return 0;
+    }
+    return check_hip(launch_sppf_maxpool_nhwc(static_cast<const __half*>(x->data), x->n_stride, x->c_stride,
+                                              static_cast<__half*>(y1->data), static_cast<__half*>(y2->data),
+                                              static_cast<__half*>(y3->data), y1->n_stride, y1->c_stride,
+                                              (int)batch, (int)h, (int)w, (int)channels, slot_ref(y1), slot_ref(y2),
+                                              slot_ref(y3), static_cast<hipStream_t>(stream)),
+                     "sppf_maxpool")
+               ? 1
+               : 0;
+}
+
 int aexrt_hip_resize_nearest(const AexrtHipTensorView* x, const AexrtHipTensorView* y, uint32_t batch,
                              uint32_t channels, uint32_t in_h, uint32_t in_w, uint32_t out_h, uint32_t out_w,
                              void* stream) {

@@ -166,6 +166,13 @@ hipError_t launch_maxpool_nhwc(const __half* x, int64_t x_nstride, int32_t x_cst
                                int64_t y_nstride, int32_t y_cstride, int N, int H, int W, int C,
                                int OH, int OW, int k, int s, int pad, SlotRef y_slots,
                                hipStream_t stream);
+// SPPF's three chained 5x5 / s1 / p2 max pools of x in one pass: y1 = pool5(x),
+// y2 = pool5(y1), y3 = pool5(y2), written to three views sharing strides, with
+// their amax slots.  sppf_fits: the (H, W) plane fits the kernel's LDS.
+bool sppf_fits(int H, int W);
+hipError_t launch_sppf_maxpool_nhwc(const __half* x, int64_t x_nstride, int32_t x_cstride, __half* y1, __half* y2,
+                                    __half* y3, int64_t y_nstride, int32_t y_cstride, int N, int H, int W, int C,
+                                    SlotRef s1, SlotRef s2, SlotRef s3, hipStream_t stream);
 hipError_t launch_resize_nearest_nhwc(const __half* x, int64_t x_nstride, int32_t x_cstride, __half* y,
                                       int64_t y_nstride, int32_t y_cstride, int N, int H, int W, int C,
                                       int OH, int OW, SlotRef y_slots, hipStream_t stream);

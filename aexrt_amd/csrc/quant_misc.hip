@@ -327,6 +327,111 @@ __global__ __launch_bounds__(kThreads) void resize_nearest_nhwc_kernel(
     if (G) slots_flush(ls, G, y_slots);
 }
 
+// Nearest 2x upsample: one thread per input (pixel, 8-channel chunk), one
+// 16-byte load and its four output copies, no loop (every load of the grid in
+// flight at once).  max|y| = max|x| of the chunk.
+__global__ __launch_bounds__(kThreads) void resize2x_nhwc_kernel(
+    const __half* x, int64_t x_nstride, int32_t x_cstride, __half* y, int64_t y_nstride, int32_t y_cstride,
+    int H, int W, int C, int chunks, ChunkDivs dv, SlotRef y_slots) {
+    __shared__ uint32_t ls[kMaxSlots];
+    const int G = y_slots.p ? C / 16 : 0;
+    slots_init(ls, G);
+    const int CC = C / 8;
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e < chunks) {
+        int n, pp, cc;
+        chunk_split((uint32_t)e, CC, H * W, dv, n, pp, cc);
+        const int iy = (int)fdiv((uint32_t)pp, dv.ow), ix = pp - iy * W;
+        const uint4 v = *reinterpret_cast<const uint4*>(x + n * x_nstride + (int64_t)pp * x_cstride + cc * 8);
+        __half* yb = y + n * y_nstride + ((int64_t)(2 * iy) * (2 * W) + 2 * ix) * y_cstride + cc * 8;
+        *reinterpret_cast<uint4*>(yb) = v;
+        *reinterpret_cast<uint4*>(yb + y_cstride) = v;
+        *reinterpret_cast<uint4*>(yb + (int64_t)(2 * W) * y_cstride) = v;
+        *reinterpret_cast<uint4*>(yb + (int64_t)(2 * W + 1) * y_cstride) = v;
+        if (G) atomicMax(&ls[cc >> 1], f2u(max8_abs(v)));
+    }
+    if (G) slots_flush(ls, G, y_slots);
+}
+
+// SPPF's three chained 5x5 / stride 1 / pad 2 max pools in one pass: with
+// -inf padding, pool5(pool5(x)) = pool9(x) and pool5(pool5(pool5(x))) =
+// pool13(x) (every window of the composition lies inside the image together
+// with a path of in-image 5x5 windows).  A block owns one (image, 8-channel
+// chunk) plane: the plane goes to LDS, a horizontal pass takes the row maxima
+// over +-2, +-4 and +-6 columns, a vertical pass the column maxima of those
+// over +-2, +-4 and +-6 rows.  Max is exact in fp16.
+__device__ __forceinline__ uint4 hmax8(uint4 a, uint4 b) {
+    // packed fp16 maximum (maxnum: a NaN operand yields the other, as fmaxf)
+    const v8h m = __builtin_elementwise_max(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b));
+    return __builtin_bit_cast(uint4, m);
+}
+
+__global__ __launch_bounds__(kThreads) void sppf_maxpool_nhwc_kernel(
+    const __half* x, int64_t x_nstride, int32_t x_cstride, __half* y1, __half* y2, __half* y3, int64_t y_nstride,
+    int32_t y_cstride, int H, int W, int C, SlotRef s1, SlotRef s2, SlotRef s3) {
+    extern __shared__ uint4 sp[];  // [4][H*W]: plane, row maxima over +-2, +-4, +-6
+    __shared__ uint32_t lm[3];
+    const int HW = H * W;
+    const int CC = C / 8;
+    const int n = blockIdx.x / CC, cc = blockIdx.x - n * CC;
+    const int tid = threadIdx.x;
+    if (tid < 3) lm[tid] = 0u;
+    const __half* xb = x + n * x_nstride + cc * 8;
+    for (int p = tid; p < HW; p += kThreads) sp[p] = *reinterpret_cast<const uint4*>(xb + (int64_t)p * x_cstride);
+    __syncthreads();
+    for (int p = tid; p < HW; p += kThreads) {
+        const int r = p / W, c = p - r * W;
+        uint4 m = sp[p];
+        for (int d = 1; d <= 6; ++d) {
+            if (c - d >= 0) m = hmax8(m, sp[p - d]);
+            if (c + d < W) m = hmax8(m, sp[p + d]);
+            if (d == 2) sp[HW + p] = m;
+            if (d == 4) sp[2 * HW + p] = m;
+        }
+        sp[3 * HW + p] = m;
+    }
+    __syncthreads();
+    float g1 = 0.0f, g2 = 0.0f, g3 = 0.0f;
+    __half* o1 = y1 + n * y_nstride + cc * 8;
+    __half* o2 = y2 + n * y_nstride + cc * 8;
+    __half* o3 = y3 + n * y_nstride + cc * 8;
+    for (int p = tid; p < HW; p += kThreads) {
+        const int r = p / W;
+        uint4 m1 = sp[HW + p], m2 = sp[2 * HW + p], m3 = sp[3 * HW + p];
+        for (int d = 1; d <= 6; ++d) {
+            if (d <= 2) {
+                if (r - d >= 0) m1 = hmax8(m1, sp[HW + p - d * W]);
+                if (r + d < H) m1 = hmax8(m1, sp[HW + p + d * W]);
+            }
+            if (d <= 4) {
+                if (r - d >= 0) m2 = hmax8(m2, sp[2 * HW + p - d * W]);
+                if (r + d < H) m2 = hmax8(m2, sp[2 * HW + p + d * W]);
+            }
+            if (r - d >= 0) m3 = hmax8(m3, sp[3 * HW + p - d * W]);
+            if (r + d < H) m3 = hmax8(m3, sp[3 * HW + p + d * W]);
+        }
+        *reinterpret_cast<uint4*>(o1 + (int64_t)p * y_cstride) = m1;
+        *reinterpret_cast<uint4*>(o2 + (int64_t)p * y_cstride) = m2;
+        *reinterpret_cast<uint4*>(o3 + (int64_t)p * y_cstride) = m3;
+        g1 = fmaxf(g1, max8_abs(m1));
+        g2 = fmaxf(g2, max8_abs(m2));
+        g3 = fmaxf(g3, max8_abs(m3));
+    }
+    g1 = wave_max(g1);
+    g2 = wave_max(g2);
+    g3 = wave_max(g3);
+    if ((tid & 63) == 0) {
+        if (g1 > 0.0f) atomicMax(&lm[0], f2u(g1));
+        if (g2 > 0.0f) atomicMax(&lm[1], f2u(g2));
+        if (g3 > 0.0f) atomicMax(&lm[2], f2u(g3));
+    }
+    __syncthreads();
+    if (tid < 3) {
+        const SlotRef& sr = tid == 0 ? s1 : (tid == 1 ? s2 : s3);
+        if (sr.p && lm[tid]) slot_max(slot_copy(sr, blockIdx.x) + (cc >> 1), u2f(lm[tid]));
+    }
+}
+
 __global__ __launch_bounds__(kThreads) void add_nhwc_kernel(
     const __half* a, int64_t a_nstride, int32_t a_cstride, const __half* b, int64_t b_nstride,
     int32_t b_cstride, __half* y, int64_t y_nstride, int32_t y_cstride, int HW, int C, int chunks,
@@ -513,9 +618,30 @@ hipError_t launch_resize_nearest_nhwc(const __half* x, int64_t x_nstride, int32_
     const int64_t chunks = (int64_t)N * OH * OW * (C / 8);
     if (chunks >= INT32_MAX || (int64_t)OH * H >= INT32_MAX || (int64_t)OW * W >= INT32_MAX)
         return hipErrorInvalidValue;
+    if (OH == 2 * H && OW == 2 * W) {
+        const int64_t in_chunks = (int64_t)N * H * W * (C / 8);
+        hipLaunchKernelGGL(resize2x_nhwc_kernel, dim3((unsigned)((in_chunks + kThreads - 1) / kThreads)),
+                           dim3(kThreads), 0, stream, x, x_nstride, x_cstride, y, y_nstride, y_cstride, H, W, C,
+                           (int)in_chunks, chunk_divs(C, H * W, W), y_slots);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(resize_nearest_nhwc_kernel, dim3(grid_cols(chunks, C)), dim3(kThreads), 0, stream, x,
                        x_nstride, x_cstride, y, y_nstride, y_cstride, H, W, C, OH, OW, (int)chunks,
                        chunk_divs(C, OH * OW, OW, OH), y_slots);
+    return hipGetLastError();
+}
+
+bool sppf_fits(int H, int W) { return H >= 1 && W >= 1 && (int64_t)H * W * 64 <= 96 * 1024; }
+
+hipError_t launch_sppf_maxpool_nhwc(const __half* x, int64_t x_nstride, int32_t x_cstride, __half* y1, __half* y2,
+                                    __half* y3, int64_t y_nstride, int32_t y_cstride, int N, int H, int W, int C,
+                                    SlotRef s1, SlotRef s2, SlotRef s3, hipStream_t stream) {
+    if (C % 8 != 0 || !sppf_fits(H, W) || ((s1.p || s2.p || s3.p) && C % 16 != 0)) return hipErrorInvalidValue;
+    const int64_t blocks = (int64_t)N * (C / 8);
+    if (blocks >= INT32_MAX) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(sppf_maxpool_nhwc_kernel, dim3((unsigned)blocks), dim3(kThreads),
+                       (size_t)H * W * 64, stream, x, x_nstride, x_cstride, y1, y2, y3, y_nstride, y_cstride, H, W,
+                       C, s1, s2, s3);
     return hipGetLastError();
 }
 

@@ -829,8 +829,10 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
             m->steps.back().writes = {V[in_v].pl.root};
         }
     }
+    std::vector<bool> done(e.commands.size(), false);  // folded into an earlier step
     for (size_t ci = 0; ci < e.commands.size(); ++ci) {
         const EngineCommand& c = e.commands[ci];
+        if (done[ci]) continue;
         switch (c.kind) {
             case kCmdConv:
             case kCmdConvSilu: {
@@ -896,6 +898,36 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
             case kCmdMaxpool: {
                 const ValueInfo& x = V[c.inputs[0]];
                 const ValueInfo& o = V[c.output];
+                // SPPF: three chained 5x5 / s1 / p2 pools run as one kernel
+                auto sppf_link = [&](size_t k, uint32_t in) {
+                    if (k >= e.commands.size()) return false;
+                    const EngineCommand& d = e.commands[k];
+                    return d.kind == kCmdMaxpool && d.inputs[0] == in && d.params[6] == 5 && d.params[8] == 1 &&
+                           d.params[10] == 2 && V[d.output].H == x.H && V[d.output].W == x.W;
+                };
+                if (sppf_link(ci, c.inputs[0]) && sppf_link(ci + 1, c.output) &&
+                    sppf_link(ci + 2, e.commands[ci + 1].output) && x.C % 16 == 0 && sppf_fits(x.H, x.W)) {
+                    const int v1 = (int)c.output, v2 = (int)e.commands[ci + 1].output,
+                              v3 = (int)e.commands[ci + 2].output;
+                    AexrtHipTensorView xv = view_of(m, (int)c.inputs[0]), a = view_of(m, v1), b = view_of(m, v2),
+                                       d = view_of(m, v3);
+                    if (a.n_stride == b.n_stride && a.n_stride == d.n_stride && a.c_stride == b.c_stride &&
+                        a.c_stride == d.c_stride) {
+                        const int N = x.N, H = x.H, W = x.W, C = x.C;
+                        m->steps.push_back(Step{(int)ci, "cmd#" + std::to_string(ci) + " SPPF MAXPOOL x3",
+                                                [=](hipStream_t st) {
+                                                    return launch_sppf_maxpool_nhwc(
+                                                        static_cast<const __half*>(xv.data), xv.n_stride, xv.c_stride,
+                                                        static_cast<__half*>(a.data), static_cast<__half*>(b.data),
+                                                        static_cast<__half*>(d.data), a.n_stride, a.c_stride, N, H,
+                                                        W, C, slot_ref(a), slot_ref(b), slot_ref(d), st);
+                                                }});
+                        m->steps.back().reads = {V[c.inputs[0]].pl.root};
+                        m->steps.back().writes = {V[v1].pl.root, V[v2].pl.root, V[v3].pl.root};
+                        done[ci + 1] = done[ci + 2] = true;
+                        break;
+                    }
+                }
                 AexrtHipTensorView xv = view_of(m, (int)c.inputs[0]), yv = view_of(m, (int)c.output);
                 const int N = x.N, H = x.H, W = x.W, C = x.C, OH = o.H, OW = o.W;
                 const int k = (int)c.params[6], st = (int)c.params[8], pad = (int)c.params[10];

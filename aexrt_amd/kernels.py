@@ -242,6 +242,15 @@ def resize_nearest(x, y, y_slots=None, stream=None) -> None:
                                                _stream(stream)), "resize_nearest")
 
 
+def sppf_maxpool(x, y1, y2, y3, slots=(None, None, None), stream=None) -> None:
+    """y1 = maxpool5(x), y2 = maxpool5(y1), y3 = maxpool5(y2) (stride 1, pad 2) in one kernel."""
+    n, h, w, c = x.shape
+    xv = view(x)
+    v1, v2, v3 = (view(t, sl) for t, sl in zip((y1, y2, y3), slots))
+    check(_lib.lib().aexrt_hip_sppf_maxpool(ctypes.byref(xv), ctypes.byref(v1), ctypes.byref(v2), ctypes.byref(v3),
+                                            n, c, h, w, _stream(stream)), "sppf_maxpool")
+
+
 def add(a, b, y, y_slots=None, stream=None) -> None:
     n, h, w, c = a.shape
     av, bv, yv = view(a), view(b), view(y, y_slots)

@@ -199,6 +199,14 @@ int aexrt_hip_copy(const AexrtHipTensorView* src, const AexrtHipTensorView* dst,
 int aexrt_hip_maxpool(const AexrtHipTensorView* x, const AexrtHipTensorView* y, uint32_t batch,
                       uint32_t channels, uint32_t in_h, uint32_t in_w, uint32_t out_h,
                       uint32_t out_w, uint32_t kernel, uint32_t stride, uint32_t pad, void* stream);
+/* SPPF's three chained MAXPOOL commands (5x5, stride 1, pad 2; RT's MAXPOOL
+ * replay, invoked three times in a row) in one pass: y1 = pool(x), y2 =
+ * pool(y1), y3 = pool(y2), with their amax slots.  No reference counterpart as
+ * one call (the runtime folds the three commands into it); y1..y3 share one
+ * geometry (slices of one concat tensor). */
+int aexrt_hip_sppf_maxpool(const AexrtHipTensorView* x, const AexrtHipTensorView* y1,
+                           const AexrtHipTensorView* y2, const AexrtHipTensorView* y3, uint32_t batch,
+                           uint32_t channels, uint32_t h, uint32_t w, void* stream);
 int aexrt_hip_resize_nearest(const AexrtHipTensorView* x, const AexrtHipTensorView* y,
                              uint32_t batch, uint32_t channels, uint32_t in_h, uint32_t in_w,
                              uint32_t out_h, uint32_t out_w, void* stream);

@@ -497,6 +497,48 @@ def test_winograd_parity(cuda, case):
     assert err <= allowed, (err, allowed)
 
 
+@pytest.mark.parametrize("n,c,h,w", [(2, 32, 10, 10), (1, 128, 20, 20), (3, 16, 13, 7), (1, 64, 1, 5)])
+def test_sppf_maxpool_equals_three_pools(cuda, n, c, h, w):
+    """The fused SPPF kernel writes exactly the three chained 5x5 pools (and
+    their amax slots) into slices of one concat tensor."""
+    import torch
+
+    rng = np.random.default_rng(71 + h)
+    x = O.round_f16(rng.standard_normal((n, c, h, w)).astype(np.float32) * 3)
+    x[:, :, 0, 0] = -1e4  # a large negative corner pixel must not leak through the padding
+    xd = _dev_nhwc(x, cuda)
+    cat = torch.zeros((n, h, w, 4 * c), dtype=torch.float16, device=cuda)
+    slots = K.new_slots(4 * c, cuda, stripes=8)
+    g = c // 16
+    K.sppf_maxpool(xd, cat[..., c:2 * c], cat[..., 2 * c:3 * c], cat[..., 3 * c:],
+                   slots=(slots[:, g:2 * g], slots[:, 2 * g:3 * g], slots[:, 3 * g:]))
+    torch.cuda.synchronize()
+    got = nhwc_to_nchw(cat.float().cpu().numpy())
+    p1 = O.maxpool(x, 5, 1, 2)
+    p2 = O.maxpool(p1, 5, 1, 2)
+    p3 = O.maxpool(p2, 5, 1, 2)
+    np.testing.assert_array_equal(got[:, c:2 * c], p1)
+    np.testing.assert_array_equal(got[:, 2 * c:3 * c], p2)
+    np.testing.assert_array_equal(got[:, 3 * c:], p3)
+    assert not got[:, :c].any()
+    want = np.concatenate([np.zeros((n, c, h, w), np.float32), p1, p2, p3], axis=1)
+    m = K.slots_max(slots)
+    np.testing.assert_array_equal(m, [np.float32(np.abs(want[:, k * 16:(k + 1) * 16]).max()).view(np.uint32)
+                                      for k in range(4 * g)])
+
+
+def test_resize_nearest_general_scale(cuda):
+    """Non-2x scales use the general kernel: floor(o * in / out) sources."""
+    import torch
+
+    rng = np.random.default_rng(72)
+    x = O.round_f16(rng.standard_normal((2, 16, 5, 7)).astype(np.float32))
+    up = torch.empty((2, 15, 14, 16), dtype=torch.float16, device=cuda)
+    K.resize_nearest(_dev_nhwc(x, cuda), up)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(nhwc_to_nchw(up.float().cpu().numpy()), O.resize_nearest(x, 15, 14))
+
+
 def test_glue_ops(cuda):
     import torch
 
