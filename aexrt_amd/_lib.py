@@ -107,6 +107,11 @@ _SIGS = {
     "aexrt_hip_amax_nchw": (c_int, [_vp, c_uint32, c_uint32, c_uint32, c_uint32, _vp, _vp]),
     "aexrt_hip_quantize": (c_int, [POINTER(TensorView), c_uint32, c_uint32, c_uint32, c_uint32, _vp, _vp]),
     "aexrt_hip_quant_pack_nchw": (c_int, [_vp, c_uint32, c_uint32, c_uint32, c_uint32, _vp, c_uint32, _vp, _vp]),
+    "aexrt_hip_amax_strips_nhwc": (c_int, [POINTER(TensorView), c_uint32, c_uint32, c_uint32, c_uint32, _vp,
+                                           _vp]),
+    "aexrt_hip_quant_fused_pg16": (c_int, [_vp, c_uint32, c_uint32, c_uint32, c_uint32, _vp, _vp, _vp]),
+    "aexrt_hip_conv2d_int8_pg16": (c_int, [POINTER(ConvDesc), c_uint32, c_uint32, _vp, _vp, _vp, _vp, _vp, _vp,
+                                           _vp]),
     "aexrt_hip_conv_weight_bytes": (c_int, [POINTER(ConvDesc), c_uint32, POINTER(c_uint64)]),
     "aexrt_hip_pack_conv_weight": (c_int, [POINTER(ConvDesc), c_uint32, c_uint32, _vp, c_uint64, _vp,
                                            c_uint64, _vp]),

@@ -311,6 +311,86 @@ int aexrt_hip_conv2d(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t f
     return launch_conv(p, algorithm, static_cast<hipStream_t>(stream)) ? 1 : 0;
 }
 
+int aexrt_hip_conv2d_int8_pg16(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t flags,
+                               const uint32_t* packed, const uint32_t* amax, const void* weight, const float* w_scale,
+                               const float* bias, void* y, void* stream) {
+    if (!desc || !packed || !amax || !weight || !w_scale || !bias || !y) {
+        set_error("conv2d_int8_pg16: null argument");
+        return 0;
+    }
+    const AexrtConv2DDesc& d = *desc;
+    if (!is_int8_algorithm(algorithm) || !generic_shape_ok(d) || !can_use_int8(d, int8_kernel_elems(algorithm)) ||
+        (algorithm == 52u && d.stride_h != 1) || (algorithm == 53u && d.stride_h != 2)) {
+        set_error("conv2d_int8_pg16: descriptor is not eligible for the int8 kernel id");
+        return 0;
+    }
+    if (d.batch == 0 || d.in_channels % 16 || d.in_channels > 4096 || d.out_h == 0 || d.out_w == 0 ||
+        (flags & ~(AEXRT_HIP_CONV_SILU | AEXRT_HIP_CONV_OUT_F32))) {
+        set_error("conv2d_int8_pg16: needs in_channels % 16 == 0 (<= 4096) and flags SILU / OUT_F32 only");
+        return 0;
+    }
+    const int64_t m = (int64_t)d.batch * d.out_h * d.out_w;
+    if (m > INT32_MAX / 2) {
+        set_error("conv2d_int8_pg16: too many output positions");
+        return 0;
+    }
+    const WeightGeom g = weight_geom(d, algorithm);
+    ConvParams p{};
+    p.x = packed;
+    p.loader = kLoaderPackedNc4;
+    p.x_slots = SlotRef{const_cast<uint32_t*>(amax) + 1, 1u, 0u};
+    p.x_nslots = (int)(d.in_channels / 16);
+    p.w = weight;
+    p.Kp = (int)g.kp;
+    p.OCp = (int)g.ocp;
+    p.w_scale = w_scale;
+    p.bias = bias;
+    p.y = y;
+    p.N = (int)d.batch;
+    p.H = (int)d.in_h;
+    p.W = (int)d.in_w;
+    p.C = (int)d.in_channels;
+    p.OH = (int)d.out_h;
+    p.OW = (int)d.out_w;
+    p.OC = (int)d.out_channels;
+    p.KH = (int)d.kernel_h;
+    p.KW = (int)d.kernel_w;
+    p.S = (int)d.stride_h;
+    p.P = (int)d.pad_top;
+    p.K = p.KH * p.KW * p.C;
+    p.M = (int)m;
+    p.flags = (int)(flags & (AEXRT_HIP_CONV_SILU | AEXRT_HIP_CONV_OUT_F32)) | kConvPg16 | kConvOutNchw;
+    return check_hip(launch_conv_int8_pg16(p, static_cast<hipStream_t>(stream)), "conv2d_int8_pg16") ? 1 : 0;
+}
+
+int aexrt_hip_amax_strips_nhwc(const AexrtHipTensorView* x, uint32_t batch, uint32_t height, uint32_t width,
+                               uint32_t channels, uint32_t* out, void* stream) {
+    if (!x || !x->data || !out || channels % 16 || x->c_stride % 8 || x->n_stride % 8 || batch == 0) {
+        set_error("amax_strips_nhwc: bad view (need C % 16 == 0, 8-element strides, an output)");
+        return 0;
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (!check_hip(launch_fill_u32(out, channels / 16, 0u, s), "amax_strips_nhwc zero")) return 0;
+    return check_hip(launch_amax_strips_nhwc(static_cast<const __half*>(x->data), x->n_stride, x->c_stride,
+                                             (int)batch, (int)(height * width), (int)channels, out, s),
+                     "amax_strips_nhwc")
+               ? 1
+               : 0;
+}
+
+int aexrt_hip_quant_fused_pg16(const void* x, uint32_t is_f16, uint32_t batch, uint32_t channels, uint32_t plane,
+                               uint32_t* packed, uint32_t* amax, void* stream) {
+    if (!x || !packed || !amax || channels % 16 || channels == 0 || batch == 0 || plane == 0) {
+        set_error("quant_fused_pg16: null argument or channels % 16 != 0");
+        return 0;
+    }
+    return check_hip(launch_quant_fused_pg16(x, is_f16 != 0, (int)batch, (int)channels, (int)plane, packed, amax,
+                                             static_cast<hipStream_t>(stream)),
+                     "quant_fused_pg16")
+               ? 1
+               : 0;
+}
+
 int aexrt_hip_amax_slots(const AexrtHipTensorView* x, uint32_t batch, uint32_t height, uint32_t width,
                          uint32_t channels, void* stream) {
     if (!x || !x->data || !x->amax_slots || channels % 16 || x->c_stride % 8 || x->n_stride % 8 ||

@@ -107,6 +107,12 @@ bool build_conv_params(const AexrtConv2DDesc& d, uint32_t algorithm, uint32_t fl
         why = "acc_out is only produced by int8 kernels";
         return false;
     }
+    const bool pg16 = (flags & AEXRT_HIP_CONV_INT8_PG16) != 0;
+    if (pg16 && (!int8 || acc_out || nchw || d.in_channels > 4096)) {
+        why = "pg16 (per-group activation scales) needs an int8 algorithm, in_channels <= 4096, no acc_out and an "
+              "NHWC input";
+        return false;
+    }
     const WeightGeom g = weight_geom(d, algorithm);
     p = ConvParams{};
     p.x = x.data;
@@ -150,11 +156,13 @@ bool build_conv_params(const AexrtConv2DDesc& d, uint32_t algorithm, uint32_t fl
     }
     p.M = (int)m;
     p.flags = (int)(flags & (AEXRT_HIP_CONV_SILU | AEXRT_HIP_CONV_RESIDUAL | AEXRT_HIP_CONV_OUT_F32));
+    if (pg16) p.flags |= kConvPg16;
     return true;
 }
 
 bool launch_conv(const ConvParams& p, uint32_t algorithm, hipStream_t stream) {
     if (is_winograd_algorithm(algorithm)) return check_hip(launch_winograd_f2x2(p, stream), "winograd conv");
+    if (p.flags & kConvPg16) return check_hip(launch_conv_int8_pg16(p, stream), "int8 pg16 conv");
     return check_hip(launch_conv_igemm(p, is_int8_algorithm(algorithm), stream),
                      is_int8_algorithm(algorithm) ? "int8 conv" : "fp16 conv");
 }

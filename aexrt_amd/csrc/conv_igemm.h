@@ -265,7 +265,7 @@ __device__ __forceinline__ void tile_store(const ConvParams& p, const AccT (&acc
             }
             if constexpr (INT8) {
                 if (p.acc_out) {
-                    const v4i av{acc[j][q][0], acc[j][q][1], acc[j][q][2], acc[j][q][3]};
+                    const v4i av{(int)acc[j][q][0], (int)acc[j][q][1], (int)acc[j][q][2], (int)acc[j][q][3]};
                     __builtin_amdgcn_raw_buffer_store_b128(av, racc, ok ? (uint32_t)(mo[q] * p.OC + oc0) * 4u : kOob,
                                                            0, 0);
                 }

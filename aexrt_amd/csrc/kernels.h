@@ -38,6 +38,8 @@ enum ConvFlags : int {
     kConvSilu = 1,      // SiLU after bias
     kConvResidual = 2,  // + residual tensor after the activation
     kConvOutF32 = 4,    // store fp32 instead of fp16
+    kConvPg16 = 16,     // int8 with per-16-input-channel activation scales (pg16)
+    kConvOutNchw = 32,  // pg16 only: dense NCHW output (the reference's layout)
 };
 
 // Views whose element (position m, channel c) sits at m * c_stride + c: the
@@ -52,6 +54,7 @@ enum LinearViews : int {
 enum Loader : int {
     kLoaderNhwc = 0,     // fp16 NHWC activation view, C % 8 == 0
     kLoaderNchwF32 = 1,  // fp32 NCHW network input, c_real <= 4 channels read as C = 8 (zero padded)
+    kLoaderPackedNc4 = 2,  // pg16 only: the reference's packed NC/4HW4 int8 words
 };
 
 // Kernel and tile of one conv launch.  kind 0: chosen by the heuristics;
@@ -145,6 +148,12 @@ hipError_t launch_winograd_f2x2(const ConvParams& p, hipStream_t stream);
 // (atomicMax, caller clears).  C % 16 == 0.
 hipError_t launch_amax_slots_nhwc(const __half* x, int64_t nstride, int32_t cstride, int N, int HW,
                                   int C, SlotRef slots, hipStream_t stream);
+// Strips of the reference's amax buffer over an NHWC fp16 view: max|x| of
+// image n, group g folded into slots[(n * C/16 + g) / N], i.e. memory strip
+// (n*C + 16g) / (16N) of the NCHW layout (slots[s] = the reference's
+// amax[1 + s]).  C % 16 == 0; the caller clears the C/16 words.
+hipError_t launch_amax_strips_nhwc(const __half* x, int64_t nstride, int32_t cstride, int N, int HW, int C,
+                                   uint32_t* slots, hipStream_t stream);
 // The reference's amax buffer over an NCHW tensor (fp16 or fp32): slot 0 =
 // whole tensor, slot 1+g = memory strip [g*16*N*HW, (g+1)*16*N*HW).
 hipError_t launch_amax_strips_nchw(const void* x, bool f16, int N, int C, int HW, uint32_t* slots,
@@ -155,6 +164,17 @@ hipError_t launch_quantize_nhwc(const __half* x, int64_t nstride, int32_t cstrid
 // The reference's NC/4HW4 pack (per-tensor slot 0, or per_group slots 1+icg/4).
 hipError_t launch_quant_pack_nchw(const void* x, bool f16, int N, int C, int HW, const uint32_t* slots,
                                   bool per_group, uint32_t* packed, hipStream_t stream);
+
+// pg16 int8 conv (native/aexrt_d3d12_runtime.cpp:4770-4923): 1x1 or 3x3,
+// C % 16 == 0.  x_slots slot g = amax of input channel group g.  Loader
+// kLoaderNhwc (fp16 view, quantized in the kernel per group) or
+// kLoaderPackedNc4 (x = the reference's packed words); output an NHWC view
+// (epilogue flags as the per-tensor kernels) or dense NCHW (kConvOutNchw).
+hipError_t launch_conv_int8_pg16(const ConvParams& p, hipStream_t stream);
+// The reference's fused pg16 amax + pack (RT:4083-4149) of an NCHW tensor:
+// amax[1 + g] = max over image 0's channels 16g..16g+15, packed NC/4HW4.
+hipError_t launch_quant_fused_pg16(const void* x, bool f16, int N, int C, int HW, uint32_t* packed,
+                                   uint32_t* amax, hipStream_t stream);
 
 // ---- glue ------------------------------------------------------------------
 hipError_t launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t stream);

@@ -114,7 +114,7 @@ __device__ __forceinline__ float max8_abs(const uint4& v) {
 
 __global__ __launch_bounds__(kThreads) void amax_slots_nhwc_kernel(
     const __half* x, int64_t nstride, int32_t cstride, int HW, int C, int chunks, ChunkDivs dv,
-    SlotRef slots) {
+    SlotRef slots, int strip_n) {
     __shared__ uint32_t ls[kMaxSlots];
     const int CC = C / 8;
     const int G = C / 16;
@@ -125,7 +125,8 @@ __global__ __launch_bounds__(kThreads) void amax_slots_nhwc_kernel(
         int n, pp, cc;
         chunk_split((uint32_t)e, CC, HW, dv, n, pp, cc);
         const uint4 v = *reinterpret_cast<const uint4*>(x + n * nstride + (int64_t)pp * cstride + cc * 8);
-        gm.add(cc >> 1, max8_abs(v), ls);
+        // strip_n > 0: the reference's NCHW memory strip of (n, group)
+        gm.add(strip_n ? (n * G + (cc >> 1)) / strip_n : cc >> 1, max8_abs(v), ls);
     }
     gm.flush(ls);
     slots_flush(ls, G, slots);
@@ -533,7 +534,17 @@ hipError_t launch_amax_slots_nhwc(const __half* x, int64_t nstride, int32_t cstr
     const int64_t chunks = (int64_t)N * HW * (C / 8);
     if (chunks >= INT32_MAX) return hipErrorInvalidValue;
     hipLaunchKernelGGL(amax_slots_nhwc_kernel, dim3(grid_cols(chunks, C)), dim3(kThreads), 0, stream, x,
-                       nstride, cstride, HW, C, (int)chunks, chunk_divs(C, HW), slots);
+                       nstride, cstride, HW, C, (int)chunks, chunk_divs(C, HW), slots, 0);
+    return hipGetLastError();
+}
+
+hipError_t launch_amax_strips_nhwc(const __half* x, int64_t nstride, int32_t cstride, int N, int HW, int C,
+                                   uint32_t* slots, hipStream_t stream) {
+    if (C % 16 != 0 || C / 16 > kMaxSlots || N < 1) return hipErrorInvalidValue;
+    const int64_t chunks = (int64_t)N * HW * (C / 8);
+    if (chunks >= INT32_MAX) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(amax_slots_nhwc_kernel, dim3(grid_cols(chunks, C)), dim3(kThreads), 0, stream, x,
+                       nstride, cstride, HW, C, (int)chunks, chunk_divs(C, HW), SlotRef{slots, 1u, 0u}, N);
     return hipGetLastError();
 }
 

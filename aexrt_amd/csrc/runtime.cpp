@@ -83,6 +83,8 @@ struct ConvState {
     void* w = nullptr;
     float* scale = nullptr;
     float* bias = nullptr;
+    bool pg16 = false;            // int8 with per-16-input-channel scales (plan flag 16)
+    uint32_t* strips = nullptr;   // pg16 at N > 1: the reference's strip amax of the input
 };
 
 struct Step {
@@ -858,18 +860,54 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                     flags |= AEXRT_HIP_CONV_RESIDUAL;
                     rvw = view_of(m, cs.residual_value);
                 }
+                // pg16: group g's scale comes from the reference's memory strip
+                // g of the NCHW tensor, which is channel group g at N = 1 (the
+                // input's own slots); at N > 1 the strips mix images and are
+                // taken by a separate pass into a buffer of this conv
+                AexrtHipTensorView strip_src{};
+                int strip_n = 0, strip_hw = 0, strip_c = 0;
+                if (cs.pg16) {
+                    flags |= AEXRT_HIP_CONV_INT8_PG16;
+                    if (d.batch > 1) {
+                        strip_src = xvw;
+                        strip_n = (int)d.batch;
+                        strip_hw = (int)(d.in_h * d.in_w);
+                        strip_c = (int)d.in_channels;
+                        cs.strips = static_cast<uint32_t*>(dev_alloc(m, d.in_channels / 16 * 4));
+                        if (!cs.strips) return fail(m, "out of device memory for pg16 strips");
+                        xvw.amax_slots = cs.strips;
+                        xvw.amax_stripes = 1;
+                        xvw.amax_stripe_stride = 0;
+                    }
+                }
                 ConvParams p{};
                 std::string why;
                 if (!build_conv_params(d, cs.algorithm, flags, xvw, cs.w, cs.scale, cs.bias,
                                        cs.fused_residual ? &rvw : nullptr, yvw, nullptr, p, why))
                     return fail(m, "command " + std::to_string(ci) + ": " + why);
                 const uint32_t alg = cs.algorithm;
-                if (m->autotune && !is_winograd_algorithm(alg) && !tune_conv(m, p, is_int8_algorithm(alg)))
-                    return false;
-                m->steps.push_back(Step{(int)ci, conv_label(c, ci, alg), [p, alg](hipStream_t s) {
-                                            if (is_winograd_algorithm(alg)) return launch_winograd_f2x2(p, s);
-                                            return launch_conv_igemm(p, is_int8_algorithm(alg), s);
-                                        }});
+                if (cs.pg16) {
+                    uint32_t* strips = cs.strips;
+                    m->steps.push_back(Step{(int)ci, conv_label(c, ci, alg) + " pg16", [=](hipStream_t s) {
+                                                if (strips) {
+                                                    hipError_t e = launch_fill_u32(strips, strip_c / 16, 0u, s);
+                                                    if (e == hipSuccess)
+                                                        e = launch_amax_strips_nhwc(
+                                                            static_cast<const __half*>(strip_src.data),
+                                                            strip_src.n_stride, strip_src.c_stride, strip_n,
+                                                            strip_hw, strip_c, strips, s);
+                                                    if (e != hipSuccess) return e;
+                                                }
+                                                return launch_conv_int8_pg16(p, s);
+                                            }});
+                } else {
+                    if (m->autotune && !is_winograd_algorithm(alg) && !tune_conv(m, p, is_int8_algorithm(alg)))
+                        return false;
+                    m->steps.push_back(Step{(int)ci, conv_label(c, ci, alg), [p, alg](hipStream_t s) {
+                                                if (is_winograd_algorithm(alg)) return launch_winograd_f2x2(p, s);
+                                                return launch_conv_igemm(p, is_int8_algorithm(alg), s);
+                                            }});
+                }
                 if (!(m->vals[xv].is_input && m->input_nchw_direct)) m->steps.back().reads.push_back(V[xv].pl.root);
                 if (cs.fused_residual) m->steps.back().reads.push_back(V[cs.residual_value].pl.root);
                 m->steps.back().writes = {V[yv].pl.root};
@@ -1152,6 +1190,9 @@ bool build_model(AexrtYoloModel* m) {
             return fail(m, "command " + std::to_string(ci) + ": conv geometry not supported (groups/dilation)");
         cs.planned = (c.plan_flags & 1u) ? c.plan_kernel : c.planned_kernel;
         cs.algorithm = resolve_algorithm(m, ci, cs.planned);
+        // plan flag 16 (engine.py:85-96): the reference packs and convolves
+        // with per-16-input-channel scales (RT:4770-4923)
+        cs.pg16 = (c.plan_flags & kPlanFlagInt8PerGroup) != 0 && is_int8_algorithm(cs.algorithm);
     }
     if (!plan_memory(m, m->copies)) return false;
     // arena

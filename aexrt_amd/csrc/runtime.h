@@ -27,6 +27,11 @@ struct EngineValue {
     uint32_t shape4[4] = {1, 1, 1, 1};
 };
 
+// Kernel-plan record flags (src/aexrt/engine.py:85-96): bit 0 authoritative,
+// bit 4 int8 with per-16-input-channel activation scales (pg16).
+constexpr uint32_t kPlanFlagAuthoritative = 1u;
+constexpr uint32_t kPlanFlagInt8PerGroup = 16u;
+
 struct EngineCommand {
     uint32_t kind = 0, output = 0, planned_kernel = 0, precision = 0;
     std::vector<uint32_t> inputs, params;

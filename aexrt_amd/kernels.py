@@ -20,6 +20,7 @@ SILU = 1
 RESIDUAL = 2
 OUT_F32 = 4
 IN_NCHW_F32 = 8
+INT8_PG16 = 16
 
 SRC_RAW_F32 = 0
 SRC_RAW_F16 = 1
@@ -117,6 +118,39 @@ def quant_pack_nchw(x, amax, per_group: bool = False, stream=None):
                                                 amax.data_ptr(), int(per_group), packed.data_ptr(),
                                                 _stream(stream)), "quant_pack_nchw")
     return packed
+
+
+def amax_strips_nhwc(x, stream=None):
+    """pg16 group amax of an NHWC fp16 tensor: word s = the reference's amax[1 + s] (NCHW memory strip s)."""
+    import torch
+
+    n, h, w, c = x.shape
+    out = torch.empty(c // 16, dtype=torch.int32, device=x.device)
+    v = view(x)
+    check(_lib.lib().aexrt_hip_amax_strips_nhwc(ctypes.byref(v), n, h, w, c, out.data_ptr(), _stream(stream)),
+          "amax_strips_nhwc")
+    return out
+
+
+def quant_fused_pg16(x, stream=None):
+    """The reference's fused pg16 amax + pack of an NCHW tensor: (packed words, amax buffer; amax[0] untouched = 0)."""
+    import torch
+
+    n, c, h, w = x.shape
+    packed = torch.empty(n * (c // 4) * h * w, dtype=torch.int32, device=x.device)
+    amax = torch.zeros(c // 16 + 1, dtype=torch.int32, device=x.device)
+    check(_lib.lib().aexrt_hip_quant_fused_pg16(x.data_ptr(), int(x.dtype == torch.float16), n, c, h * w,
+                                                 packed.data_ptr(), amax.data_ptr(), _stream(stream)),
+          "quant_fused_pg16")
+    return packed, amax
+
+
+def conv2d_int8_pg16(pc: "PreparedConv", packed, amax, y, *, flags: int = SILU, stream=None) -> None:
+    """pg16 conv on the reference's operands: packed NC/4HW4 words + amax buffer -> dense NCHW y."""
+    d = ConvDesc.from_params(pc.params)
+    check(_lib.lib().aexrt_hip_conv2d_int8_pg16(
+        ctypes.byref(d), pc.algorithm, flags, packed.data_ptr(), amax.data_ptr(), pc.weight.data_ptr(),
+        _ptr(pc.w_scale), pc.bias.data_ptr(), y.data_ptr(), _stream(stream)), "conv2d_int8_pg16")
 
 
 def can_use_conv_int8(params: Sequence[int], kernel_elems: int) -> bool:

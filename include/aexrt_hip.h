@@ -88,6 +88,10 @@ typedef struct AexrtHipTensorView {
                                        * <= 4 channels, read as in_channels = 8 (weights
                                        * packed for 8, zero past c); fp16 3x3 pad-1 SiLU
                                        * convs with fp16 output only */
+#define AEXRT_HIP_CONV_INT8_PG16 16u  /* int8 with per-16-input-channel activation scales
+                                       * (plan flag 16, native/aexrt_d3d12_runtime.cpp:
+                                       * 4770-4923): slot g of x->amax_slots is group g's
+                                       * amax (the reference's amax[1 + g]); no acc_out */
 
 /* Weight source layouts accepted by aexrt_hip_pack_conv_weight: the
  * reference's packed layouts (src/aexrt/engine.py:59-71) plus raw constants. */
@@ -141,6 +145,22 @@ int aexrt_hip_quant_pack_nchw(const void* x, uint32_t is_f16, uint32_t batch, ui
                               uint32_t plane, const uint32_t* amax, uint32_t per_group,
                               uint32_t* packed, void* stream);
 
+/* a1 strips over an NHWC fp16 view, for pg16 scales: max|x| of image n and
+ * channel group g is folded into out[(n * C/16 + g) / N], which is the
+ * reference's amax[1 + s] of memory strip s of 16*N*H*W elements of the same
+ * tensor in NCHW layout (native/aexrt_d3d12_runtime.cpp:3219-3259).  out
+ * (C/16 words) is cleared by this call; x->amax_slots is not used. */
+int aexrt_hip_amax_strips_nhwc(const AexrtHipTensorView* x, uint32_t batch, uint32_t height,
+                               uint32_t width, uint32_t channels, uint32_t* out, void* stream);
+
+/* a3: the reference's fused pg16 amax + pack of an NCHW tensor (fp16 when
+ * is_f16, else fp32), native/aexrt_d3d12_runtime.cpp:4083-4149: amax[1 + g]
+ * = max|x| over channels 16g..16g+15 of image 0 (used for every image, as
+ * in the reference), packed = NC/4HW4 int8 words of every image quantized
+ * with 127/amax[1 + g].  amax[0] is not written.  C % 16 == 0. */
+int aexrt_hip_quant_fused_pg16(const void* x, uint32_t is_f16, uint32_t batch, uint32_t channels,
+                               uint32_t plane, uint32_t* packed, uint32_t* amax, void* stream);
+
 /* a4 (load side): size and host-side repack of a conv weight into the
  * layout the kernel of `algorithm` consumes.  algorithm is the reference's
  * AexrtTileFlowConvAlgorithm id (native/aexrt_d3d12_runtime.cpp:8881-8940):
@@ -165,6 +185,18 @@ int aexrt_hip_conv2d(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t f
                      const AexrtHipTensorView* x, const void* weight, const float* w_scale,
                      const float* bias, const AexrtHipTensorView* residual,
                      const AexrtHipTensorView* y, int32_t* acc_out, void* stream);
+
+/* a6, reference form: the pg16 int8 conv on the reference's own operands,
+ * native/aexrt_d3d12_runtime.cpp:4770-4923 (dispatch 24152-24258): packed =
+ * NC/4HW4 int8 words (aexrt_hip_quant_pack_nchw with per_group = 1, or
+ * aexrt_hip_quant_fused_pg16), amax = that buffer (amax[1 + g] scales group
+ * g), weight packed by aexrt_hip_pack_conv_weight for algorithm 51/52/53,
+ * w_scale/bias per output channel.  y = dense NCHW, fp16, or fp32 with
+ * AEXRT_HIP_CONV_OUT_F32; flags also AEXRT_HIP_CONV_SILU.  in_channels % 16
+ * == 0 (<= 4096). */
+int aexrt_hip_conv2d_int8_pg16(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t flags,
+                               const uint32_t* packed, const uint32_t* amax, const void* weight,
+                               const float* w_scale, const float* bias, void* y, void* stream);
 
 /* a10: int8 eligibility of a conv for kernel family kernel_elems (1 or 9),
  * native/aexrt_d3d12_runtime.cpp:9399-9422, plus this backend's own

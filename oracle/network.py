@@ -13,8 +13,8 @@ from typing import Dict, Iterable, Optional
 
 import numpy as np
 
-from . import (amax, conv_desc, conv_int8_acc, conv_int8_epilogue, cpu_conv2d, maxpool, quantize,
-               resize_nearest, round_f16, weight_quant)
+from . import (amax, amax_slots, conv_desc, conv_int8_acc, conv_int8_epilogue, conv_int8_pg, cpu_conv2d, maxpool,
+               quant_pack, quantize, resize_nearest, round_f16, weight_quant)
 
 
 def _silu_map(graph):
@@ -38,14 +38,23 @@ def _silu_map(graph):
 
 
 def conv_layer(x: np.ndarray, w: np.ndarray, b: np.ndarray, attrs: dict, *, int8: bool, silu: bool,
-               threads: int = 1) -> np.ndarray:
-    """One conv of the network on an fp16-valued input, fp32 result (unrounded)."""
+               threads: int = 1, pg16: bool = False) -> np.ndarray:
+    """One conv of the network on an fp16-valued input, fp32 result (unrounded).
+
+    pg16: the reference's per-group path (plan flag 16): strip amax
+    (RT:3219-3259), per-group pack (RT:3314-3346), pg16 conv (RT:4770-4923).
+    """
     n, c, h, wd = x.shape
     k = int(w.shape[2])
     s = int(attrs.get("strides", [1, 1])[0])
     p = int(attrs.get("pads", [0, 0, 0, 0])[0])
     desc = conv_desc(n, c, h, wd, int(w.shape[0]), k, s, p)
     bias = round_f16(b)
+    if int8 and pg16:
+        slots = amax_slots(x)
+        packed = quant_pack(x, slots, per_group=True)
+        qw, ws = weight_quant(w, fp16_round=True)
+        return conv_int8_pg(packed, qw, desc, slots, ws, bias, silu)
     if int8:
         a = amax(x)
         qa = quantize(x, a)

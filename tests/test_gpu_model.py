@@ -74,6 +74,7 @@ def _layer_check(model: NativeHipYoloModel, graph: Graph, plan: dict, tol=1e-2):
             continue
         pk = plan["plans"][i]["planned_kernel"]
         int8 = pk in E.INT8_KERNELS and E.int8_eligible(c["params"])
+        pg16 = bool(plan["plans"][i]["flags"] & E.PLAN_FLAG_INT8_PERGROUP)
         xin, wid, bid = c["inputs"]
         wname = names[wid]
         node = convs[wname.rsplit(".w", 1)[0]]
@@ -84,7 +85,7 @@ def _layer_check(model: NativeHipYoloModel, graph: Graph, plan: dict, tol=1e-2):
         if xin == replay["input_value"]:
             x = O.round_f16(x)
         y_ref = ON.conv_layer(x, graph.constants[wname], graph.constants[names[bid]], node.attrs, int8=int8,
-                              silu=c["kind"] == "CONV_SILU")
+                              silu=c["kind"] == "CONV_SILU", pg16=pg16)
         out = c["output"]
         rank_y, _ = model.value_info(out)
         if rank_y == 0:  # fused into the residual add that consumes it
@@ -141,6 +142,28 @@ def test_c2f_w8a8_block_layer_parity(cuda, batch):
         m.run(x)
         checked, _ = _layer_check(m, g, plan)
         assert checked == 6
+
+
+@pytest.mark.parametrize("batch", [1, 2])
+def test_c2f_w8a8_pg16_block_layer_parity(cuda, batch):
+    """Plan flag 16 on every int8 conv: per-group scales from the reference's strips (image-mixing at N > 1)."""
+    g = _c2f_graph(batch=batch, c=64, dim=20, seed=6)
+    replay = E.lower_graph(g)
+    algo = E.w8a8_algo_map(replay)
+    pg = sorted(algo)
+    plan = E.compile_plan(g, precision="fp16", algo_overrides=algo, int8_pergroup=pg)
+    assert sum(1 for p in plan["plans"] if p["flags"] & E.PLAN_FLAG_INT8_PERGROUP) == 6
+    data = E.build_aexrt_engine(g, precision="fp16", algo_overrides=algo, int8_pergroup=pg)
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((batch, 64, 20, 20)).astype(np.float32)
+    x[:, 32:] *= 4.0
+    with NativeHipYoloModel(data) as m:
+        m.run(x)
+        out1 = m.output()
+        checked, _ = _layer_check(m, g, plan)
+        assert checked == 6
+        m.run(x)
+        np.testing.assert_array_equal(m.output(), out1)
 
 
 def test_yolov8n_160_w8a8_layers_and_end_to_end(cuda):
