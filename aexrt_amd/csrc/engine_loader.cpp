@@ -2,6 +2,7 @@
 // against the buffer before it is read, every section's CRC32 is verified,
 // and an engine whose plan disagrees with its packed weights is rejected
 // (the loader's fail-closed rules, native/aexrt_d3d12_runtime.cpp:17560-18164).
+#include <algorithm>
 #include <cstring>
 #include <string>
 
@@ -41,6 +42,76 @@ uint32_t crc32_ieee(const uint8_t* data, size_t size) {
     uint32_t c = 0xFFFFFFFFu;
     for (size_t i = 0; i < size; ++i) c = table[(c ^ data[i]) & 0xFFu] ^ (c >> 8);
     return c ^ 0xFFFFFFFFu;
+}
+
+bool expand_fused_commands(Engine& e, std::string& err) {
+    std::vector<EngineCommand> cmds;
+    std::vector<uint32_t> src;
+    cmds.reserve(e.commands.size() + 16);
+    for (size_t i = 0; i < e.commands.size(); ++i) {
+        const EngineCommand& c = e.commands[i];
+        if (c.kind != kCmdConcatConv1x1) {
+            cmds.push_back(c);
+            src.push_back((uint32_t)i);
+            continue;
+        }
+        const std::vector<uint32_t>& p = c.params;
+        if (c.inputs.size() < 3 || p.size() < 5 + (c.inputs.size() - 2)) {
+            err = "command " + std::to_string(i) + ": malformed CONCAT_CONV1X1";
+            return false;
+        }
+        const size_t k = c.inputs.size() - 2;
+        const uint32_t N = p[0], H = p[1], W = p[2], OC = p[3];
+        uint64_t sum = 0;
+        for (size_t j = 0; j < k; ++j) sum += p[5 + j];
+        if (N == 0 || H == 0 || W == 0 || OC == 0 || sum == 0 || sum > 0xFFFFFFu || k > 8) {
+            err = "command " + std::to_string(i) + ": bad CONCAT_CONV1X1 geometry";
+            return false;
+        }
+        // the concatenated input as a value of its own
+        const uint32_t vid = (uint32_t)e.values.size();
+        EngineValue v;
+        v.id = vid;
+        v.flags = 0;
+        v.elements = uint64_t(N) * sum * H * W;
+        v.shape4[0] = N, v.shape4[1] = (uint32_t)sum, v.shape4[2] = H, v.shape4[3] = W;
+        e.values.push_back(v);
+        e.constants.push_back(EngineConstant{});
+        e.packed.push_back(EnginePacked{});
+        EngineCommand cat;
+        cat.kind = kCmdConcat;
+        cat.output = vid;
+        cat.precision = c.precision;
+        cat.inputs.assign(c.inputs.begin(), c.inputs.begin() + k);
+        // engine.py CONCAT params: elements, rank, axis, count, shape4, sizes
+        cat.params = {(uint32_t)std::min<uint64_t>(v.elements, 0xFFFFFFFFu), 4u, 1u, (uint32_t)k, N, (uint32_t)sum, H, W};
+        for (size_t j = 0; j < 8; ++j) cat.params.push_back(p[5 + std::min(j, k - 1)]);
+        cat.params.push_back(0u);
+        cat.params.push_back(0u);
+        cat.plan_flags = kPlanFlagAuthoritative;
+        EngineCommand conv;
+        conv.kind = p[4] ? kCmdConvSilu : kCmdConv;
+        conv.output = c.output;
+        conv.precision = c.precision;
+        conv.inputs = {vid, c.inputs[k], c.inputs[k + 1]};
+        conv.params = {N, (uint32_t)sum, H, W, OC, H, W, 1u, 1u, 1u, 1u, 0u, 0u, 1u, 1u, 1u};
+        // plan kernel 3 = the native fp16 concat + 1x1 kernel on the layout-4
+        // weight (engine.py:1080-1089): the fp16 1x1 kernel id 45 reads that
+        // layout; 1 / 0 (generic fp32 paths) run on the generic kernel
+        const uint32_t kern = c.plan_kernel == 3 ? 45u : 5u;
+        conv.planned_kernel = kern;
+        conv.plan_kernel = kern;
+        conv.plan_precision = c.plan_precision;
+        conv.packed_value = c.packed_value;
+        conv.plan_flags = c.plan_flags;
+        cmds.push_back(std::move(cat));
+        src.push_back((uint32_t)i);
+        cmds.push_back(std::move(conv));
+        src.push_back((uint32_t)i);
+    }
+    e.commands = std::move(cmds);
+    e.src_cmd = std::move(src);
+    return true;
 }
 
 bool parse_engine(const uint8_t* data, size_t size, Engine& out, std::string& err) {

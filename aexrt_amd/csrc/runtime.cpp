@@ -888,7 +888,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                 const uint32_t alg = cs.algorithm;
                 if (cs.pg16) {
                     uint32_t* strips = cs.strips;
-                    m->steps.push_back(Step{(int)ci, conv_label(c, ci, alg) + " pg16", [=](hipStream_t s) {
+                    m->steps.push_back(Step{(int)ci, conv_label(c, e.src_cmd[ci], alg) + " pg16", [=](hipStream_t s) {
                                                 if (strips) {
                                                     hipError_t e = launch_fill_u32(strips, strip_c / 16, 0u, s);
                                                     if (e == hipSuccess)
@@ -903,7 +903,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                 } else {
                     if (m->autotune && !is_winograd_algorithm(alg) && !tune_conv(m, p, is_int8_algorithm(alg)))
                         return false;
-                    m->steps.push_back(Step{(int)ci, conv_label(c, ci, alg), [p, alg](hipStream_t s) {
+                    m->steps.push_back(Step{(int)ci, conv_label(c, e.src_cmd[ci], alg), [p, alg](hipStream_t s) {
                                                 if (is_winograd_algorithm(alg)) return launch_winograd_f2x2(p, s);
                                                 return launch_conv_igemm(p, is_int8_algorithm(alg), s);
                                             }});
@@ -922,7 +922,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                     AexrtHipTensorView s = view_of(m, j.src), dv = view_of_pl(m, j.dst);
                     if (x.C % 8) return fail(m, "command " + std::to_string(ci) + ": concat copy needs C % 8 == 0");
                     const int N = x.N, HW = x.H * x.W, C = x.C;
-                    m->steps.push_back(Step{(int)ci, "cmd#" + std::to_string(ci) + " CONCAT copy", [=](hipStream_t st) {
+                    m->steps.push_back(Step{(int)ci, "cmd#" + std::to_string(e.src_cmd[ci]) + " CONCAT copy", [=](hipStream_t st) {
                                                 return launch_copy_nhwc(static_cast<const __half*>(s.data), s.n_stride,
                                                                         s.c_stride, static_cast<__half*>(dv.data),
                                                                         dv.n_stride, dv.c_stride, N, HW, C,
@@ -952,7 +952,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                     if (a.n_stride == b.n_stride && a.n_stride == d.n_stride && a.c_stride == b.c_stride &&
                         a.c_stride == d.c_stride) {
                         const int N = x.N, H = x.H, W = x.W, C = x.C;
-                        m->steps.push_back(Step{(int)ci, "cmd#" + std::to_string(ci) + " SPPF MAXPOOL x3",
+                        m->steps.push_back(Step{(int)ci, "cmd#" + std::to_string(e.src_cmd[ci]) + " SPPF MAXPOOL x3",
                                                 [=](hipStream_t st) {
                                                     return launch_sppf_maxpool_nhwc(
                                                         static_cast<const __half*>(xv.data), xv.n_stride, xv.c_stride,
@@ -970,7 +970,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                 const int N = x.N, H = x.H, W = x.W, C = x.C, OH = o.H, OW = o.W;
                 const int k = (int)c.params[6], st = (int)c.params[8], pad = (int)c.params[10];
                 if (C % 8) return fail(m, "command " + std::to_string(ci) + ": MAXPOOL needs C % 8 == 0");
-                m->steps.push_back(Step{(int)ci, "cmd#" + std::to_string(ci) + " MAXPOOL", [=](hipStream_t s) {
+                m->steps.push_back(Step{(int)ci, "cmd#" + std::to_string(e.src_cmd[ci]) + " MAXPOOL", [=](hipStream_t s) {
                                             return launch_maxpool_nhwc(static_cast<const __half*>(xv.data), xv.n_stride,
                                                                        xv.c_stride, static_cast<__half*>(yv.data),
                                                                        yv.n_stride, yv.c_stride, N, H, W, C, OH, OW, k,
@@ -986,7 +986,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                 AexrtHipTensorView xv = view_of(m, (int)c.inputs[0]), yv = view_of(m, (int)c.output);
                 const int N = x.N, H = x.H, W = x.W, C = x.C, OH = o.H, OW = o.W;
                 if (C % 8) return fail(m, "command " + std::to_string(ci) + ": RESIZE needs C % 8 == 0");
-                m->steps.push_back(Step{(int)ci, "cmd#" + std::to_string(ci) + " RESIZE", [=](hipStream_t s) {
+                m->steps.push_back(Step{(int)ci, "cmd#" + std::to_string(e.src_cmd[ci]) + " RESIZE", [=](hipStream_t s) {
                                             return launch_resize_nearest_nhwc(
                                                 static_cast<const __half*>(xv.data), xv.n_stride, xv.c_stride,
                                                 static_cast<__half*>(yv.data), yv.n_stride, yv.c_stride, N, H, W, C, OH,
@@ -1003,7 +1003,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                                    yv = view_of(m, (int)c.output);
                 const int N = o.N, HW = o.H * o.W, C = o.C;
                 if (C % 8) return fail(m, "command " + std::to_string(ci) + ": BINARY needs C % 8 == 0");
-                m->steps.push_back(Step{(int)ci, "cmd#" + std::to_string(ci) + " BINARY add", [=](hipStream_t s) {
+                m->steps.push_back(Step{(int)ci, "cmd#" + std::to_string(e.src_cmd[ci]) + " BINARY add", [=](hipStream_t s) {
                                             return launch_add_nhwc(static_cast<const __half*>(av.data), av.n_stride,
                                                                    av.c_stride, static_cast<const __half*>(bv.data),
                                                                    bv.n_stride, bv.c_stride,
@@ -1256,7 +1256,7 @@ AexrtYoloModel* load_from_bytes(AexrtDevice* device, const uint8_t* data, size_t
     AexrtYoloModel* m = new AexrtYoloModel();
     m->device = device;
     std::string err;
-    if (!parse_engine(data, n, m->eng, err)) {
+    if (!parse_engine(data, n, m->eng, err) || !expand_fused_commands(m->eng, err)) {
         set_error(err);
         free_model(m);
         return nullptr;
@@ -1558,7 +1558,7 @@ int aexrt_yolo_conv_plan_info(AexrtYoloModel* m, uint32_t index, AexrtConvPlanIn
         if (!m->convs[ci].is_conv) continue;
         if (k++ != index) continue;
         const EngineCommand& c = m->eng.commands[ci];
-        out->command_index = (uint32_t)ci;
+        out->command_index = m->eng.src_cmd[ci];
         out->kind_is_silu = c.kind == kCmdConvSilu ? 1u : 0u;
         out->desc = desc_of(c);
         out->current_algorithm = m->convs[ci].algorithm;
@@ -1570,8 +1570,14 @@ int aexrt_yolo_conv_plan_info(AexrtYoloModel* m, uint32_t index, AexrtConvPlanIn
     return 0;
 }
 
-int aexrt_yolo_override_conv_algorithm(AexrtYoloModel* m, uint32_t command_index, uint32_t algorithm_id) {
-    if (!m || command_index >= m->convs.size() || !m->convs[command_index].is_conv) {
+int aexrt_yolo_override_conv_algorithm(AexrtYoloModel* m, uint32_t engine_command, uint32_t algorithm_id) {
+    // engine-file command index -> the conv it became (a CONCAT_CONV1X1 is a
+    // concat followed by its conv)
+    size_t command_index = SIZE_MAX;
+    if (m)
+        for (size_t ci = 0; ci < m->convs.size(); ++ci)
+            if (m->eng.src_cmd[ci] == engine_command && m->convs[ci].is_conv) command_index = ci;
+    if (!m || command_index == SIZE_MAX) {
         set_error("override: not a conv command");
         if (m) m->last_error = "override: not a conv command";
         return 0;

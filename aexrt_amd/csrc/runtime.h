@@ -59,6 +59,9 @@ struct Engine {
     std::vector<EngineCommand> commands;
     std::vector<EngineConstant> constants;  // indexed by value id
     std::vector<EnginePacked> packed;       // indexed by value id
+    // after expand_fused_commands: the engine-file command each command came
+    // from (the conv plan API speaks in engine-file indices)
+    std::vector<uint32_t> src_cmd;
 };
 
 enum CommandKind : uint32_t {
@@ -68,6 +71,13 @@ enum CommandKind : uint32_t {
 };
 
 bool parse_engine(const uint8_t* data, size_t size, Engine& out, std::string& err);
+// Rewrites each CONCAT_CONV1X1 command (yolo.py:771-779: inputs x0..x(k-1),
+// weight, bias; params N, H, W, OC, silu, then the k input channel counts)
+// into a channel CONCAT into a new value followed by a 1x1 CONV / CONV_SILU
+// on it, and fills src_cmd.  The concat is then placed like every other one
+// (producers write straight into its channel slices), so the fused command
+// costs one 1x1 conv over the concatenated channels.
+bool expand_fused_commands(Engine& e, std::string& err);
 uint32_t crc32_ieee(const uint8_t* data, size_t size);
 
 }  // namespace aexrt

@@ -131,8 +131,36 @@ def _silu_patterns(graph: Graph) -> Dict[int, int]:
     return out
 
 
-def lower_graph(graph: Graph) -> Dict[str, Any]:
-    """Graph -> replay dict {values, commands, input_value, output_value}."""
+def _concat_conv1x1_patterns(graph: Graph, silu: Dict[int, int]) -> Dict[int, int]:
+    """concat node index -> conv node index for Concat immediately followed by the 1x1 conv that is
+    the concat's only consumer (yolo.py:586-596, 624-659)."""
+    uses: Dict[str, int] = {}
+    for n in graph.nodes:
+        for v in n.inputs:
+            uses[v] = uses.get(v, 0) + 1
+    out: Dict[int, int] = {}
+    for i, n in enumerate(graph.nodes[:-1]):
+        conv = graph.nodes[i + 1]
+        if n.op != "Concat" or len(n.outputs) != 1 or uses.get(n.outputs[0], 0) != 1:
+            continue
+        if conv.op != "Conv" or not conv.inputs or conv.inputs[0] != n.outputs[0] or len(conv.inputs) < 2:
+            continue
+        w = graph.constants.get(conv.inputs[1])
+        if w is None or np.asarray(w).ndim != 4 or tuple(np.asarray(w).shape[2:]) != (1, 1):
+            continue
+        out[i] = i + 1
+    return out
+
+
+def lower_graph(graph: Graph, *, fuse_concat_min_h: Optional[int] = None) -> Dict[str, Any]:
+    """Graph -> replay dict {values, commands, input_value, output_value}.
+
+    fuse_concat_min_h: None keeps every Concat + 1x1 conv separate (so that
+    the int8 plan can claim the conv); otherwise a Concat feeding a 1x1 conv
+    whose output is taller than fuse_concat_min_h rows becomes one
+    CONCAT_CONV1X1 command (yolo.py:473-488: -1 fuses all, the reference's
+    default; 20 / 44 are its AEXRTC_UNFUSE_SMALL_CONCAT=1 / 2 settings).
+    """
     if len(graph.inputs) != 1 or len(graph.outputs) != 1:
         raise ValueError("the conv-path compiler takes one input and one output")
     specs = infer_value_specs(graph)
@@ -143,22 +171,45 @@ def lower_graph(graph: Graph) -> Dict[str, Any]:
                and graph.nodes[j].inputs == [graph.nodes[ci].outputs[0]]]
         skip.update(sig)
         skip.add(mi)
+    fused: Dict[int, int] = {}
+    if fuse_concat_min_h is not None:
+        for ci, vi in _concat_conv1x1_patterns(graph, silu).items():
+            y = graph.nodes[silu[vi]].outputs[0] if vi in silu else graph.nodes[vi].outputs[0]
+            if int(specs[y].shape[2]) > fuse_concat_min_h:
+                fused[ci] = vi
+    fused_convs = set(fused.values())
     generated: Dict[str, np.ndarray] = {}
     raw_cmds: List[Dict[str, Any]] = []
+
+    def conv_bias(n, w) -> str:
+        if len(n.inputs) >= 3:
+            return n.inputs[2]
+        oc = specs[w].shape[0]
+        b = f"__aexrt_zero_bias_{len(raw_cmds)}_{oc}"
+        generated[b] = np.zeros((oc,), np.float32)
+        specs[b] = TensorSpec((oc,), "float32")
+        return b
+
     for i, n in enumerate(graph.nodes):
-        if i in skip:
+        if i in skip or i in fused_convs:
             continue
         op = n.op
+        if i in fused:
+            # CONCAT_CONV1X1 params: N, H, W, OC, silu, then the channels of
+            # each concat input (yolo.py:771-779)
+            vi = fused[i]
+            conv = graph.nodes[vi]
+            y = graph.nodes[silu[vi]].outputs[0] if vi in silu else conv.outputs[0]
+            w = conv.inputs[1]
+            b = conv_bias(conv, w)
+            nb, oc, oh, ow = specs[y].shape
+            params = [nb, oh, ow, oc, 1 if vi in silu else 0, *[int(specs[v].shape[1]) for v in n.inputs]]
+            raw_cmds.append(dict(kind="CONCAT_CONV1X1", out=[y], ins=[*n.inputs, w, b], params=params))
+            continue
         if op == "Conv":
             x, w = n.inputs[0], n.inputs[1]
             y = graph.nodes[silu[i]].outputs[0] if i in silu else n.outputs[0]
-            if len(n.inputs) >= 3:
-                b = n.inputs[2]
-            else:
-                oc = specs[w].shape[0]
-                b = f"__aexrt_zero_bias_{len(raw_cmds)}_{oc}"
-                generated[b] = np.zeros((oc,), np.float32)
-                specs[b] = TensorSpec((oc,), "float32")
+            b = conv_bias(n, w)
             params = conv_params(specs[x].shape, specs[w].shape, specs[y].shape, n.attrs)
             raw_cmds.append(dict(kind="CONV_SILU" if i in silu else "CONV", out=[y], ins=[x, w, b],
                                  params=params))
@@ -362,6 +413,24 @@ def uses_native_fp16_pos2_40x40_64x64(params) -> bool:
             and pt == pl == 1 and dh == dw == 1 and g == 1)
 
 
+_NATIVE_FP16_CONCAT_CONV1X1 = {
+    (1, 80, 80, 64, 64, 1, (32, 32)), (1, 40, 40, 128, 128, 1, (64, 64)), (1, 40, 40, 512, 128, 1, (256, 256)),
+    (1, 40, 40, 192, 128, 1, (64, 64, 64)), (1, 20, 20, 128, 128, 1, (64, 64)),
+    (1, 20, 20, 256, 128, 1, (64, 64, 64, 64)), (1, 20, 20, 384, 256, 1, (128, 128, 128)),
+    (1, 10, 10, 384, 256, 1, (128, 128, 128)),
+}
+
+
+def uses_native_fp16_concat_conv1x1(cmd) -> bool:
+    """engine.py:1643-1670: the measured shapes of the native fp16 concat + 1x1 kernel."""
+    k = len(cmd["inputs"]) - 2
+    p = [int(v) for v in cmd["params"]]
+    if k <= 0 or k > 8 or len(p) < 5 + k:
+        return False
+    ch = tuple(p[5:5 + k])
+    return (p[0], p[1], p[2], sum(ch), p[3], p[4], ch) in _NATIVE_FP16_CONCAT_CONV1X1
+
+
 def build_kernel_plan(replay: Dict[str, Any], precision: int) -> List[Dict[str, int]]:
     plans = []
     for index, cmd in enumerate(replay["commands"]):
@@ -384,9 +453,20 @@ def build_kernel_plan(replay: Dict[str, Any], precision: int) -> List[Dict[str, 
                     kernel = 43
             if len(cmd["inputs"]) >= 2 and (kernel in (32, 33, 34, 39, 43, 44, 45, 47) or winograd):
                 packed_value = int(cmd["inputs"][1])
+        elif kind == "CONCAT_CONV1X1":
+            # engine.py:1080-1089: 3 = native fp16 (layout-4 weight), else 1 / 0
+            p = cmd["params"]
+            total_in = sum(int(v) for v in p[5:5 + max(0, len(cmd["inputs"]) - 2)])
+            oc, spatial = int(p[3]), int(p[1]) * int(p[2])
+            if precision == PRECISION_FLOAT16 and uses_native_fp16_concat_conv1x1(cmd):
+                kernel = 3
+                packed_value = int(cmd["inputs"][-2])
+            else:
+                kernel = 1 if total_in >= 64 and oc >= 64 and oc % 4 == 0 and spatial >= 100 else 0
         heavy = kind in ("CONV", "CONV_SILU", "CONCAT_CONV1X1", "MATMUL")
         flags = PLAN_FLAG_AUTHORITATIVE
-        native_fp16 = kind in ("CONV", "CONV_SILU") and (kernel in (43, 44, 45, 47) or winograd)
+        native_fp16 = (kind in ("CONV", "CONV_SILU") and (kernel in (43, 44, 45, 47) or winograd)) or (
+            kind == "CONCAT_CONV1X1" and kernel == 3)
         if precision == PRECISION_FLOAT16 and (not heavy or native_fp16):
             flags |= PLAN_FLAG_DXIL
         plans.append(dict(command_index=index, kind_id=int(cmd["kind_id"]), planned_kernel=kernel,
@@ -491,6 +571,15 @@ def build_packed_weights(replay: Dict[str, Any], plans: List[Dict[str, int]], pr
                            data=data)
 
     for cmd, plan in zip(replay["commands"], plans):
+        if cmd["kind"] == "CONCAT_CONV1X1" and int(plan["planned_kernel"]) == 3:
+            # engine.py:2157-2164: layout 4 over the concatenated input channels
+            p = cmd["params"]
+            ic = sum(int(v) for v in p[5:5 + len(cmd["inputs"]) - 2])
+            oc = int(p[3])
+            wid = int(cmd["inputs"][-2])
+            w = _weight_array(values, wid, (oc, ic, 1, 1))
+            put(wid, packing.PACKED_LAYOUT_CONV1X1_OC8_FP16, ic, oc, oc * ic, packing.pack_conv1x1_oc8_fp16(w))
+            continue
         if cmd["kind"] not in ("CONV", "CONV_SILU"):
             continue
         p = cmd["params"]
@@ -658,10 +747,11 @@ def _precision_id(precision: str) -> int:
 
 
 def compile_plan(graph: Graph, *, precision: str = "fp16", algo_overrides: Optional[Dict[int, int]] = None,
-                 int8_pergroup: Optional[Sequence[int]] = None) -> Dict[str, Any]:
+                 int8_pergroup: Optional[Sequence[int]] = None,
+                 fuse_concat_min_h: Optional[int] = None) -> Dict[str, Any]:
     """Lowering + kernel plan + packed weights (everything but the bytes)."""
     prec = _precision_id(precision)
-    replay = lower_graph(graph)
+    replay = lower_graph(graph, fuse_concat_min_h=fuse_concat_min_h)
     plans = build_kernel_plan(replay, prec)
     if algo_overrides:
         apply_algo_overrides(replay, plans, algo_overrides)
@@ -678,8 +768,9 @@ def build_aexrt_engine(graph: Graph, *, precision: str = "fp16", classes: Option
                        algo_overrides: Optional[Dict[int, int]] = None,
                        int8_pergroup: Optional[Sequence[int]] = None, max_candidates: int = 512,
                        max_detections: int = 100, conf_threshold: float = 0.25,
-                       iou_threshold: float = 0.45) -> bytes:
-    plan = compile_plan(graph, precision=precision, algo_overrides=algo_overrides, int8_pergroup=int8_pergroup)
+                       iou_threshold: float = 0.45, fuse_concat_min_h: Optional[int] = None) -> bytes:
+    plan = compile_plan(graph, precision=precision, algo_overrides=algo_overrides, int8_pergroup=int8_pergroup,
+                        fuse_concat_min_h=fuse_concat_min_h)
     replay, plans, packed, prec = plan["replay"], plan["plans"], plan["packed"], plan["precision"]
     out_v = replay["values"][replay["output_value"]]
     out_shape = [d for d in out_v["shape4"]]

@@ -140,3 +140,76 @@ def test_inspect_reports_crc_mismatch():
     data[-3] ^= 1
     with pytest.raises(ValueError, match="checksum"):
         E.inspect_aexrt_engine(bytes(data))
+
+
+def _val(vid, shape, raw=b""):
+    n = int(np.prod(shape))
+    return dict(id=vid, name=f"v{vid}", flags=E.VALUE_CONSTANT if raw else 0, elements=n,
+                shape4=tuple(([1] * (4 - len(shape))) + list(shape)), raw=raw, rank=len(shape))
+
+
+def _concat_conv_replay(chans, oc, h, silu=1):
+    ic = sum(chans)
+    k = len(chans)
+    values = [_val(i, (1, c, h, h)) for i, c in enumerate(chans)]
+    wid = k
+    values.append(_val(wid, (oc, ic, 1, 1), (np.arange(oc * ic, dtype=np.float32) / 1024.0).tobytes()))
+    values.append(_val(k + 1, (oc,), np.zeros(oc, np.float32).tobytes()))
+    values.append(_val(k + 2, (1, oc, h, h)))
+    cmd = dict(kind="CONCAT_CONV1X1", kind_id=E.COMMAND_KIND["CONCAT_CONV1X1"], inputs=[*range(k), wid, k + 1],
+               output=k + 2, params=[1, h, h, oc, silu, *chans])
+    return dict(values=values, commands=[cmd]), wid
+
+
+# reference: tests/test_engine_fp16_1x1_plan.py:165-206 (generic plan 1, no packed weight, flags 1)
+@pytest.mark.parametrize("oc", [64, 68])
+def test_concat_conv1x1_generic_plan_matches_reference_kat(oc):
+    replay, _ = _concat_conv_replay([32, 32], oc, 20)
+    plans = E.build_kernel_plan(replay, E.PRECISION_FLOAT16)
+    p = plans[0]
+    assert (p["planned_kernel"], p["precision"], p["packed_value"], p["flags"]) == (1, 2, E.NO_VALUE, 1)
+    assert E.build_packed_weights(replay, plans, E.PRECISION_FLOAT16) == []
+
+
+def test_concat_conv1x1_small_plans_zero():
+    replay, _ = _concat_conv_replay([16, 16], 32, 8)
+    assert E.build_kernel_plan(replay, E.PRECISION_FLOAT16)[0]["planned_kernel"] == 0
+
+
+# reference: tests/test_engine_fp16_1x1_plan.py:318-360 ((1, 20, 20, 384 -> 256, silu, 3 x 128) is native)
+def test_concat_conv1x1_native_fp16_plan_and_layout4_weight():
+    replay, wid = _concat_conv_replay([128, 128, 128], 256, 20)
+    assert E.uses_native_fp16_concat_conv1x1(replay["commands"][0])
+    plans = E.build_kernel_plan(replay, E.PRECISION_FLOAT16)
+    p = plans[0]
+    assert (p["planned_kernel"], p["packed_value"], p["flags"]) == (3, wid, E.PLAN_FLAG_AUTHORITATIVE | E.PLAN_FLAG_DXIL)
+    packed = E.build_packed_weights(replay, plans, E.PRECISION_FLOAT16)
+    assert len(packed) == 1 and packed[0]["layout"] == 4
+    assert (packed[0]["in_channels"], packed[0]["out_channels"], packed[0]["elements"]) == (384, 256, 384 * 256)
+    # fp32 engines never take the native kernel
+    assert E.build_kernel_plan(replay, E.PRECISION_FLOAT32)[0]["planned_kernel"] == 1
+
+
+@pytest.mark.parametrize("threshold,count", [(None, 0), (-1, 13), (20, 4), (44, 1)])
+def test_yolov8n_concat_conv1x1_fusion_thresholds(threshold, count):
+    """yolo.py:473-488: fused by default; AEXRTC_UNFUSE_SMALL_CONCAT=1/2 keep only outputs taller than 20/44."""
+    g = build_yolov8n(batch=1, imgsz=320, seed=4)
+    r = E.lower_graph(g, fuse_concat_min_h=threshold)
+    cc = [c for c in r["commands"] if c["kind"] == "CONCAT_CONV1X1"]
+    assert len(cc) == count
+    n_conv = sum(1 for c in r["commands"] if c["kind"] in ("CONV", "CONV_SILU"))
+    assert n_conv + count == 63
+    for c in cc:
+        n, h, w, oc, silu, *chans = c["params"]
+        out = r["values"][c["output"]]
+        assert (n, oc, h, w) == tuple(out["shape4"]) and silu == 1
+        assert chans == [r["values"][v]["shape4"][1] for v in c["inputs"][:-2]]
+        assert r["values"][c["inputs"][-2]]["shape4"] == (oc, sum(chans), 1, 1)
+
+
+def test_fused_engine_validates():
+    g = build_yolov8n(batch=1, imgsz=160, seed=4)
+    data = E.build_aexrt_engine(g, precision="fp16", classes=80, fuse_concat_min_h=-1)
+    L = _lib.lib()
+    buf = ctypes.create_string_buffer(data, len(data))
+    assert L.aexrt_hip_validate_engine(buf, len(data))

@@ -59,9 +59,16 @@ def _c2f_graph(batch=1, c=128, dim=40, seed=3, shortcut=True) -> Graph:
 
 
 def _layer_check(model: NativeHipYoloModel, graph: Graph, plan: dict, tol=1e-2):
+    """Every conv (and CONCAT_CONV1X1) of the plan against the oracle fed the GPU's own inputs.
+
+    The oracle runs the W8A8 chain where the model's conv runs an int8 kernel
+    (its current algorithm, overrides included), pg16 where the plan says so,
+    and the fp16 direct conv otherwise.
+    """
     replay = plan["replay"]
     names = replay["names"]
     cmds = replay["commands"]
+    current = {i["command_index"]: i["current_algorithm"] for i in model.conv_plan()}
     consumers = {}
     for i, c in enumerate(cmds):
         for v in c["inputs"]:
@@ -70,22 +77,30 @@ def _layer_check(model: NativeHipYoloModel, graph: Graph, plan: dict, tol=1e-2):
     checked = 0
     worst = 0.0
     for i, c in enumerate(cmds):
-        if c["kind"] not in ("CONV", "CONV_SILU"):
+        if c["kind"] not in ("CONV", "CONV_SILU", "CONCAT_CONV1X1"):
             continue
-        pk = plan["plans"][i]["planned_kernel"]
-        int8 = pk in E.INT8_KERNELS and E.int8_eligible(c["params"])
+        int8 = current[i] in E.INT8_KERNELS
         pg16 = bool(plan["plans"][i]["flags"] & E.PLAN_FLAG_INT8_PERGROUP)
-        xin, wid, bid = c["inputs"]
+        if c["kind"] == "CONCAT_CONV1X1":
+            srcs, wid, bid = c["inputs"][:-2], c["inputs"][-2], c["inputs"][-1]
+            parts = [model.value(v) for v in srcs]
+            if any(p.ndim == 3 for p in parts):
+                continue
+            x = np.concatenate(parts, axis=1)
+            silu = bool(c["params"][4])
+        else:
+            xin, wid, bid = c["inputs"]
+            rank_x, _ = model.value_info(xin)
+            x = model.value(xin)
+            if x.ndim == 3:
+                continue
+            if xin == replay["input_value"]:
+                x = O.round_f16(x)
+            silu = c["kind"] == "CONV_SILU"
         wname = names[wid]
         node = convs[wname.rsplit(".w", 1)[0]]
-        rank_x, _ = model.value_info(xin)
-        x = model.value(xin)
-        if x.ndim == 3:
-            continue
-        if xin == replay["input_value"]:
-            x = O.round_f16(x)
         y_ref = ON.conv_layer(x, graph.constants[wname], graph.constants[names[bid]], node.attrs, int8=int8,
-                              silu=c["kind"] == "CONV_SILU", pg16=pg16)
+                              silu=silu, pg16=pg16)
         out = c["output"]
         rank_y, _ = model.value_info(out)
         if rank_y == 0:  # fused into the residual add that consumes it
@@ -97,7 +112,7 @@ def _layer_check(model: NativeHipYoloModel, graph: Graph, plan: dict, tol=1e-2):
         if y.ndim == 3:
             y = y.reshape(y_ref.shape)
         err, allowed = tol_range(y_ref, y, tol)
-        assert err <= allowed, (i, names[out], pk, err, allowed)
+        assert err <= allowed, (i, names[out], current[i], err, allowed)
         worst = max(worst, err / max(allowed, 1e-30) * tol)
         checked += 1
     return checked, worst
@@ -164,6 +179,54 @@ def test_c2f_w8a8_pg16_block_layer_parity(cuda, batch):
         assert checked == 6
         m.run(x)
         np.testing.assert_array_equal(m.output(), out1)
+
+
+def test_c2f_fused_concat_conv1x1_fp16_and_int8_override(cuda):
+    """The reference compiler's default CONCAT_CONV1X1 command (yolo.py:473-488, 771-779) runs as a
+    placed concat + 1x1 conv; the fused conv can be moved onto the int8 kernel by engine index."""
+    g = _c2f_graph(batch=1, c=128, dim=20, seed=7)
+    plan = E.compile_plan(g, precision="fp16", fuse_concat_min_h=-1)
+    cc = [i for i, c in enumerate(plan["replay"]["commands"]) if c["kind"] == "CONCAT_CONV1X1"]
+    assert len(cc) == 1
+    # (1, 20, 20, 256 -> 128, silu, 4 x 64) is one of the reference's native fp16 shapes: kernel 3 on a
+    # layout-4 weight
+    assert plan["plans"][cc[0]]["planned_kernel"] == 3
+    assert any(p["layout"] == 4 and p["in_channels"] == 256 for p in plan["packed"])
+    data = E.build_aexrt_engine(g, precision="fp16", fuse_concat_min_h=-1)
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((1, 128, 20, 20)).astype(np.float32)
+    ref = ON.run_graph(g, x)[g.outputs[0]]
+    with NativeHipYoloModel(data) as m:
+        info = {i["command_index"]: i for i in m.conv_plan()}
+        assert cc[0] in info and info[cc[0]]["desc"][1] == 256
+        m.run(x)
+        checked, _ = _layer_check(m, g, plan)
+        assert checked == 6
+        err, allowed = tol_range(ref, m.output().reshape(ref.shape), 1e-2)
+        assert err <= allowed, (err, allowed)
+        m.override_conv_algorithm(cc[0], 51)
+        assert {i["command_index"]: i for i in m.conv_plan()}[cc[0]]["current_algorithm"] == 51
+        m.run(x)
+        checked, _ = _layer_check(m, g, plan)
+        assert checked == 6
+
+
+def test_yolov8n_160_fused_concat_engine_fp16(cuda):
+    g = build_yolov8n(batch=1, imgsz=160, seed=4)
+    plan = E.compile_plan(g, precision="fp16", fuse_concat_min_h=-1)
+    n_cc = sum(1 for c in plan["replay"]["commands"] if c["kind"] == "CONCAT_CONV1X1")
+    assert n_cc == 13
+    data = E.build_aexrt_engine(g, precision="fp16", classes=80, fuse_concat_min_h=-1)
+    rng = np.random.default_rng(4)
+    x = rng.random((1, 3, 160, 160)).astype(np.float32)
+    with NativeHipYoloModel(data) as m:
+        m.run(x)
+        checked, _ = _layer_check(m, g, plan)
+        assert checked == 63
+        out = m.output()
+    ref = ON.run_graph(g, x, threads=8)["output0"]
+    err, allowed = tol_range(ref, out.reshape(ref.shape), 5e-2)
+    assert err <= allowed, (err, allowed)
 
 
 def test_yolov8n_160_w8a8_layers_and_end_to_end(cuda):
