@@ -107,6 +107,11 @@ _SIGS = {
     "aexrt_hip_amax_nchw": (c_int, [_vp, c_uint32, c_uint32, c_uint32, c_uint32, _vp, _vp]),
     "aexrt_hip_quantize": (c_int, [POINTER(TensorView), c_uint32, c_uint32, c_uint32, c_uint32, _vp, _vp]),
     "aexrt_hip_quant_pack_nchw": (c_int, [_vp, c_uint32, c_uint32, c_uint32, c_uint32, _vp, c_uint32, _vp, _vp]),
+    "aexrt_hip_yolo_decode_nms_topk": (c_int, [_vp, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32,
+                                               ctypes.c_float, ctypes.c_float, c_uint32, c_uint32, _vp, _vp,
+                                               _vp]),
+    "aexrt_hip_yolo_dfl_decode_nms_topk": (c_int, [_vp, c_uint32, c_uint32, _vp, _vp, c_uint32, ctypes.c_float,
+                                                   ctypes.c_float, c_uint32, c_uint32, _vp, _vp, _vp]),
     "aexrt_hip_amax_strips_nhwc": (c_int, [POINTER(TensorView), c_uint32, c_uint32, c_uint32, c_uint32, _vp,
                                            _vp]),
     "aexrt_hip_quant_fused_pg16": (c_int, [_vp, c_uint32, c_uint32, c_uint32, c_uint32, _vp, _vp, _vp]),
@@ -154,6 +159,7 @@ _MODEL_SIGS = {
     "aexrt_yolo_is_executable": (c_int, [_vp]),
     "aexrt_yolo_run": (c_int, [_vp, _vp, _vp, c_uint64, POINTER(YoloDetection), c_uint32, POINTER(c_uint32)]),
     "aexrt_yolo_run_device": (c_int, [_vp, _vp, _vp, _vp]),
+    "aexrt_yolo_postprocess_device": (c_int, [_vp, _vp, POINTER(_vp), POINTER(_vp)]),
     "aexrt_yolo_debug_output": (c_int, [_vp, _vp, c_uint64]),
     "aexrt_yolo_debug_value": (c_int, [_vp, c_uint32, _vp, c_uint64]),
     "aexrt_yolo_value_info": (c_int, [_vp, c_uint32, POINTER(c_uint32)]),

@@ -363,6 +363,69 @@ int aexrt_hip_conv2d_int8_pg16(const AexrtConv2DDesc* desc, uint32_t algorithm, 
     return check_hip(launch_conv_int8_pg16(p, static_cast<hipStream_t>(stream)), "conv2d_int8_pg16") ? 1 : 0;
 }
 
+int aexrt_hip_yolo_decode_nms_topk(const float* output, uint32_t layout, uint32_t anchors, uint32_t channels,
+                                   uint32_t classes, uint32_t has_objectness, float conf_threshold,
+                                   float iou_threshold, uint32_t max_candidates, uint32_t max_detections,
+                                   float* detections, uint32_t* count, void* stream) {
+    const uint32_t cls_off = has_objectness ? 5u : 4u;
+    if ((!output && anchors) || !detections || !count || anchors > 0x7FFFFFFFu || channels > 0xFFFFFFu ||
+        channels < classes + cls_off || max_candidates < 1 || max_candidates > (uint32_t)kYoloMaxCandidates ||
+        max_detections < 1 || max_detections > 0x7FFFFFFFu || uint64_t(anchors) * channels > 0x7FFFFFFFull) {
+        set_error("yolo_decode_nms_topk: bad arguments (need channels >= classes + 4 (+1 objectness), "
+                  "1 <= max_candidates <= 2048, max_detections >= 1)");
+        return 0;
+    }
+    // layout 2: channels last ([A][C]); otherwise channels first ([C][A])
+    const bool last = layout == 2u;
+    return check_hip(launch_yolo_decode_nms_topk(output, last ? 1 : (int)anchors, last ? (int)channels : 1,
+                                                 (int)anchors, (int)classes, (int)has_objectness, conf_threshold,
+                                                 iou_threshold, (int)max_candidates, (int)max_detections, detections,
+                                                 count, static_cast<hipStream_t>(stream)),
+                     "yolo_decode_nms_topk")
+               ? 1
+               : 0;
+}
+
+int aexrt_hip_yolo_dfl_decode_nms_topk(const float* head, uint32_t layout, uint32_t num_levels,
+                                       const uint32_t* level_hw, const float* level_strides, uint32_t classes,
+                                       float conf_threshold, float iou_threshold, uint32_t max_candidates,
+                                       uint32_t max_detections, float* detections, uint32_t* count, void* stream) {
+    if (!level_hw || !level_strides || num_levels < 1 || num_levels > (uint32_t)kYoloMaxLevels || classes < 1 ||
+        classes > 0xFFFFu || !detections || !count || max_candidates < 1 ||
+        max_candidates > (uint32_t)kYoloMaxCandidates || max_detections < 1 || max_detections > 0x7FFFFFFFu) {
+        set_error("yolo_dfl_decode_nms_topk: bad arguments (1..4 levels, classes >= 1, "
+                  "1 <= max_candidates <= 2048, max_detections >= 1)");
+        return 0;
+    }
+    YoloLevels lv{};
+    lv.n = (int)num_levels;
+    uint64_t anchors = 0;
+    for (uint32_t l = 0; l < num_levels; ++l) {
+        if (level_hw[2 * l] == 0 || level_hw[2 * l + 1] == 0 || level_hw[2 * l] > 0xFFFFu ||
+            level_hw[2 * l + 1] > 0xFFFFu) {
+            set_error("yolo_dfl_decode_nms_topk: empty or oversized level grid");
+            return 0;
+        }
+        lv.h[l] = (int)level_hw[2 * l];
+        lv.w[l] = (int)level_hw[2 * l + 1];
+        lv.stride[l] = level_strides[l];
+        anchors += uint64_t(lv.h[l]) * lv.w[l];
+    }
+    const uint64_t channels = 64u + classes;
+    if (!head || anchors * channels > 0x7FFFFFFFull) {
+        set_error("yolo_dfl_decode_nms_topk: null head or head too large");
+        return 0;
+    }
+    const bool last = layout == 2u;
+    return check_hip(launch_yolo_decode_nms_topk(head, last ? 1 : (int)anchors, last ? (int)channels : 1, (int)anchors,
+                                                 (int)classes, 0, conf_threshold, iou_threshold, (int)max_candidates,
+                                                 (int)max_detections, detections, count,
+                                                 static_cast<hipStream_t>(stream), &lv),
+                     "yolo_dfl_decode_nms_topk")
+               ? 1
+               : 0;
+}
+
 int aexrt_hip_amax_strips_nhwc(const AexrtHipTensorView* x, uint32_t batch, uint32_t height, uint32_t width,
                                uint32_t channels, uint32_t* out, void* stream) {
     if (!x || !x->data || !out || channels % 16 || x->c_stride % 8 || x->n_stride % 8 || batch == 0) {

@@ -176,6 +176,25 @@ hipError_t launch_conv_int8_pg16(const ConvParams& p, hipStream_t stream);
 hipError_t launch_quant_fused_pg16(const void* x, bool f16, int N, int C, int HW, uint32_t* packed,
                                    uint32_t* amax, hipStream_t stream);
 
+// YOLO output0 postprocess (decode + filter, class-wise NMS, top-k) in one
+// block; element (channel ch, anchor a) of output0 at out[ch * ch_stride + a *
+// a_stride].  Writes count[0] = detections and dets[0 .. count) as x1, y1,
+// x2, y2, score, class.  1 <= max_candidates <= kYoloMaxCandidates.  With
+// levels, out is the raw Detect head (64 DFL bin logits, then class logits;
+// anchors level by level, h x w each) and is decoded here; without, out is
+// the decoded [4 (+1) + classes][anchors] tensor.
+constexpr int kYoloMaxCandidates = 2048;
+constexpr int kYoloMaxLevels = 4;
+struct YoloLevels {
+    int n;
+    int h[kYoloMaxLevels], w[kYoloMaxLevels];
+    float stride[kYoloMaxLevels];
+};
+hipError_t launch_yolo_decode_nms_topk(const float* out, int ch_stride, int a_stride, int anchors, int classes,
+                                       int has_objectness, float conf, float iou, int max_candidates,
+                                       int max_detections, float* dets, uint32_t* count, hipStream_t stream,
+                                       const YoloLevels* levels = nullptr);
+
 // ---- glue ------------------------------------------------------------------
 hipError_t launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t stream);
 // dst view (channels [0,C)) = src view; amax slots of dst updated when non-null.

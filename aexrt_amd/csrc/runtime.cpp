@@ -18,6 +18,7 @@
 // frame structure, native/aexrt_d3d12_runtime.cpp:28758-29944).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -164,6 +165,12 @@ struct AexrtYoloModel {
     AexrtYoloRunTiming timing{};
     std::string last_error;
     bool executable = false;
+    // YOLO postprocess of output0 (decode + filter, NMS, top-k)
+    bool post_ok = false;
+    bool post_dfl = false;            // output0 is the raw Detect head (DFL bins + class logits)
+    aexrt::YoloLevels post_levels{};
+    float* dets_dev = nullptr;        // [max_detections][6]
+    uint32_t* det_count_dev = nullptr;
     std::mutex mutex;
 };
 
@@ -1176,6 +1183,55 @@ bool choose_lanes(AexrtYoloModel* m) {
     return true;
 }
 
+// The manifest's YOLO head description (channels, anchors, classes,
+// objectness) must match the network output for the postprocess to run:
+// either a decoded output0 (4 box values, optional objectness, class
+// scores) or the raw Detect head (64 DFL bin logits + class logits over the
+// stride-8/16/32 grids of the input); any other output keeps output0 only.
+void setup_postprocess(AexrtYoloModel* m) {
+    const EngineManifest& mf = m->eng.manifest;
+    const ValueInfo& o = m->vals[mf.output_value];
+    const uint32_t cls_off = mf.has_objectness ? 5u : 4u;
+    m->post_ok = o.known && o.pl.valid && o.rank == 3 && m->roots[o.pl.root].f32 && mf.classes > 0 &&
+                 mf.channels == (uint32_t)o.C && mf.anchors == (uint32_t)o.H && mf.max_candidates >= 1 &&
+                 mf.max_candidates <= (uint32_t)kYoloMaxCandidates && mf.max_detections >= 1;
+    if (!m->post_ok) return;
+    m->post_dfl = false;
+    if (mf.channels != mf.classes + cls_off) {
+        const ValueInfo& in = m->vals[mf.input_value];
+        YoloLevels lv{};
+        lv.n = 3;
+        int total = 0;
+        for (int l = 0; l < 3; ++l) {
+            const int st = 8 << l;
+            lv.h[l] = in.H / st;
+            lv.w[l] = in.W / st;
+            lv.stride[l] = (float)st;
+            total += lv.h[l] * lv.w[l];
+        }
+        m->post_ok = !mf.has_objectness && mf.channels == mf.classes + 64 && in.H % 32 == 0 && in.W % 32 == 0 &&
+                     total == (int)mf.anchors;
+        if (!m->post_ok) return;
+        m->post_dfl = true;
+        m->post_levels = lv;
+    }
+    m->dets_dev = static_cast<float*>(dev_alloc(m, size_t(mf.max_detections) * 6 * 4));
+    m->det_count_dev = static_cast<uint32_t*>(dev_alloc(m, 256));
+    m->post_ok = m->dets_dev && m->det_count_dev;
+}
+
+bool launch_postprocess(AexrtYoloModel* m, hipStream_t s) {
+    const EngineManifest& mf = m->eng.manifest;
+    const AexrtHipTensorView ov = view_of(m, (int)mf.output_value);
+    // image 0 of output0, element (channel, anchor) at anchor * c_stride + channel
+    return check_hip(launch_yolo_decode_nms_topk(static_cast<const float*>(ov.data), 1, ov.c_stride, (int)mf.anchors,
+                                                 (int)mf.classes, (int)mf.has_objectness, mf.conf_threshold,
+                                                 mf.iou_threshold, (int)mf.max_candidates, (int)mf.max_detections,
+                                                 m->dets_dev, m->det_count_dev, s,
+                                                 m->post_dfl ? &m->post_levels : nullptr),
+                     "yolo postprocess");
+}
+
 bool build_model(AexrtYoloModel* m) {
     if (!infer_dims(m)) return false;
     fuse_residuals(m);
@@ -1227,6 +1283,7 @@ bool build_model(AexrtYoloModel* m) {
     if (m->autotune && !choose_lanes(m)) return false;
     const char* prof = std::getenv("AEXRT_HIP_PROFILE");
     m->profile = prof && prof[0] == '1';
+    setup_postprocess(m);
     m->executable = true;
     return true;
 }
@@ -1436,10 +1493,23 @@ int aexrt_yolo_run_device(AexrtYoloModel* m, const float* input, void* stream, v
     return run_network(m, s) ? 1 : 0;
 }
 
+int aexrt_yolo_postprocess_device(AexrtYoloModel* m, void* stream, float** detections_device,
+                                  uint32_t** count_device) {
+    if (!m || !m->executable || !m->post_ok) {
+        set_error("postprocess_device: the engine's output is not a YOLO head this backend decodes");
+        if (m) m->last_error = "postprocess_device: no YOLO postprocess for this engine";
+        return 0;
+    }
+    std::lock_guard<std::mutex> lock(m->mutex);
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : m->stream;
+    if (!launch_postprocess(m, s)) return fail(m, last_error()) ? 1 : 0;
+    if (detections_device) *detections_device = m->dets_dev;
+    if (count_device) *count_device = m->det_count_dev;
+    return 1;
+}
+
 int aexrt_yolo_run(AexrtDevice* device, AexrtYoloModel* m, const float* input, uint64_t input_element_count,
                    AexrtYoloDetection* detections, uint32_t max_detections, uint32_t* out_detection_count) {
-    (void)detections;
-    (void)max_detections;
     if (!device || !m || !input) {
         set_error("run: null argument");
         if (m) m->last_error = "run: null argument";
@@ -1464,10 +1534,29 @@ int aexrt_yolo_run(AexrtDevice* device, AexrtYoloModel* m, const float* input, u
         return fail(m, last_error()) ? 1 : 0;
     auto t1 = clk::now();
     if (!run_network(m, m->stream)) return 0;
+    // decode + NMS + top-k of output0 on the device (RT:27104-27219), then
+    // the reference's readback: count = min(device count, caller capacity,
+    // the engine's max_detections) (RT:29699-29728)
+    uint32_t raw_count = 0;
+    std::vector<float> dets_host;
+    if (m->post_ok) {
+        dets_host.resize(size_t(m->eng.manifest.max_detections) * 6);
+        if (!launch_postprocess(m, m->stream) ||
+            !check_hip(hipMemcpyAsync(&raw_count, m->det_count_dev, 4, hipMemcpyDeviceToHost, m->stream),
+                       "detection count readback") ||
+            !check_hip(hipMemcpyAsync(dets_host.data(), m->dets_dev, dets_host.size() * 4, hipMemcpyDeviceToHost,
+                                      m->stream),
+                       "detection readback"))
+            return fail(m, last_error()) ? 1 : 0;
+    }
     auto t2 = clk::now();
     if (!check_hip(hipStreamSynchronize(m->stream), "run sync")) return fail(m, last_error()) ? 1 : 0;
     auto t3 = clk::now();
-    if (out_detection_count) *out_detection_count = 0;
+    uint32_t cap = 0;
+    if (m->post_ok && detections)
+        cap = std::min({raw_count, max_detections, m->eng.manifest.max_detections});
+    if (cap) std::memcpy(detections, dets_host.data(), size_t(cap) * sizeof(AexrtYoloDetection));
+    if (out_detection_count) *out_detection_count = cap;
     auto t4 = clk::now();
     auto ms = [](clk::time_point a, clk::time_point b) {
         return std::chrono::duration<double, std::milli>(b - a).count();

@@ -153,6 +153,44 @@ def conv2d_int8_pg16(pc: "PreparedConv", packed, amax, y, *, flags: int = SILU, 
         _ptr(pc.w_scale), pc.bias.data_ptr(), y.data_ptr(), _stream(stream)), "conv2d_int8_pg16")
 
 
+def yolo_decode_nms_topk(out, *, classes: int, layout: int = 1, has_objectness: bool = False, conf: float = 0.25,
+                         iou: float = 0.45, max_candidates: int = 512, max_detections: int = 100, stream=None):
+    """YOLO postprocess of one output0 image on the device ([C, A] fp32, or [A, C] with layout 2).
+
+    Returns the [count, 6] detections (x1, y1, x2, y2, score, class) as a device tensor."""
+    import torch
+
+    a = out[0] if out.dim() == 3 else out
+    if a.dtype != torch.float32 or not a.is_contiguous():
+        raise ValueError("output0 must be a contiguous fp32 tensor")
+    channels, anchors = (a.shape[1], a.shape[0]) if layout == 2 else (a.shape[0], a.shape[1])
+    dets = torch.zeros((max_detections, 6), dtype=torch.float32, device=a.device)
+    count = torch.zeros(1, dtype=torch.int32, device=a.device)
+    check(_lib.lib().aexrt_hip_yolo_decode_nms_topk(
+        a.data_ptr(), layout, anchors, channels, classes, int(has_objectness), float(conf), float(iou),
+        max_candidates, max_detections, dets.data_ptr(), count.data_ptr(), _stream(stream)), "yolo_decode_nms_topk")
+    return dets[: int(count.item())]
+
+
+def yolo_dfl_decode_nms_topk(head, levels, *, classes: int, layout: int = 1, conf: float = 0.25, iou: float = 0.45,
+                             max_candidates: int = 512, max_detections: int = 100, stream=None):
+    """YOLO postprocess of one raw Detect-head image on the device ([64 + classes, A] fp32, or [A, 64 + classes]
+    with layout 2; levels = [(h, w, stride)]).  Returns the [count, 6] detections as a device tensor."""
+    import torch
+
+    a = head[0] if head.dim() == 3 else head
+    if a.dtype != torch.float32 or not a.is_contiguous():
+        raise ValueError("head must be a contiguous fp32 tensor")
+    hw = (ctypes.c_uint32 * (2 * len(levels)))(*[int(v) for h, w, _ in levels for v in (h, w)])
+    st = (ctypes.c_float * len(levels))(*[float(s) for _, _, s in levels])
+    dets = torch.zeros((max_detections, 6), dtype=torch.float32, device=a.device)
+    count = torch.zeros(1, dtype=torch.int32, device=a.device)
+    check(_lib.lib().aexrt_hip_yolo_dfl_decode_nms_topk(
+        a.data_ptr(), layout, len(levels), hw, st, classes, float(conf), float(iou), max_candidates, max_detections,
+        dets.data_ptr(), count.data_ptr(), _stream(stream)), "yolo_dfl_decode_nms_topk")
+    return dets[: int(count.item())]
+
+
 def can_use_conv_int8(params: Sequence[int], kernel_elems: int) -> bool:
     d = ConvDesc.from_params(params)
     return bool(_lib.lib().aexrt_hip_can_use_conv_int8(ctypes.byref(d), kernel_elems))

@@ -198,6 +198,36 @@ int aexrt_hip_conv2d_int8_pg16(const AexrtConv2DDesc* desc, uint32_t algorithm, 
                                const uint32_t* packed, const uint32_t* amax, const void* weight,
                                const float* w_scale, const float* bias, void* y, void* stream);
 
+/* YOLO postprocess on one output0 image in device memory, the reference's
+ * dispatch_yolo_decode_nms_float32 (native/aexrt_d3d12_runtime.cpp:
+ * 15300-15356, 15637-15735): layout 2 = channels last ([anchors][channels]),
+ * otherwise channels first.  A candidate is an anchor whose best class score
+ * (times objectness) is not below conf_threshold, at most max_candidates of
+ * them in anchor order; one is dropped when a candidate of its class with a
+ * higher score (equal: earlier) overlaps it with IoU > iou_threshold;
+ * detections = the kept ones by score, at most max_detections, written as
+ * [count][6] floats with *count (device memory).  max_candidates <= 2048. */
+int aexrt_hip_yolo_decode_nms_topk(const float* output, uint32_t layout, uint32_t anchors, uint32_t channels,
+                                   uint32_t classes, uint32_t has_objectness, float conf_threshold,
+                                   float iou_threshold, uint32_t max_candidates, uint32_t max_detections,
+                                   float* detections, uint32_t* count, void* stream);
+
+/* YOLO postprocess on the raw Detect head of one image (the post-conv part
+ * of the reference's fused head decode, native/aexrt_d3d12_runtime.cpp:
+ * 15465-15636, then NMS and top-k as above): head = [64 + classes][anchors]
+ * fp32 (layout 2: [anchors][64 + classes]), channels 0..63 the 4 x 16 DFL
+ * bin logits (side-major), then the class logits; anchors level by level,
+ * level l a level_hw[2l] x level_hw[2l+1] grid with stride level_strides[l].
+ * score = sigmoid(logit); side distance = softmax expectation of its 16
+ * bins; box = ((gx + 0.5 - l) s, (gy + 0.5 - t) s, (gx + 0.5 + r) s,
+ * (gy + 0.5 + b) s).  exp is computed by Cody-Waite reduction and a
+ * degree-7 Taylor polynomial (the reference's comes from its shader
+ * compiler).  level_hw and level_strides are host arrays. */
+int aexrt_hip_yolo_dfl_decode_nms_topk(const float* head, uint32_t layout, uint32_t num_levels,
+                                       const uint32_t* level_hw, const float* level_strides, uint32_t classes,
+                                       float conf_threshold, float iou_threshold, uint32_t max_candidates,
+                                       uint32_t max_detections, float* detections, uint32_t* count, void* stream);
+
 /* a10: int8 eligibility of a conv for kernel family kernel_elems (1 or 9),
  * native/aexrt_d3d12_runtime.cpp:9399-9422, plus this backend's own
  * requirement in_channels % 16 == 0 (amax is kept per 16 channels). */
@@ -320,9 +350,12 @@ uint32_t aexrt_yolo_prepared_command_count(AexrtYoloModel* model);
 int aexrt_yolo_is_executable(AexrtYoloModel* model);
 
 /* native/aexrt.h:391-398: one inference from a host fp32 CHW input.  The
- * network runs on the device; detections are the output of the YOLO
- * post-process, which this backend does not run yet: *out_detection_count
- * is set to 0 and the raw head output is available through
+ * network and the YOLO postprocess of output0 (decode + confidence filter,
+ * class-wise NMS, top-k; native/aexrt_d3d12_runtime.cpp:27104-27219) run on
+ * the device; *out_detection_count = min(detections found, max_detections,
+ * the engine's max_detections), best score first.  Engines whose output is
+ * not a YOLO head (manifest channels/anchors/classes do not match output0)
+ * report 0 detections; the raw output is available through
  * aexrt_yolo_debug_output. */
 int aexrt_yolo_run(AexrtDevice* device, AexrtYoloModel* model, const float* input,
                    uint64_t input_element_count, AexrtYoloDetection* detections,
@@ -332,6 +365,13 @@ int aexrt_yolo_run(AexrtDevice* device, AexrtYoloModel* model, const float* inpu
  * tensor copied into the model's input buffer first; the network then runs
  * on `stream` (NULL = the model's own stream).  No host synchronisation. */
 int aexrt_yolo_run_device(AexrtYoloModel* model, const float* input, void* stream, void* reserved);
+/* Device-side postprocess of the last run's output0 on `stream` (NULL = the
+ * model's stream), without host synchronisation: *detections_device gets the
+ * model's [max_detections][6] float buffer (x1, y1, x2, y2, score, class) and
+ * *count_device its uint32 detection count.  No counterpart in the reference
+ * (whose run always reads back); for callers that keep results in HBM. */
+int aexrt_yolo_postprocess_device(AexrtYoloModel* model, void* stream, float** detections_device,
+                                  uint32_t** count_device);
 /* Device pointers of the model's input (fp32 NCHW) and output buffers. */
 void* aexrt_yolo_input_device_ptr(AexrtYoloModel* model);
 /* native/aexrt.h:465 zero-copy host input (pinned). */

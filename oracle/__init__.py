@@ -37,6 +37,17 @@ Pinning status (what, besides retyping, holds each function in place):
 * ``winograd_conv``: the Lavin-Gray identity -- equals direct convolution
   of the same (fp16-rounded) weights to fp32 rounding.
 * ``maxpool`` / ``resize_nearest``: ``torch.nn.functional`` equivalents.
+* ``quant_fused_pg16``: equals ``amax_slots`` + ``quant_pack(per_group)``
+  at N = 1; at N > 1 every image is packed with image 0's group maxima
+  (the reference's strip start has no image offset), checked as that
+  composition.
+* ``yolo_decode_nms_topk``: the reference's own known-answer vectors
+  (tests/test_runtime.py:442-463 CPU path, 3412-3448 GPU path); the NMS
+  invariants (kept same-class boxes overlap <= iou, every dropped box has
+  an outranking overlap); equality with greedy NMS (the reference's CPU
+  ``yolo_postprocess``) where no suppression chains exist, and a planted
+  chain where the GPU's mark rule differs from greedy NMS.  The anchor-order
+  append is one of the orders the reference's atomic counter can produce.
 """
 from __future__ import annotations
 
@@ -99,6 +110,11 @@ def lib():
         "or_winograd_f2x2_conv": (None, [_f32p, _f32p, _f32p, _u32p, _f32p]),
         "or_maxpool": (None, [_f32p, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _f32p, _u32, _u32]),
         "or_resize_nearest": (None, [_f32p, _u32, _u32, _u32, _u32, _f32p, _u32, _u32]),
+        "or_yolo_decode_nms_topk": (_u32, [_f32p, _u32, _u32, _u32, _u32, _u32, ctypes.c_float, ctypes.c_float,
+                                           _u32, _u32, _f32p, _u32p, _f32p]),
+        "or_yolo_dfl_decode_nms_topk": (_u32, [_f32p, _u32, _u32, _u32p, _f32p, _u32, ctypes.c_float,
+                                               ctypes.c_float, _u32, _u32, _f32p, _u32p, _f32p]),
+        "or_post_exp": (ctypes.c_float, [ctypes.c_float]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -314,3 +330,43 @@ def resize_nearest(x, oh: int, ow: int) -> np.ndarray:
     y = np.empty((n, c, oh, ow), dtype=np.float32)
     lib().or_resize_nearest(a.reshape(-1), n, c, h, w, y.reshape(-1), oh, ow)
     return y
+
+
+# --- YOLO postprocess ---------------------------------------------------------
+
+def yolo_decode_nms_topk(out, *, layout: int = 1, classes: int, has_objectness: bool = False,
+                         conf: float = 0.25, iou: float = 0.45, max_candidates: int = 512,
+                         max_detections: int = 100) -> np.ndarray:
+    """The reference's GPU postprocess of one output0 image ([C, A], or [A, C] for layout 2):
+    [count, 6] float32 rows x1, y1, x2, y2, score, class, best first."""
+    a = _f32(out)
+    if a.ndim == 3:
+        a = a[0]
+    channels, anchors = (a.shape[1], a.shape[0]) if layout == 2 else a.shape
+    cand = np.zeros(max_candidates * 6, np.float32)
+    keep = np.zeros(max_candidates, np.uint32)
+    dets = np.zeros(max_detections * 6, np.float32)
+    n = lib().or_yolo_decode_nms_topk(a.reshape(-1), layout, anchors, channels, classes, int(has_objectness),
+                                      float(conf), float(iou), max_candidates, max_detections, cand, keep, dets)
+    return dets.reshape(max_detections, 6)[:n].copy()
+
+
+def post_exp(x: float) -> float:
+    return float(lib().or_post_exp(float(x)))
+
+
+def yolo_dfl_decode_nms_topk(head, levels, *, classes: int, layout: int = 1, conf: float = 0.25,
+                             iou: float = 0.45, max_candidates: int = 512, max_detections: int = 100) -> np.ndarray:
+    """Raw Detect head [64 + classes, A] (layout 2: [A, 64 + classes]) of one image, levels = [(h, w, stride)]:
+    the reference's head decode + NMS + top-k, [count, 6] rows x1, y1, x2, y2, score, class."""
+    a = _f32(head)
+    if a.ndim == 3:
+        a = a[0]
+    hw = np.array([[h, w] for h, w, _ in levels], np.uint32).reshape(-1)
+    st = np.array([s for _, _, s in levels], np.float32)
+    cand = np.zeros(max_candidates * 6, np.float32)
+    keep = np.zeros(max_candidates, np.uint32)
+    dets = np.zeros(max_detections * 6, np.float32)
+    n = lib().or_yolo_dfl_decode_nms_topk(a.reshape(-1), layout, len(levels), hw, st, classes, float(conf),
+                                          float(iou), max_candidates, max_detections, cand, keep, dets)
+    return dets.reshape(max_detections, 6)[:n].copy()

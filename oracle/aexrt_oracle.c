@@ -718,3 +718,155 @@ EXPORT void or_resize_nearest(const float* x, uint32_t N, uint32_t C, uint32_t H
         y[(nc * OH + oy) * OW + ox] = x[(nc * H + iy) * W + ix];
     }
 }
+
+/* ------------------------------------------------------------------ */
+/* YOLO postprocess of output0 (the reference's GPU path)              */
+/* ------------------------------------------------------------------ */
+
+static float yolo_iou(const float* a, const float* b) {
+    const float x1 = fmaxf(a[0], b[0]), y1 = fmaxf(a[1], b[1]);
+    const float x2 = fminf(a[2], b[2]), y2 = fminf(a[3], b[3]);
+    const float iw = fmaxf(0.0f, x2 - x1), ih = fmaxf(0.0f, y2 - y1);
+    const float inter = iw * ih;
+    const float area_a = fmaxf(0.0f, a[2] - a[0]) * fmaxf(0.0f, a[3] - a[1]);
+    const float area_b = fmaxf(0.0f, b[2] - b[0]) * fmaxf(0.0f, b[3] - b[1]);
+    return inter / fmaxf(area_a + area_b - inter, 1e-7f);
+}
+
+static int yolo_outranks(float sj, uint32_t j, float si, uint32_t i) { return sj > si || (sj == si && j < i); }
+
+/* NMS mark (RT:15637-15691) and top-k (RT:15693-15735) over count
+ * candidates: a candidate is dropped when a candidate of the same class
+ * that outranks it (higher score, or equal score and lower index) has
+ * IoU > iou with it -- every such candidate counts, suppressed or not
+ * (unlike greedy NMS); a kept candidate's rank among the kept ones is its
+ * output slot; returns min(kept, max_det). */
+static uint32_t yolo_nms_topk(const float* cand, uint32_t count, float iou, uint32_t max_det,
+                              uint32_t* keep, float* dets) {
+    for (uint32_t i = 0; i < count; ++i) {
+        keep[i] = 1u;
+        for (uint32_t j = 0; j < count; ++j) {
+            if (j == i || cand[6u * j + 5u] != cand[6u * i + 5u]) continue;
+            if (yolo_outranks(cand[6u * j + 4u], j, cand[6u * i + 4u], i) &&
+                yolo_iou(cand + 6u * i, cand + 6u * j) > iou) { keep[i] = 0u; break; }
+        }
+    }
+    uint32_t kept = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        if (!keep[i]) continue;
+        ++kept;
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < count; ++j)
+            if (j != i && keep[j] && yolo_outranks(cand[6u * j + 4u], j, cand[6u * i + 4u], i)) ++rank;
+        if (rank < max_det) memcpy(dets + 6u * rank, cand + 6u * i, 6u * sizeof(float));
+    }
+    return kept < max_det ? kept : max_det;
+}
+
+/* decode/filter of a decoded output0 (RT:15300-15356): per anchor the best
+ * class score times objectness (strict >: first max wins), kept unless
+ * score < conf, box cx -/+ 0.5 w; the reference appends with an atomic
+ * counter, restated here in anchor order (one order it can produce) and
+ * capped at max_cand.  layout 2: out[a * channels + ch], else
+ * out[ch * anchors + a].  cand: scratch of max_cand * 6 floats, keep:
+ * max_cand words. */
+EXPORT uint32_t or_yolo_decode_nms_topk(const float* out, uint32_t layout, uint32_t anchors,
+                                        uint32_t channels, uint32_t classes, uint32_t has_obj,
+                                        float conf, float iou, uint32_t max_cand, uint32_t max_det,
+                                        float* cand, uint32_t* keep, float* dets) {
+#define RD(ch, a) (layout == 2u ? out[(uint64_t)(a) * channels + (ch)] : out[(uint64_t)(ch) * anchors + (a)])
+    const uint32_t cls_off = has_obj ? 5u : 4u;
+    uint32_t total = 0;
+    for (uint32_t a = 0; a < anchors && classes > 0; ++a) {
+        const float obj = has_obj ? RD(4u, a) : 1.0f;
+        float best = obj * RD(cls_off, a);
+        uint32_t best_cls = 0;
+        for (uint32_t c = 1; c < classes; ++c) {
+            const float s = obj * RD(cls_off + c, a);
+            if (s > best) { best = s; best_cls = c; }
+        }
+        if (best < conf) continue;
+        const uint32_t idx = total++;
+        if (idx >= max_cand) continue;
+        const float cx = RD(0u, a), cy = RD(1u, a), w = RD(2u, a), h = RD(3u, a);
+        const float hw = 0.5f * w, hh = 0.5f * h;
+        float* c = cand + 6u * idx;
+        c[0] = cx - hw; c[1] = cy - hh; c[2] = cx + hw; c[3] = cy + hh;
+        c[4] = best; c[5] = (float)best_cls;
+    }
+#undef RD
+    return yolo_nms_topk(cand, total < max_cand ? total : max_cand, iou, max_det, keep, dets);
+}
+
+/* e^x of the postprocess: Cody-Waite reduction x = k ln2 + r (ln2 as a
+ * 16-bit head, so k * head is exact, plus a tail), |r| <= ln2/2, e^r by
+ * the degree-7 Taylor polynomial in Horner form, times 2^k; 0 below -87,
+ * infinity above 88.5.  The product kernel computes the same operations
+ * (the reference's exp belongs to its shader compiler and driver). */
+EXPORT float or_post_exp(float x) {
+    if (x != x) return x;
+    if (x < -87.0f) return 0.0f;
+    if (x > 88.5f) return INFINITY;
+    const float k = rintf(x * 1.44269504f);
+    const float r = (x - k * 0.693145751953125f) - k * 1.42860677e-06f;
+    float p = 1.0f / 5040.0f;
+    p = p * r + 1.0f / 720.0f;
+    p = p * r + 1.0f / 120.0f;
+    p = p * r + 1.0f / 24.0f;
+    p = p * r + 1.0f / 6.0f;
+    p = p * r + 0.5f;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    return ldexpf(p, (int)k);
+}
+
+/* Raw Detect head (the post-conv part of RT:15465-15636): head[ch][a]
+ * (layout 2: [a][ch]) with channels 0..63 the 4 x 16 DFL bin logits and
+ * 64.. the class logits; score = 1 / (1 + exp(-logit)), best class strict
+ * >; kept unless score < conf; side d = sum_b e_b b / max(sum_b e_b,
+ * 1e-20), e_b = exp(l_b - max_b l_b); anchors level by level (lev_hw[2l] x
+ * lev_hw[2l+1], stride lev_stride[l]), centre (gx + 0.5, gy + 0.5), box =
+ * ((ax - d0) s, (ay - d1) s, (ax + d2) s, (ay + d3) s). */
+EXPORT uint32_t or_yolo_dfl_decode_nms_topk(const float* head, uint32_t layout, uint32_t nlev,
+                                            const uint32_t* lev_hw, const float* lev_stride,
+                                            uint32_t classes, float conf, float iou, uint32_t max_cand,
+                                            uint32_t max_det, float* cand, uint32_t* keep, float* dets) {
+    uint32_t anchors = 0;
+    for (uint32_t l = 0; l < nlev; ++l) anchors += lev_hw[2u * l] * lev_hw[2u * l + 1u];
+    const uint32_t channels = 64u + classes;
+#define RD(ch, a) (layout == 2u ? head[(uint64_t)(a) * channels + (ch)] : head[(uint64_t)(ch) * anchors + (a)])
+    uint32_t total = 0, a = 0;
+    for (uint32_t l = 0; l < nlev; ++l) {
+        const uint32_t gh = lev_hw[2u * l], gw = lev_hw[2u * l + 1u];
+        for (uint32_t pos = 0; pos < gh * gw; ++pos, ++a) {
+            float best = 1.0f / (1.0f + or_post_exp(-RD(64u, a)));
+            uint32_t best_cls = 0;
+            for (uint32_t c = 1; c < classes; ++c) {
+                const float s = 1.0f / (1.0f + or_post_exp(-RD(64u + c, a)));
+                if (s > best) { best = s; best_cls = c; }
+            }
+            if (best < conf) continue;
+            const uint32_t idx = total++;
+            if (idx >= max_cand) continue;
+            float dist[4];
+            for (uint32_t d = 0; d < 4u; ++d) {
+                float m = -3.402823e38f;
+                for (uint32_t b = 0; b < 16u; ++b) m = fmaxf(m, RD(16u * d + b, a));
+                float sum = 0.0f, acc = 0.0f;
+                for (uint32_t b = 0; b < 16u; ++b) {
+                    const float e = or_post_exp(RD(16u * d + b, a) - m);
+                    sum = sum + e;
+                    acc = acc + e * (float)b;
+                }
+                dist[d] = acc / fmaxf(sum, 1e-20f);
+            }
+            const float ax = (float)(pos % gw) + 0.5f, ay = (float)(pos / gw) + 0.5f, s = lev_stride[l];
+            float* c = cand + 6u * idx;
+            c[0] = (ax - dist[0]) * s; c[1] = (ay - dist[1]) * s;
+            c[2] = (ax + dist[2]) * s; c[3] = (ay + dist[3]) * s;
+            c[4] = best; c[5] = (float)best_cls;
+        }
+    }
+#undef RD
+    return yolo_nms_topk(cand, total < max_cand ? total : max_cand, iou, max_det, keep, dets);
+}

@@ -328,3 +328,226 @@ def test_maxpool_and_resize_against_torch():
     up = O.resize_nearest(x, 14, 18)
     ref_up = torch.nn.functional.interpolate(torch.from_numpy(x), size=(14, 18), mode="nearest").numpy()
     np.testing.assert_array_equal(up, ref_up)
+
+
+def test_fused_pg16_uses_image0_group_max_at_batch_gt_one():
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((3, 32, 5, 4)).astype(np.float32)
+    x[1:] *= 3.0
+    packed, slots = O.quant_fused_pg16(x)
+    s0 = O.amax_slots(x[:1])  # image 0's channel groups (N = 1: strips = groups)
+    np.testing.assert_array_equal(slots[1:], s0[1:])
+    for n in range(3):
+        want = O.quant_pack(x[n:n + 1], s0, per_group=True)
+        np.testing.assert_array_equal(packed.reshape(3, -1)[n], want)
+
+
+# ---- YOLO postprocess ----------------------------------------------------------
+
+def _scores_classes(d):
+    return [round(float(v), 2) for v in d[:, 4]], [int(v) for v in d[:, 5]]
+
+
+def test_yolo_post_reference_gpu_kat():
+    """tests/test_runtime.py:3412-3448 of the reference (its GPU decode + NMS + top-k)."""
+    out = np.zeros((6, 5), dtype="float32")
+    out[:4, 0] = [10, 10, 10, 10]
+    out[:4, 1] = [11, 10, 10, 10]
+    out[:4, 2] = [50, 50, 8, 8]
+    out[:4, 3] = [80, 80, 8, 8]
+    out[:4, 4] = [70, 70, 8, 8]
+    out[4:, 0] = [0.9, 0.1]
+    out[4:, 1] = [0.8, 0.1]
+    out[4:, 2] = [0.1, 0.7]
+    out[4:, 3] = [0.2, 0.1]
+    out[4:, 4] = [0.4, 0.2]
+    d = O.yolo_decode_nms_topk(out, classes=2, conf=0.25, iou=0.5, max_candidates=8, max_detections=4)
+    assert d.shape[0] == 3
+    assert _scores_classes(d) == ([0.9, 0.7, 0.4], [0, 1, 0])
+    np.testing.assert_array_equal(d[0, :4], np.float32([5, 5, 15, 15]))
+
+
+def test_yolo_post_reference_cpu_kats():
+    """tests/test_runtime.py:442-463 of the reference (channels first; channels last with objectness)."""
+    out = np.zeros((1, 6, 4), dtype="float32")
+    out[0, :4, 0] = [10, 10, 10, 10]
+    out[0, :4, 1] = [11, 10, 10, 10]
+    out[0, :4, 2] = [50, 50, 8, 8]
+    out[0, :4, 3] = [80, 80, 8, 8]
+    out[0, 4:, 0] = [0.9, 0.1]
+    out[0, 4:, 1] = [0.8, 0.1]
+    out[0, 4:, 2] = [0.1, 0.7]
+    out[0, 4:, 3] = [0.2, 0.1]
+    d = O.yolo_decode_nms_topk(out, classes=2, conf=0.25, iou=0.5)
+    assert list(zip(_scores_classes(d)[1], _scores_classes(d)[0])) == [(0, 0.9), (1, 0.7)]
+    out = np.zeros((1, 5, 7), dtype="float32")
+    out[0, 0, :4] = [10, 10, 10, 10]
+    out[0, 0, 4:] = [0.5, 0.9, 0.1]
+    out[0, 1, :4] = [50, 50, 8, 8]
+    out[0, 1, 4:] = [0.8, 0.1, 0.7]
+    d = O.yolo_decode_nms_topk(out, layout=2, classes=2, has_objectness=True, conf=0.25, iou=0.5)
+    assert list(zip(_scores_classes(d)[1], _scores_classes(d)[0])) == [(1, 0.56), (0, 0.45)]
+
+
+def _greedy_nms_reference(out, classes, conf, iou):
+    """The reference's CPU yolo_postprocess (src/aexrt/yolo.py:92-140, 996-1018), restated with numpy."""
+    y = out
+    boxes = y[:4].T.astype(np.float64)
+    scores = y[4:4 + classes].T
+    cls = np.argmax(scores, axis=1)
+    sc = scores[np.arange(scores.shape[0]), cls]
+    keep = sc >= conf
+    b = boxes[keep]
+    xyxy = np.stack([b[:, 0] - b[:, 2] / 2, b[:, 1] - b[:, 3] / 2, b[:, 0] + b[:, 2] / 2, b[:, 1] + b[:, 3] / 2], 1)
+    sc, cls = sc[keep], cls[keep]
+    res = []
+    for c in np.unique(cls):
+        idx = np.where(cls == c)[0]
+        order = idx[np.argsort(-sc[idx], kind="stable")]
+        while order.size:
+            i = order[0]
+            res.append((float(sc[i]), int(c)))
+            rest = order[1:]
+            x1 = np.maximum(xyxy[i, 0], xyxy[rest, 0]); y1 = np.maximum(xyxy[i, 1], xyxy[rest, 1])
+            x2 = np.minimum(xyxy[i, 2], xyxy[rest, 2]); y2 = np.minimum(xyxy[i, 3], xyxy[rest, 3])
+            inter = np.maximum(0, x2 - x1) * np.maximum(0, y2 - y1)
+            a0 = (xyxy[i, 2] - xyxy[i, 0]) * (xyxy[i, 3] - xyxy[i, 1])
+            a1 = (xyxy[rest, 2] - xyxy[rest, 0]) * (xyxy[rest, 3] - xyxy[rest, 1])
+            order = rest[inter / np.maximum(a0 + a1 - inter, 1e-7) <= iou]
+    return sorted(res, key=lambda t: -t[0])
+
+
+def _pair_clusters(rng, n_pairs, classes):
+    """Boxes in far-apart pairs (each pair overlapping or not): no suppression chains exist."""
+    a = 2 * n_pairs
+    out = np.zeros((4 + classes, a), np.float32)
+    for k in range(n_pairs):
+        cx, cy = 100.0 * (k % 10) + 50, 100.0 * (k // 10) + 50
+        for m in range(2):
+            j = 2 * k + m
+            out[:4, j] = [cx + rng.uniform(-8, 8), cy + rng.uniform(-8, 8), rng.uniform(10, 30), rng.uniform(10, 30)]
+            out[4:, j] = rng.uniform(0, 1, classes).astype(np.float32)
+    return out
+
+
+def test_yolo_post_equals_greedy_nms_without_chains():
+    rng = np.random.default_rng(5)
+    for trial in range(20):
+        out = _pair_clusters(rng, 30, 3)
+        d = O.yolo_decode_nms_topk(out, classes=3, conf=0.3, iou=0.3, max_candidates=512, max_detections=512)
+        want = _greedy_nms_reference(out, 3, 0.3, 0.3)
+        got = [(float(s), int(c)) for s, c in zip(d[:, 4], d[:, 5])]
+        assert [c for _, c in got] == [c for _, c in want] and np.allclose([s for s, _ in got], [s for s, _ in want])
+
+
+def test_yolo_post_mark_rule_differs_from_greedy_on_a_chain():
+    """A > B > C in one class, A overlaps B, B overlaps C, A does not overlap C: greedy NMS keeps A and C,
+    the reference's GPU mark rule drops C too (B outranks C and overlaps it, suppressed or not)."""
+    out = np.zeros((5, 3), np.float32)
+    out[:4, 0] = [10, 10, 10, 10]
+    out[:4, 1] = [14, 10, 10, 10]  # IoU(A, B) = IoU(B, C) = 0.43, IoU(A, C) = 0.11
+    out[:4, 2] = [18, 10, 10, 10]
+    out[4, :] = [0.9, 0.8, 0.7]
+    d = O.yolo_decode_nms_topk(out, classes=1, conf=0.25, iou=0.3)
+    assert _scores_classes(d)[0] == [0.9]
+    assert [s for s, _ in _greedy_nms_reference(out, 1, 0.25, 0.3)] == pytest.approx([0.9, 0.7])
+
+
+def test_yolo_post_invariants_and_candidate_cap():
+    rng = np.random.default_rng(9)
+    out = np.zeros((4 + 5, 600), np.float32)
+    out[:2] = rng.uniform(0, 320, (2, 600))
+    out[2:4] = rng.uniform(10, 60, (2, 600))
+    out[4:] = rng.uniform(0, 1, (5, 600))
+    for cap in (64, 512):
+        d = O.yolo_decode_nms_topk(out, classes=5, conf=0.2, iou=0.45, max_candidates=cap, max_detections=1000)
+        assert np.all(np.diff(d[:, 4]) <= 0)
+        for i in range(len(d)):
+            for j in range(i + 1, len(d)):
+                if d[i, 5] != d[j, 5]:
+                    continue
+                x1, y1 = max(d[i, 0], d[j, 0]), max(d[i, 1], d[j, 1])
+                x2, y2 = min(d[i, 2], d[j, 2]), min(d[i, 3], d[j, 3])
+                inter = max(0, x2 - x1) * max(0, y2 - y1)
+                ai = (d[i, 2] - d[i, 0]) * (d[i, 3] - d[i, 1]); aj = (d[j, 2] - d[j, 0]) * (d[j, 3] - d[j, 1])
+                assert inter / max(ai + aj - inter, 1e-7) <= 0.45 + 1e-6
+        # only the first `cap` passing anchors (in anchor order) are candidates
+        sc = out[4:].max(axis=0)
+        first = np.where(sc >= 0.2)[0][:cap]
+        assert set(np.round(d[:, 4], 6)) <= set(np.round(sc[first], 6))
+    small = O.yolo_decode_nms_topk(out, classes=5, conf=0.2, iou=0.45, max_candidates=512, max_detections=7)
+    assert small.shape[0] == 7
+
+
+def test_post_exp_against_numpy():
+    xs = np.concatenate([np.linspace(-87, 88.5, 20001, dtype=np.float32), np.float32([0, 1, -1, 0.5, -0.5])])
+    got = np.array([O.post_exp(float(x)) for x in xs], np.float64)
+    want = np.exp(xs.astype(np.float64))
+    assert np.max(np.abs(got - want) / want) < 3e-7
+    assert O.post_exp(0.0) == 1.0 and O.post_exp(-100.0) == 0.0 and O.post_exp(100.0) == float("inf")
+    assert np.isnan(O.post_exp(float("nan")))
+
+
+def _dfl_head(levels, classes, rng=None, onehot=None):
+    a = sum(h * w for h, w, _ in levels)
+    head = np.zeros((64 + classes, a), np.float32)
+    if rng is not None:
+        head[:] = rng.normal(0, 2, head.shape)
+    if onehot is not None:
+        head[:64] = 0
+        for i in range(a):
+            for d in range(4):
+                head[16 * d + onehot[i][d], i] = 40.0
+    return head
+
+
+def test_dfl_decode_closed_form_boxes_and_grid():
+    """One-hot bins give integer distances; the box is (grid centre -/+ distance) * stride per level."""
+    levels = [(4, 6, 8.0), (2, 3, 16.0), (1, 2, 32.0)]
+    a = sum(h * w for h, w, _ in levels)
+    rng = np.random.default_rng(3)
+    onehot = rng.integers(0, 16, (a, 4))
+    head = _dfl_head(levels, 2, onehot=onehot)
+    head[64:] = -5.0
+    head[64 + 1, :] = np.linspace(0, 4, a)  # class 1 wins, scores increase with the anchor index
+    d = O.yolo_dfl_decode_nms_topk(head, levels, classes=2, conf=0.0, iou=1.0, max_candidates=a, max_detections=a)
+    assert d.shape[0] == a
+    i = 0
+    want = {}
+    for h, w, s in levels:
+        for pos in range(h * w):
+            gx, gy = pos % w + 0.5, pos // w + 0.5
+            l, t, r, b = onehot[i]
+            sc = 1.0 / (1.0 + np.exp(-np.float64(head[65, i])))
+            want[i] = ((gx - l) * s, (gy - t) * s, (gx + r) * s, (gy + b) * s, sc)
+            i += 1
+    # rank order = descending score = descending anchor index
+    for rank, row in enumerate(d):
+        wx = want[a - 1 - rank]
+        np.testing.assert_array_equal(row[:4], np.float32(wx[:4]))
+        assert abs(row[4] - wx[4]) < 2e-7 and row[5] == 1.0
+
+
+def test_dfl_decode_matches_float64_softmax_expectation():
+    levels = [(5, 5, 8.0), (3, 3, 16.0)]
+    rng = np.random.default_rng(8)
+    head = _dfl_head(levels, 3, rng=rng)
+    d = O.yolo_dfl_decode_nms_topk(head, levels, classes=3, conf=0.0, iou=1.0, max_candidates=64, max_detections=64)
+    # recompute every anchor in float64 and match rows by score
+    a = head.shape[1]
+    rows = {}
+    i = 0
+    for h, w, s in levels:
+        for pos in range(h * w):
+            lg = head[:64, i].astype(np.float64).reshape(4, 16)
+            e = np.exp(lg - lg.max(axis=1, keepdims=True))
+            dist = (e * np.arange(16)).sum(1) / e.sum(1)
+            gx, gy = pos % w + 0.5, pos // w + 0.5
+            sc = 1 / (1 + np.exp(-head[64:, i].astype(np.float64)))
+            rows[i] = (np.array([(gx - dist[0]) * s, (gy - dist[1]) * s, (gx + dist[2]) * s, (gy + dist[3]) * s]),
+                       sc.max(), int(sc.argmax()))
+            i += 1
+    assert d.shape[0] == a
+    for row in d:
+        k = min(rows, key=lambda j: abs(rows[j][1] - row[4]) + 10 * (rows[j][2] != row[5]))
+        np.testing.assert_allclose(row[:4], rows[k][0], rtol=1e-5, atol=1e-4)
