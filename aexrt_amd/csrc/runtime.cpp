@@ -150,6 +150,7 @@ struct AexrtYoloModel {
     bool autotune = true;            // measure every conv's kernel/tile choices at load
     bool tune_log = false;           // print each measured choice (AEXRT_HIP_TUNE_LOG=1)
     std::map<std::string, ConvChoice> tuned;  // conv shape -> measured choice
+    std::string tune_cache;                    // AEXRT_HIP_TUNE_CACHE file, empty: none
     hipStream_t lane_stream[kLanes] = {};      // capture-time streams of lanes 1..kLanes-1
     int n_lanes = 1;                           // lanes the schedule uses (measured at load)
     std::vector<hipEvent_t> step_events;      // per step, recorded when a step signals
@@ -711,15 +712,54 @@ std::string tune_key(const ConvParams& p, bool int8) {
     return buf;
 }
 
+bool same_choice(const ConvChoice& a, const ConvChoice& b) {
+    return a.kind == b.kind && a.jn == b.jn && a.pw == b.pw && a.ksw == b.ksw && a.tr == b.tr && a.tc == b.tc &&
+           a.cc == b.cc && a.nw == b.nw;
+}
+
+// AEXRT_HIP_TUNE_CACHE=<file>: measured choices are read from the file at load
+// (each still checked against the shape's candidates) and the file is
+// rewritten with every choice of the model, so that later loads of the same
+// engine (or of another with the same conv shapes) launch the same kernels.
+// One line per conv shape: key, tab, kind jn pw ksw tr tc cc nw.
+void load_tune_cache(AexrtYoloModel* m) {
+    std::ifstream f(m->tune_cache);
+    std::string line;
+    while (std::getline(f, line)) {
+        const size_t tab = line.find('\t');
+        if (tab == std::string::npos) continue;
+        ConvChoice c{};
+        if (std::sscanf(line.c_str() + tab + 1, "%d %d %d %d %d %d %d %d", &c.kind, &c.jn, &c.pw, &c.ksw, &c.tr,
+                        &c.tc, &c.cc, &c.nw) == 8)
+            m->tuned[line.substr(0, tab)] = c;
+    }
+}
+
+void save_tune_cache(AexrtYoloModel* m) {
+    const std::string tmp = m->tune_cache + ".tmp";
+    {
+        std::ofstream f(tmp, std::ios::trunc);
+        for (const auto& [key, c] : m->tuned)
+            f << key << '\t' << c.kind << ' ' << c.jn << ' ' << c.pw << ' ' << c.ksw << ' ' << c.tr << ' ' << c.tc
+              << ' ' << c.cc << ' ' << c.nw << '\n';
+        if (!f) return;
+    }
+    std::rename(tmp.c_str(), m->tune_cache.c_str());
+}
+
 bool tune_conv(AexrtYoloModel* m, ConvParams& p, bool int8) {
     const std::string key = tune_key(p, int8);
-    auto it = m->tuned.find(key);
-    if (it != m->tuned.end()) {
-        p.choice = it->second;
-        return true;
-    }
     ConvChoice cand[128];
     const int n = enumerate_conv_choices(p, int8, cand, 128);
+    auto it = m->tuned.find(key);
+    if (it != m->tuned.end()) {
+        for (int i = 0; i < n; ++i)
+            if (same_choice(cand[i], it->second)) {
+                p.choice = it->second;
+                return true;
+            }
+        m->tuned.erase(it);  // a cached choice this build does not offer
+    }
     hipEvent_t e0 = nullptr, e1 = nullptr;
     if (!check_hip(hipEventCreate(&e0), "tune event") || !check_hip(hipEventCreate(&e1), "tune event")) {
         if (e0) (void)hipEventDestroy(e0);
@@ -1278,9 +1318,15 @@ bool build_model(AexrtYoloModel* m) {
     m->autotune = !(tune && tune[0] == '0');
     const char* tlog = std::getenv("AEXRT_HIP_TUNE_LOG");
     m->tune_log = tlog && tlog[0] == '1';
+    const char* tcache = std::getenv("AEXRT_HIP_TUNE_CACHE");
+    if (m->autotune && tcache && tcache[0]) {
+        m->tune_cache = tcache;
+        load_tune_cache(m);
+    }
     m->n_lanes = 1;
     if (!build_steps(m, m->copies)) return false;
     if (m->autotune && !choose_lanes(m)) return false;
+    if (!m->tune_cache.empty()) save_tune_cache(m);
     const char* prof = std::getenv("AEXRT_HIP_PROFILE");
     m->profile = prof && prof[0] == '1';
     setup_postprocess(m);

@@ -54,10 +54,12 @@ def fill_input(model, batch: int, imgsz: int, seed: int = 4) -> None:
     from aexrt_amd import _lib
 
     x = np.random.default_rng(seed).random((batch, 3, imgsz, imgsz), dtype=np.float32)
-    _lib.lib()
-    hip = ctypes.CDLL("libamdhip64.so")
-    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
-    rc = hip.hipMemcpy(ctypes.c_void_p(model.input_device_ptr), x.ctypes.data_as(ctypes.c_void_p), x.nbytes, 1)
+    # hipMemcpy of the HIP runtime the library is linked against (found
+    # through the library's handle), kind 1 = host to device
+    memcpy = _lib.lib().hipMemcpy
+    memcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    memcpy.restype = ctypes.c_int
+    rc = memcpy(ctypes.c_void_p(model.input_device_ptr), x.ctypes.data_as(ctypes.c_void_p), x.nbytes, 1)
     if rc != 0:
         raise RuntimeError(f"hipMemcpy failed: {rc}")
 
@@ -98,6 +100,23 @@ def profile_kernels(model, plan, reps: int = 5):
             totals[label] = totals.get(label, 0.0) + ms
     model.set_profiling(False)
     return {k: v / reps for k, v in totals.items()}
+
+
+TRAFFIC_TABLE = os.path.join(ROOT, "profiles", "hbm_traffic_yolov8n320_bs64.md")
+
+
+def measured_traffic(label: str, batch: int):
+    """HBM bytes per launch of a step, from the committed rocprofv3 counter summary of this
+    workload (FETCH_SIZE + WRITE_SIZE, calibrated against a copy of known size); None when the
+    summary has no row for this step."""
+    if batch != 64 or not os.path.exists(TRAFFIC_TABLE):
+        return None
+    with open(TRAFFIC_TABLE) as f:
+        for line in f:
+            cells = [c.strip() for c in line.strip().strip("|").split("|")]
+            if len(cells) >= 5 and cells[0] == label:
+                return int(round((float(cells[3]) + float(cells[4])) * 1e6))
+    return None
 
 
 def roofline_for(prof: dict, replay, plans):
@@ -166,6 +185,36 @@ def cpu_baseline(graph_bs1, images_budget_s: float = 12.0):
                       f"{dt:.1f} s)"}
 
 
+CAL_ELEMS = 64 << 20  # fp32 elements of the counter-calibration copy (256 MiB read, 256 MiB written)
+
+
+def pmc_pass(batch: int) -> int:
+    """One pass for rocprofv3 --pmc: a negation of CAL_ELEMS fp32 values (known
+    HBM traffic, the counters' scale), then one event-profiled forward of the
+    network, every step launched on its own; prints the step labels in launch
+    order so that aexrt_amd/profiling.py can match dispatches to steps."""
+    import torch
+
+    torch.cuda.init()
+    g, model = build_model(batch)
+    fill_input(model, batch, 320)
+    model.run_device()
+    torch.cuda.synchronize()
+    a = torch.ones(CAL_ELEMS, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    torch.neg(a, out=b)
+    torch.cuda.synchronize()
+    del a, b
+    model.set_profiling(True)
+    model.run_device()
+    labels = [lab for lab, _ in model.profile_events()]
+    model.set_profiling(False)
+    print(json.dumps({"pmc_pass": {"batch": batch, "calibration_bytes": CAL_ELEMS * 4, "steps": labels}}))
+    model.close()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -173,7 +222,11 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="one calibration copy and one profiled forward at --batch, for rocprofv3 --pmc")
     args = ap.parse_args()
+    if args.pmc_pass:
+        return pmc_pass(args.batch)
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on exactly one GPU; multi-GPU runs are not part of this "
                                    "build (per-tensor amax would need a batch-wide max-reduce across GPUs)"}))
@@ -200,6 +253,8 @@ def main() -> int:
         plan_replay[bs] = replay
     big = results[args.batch]
     roof, _ = roofline_for(big["prof"], big["replay"], None)
+    if roof:
+        roof["traffic"] = measured_traffic(roof["kernel"], args.batch)
     tops = int8_tops(big["prof"], big["replay"])
     line = {
         "metric": "YOLOv8n-320 W8A8 images/s (bs1, bs64); int8 conv TOPS vs MFMA peak",

@@ -266,3 +266,27 @@ def test_engine_file_roundtrip_and_fail_closed(cuda, tmp_path):
     data[-1] ^= 0xFF  # corrupt the last section payload
     with pytest.raises(RuntimeError, match="checksum"):
         NativeHipYoloModel(bytes(data))
+
+
+def test_tune_cache_file_roundtrip(cuda, tmp_path, monkeypatch):
+    """AEXRT_HIP_TUNE_CACHE: choices written at load, reused by the next load, bad entries re-measured."""
+    g = _c2f_graph(batch=1, c=64, dim=20, seed=5)
+    replay = E.lower_graph(g)
+    algo = E.w8a8_algo_map(replay)
+    data = E.build_aexrt_engine(g, precision="fp16", algo_overrides=algo)
+    cache = tmp_path / "tune.txt"
+    monkeypatch.setenv("AEXRT_HIP_TUNE_CACHE", str(cache))
+    x = np.random.default_rng(5).standard_normal((1, 64, 20, 20)).astype(np.float32)
+    with NativeHipYoloModel(data) as m:
+        m.run(x)
+        out1 = m.output()
+    lines = cache.read_text().splitlines()
+    assert len(lines) >= 3 and all("\t" in ln for ln in lines)
+    # a choice this build does not offer is dropped and measured again
+    key = lines[0].split("\t")[0]
+    cache.write_text("\n".join([f"{key}\t1 9 9 0 0 0 0 4"] + lines[1:]) + "\n")
+    with NativeHipYoloModel(data) as m:
+        m.run(x)
+        np.testing.assert_array_equal(m.output(), out1)
+    again = dict(ln.split("\t") for ln in cache.read_text().splitlines())
+    assert again[key] != "1 9 9 0 0 0 0 4"
