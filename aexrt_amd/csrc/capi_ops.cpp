@@ -188,6 +188,14 @@ int aexrt_hip_set_conv3x3_halo(int32_t mode, int32_t jn, int32_t pw, int32_t tr,
     return 1;
 }
 
+int aexrt_hip_set_conv_stem(int32_t mode, int32_t tr) {
+    if (!set_conv_stem(mode, tr)) {
+        set_error("set_conv_stem: bad mode or band rows");
+        return 0;
+    }
+    return 1;
+}
+
 int aexrt_hip_conv_weight_bytes(const AexrtConv2DDesc* desc, uint32_t algorithm, uint64_t* out_nbytes) {
     if (!desc || !out_nbytes) {
         set_error("conv_weight_bytes: null argument");

@@ -114,6 +114,7 @@ int enumerate_conv_choices(const ConvParams& p, bool int8, ConvChoice* out, int 
             out[n++] = c;
         }
     }
+    if (n < cap && nchw && !int8) n += enumerate_stem_choices(p, out + n, cap - n);
     if (n < cap) n += enumerate_halo_choices(p, int8, out + n, cap - n);
     return n;
 }
@@ -185,7 +186,10 @@ hipError_t launch_conv_igemm(const ConvParams& p0, bool int8, hipStream_t stream
         p.fd_ow = make_fastdiv((uint32_t)p.OW);
         p.fd_c = make_fastdiv((uint32_t)p.C);
         p.fd_kw = make_fastdiv((uint32_t)p.KW);
-        hipError_t e = p.choice.kind == 1 ? hipErrorNotSupported : launch_conv_halo(p, int8, epi, stream);
+        hipError_t e = hipErrorNotSupported;
+        if (nchw && !int8 && (p.choice.kind == 0 || p.choice.kind == 3)) e = launch_conv_stem(p, stream);
+        if (e == hipErrorNotSupported && p.choice.kind != 1 && p.choice.kind != 3)
+            e = launch_conv_halo(p, int8, epi, stream);
         if (e == hipErrorNotSupported && !nchw && p.choice.kind != 2) e = launch_variant(int8, mc, epi, p, t, stream);
         if (e != hipSuccess) return e;
     }

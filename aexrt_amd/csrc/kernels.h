@@ -133,6 +133,16 @@ hipError_t launch_conv_halo(const ConvParams& p, bool int8, int epi, hipStream_t
 // tr x tc output positions per tile, cc channels per chunk; a 3x3 conv the
 // tile does not fit then fails).  False for a tile without a kernel instance.
 bool set_conv3x3_halo(int mode, int jn, int pw, int tr, int tc, int cc);
+// Band kernel of the network's first conv (3x3 pad 1, stride 1/2, fp32 NCHW
+// input of at most 3 channels read directly, fp16 SiLU output, OCp <= 64,
+// W % 4 == 0): whole output rows per tile, one fp16 MFMA per 16 positions and
+// 16 channels.  hipErrorNotSupported for other convs or when switched off.
+hipError_t launch_conv_stem(const ConvParams& p, hipStream_t stream);
+bool stem_shape_ok(const ConvParams& p);
+int enumerate_stem_choices(const ConvParams& p, ConvChoice* out, int cap);
+// Stem kernel selection: mode 0 automatic (band kernel when the conv fits),
+// 1 never (halo-tile kernel), 2 forced band of tr output rows.
+bool set_conv_stem(int mode, int tr);
 // Input staging of the network's first conv: fp32 NCHW -> fp16 NHWC with the
 // channels zero-padded to a multiple of 8 (one 16-byte store per pixel and
 // 8 channels).  y has c_stride Cp = C rounded up to 8, dense.

@@ -1325,7 +1325,16 @@ bool build_model(AexrtYoloModel* m) {
     }
     m->n_lanes = 1;
     if (!build_steps(m, m->copies)) return false;
-    if (m->autotune && !choose_lanes(m)) return false;
+    // AEXRT_HIP_LANES=<n>: fixed number of streams for the captured schedule
+    // (1 = steps in launch order, e.g. for a per-kernel trace); otherwise the
+    // faster of kLanes and 1, measured
+    const char* lanes = std::getenv("AEXRT_HIP_LANES");
+    if (lanes && lanes[0] >= '1' && lanes[0] <= '9') {
+        m->n_lanes = std::min(kLanes, std::atoi(lanes));
+        schedule_steps(m);
+    } else if (m->autotune && !choose_lanes(m)) {
+        return false;
+    }
     if (!m->tune_cache.empty()) save_tune_cache(m);
     const char* prof = std::getenv("AEXRT_HIP_PROFILE");
     m->profile = prof && prof[0] == '1';

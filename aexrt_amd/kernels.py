@@ -210,6 +210,16 @@ def set_conv3x3_halo(mode: int = HALO_AUTO, jn: int = 0, pw: int = 0, tr: int = 
     check(_lib.lib().aexrt_hip_set_conv3x3_halo(mode, jn, pw, tr, tc, cc), "set_conv3x3_halo")
 
 
+STEM_AUTO, STEM_OFF, STEM_FORCE, STEM_FORCE_ONE = 0, 1, 2, 3
+
+
+def set_conv_stem(mode: int = STEM_AUTO, tr: int = 0) -> None:
+    """Select the kernel of the first conv on the fp32 NCHW input: automatic (band kernel when it
+    fits), off (halo-tile kernel), or a forced band of ``tr`` output rows (STEM_FORCE: a grid of
+    resident blocks walking runs of bands, STEM_FORCE_ONE: one band per block)."""
+    check(_lib.lib().aexrt_hip_set_conv_stem(mode, tr), "set_conv_stem")
+
+
 def conv_weight_bytes(params: Sequence[int], algorithm: int) -> int:
     d = ConvDesc.from_params(params)
     n = ctypes.c_uint64()

@@ -250,6 +250,15 @@ int aexrt_hip_set_conv_tile(int32_t jn, int32_t pw, int32_t ksw);
  * bad request. */
 int aexrt_hip_set_conv3x3_halo(int32_t mode, int32_t jn, int32_t pw, int32_t tr, int32_t tc, int32_t cc);
 
+/* Kernel of the network's first conv (3x3 pad 1, stride 1/2, the fp32 NCHW
+ * input with at most 3 channels read directly, SiLU, fp16 output; a kernel
+ * choice of the reference's replay_conv_algorithm, RT:9424-9500): mode 0
+ * automatic (a band kernel of whole output rows when the conv fits it),
+ * 1 never (the halo-tile kernel), 2 forced band of tr output rows on a grid
+ * of resident blocks, 3 the same with one band per block (a conv the band
+ * does not fit then fails).  Returns 0 for a bad request. */
+int aexrt_hip_set_conv_stem(int32_t mode, int32_t tr);
+
 /* Glue ops of the replay stream on NHWC fp16 views. */
 int aexrt_hip_fill_u32(uint32_t* dst, uint64_t count, uint32_t value, void* stream);
 int aexrt_hip_nchw_f32_to_nhwc(const float* x, uint32_t batch, uint32_t channels, uint32_t plane,

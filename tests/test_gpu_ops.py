@@ -270,7 +270,11 @@ def test_stem_conv_reads_fp32_nchw_input(cuda, n, h, w, oc, s):
     y1 = torch.empty_like(y0)
     s0, s1 = K.new_slots(oc, cuda), K.new_slots(oc, cuda)
     K.conv2d(pc, staged, y0, flags=K.SILU, y_slots=s0)
-    K.conv2d(pc, xf, y1, flags=K.SILU | K.IN_NCHW_F32, y_slots=s1)
+    K.set_conv_stem(K.STEM_OFF)  # the halo-tile kernel: same k order as the staged path
+    try:
+        K.conv2d(pc, xf, y1, flags=K.SILU | K.IN_NCHW_F32, y_slots=s1)
+    finally:
+        K.set_conv_stem(K.STEM_AUTO)
     torch.cuda.synchronize()
     assert torch.equal(y0, y1)
     np.testing.assert_array_equal(_u32(s0), _u32(s1))
@@ -278,6 +282,54 @@ def test_stem_conv_reads_fp32_nchw_input(cuda, n, h, w, oc, s):
     y_ref = O.cpu_conv2d(O.round_f16(x), O.round_f16(wt), b, desc, silu=True)
     err, allowed = tol_range(y_ref, nhwc_to_nchw(y1.float().cpu().numpy()), FP16_TOL)
     assert err <= allowed, (err, allowed)
+
+
+@pytest.mark.parametrize("n,ic,h,w,oc,s", [(2, 3, 64, 64, 16, 2), (1, 3, 36, 28, 32, 2), (3, 3, 20, 20, 24, 1),
+                                            (1, 3, 160, 160, 16, 2), (2, 3, 33, 40, 48, 2), (1, 1, 24, 16, 16, 2),
+                                            (2, 2, 17, 12, 64, 1)])
+@pytest.mark.parametrize("tr", [0, 1, 2, 4, 8])
+def test_stem_band_kernel(cuda, n, ic, h, w, oc, s, tr):
+    """The band kernel of the first conv (whole output rows per tile, k = c * 9 + tap in one
+    MFMA) against the fp32 direct conv of the fp16-rounded operands, against the halo-tile
+    kernel, and its amax slot against max|y| of what it stored."""
+    import torch
+
+    rng = np.random.default_rng(71 + h + ic)
+    cp = 8
+    x = rng.standard_normal((n, ic, h, w)).astype(np.float32)
+    wt = he_weight(rng, oc, ic, 3)
+    b = packing.fp16_round(rng.uniform(-0.1, 0.1, oc).astype(np.float32))
+    wpad = np.zeros((oc, cp, 3, 3), np.float32)
+    wpad[:, :ic] = wt
+    dpad = O.conv_desc(n, cp, h, w, oc, 3, s, 1)
+    pc = K.prepare_conv(dpad, 5, K.SRC_RAW_F32, wpad, b, device=cuda)
+    _, _, oh, ow = O.out_shape(dpad)
+    xf = torch.from_numpy(x).to(cuda)
+    y_band = torch.full((n, oh, ow, oc), float("nan"), dtype=torch.float16, device=cuda)
+    y_halo = torch.empty_like(y_band)
+    s_band, s_halo = K.new_slots(oc, cuda), K.new_slots(oc, cuda)
+    K.set_conv_stem(K.STEM_FORCE if tr else K.STEM_AUTO, tr)
+    try:
+        K.conv2d(pc, xf, y_band, flags=K.SILU | K.IN_NCHW_F32, y_slots=s_band)
+        K.set_conv_stem(K.STEM_OFF)
+        K.conv2d(pc, xf, y_halo, flags=K.SILU | K.IN_NCHW_F32, y_slots=s_halo)
+    finally:
+        K.set_conv_stem(K.STEM_AUTO)
+    torch.cuda.synchronize()
+    got = y_band.float().cpu().numpy()
+    assert np.isfinite(got).all()  # every output position written
+    desc = O.conv_desc(n, ic, h, w, oc, 3, s, 1)
+    y_ref = O.cpu_conv2d(O.round_f16(x), O.round_f16(wt), b, desc, silu=True)
+    err, allowed = tol_range(y_ref, nhwc_to_nchw(got), FP16_TOL)
+    assert err <= allowed, (err, allowed)
+    err_h, _ = tol_range(y_halo.float().cpu().numpy(), got, FP16_TOL)
+    assert err_h <= allowed, (err_h, allowed)
+    amax_stored = np.abs(got.reshape(-1, oc)).reshape(-1, (oc + 15) // 16, 16).max(axis=(0, 2)) \
+        if oc % 16 == 0 else None
+    slots = _u32(s_band).view(np.float32)
+    if amax_stored is not None:
+        np.testing.assert_array_equal(slots, amax_stored.astype(np.float32))
+    assert float(slots.max()) == float(np.abs(got).max())
 
 
 def test_stem_conv_nchw_input_rejects_unsupported(cuda):
