@@ -57,7 +57,7 @@ struct HaloParams {
 // Largest k-step count of one chunk (table of tap offsets).
 constexpr int kHaloMaxSpc = 32;
 // 16-byte weight pieces per thread: the block's weights are at most
-// 256 * kHaloWeightRounds * 16 bytes (64 KB) with 4 waves.
+// 64 * NW * kHaloWeightRounds * 16 bytes (64 KB with 4 waves, 128 KB with 8).
 constexpr int kHaloWeightRounds = 16;
 
 namespace halo {
@@ -78,9 +78,8 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_halo_kernel(HaloParams h) {
     constexpr int WQ = Frag<INT8>::wq;   // MFMAs (and weight pieces) per 64-k step
     constexpr int ESZ = Frag<INT8>::esz;
     constexpr int R = JN * 16;           // output channels of the block
-    constexpr int LOG2R = JN == 1 ? 4 : (JN == 2 ? 5 : (JN == 4 ? 6 : 7));
     constexpr int PIECE = 8 * ESZ;       // LDS bytes of one 8-channel input piece
-    static_assert((1 << LOG2R) == R, "JN must be 1, 2, 4 or 8");
+    static_assert(JN >= 1 && JN <= 8, "JN must be 1..8");
     static_assert(!(NCHW && INT8), "the NCHW input loader is fp16 only");
     typedef typename std::conditional<INT8, v4i, v4f>::type acc_t;
 
@@ -122,13 +121,13 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_halo_kernel(HaloParams h) {
 
     // ---- weights: [chunk * spc + s][h][row][grp * 16 B], gathered ----------
     // 16-byte piece e: grp = e & 3, row = (e >> 2) % R, (gs, h) from the rest;
-    // chunk-local k = g * 16 + h * 8 = tap * CC + c.  At most 64 KB: one
-    // round of kHaloWeightRounds pieces per thread.
+    // chunk-local k = g * 16 + h * 8 = tap * CC + c.  At most NT *
+    // kHaloWeightRounds pieces: one round of loads per thread.
     const int wpieces = h.wbytes >> 4;
     auto wload = [&](int e) {
         const int g4 = e & 3;
-        const int row = (e >> 2) & (R - 1);
-        const int gsh = e >> (2 + LOG2R);
+        const int row = (e >> 2) % R;
+        const int gsh = (e >> 2) / R;
         const int gs = gsh / WQ, hh = gsh - (gsh / WQ) * WQ;
         const int ch = (int)fdiv((uint32_t)gs, h.fd_spc);
         const int kk = ((gs - ch * h.spc) * 4 + g4) * 16 + hh * 8;
@@ -508,6 +507,11 @@ hipError_t halo_launch_family(const HaloParams& h, int jn, int pw, int np, int n
     AEXRT_HALO_CASE8(1, 1, 4) AEXRT_HALO_CASE8(1, 2, 4) AEXRT_HALO_CASE8(2, 1, 4) AEXRT_HALO_CASE8(2, 2, 4)
     AEXRT_HALO_CASE8(4, 1, 4) AEXRT_HALO_CASE8(4, 2, 4) AEXRT_HALO_CASE8(1, 1, 8) AEXRT_HALO_CASE8(1, 2, 8)
     AEXRT_HALO_CASE8(2, 1, 8) AEXRT_HALO_CASE8(2, 2, 8) AEXRT_HALO_CASE8(4, 1, 8) AEXRT_HALO_CASE8(4, 2, 8)
+    // every output channel of an 80-channel conv in one block (weights up to
+    // 128 KB, one block per CU)
+    if constexpr (!INT8) {
+        AEXRT_HALO_CASE8(5, 1, 4) AEXRT_HALO_CASE8(5, 2, 4) AEXRT_HALO_CASE8(5, 1, 8) AEXRT_HALO_CASE8(5, 2, 8)
+    }
 #undef AEXRT_HALO_CASE8
     return hipErrorInvalidValue;
 }

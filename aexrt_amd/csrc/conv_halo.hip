@@ -19,8 +19,10 @@ std::atomic<int> g_halo_mode{0};
 std::atomic<uint64_t> g_force{0};  // jn | pw << 8 | tr << 16 | tc << 32 | cc << 48 (8/8/16/16/16 bits)
 std::atomic<int> g_force_nw{4};     // waves per block of the forced tile
 
-// dynamic LDS of one block (static tables aside): two blocks fit a CU's 160 KB
+// dynamic LDS of one block (static tables aside): two blocks fit a CU's 160 KB;
+// 8-wave blocks may take most of a CU (one block per CU)
 constexpr int kLdsBudget = 80 * 1024 - 2048;
+constexpr int kLdsBudget8 = 152 * 1024;
 
 struct HaloTile {
     int jn, pw, np, TR, TC, CC;
@@ -72,7 +74,9 @@ bool halo_geometry(HaloParams& h, const HaloTile& t, bool int8) {
     // on the network, its larger windows cost occupancy
     h.pstride = t.CC * esz;
     h.tbytes = (h.IR * h.ICOL * h.pstride + 15) & ~15;
-    if (h.wbytes + 2 * h.tbytes > kLdsBudget || h.wbytes > 64 * t.nw * kHaloWeightRounds * 16) return false;
+    if (h.wbytes + 2 * h.tbytes > (t.nw == 8 ? kLdsBudget8 : kLdsBudget) ||
+        h.wbytes > 64 * t.nw * kHaloWeightRounds * 16)
+        return false;
     h.c.ntn = (p.OCp / 16 + t.jn - 1) / t.jn;
     h.fd_cc8 = make_fastdiv((uint32_t)(t.CC / 8));
     h.fd_icol = make_fastdiv((uint32_t)h.ICOL);
@@ -180,7 +184,9 @@ int enumerate_halo_choices(const ConvParams& p, bool int8, ConvChoice* out, int 
         const int CC = p.C / div;
         if (CC % (int8 ? 16 : 8) || CC > (int8 ? 128 : 64)) continue;
         for (int nw = 4; nw <= (nchw ? 4 : 8) && n < cap; nw <<= 1)
-        for (int jn = 1; jn <= std::min(4, pow2_at_least(ocj, 4)) && n < cap; jn <<= 1) {
+        for (int jn = 1; jn <= (ocj == 5 && nw == 8 && !int8 ? 5 : std::min(4, pow2_at_least(ocj, 4))) && n < cap;
+             jn = jn == 4 ? 5 : jn << 1) {
+            if (jn == 5 && ocj != 5) continue;
             for (int pw = nchw ? 2 : 1; pw <= (nw == 8 ? 2 : 4) && n < cap; pw <<= 1) {
                 const int npos = 16 * nw * pw;  // positions of a tile
                 const int tcs[7] = {p.OW, ow4, 16, 32, 48, 64, 80};
@@ -219,14 +225,38 @@ bool set_conv3x3_halo(int mode, int jn, int pw, int tr, int tc, int cc) {
         g_halo_mode.store(mode);
         return true;
     }
-    // mode 2: 4 waves per block, mode 3: 8 waves (pw 1 or 2)
-    if ((mode != 2 && mode != 3) || !(jn == 1 || jn == 2 || jn == 4) || !(pw == 1 || pw == 2 || pw == 4) ||
+    if (mode == 4) {
+        // the wide-tile fp16 kernel: jn 4 or 5 channel subtiles, pw 2 or 4
+        if (!(jn == 4 || jn == 5) || !(pw == 2 || pw == 4) || tr < 1 || tr > 0xFFFF || tc < 1 || tc > 0xFFFF ||
+            cc < 8 || cc > 0xFFFF)
+            return false;
+        g_force.store((uint64_t)jn | ((uint64_t)pw << 8) | ((uint64_t)tr << 16) | ((uint64_t)tc << 32) |
+                      ((uint64_t)cc << 48));
+        g_halo_mode.store(4);
+        return true;
+    }
+    // mode 2: 4 waves per block, mode 3: 8 waves (pw 1 or 2; jn 5 only with 8 waves)
+    if ((mode != 2 && mode != 3) || !(jn == 1 || jn == 2 || jn == 4 || (jn == 5 && mode == 3)) ||
+        !(pw == 1 || pw == 2 || pw == 4) ||
         (mode == 3 && pw == 4) || tr < 1 || tr > 0xFFFF || tc < 1 || tc > 0xFFFF || cc < 8 || cc > 0xFFFF)
         return false;
     g_force.store((uint64_t)jn | ((uint64_t)pw << 8) | ((uint64_t)tr << 16) | ((uint64_t)tc << 32) |
                   ((uint64_t)cc << 48));
     g_force_nw.store(mode == 3 ? 8 : 4);
     g_halo_mode.store(2);
+    return true;
+}
+
+bool forced_wide_choice(ConvChoice& c) {
+    if (g_halo_mode.load(std::memory_order_relaxed) != 4) return false;
+    const uint64_t f = g_force.load(std::memory_order_relaxed);
+    c = ConvChoice{};
+    c.kind = 4;
+    c.jn = (int)(f & 0xFF);
+    c.pw = (int)((f >> 8) & 0xFF);
+    c.tr = (int)((f >> 16) & 0xFFFF);
+    c.tc = (int)((f >> 32) & 0xFFFF);
+    c.cc = (int)((f >> 48) & 0xFFFF);
     return true;
 }
 

@@ -133,6 +133,13 @@ hipError_t launch_conv_halo(const ConvParams& p, bool int8, int epi, hipStream_t
 // tr x tc output positions per tile, cc channels per chunk; a 3x3 conv the
 // tile does not fit then fails).  False for a tile without a kernel instance.
 bool set_conv3x3_halo(int mode, int jn, int pw, int tr, int tc, int cc);
+// Wide-tile fp16 3x3 conv (choice kind 4): every output channel (49..80) in
+// each wave, weights and input window streamed through LDS per channel chunk.
+// epi 0 any flags / 1 SiLU; no residual or accumulator output.
+int enumerate_wide_choices(const ConvParams& p, ConvChoice* out, int cap);
+hipError_t launch_conv_wide(const ConvParams& p, int epi, hipStream_t stream);
+// The tile forced by set_conv3x3_halo mode 4 (false: none).
+bool forced_wide_choice(ConvChoice& c);
 // Band kernel of the network's first conv (3x3 pad 1, stride 1/2, fp32 NCHW
 // input of at most 3 channels read directly, fp16 SiLU output, OCp <= 64,
 // W % 4 == 0): whole output rows per tile, one fp16 MFMA per 16 positions and

@@ -27,6 +27,7 @@
 #include <fstream>
 #include <functional>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -44,7 +45,7 @@ namespace {
 
 // Copies of the model's amax slot array: the workgroups of a layer spread
 // their slot updates over this many cache lines (4 KB apart).
-constexpr uint32_t kSlotStripes = 8;
+constexpr uint32_t kSlotStripes = 16;
 
 struct Placement {
     bool valid = false;
@@ -101,6 +102,17 @@ struct Step {
     bool signal = false;  // a later step on another lane waits for this one
 };
 
+// A conv whose kernel choice is measured: its launch reads p (the choice
+// can change after the step list is built).
+struct TunedConv {
+    int cmd = -1;
+    size_t step = 0;
+    ConvParams p{};
+    bool int8 = false;
+    std::vector<ConvChoice> cands;  // fastest first, as measured on their own
+    bool done = false;              // choice measured in the running network (or read from the cache)
+};
+
 // Streams a captured graph spreads independent steps over.
 constexpr int kLanes = 4;
 
@@ -150,6 +162,9 @@ struct AexrtYoloModel {
     bool autotune = true;            // measure every conv's kernel/tile choices at load
     bool tune_log = false;           // print each measured choice (AEXRT_HIP_TUNE_LOG=1)
     std::map<std::string, ConvChoice> tuned;  // conv shape -> measured choice
+    std::map<std::string, std::vector<ConvChoice>> tuned_top;  // conv shape -> fastest candidates
+    std::vector<std::unique_ptr<TunedConv>> tunables;         // convs of the step list with measured choices
+    std::map<int, ConvChoice> refined;                        // command -> choice measured in the network
     std::string tune_cache;                    // AEXRT_HIP_TUNE_CACHE file, empty: none
     hipStream_t lane_stream[kLanes] = {};      // capture-time streams of lanes 1..kLanes-1
     int n_lanes = 1;                           // lanes the schedule uses (measured at load)
@@ -730,7 +745,12 @@ void load_tune_cache(AexrtYoloModel* m) {
         if (tab == std::string::npos) continue;
         ConvChoice c{};
         if (std::sscanf(line.c_str() + tab + 1, "%d %d %d %d %d %d %d %d", &c.kind, &c.jn, &c.pw, &c.ksw, &c.tr,
-                        &c.tc, &c.cc, &c.nw) == 8)
+                        &c.tc, &c.cc, &c.nw) != 8)
+            continue;
+        int cmd = -1;
+        if (line.compare(0, 4, "cmd ") == 0 && std::sscanf(line.c_str() + 4, "%d", &cmd) == 1 && cmd >= 0)
+            m->refined[cmd] = c;  // a conv's choice measured in the network
+        else
             m->tuned[line.substr(0, tab)] = c;
     }
 }
@@ -739,15 +759,21 @@ void save_tune_cache(AexrtYoloModel* m) {
     const std::string tmp = m->tune_cache + ".tmp";
     {
         std::ofstream f(tmp, std::ios::trunc);
-        for (const auto& [key, c] : m->tuned)
+        auto put = [&](const std::string& key, const ConvChoice& c) {
             f << key << '\t' << c.kind << ' ' << c.jn << ' ' << c.pw << ' ' << c.ksw << ' ' << c.tr << ' ' << c.tc
               << ' ' << c.cc << ' ' << c.nw << '\n';
+        };
+        for (const auto& [key, c] : m->tuned) put(key, c);
+        for (const auto& [cmd, c] : m->refined) put("cmd " + std::to_string(cmd), c);
         if (!f) return;
     }
     std::rename(tmp.c_str(), m->tune_cache.c_str());
 }
 
-bool tune_conv(AexrtYoloModel* m, ConvParams& p, bool int8) {
+// Candidates of a shape kept for the measurement in the running network.
+constexpr int kContextCands = 4;
+
+bool tune_conv(AexrtYoloModel* m, ConvParams& p, bool int8, std::vector<ConvChoice>* top) {
     const std::string key = tune_key(p, int8);
     ConvChoice cand[128];
     const int n = enumerate_conv_choices(p, int8, cand, 128);
@@ -756,10 +782,13 @@ bool tune_conv(AexrtYoloModel* m, ConvParams& p, bool int8) {
         for (int i = 0; i < n; ++i)
             if (same_choice(cand[i], it->second)) {
                 p.choice = it->second;
+                auto tt = m->tuned_top.find(key);
+                if (top) *top = tt != m->tuned_top.end() ? tt->second : std::vector<ConvChoice>{it->second};
                 return true;
             }
         m->tuned.erase(it);  // a cached choice this build does not offer
     }
+    std::vector<std::pair<float, ConvChoice>> timed;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     if (!check_hip(hipEventCreate(&e0), "tune event") || !check_hip(hipEventCreate(&e1), "tune event")) {
         if (e0) (void)hipEventDestroy(e0);
@@ -778,6 +807,7 @@ bool tune_conv(AexrtYoloModel* m, ConvParams& p, bool int8) {
              check_hip(hipEventSynchronize(e1), "tune sync");
         float ms = 0.0f;
         ok = ok && check_hip(hipEventElapsedTime(&ms, e0, e1), "tune elapsed");
+        if (ok) timed.emplace_back(ms, cand[i]);
         if (ok && (best.kind == 0 || ms < best_ms)) {
             best = cand[i];
             best_ms = ms;
@@ -786,7 +816,15 @@ bool tune_conv(AexrtYoloModel* m, ConvParams& p, bool int8) {
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
     if (!ok) return fail(m, last_error());
+    std::stable_sort(timed.begin(), timed.end(),
+                     [](const std::pair<float, ConvChoice>& a, const std::pair<float, ConvChoice>& b) {
+                         return a.first < b.first;
+                     });
+    std::vector<ConvChoice> fastest;
+    for (size_t i = 0; i < timed.size() && (int)fastest.size() < kContextCands; ++i) fastest.push_back(timed[i].second);
     m->tuned[key] = best;
+    m->tuned_top[key] = fastest;
+    if (top) *top = fastest;
     p.choice = best;
     if (m->tune_log)
         std::fprintf(stderr, "aexrt tune %s: kind %d jn %d pw %d ksw %d tr %d tc %d cc %d nw %d  %.2f us (%d candidates)\n",
@@ -850,6 +888,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
     Engine& e = m->eng;
     auto& V = m->vals;
     m->steps.clear();
+    m->tunables.clear();
     {
         uint32_t* slots = m->slots;
         const int64_t n = int64_t(kSlotStripes) * m->slot_stride;
@@ -947,9 +986,31 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                                                 }
                                                 return launch_conv_int8_pg16(p, s);
                                             }});
+                } else if (m->autotune && !is_winograd_algorithm(alg)) {
+                    auto tc = std::make_unique<TunedConv>();
+                    tc->cmd = (int)ci;
+                    tc->int8 = is_int8_algorithm(alg);
+                    if (!tune_conv(m, p, tc->int8, &tc->cands)) return false;
+                    auto rf = m->refined.find((int)ci);
+                    if (rf != m->refined.end()) {
+                        for (const ConvChoice& k : tc->cands) tc->done = tc->done || same_choice(k, rf->second);
+                        if (!tc->done) {
+                            // a choice of an earlier measurement in the network: kept when this
+                            // build still offers it for the conv
+                            ConvChoice all[128];
+                            const int na = enumerate_conv_choices(p, tc->int8, all, 128);
+                            for (int k = 0; k < na; ++k) tc->done = tc->done || same_choice(all[k], rf->second);
+                        }
+                        if (tc->done) p.choice = rf->second;
+                    }
+                    tc->p = p;
+                    tc->step = m->steps.size();
+                    TunedConv* t = tc.get();
+                    m->tunables.push_back(std::move(tc));
+                    m->steps.push_back(Step{(int)ci, conv_label(c, e.src_cmd[ci], alg), [t](hipStream_t s) {
+                                                return launch_conv_igemm(t->p, t->int8, s);
+                                            }});
                 } else {
-                    if (m->autotune && !is_winograd_algorithm(alg) && !tune_conv(m, p, is_int8_algorithm(alg)))
-                        return false;
                     m->steps.push_back(Step{(int)ci, conv_label(c, e.src_cmd[ci], alg), [p, alg](hipStream_t s) {
                                                 if (is_winograd_algorithm(alg)) return launch_winograd_f2x2(p, s);
                                                 return launch_conv_igemm(p, is_int8_algorithm(alg), s);
@@ -1183,6 +1244,58 @@ bool run_network(AexrtYoloModel* m, hipStream_t s) {
     return check_hip(hipGraphLaunch(m->graph_exec, s), "graph launch") ? true : fail(m, last_error());
 }
 
+// The isolated measurement of tune_conv runs a conv back to back on its own
+// buffers, with its input, output and weights warm in L2 and the MALL; in the
+// network the input was just written by another kernel and the weights are
+// cold, and the fastest isolated choice is often not the fastest there.
+// Every conv's kContextCands fastest isolated candidates are therefore timed
+// again inside the network: in round r each conv runs its r-th candidate, the
+// steps are launched one by one between events (one warm-up pass, then
+// kContextReps passes, the minimum per step counts), and each conv keeps the
+// candidate with its shortest step.
+constexpr int kContextReps = 3;
+
+bool refine_in_context(AexrtYoloModel* m) {
+    size_t rounds = 0;
+    for (const auto& t : m->tunables)
+        if (!t->done && t->cands.size() > 1) rounds = std::max(rounds, t->cands.size());
+    if (rounds == 0) return true;
+    std::vector<std::vector<float>> ms(m->tunables.size());
+    const bool prof = m->profile;
+    m->profile = true;
+    bool ok = true;
+    for (size_t r = 0; r < rounds && ok; ++r) {
+        for (auto& t : m->tunables)
+            if (!t->done && !t->cands.empty()) t->p.choice = t->cands[std::min(r, t->cands.size() - 1)];
+        std::vector<float> lo(m->steps.size(), 1e30f);
+        for (int rep = 0; rep <= kContextReps && ok; ++rep) {
+            ok = run_network(m, m->stream);
+            for (size_t i = 0; ok && rep > 0 && i < m->steps.size() && i < m->prof_ms.size(); ++i)
+                lo[i] = std::min(lo[i], (float)m->prof_ms[i]);
+        }
+        for (size_t k = 0; ok && k < m->tunables.size(); ++k) ms[k].push_back(lo[m->tunables[k]->step]);
+    }
+    m->profile = prof;
+    m->prof_labels.clear();
+    m->prof_ms.clear();
+    if (!ok) return false;
+    for (size_t k = 0; k < m->tunables.size(); ++k) {
+        TunedConv& t = *m->tunables[k];
+        if (t.done || t.cands.empty()) continue;
+        size_t bi = 0;
+        for (size_t r = 1; r < t.cands.size(); ++r)
+            if (ms[k][r] < ms[k][bi]) bi = r;
+        t.p.choice = t.cands[bi];
+        t.done = true;
+        m->refined[t.cmd] = t.p.choice;
+        if (m->tune_log)
+            std::fprintf(stderr, "aexrt in-network %s: candidate %zu of %zu  %.2f us (first %.2f us)\n",
+                         m->steps[t.step].label.c_str(), bi, t.cands.size(), ms[k][bi] * 1000.0f, ms[k][0] * 1000.0f);
+    }
+    drop_graph(m);
+    return true;
+}
+
 // Spreading independent steps over streams pays when kernels are long enough to
 // overlap (large batch) and costs cross-queue synchronization when they are not
 // (batch 1): both schedules are captured and timed at load, the faster one kept.
@@ -1325,6 +1438,7 @@ bool build_model(AexrtYoloModel* m) {
     }
     m->n_lanes = 1;
     if (!build_steps(m, m->copies)) return false;
+    if (m->autotune && !refine_in_context(m)) return false;
     // AEXRT_HIP_LANES=<n>: fixed number of streams for the captured schedule
     // (1 = steps in launch order, e.g. for a per-kernel trace); otherwise the
     // faster of kLanes and 1, measured
@@ -1746,8 +1860,10 @@ int aexrt_yolo_override_conv_algorithm(AexrtYoloModel* m, uint32_t engine_comman
         return 0;
     }
     drop_graph(m);
+    m->refined.erase((int)command_index);
     // placement does not depend on the kernel choice: rebuild the launch list
-    return build_steps(m, m->copies) ? 1 : 0;
+    if (!build_steps(m, m->copies)) return 0;
+    return !m->autotune || refine_in_context(m) ? 1 : 0;
 }
 
 void aexrt_yolo_destroy(AexrtYoloModel* m) { free_model(m); }

@@ -246,8 +246,11 @@ int aexrt_hip_set_conv_tile(int32_t jn, int32_t pw, int32_t ksw);
  * subtiles (1/2/4), pw 16-position subtiles per wave (1/2/4), tr x tc output
  * positions (tr * tc <= 16 * waves * pw), cc input channels per LDS chunk
  * (C % cc == 0; cc % 16 == 0 for int8, % 8 for fp16); a 3x3 conv that the
- * forced tile does not fit (LDS, channel chunk) then fails.  Returns 0 for a
- * bad request. */
+ * forced tile does not fit (LDS, channel chunk) then fails.  jn 5 (80
+ * channels) exists with 8 waves.  mode 4 = force the wide-tile fp16 kernel on
+ * fp16 convs (every output channel, 49..80, in each wave; jn 4 or 5, pw 2 or
+ * 4, tr * tc <= 64 * pw, cc channels per chunk with weights streamed).
+ * Returns 0 for a bad request. */
 int aexrt_hip_set_conv3x3_halo(int32_t mode, int32_t jn, int32_t pw, int32_t tr, int32_t tc, int32_t cc);
 
 /* Kernel of the network's first conv (3x3 pad 1, stride 1/2, the fp32 NCHW

@@ -510,6 +510,86 @@ def test_halo_every_tile(cuda, jn, pw, tc, ccd, nw):
     assert ran >= 3
 
 
+# 80-channel fp16 tiles: every output channel in one 8-wave block (jn 5, weights up to 128 KB)
+HALO80 = [(1, 64, 40, 40, 1, 2, 8, 16, 32), (2, 80, 12, 20, 1, 2, 8, 16, 40), (1, 80, 9, 11, 1, 1, 5, 11, 80),
+          (2, 64, 13, 7, 2, 2, 7, 4, 64), (1, 64, 10, 10, 1, 1, 8, 16, 64)]
+
+
+@pytest.mark.parametrize("n,c,h,w,s,pw,tr,tc,cc", HALO80, ids=[f"c{t[1]}_{t[2]}x{t[3]}_s{t[4]}_pw{t[5]}_cc{t[8]}"
+                                                             for t in HALO80])
+def test_halo_all_80_channels_in_one_block(cuda, n, c, h, w, s, pw, tr, tc, cc):
+    """fp16 3x3 convs with 80 output channels on the jn 5 halo tile: against the fp32 direct conv
+    of the fp16 operands, with the amax slots of what was stored."""
+    import torch
+
+    oc = 80
+    rng = np.random.default_rng(97 + c + h)
+    x = O.round_f16(rng.standard_normal((n, c, h, w)).astype(np.float32))
+    wt = he_weight(rng, oc, c, 3)
+    b = packing.fp16_round(rng.uniform(-0.1, 0.1, oc).astype(np.float32))
+    desc = O.conv_desc(n, c, h, w, oc, 3, s, 1)
+    _, _, oh, ow = O.out_shape(desc)
+    pc = K.prepare_conv(desc, 5, K.SRC_RAW_F32, wt, b, device=cuda)
+    y = torch.full((n, oh, ow, oc), float("nan"), dtype=torch.float16, device=cuda)
+    slots = K.new_slots(oc, cuda)
+    K.set_conv3x3_halo(K.HALO_FORCE8, 5, pw, min(tr, oh), min(tc, ow), cc)
+    try:
+        K.conv2d(pc, _dev_nhwc(x, cuda), y, flags=K.SILU, y_slots=slots)
+    finally:
+        K.set_conv3x3_halo(K.HALO_AUTO)
+    torch.cuda.synchronize()
+    got = nhwc_to_nchw(y.float().cpu().numpy())
+    assert np.isfinite(got).all()
+    y_ref = O.cpu_conv2d(x, O.round_f16(wt), b, desc, silu=True)
+    err, allowed = tol_range(y_ref, got, FP16_TOL)
+    assert err <= allowed, (err, allowed)
+    want = np.array([np.float32(np.abs(got[:, g * 16:(g + 1) * 16]).max()).view(np.uint32) for g in range(5)],
+                    dtype=np.uint32)
+    np.testing.assert_array_equal(_u32(slots), want)
+
+
+# Wide-tile fp16 kernel: (n, c, h, w, oc, s, jn, pw, tr, tc, cc, silu, out_f32)
+WIDE = [(2, 80, 12, 20, 80, 1, 5, 2, 6, 20, 16, True, False), (1, 64, 40, 40, 80, 1, 5, 4, 6, 40, 16, True, False),
+        (1, 64, 17, 23, 64, 1, 4, 2, 8, 16, 16, True, False), (2, 128, 10, 10, 80, 1, 5, 2, 10, 10, 16, True, False),
+        (1, 256, 10, 10, 64, 1, 4, 4, 10, 10, 8, True, False), (2, 48, 13, 11, 64, 2, 4, 2, 7, 6, 24, False, True),
+        (1, 24, 9, 7, 56, 1, 4, 4, 9, 7, 8, False, False)]
+
+
+@pytest.mark.parametrize("case", WIDE, ids=[f"c{t[1]}_{t[2]}x{t[3]}_oc{t[4]}_s{t[5]}_jn{t[6]}_pw{t[7]}_cc{t[10]}"
+                                            for t in WIDE])
+def test_wide_tile_fp16_conv(cuda, case):
+    """The wide-tile fp16 3x3 kernel (every output channel per wave, weights streamed per
+    channel chunk) on forced tiles: ragged tiles, several chunks, stride 2, fp32 output."""
+    import torch
+
+    n, c, h, w, oc, s, jn, pw, tr, tc, cc, silu, out_f32 = case
+    rng = np.random.default_rng(131 + c + h + oc)
+    x = O.round_f16(rng.standard_normal((n, c, h, w)).astype(np.float32))
+    wt = he_weight(rng, oc, c, 3)
+    b = packing.fp16_round(rng.uniform(-0.1, 0.1, oc).astype(np.float32))
+    desc = O.conv_desc(n, c, h, w, oc, 3, s, 1)
+    _, _, oh, ow = O.out_shape(desc)
+    pc = K.prepare_conv(desc, 5, K.SRC_RAW_F32, wt, b, device=cuda)
+    y = torch.full((n, oh, ow, oc), float("nan"), dtype=torch.float32 if out_f32 else torch.float16, device=cuda)
+    slots = K.new_slots(oc, cuda)
+    flags = (K.SILU if silu else 0) | (K.OUT_F32 if out_f32 else 0)
+    K.set_conv3x3_halo(K.HALO_FORCE_WIDE, jn, pw, min(tr, oh), min(tc, ow), cc)
+    try:
+        K.conv2d(pc, _dev_nhwc(x, cuda), y, flags=flags, y_slots=slots)
+    finally:
+        K.set_conv3x3_halo(K.HALO_AUTO)
+    torch.cuda.synchronize()
+    got = nhwc_to_nchw(y.float().cpu().numpy())
+    assert np.isfinite(got).all()
+    y_ref = O.cpu_conv2d(x, O.round_f16(wt), b, desc, silu=silu)
+    err, allowed = tol_range(y_ref, got, FP32_TOL if out_f32 else FP16_TOL)
+    assert err <= allowed, (err, allowed)
+    g = (oc + 15) // 16
+    want = np.array([np.float32(np.abs(got[:, k * 16:(k + 1) * 16]).max()).view(np.uint32) for k in range(g)],
+                    dtype=np.uint32)
+    np.testing.assert_array_equal(_u32(slots), want)
+
+
 def test_halo_forced_tile_that_does_not_fit_fails(cuda):
     K.set_conv3x3_halo(K.HALO_FORCE, 1, 1, 4, 16, 48)  # C = 64 is not a multiple of 48
     try:
