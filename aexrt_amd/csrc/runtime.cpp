@@ -72,6 +72,9 @@ struct Root {
     bool f32 = false;
     int C = 0;
     int slot_base = -1;
+    // an int8 conv reads a value of this root: its producers keep its amax
+    // slots (slot updates of roots no int8 conv reads are skipped)
+    bool slots_read = true;
     size_t byte_offset = 0;
 };
 
@@ -384,6 +387,19 @@ bool is_fused_add(AexrtYoloModel* m, size_t ci) {
     return false;
 }
 
+// Only int8 convs read amax slots (the per-tensor scale of their input): the
+// producers of every other root skip their slot updates, which are atomics
+// on a few shared cache lines.
+void mark_slot_readers(AexrtYoloModel* m) {
+    for (Root& r : m->roots) r.slots_read = false;
+    for (size_t ci = 0; ci < m->eng.commands.size(); ++ci) {
+        const ConvState& cs = m->convs[ci];
+        if (!cs.is_conv || !is_int8_algorithm(cs.algorithm)) continue;
+        const ValueInfo& x = m->vals[m->eng.commands[ci].inputs[0]];
+        if (x.pl.valid && x.pl.root >= 0) m->roots[x.pl.root].slots_read = true;
+    }
+}
+
 // ---- placement ------------------------------------------------------------------------
 int new_root(AexrtYoloModel* m, int v, bool f32) {
     ValueInfo& x = m->vals[v];
@@ -680,7 +696,7 @@ AexrtHipTensorView view_of(AexrtYoloModel* m, int v) {
     tv.data = m->arena + r.byte_offset + x.pl.offset * (r.f32 ? 4 : 2);
     tv.n_stride = x.pl.nstride;
     tv.c_stride = x.pl.cstride;
-    tv.amax_slots = x.pl.slot >= 0 ? m->slots + x.pl.slot : nullptr;
+    tv.amax_slots = x.pl.slot >= 0 && r.slots_read ? m->slots + x.pl.slot : nullptr;
     tv.amax_stripes = tv.amax_slots ? kSlotStripes : 0u;
     tv.amax_stripe_stride = m->slot_stride;
     return tv;
@@ -692,7 +708,7 @@ AexrtHipTensorView view_of_pl(AexrtYoloModel* m, const Placement& pl) {
     tv.data = m->arena + r.byte_offset + pl.offset * (r.f32 ? 4 : 2);
     tv.n_stride = pl.nstride;
     tv.c_stride = pl.cstride;
-    tv.amax_slots = pl.slot >= 0 ? m->slots + pl.slot : nullptr;
+    tv.amax_slots = pl.slot >= 0 && r.slots_read ? m->slots + pl.slot : nullptr;
     tv.amax_stripes = tv.amax_slots ? kSlotStripes : 0u;
     tv.amax_stripe_stride = m->slot_stride;
     return tv;
@@ -1404,6 +1420,7 @@ bool build_model(AexrtYoloModel* m) {
         cs.pg16 = (c.plan_flags & kPlanFlagInt8PerGroup) != 0 && is_int8_algorithm(cs.algorithm);
     }
     if (!plan_memory(m, m->copies)) return false;
+    mark_slot_readers(m);
     // arena
     size_t total = 0;
     for (Root& r : m->roots) {
@@ -1861,6 +1878,7 @@ int aexrt_yolo_override_conv_algorithm(AexrtYoloModel* m, uint32_t engine_comman
     }
     drop_graph(m);
     m->refined.erase((int)command_index);
+    mark_slot_readers(m);
     // placement does not depend on the kernel choice: rebuild the launch list
     if (!build_steps(m, m->copies)) return 0;
     return !m->autotune || refine_in_context(m) ? 1 : 0;
