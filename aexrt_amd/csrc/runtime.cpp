@@ -109,6 +109,7 @@ struct Step {
 // can change after the step list is built).
 struct TunedConv {
     int cmd = -1;
+    std::string key;  // "cmd <index> <shape key>" of the measured choice
     size_t step = 0;
     ConvParams p{};
     bool int8 = false;
@@ -167,7 +168,9 @@ struct AexrtYoloModel {
     std::map<std::string, ConvChoice> tuned;  // conv shape -> measured choice
     std::map<std::string, std::vector<ConvChoice>> tuned_top;  // conv shape -> fastest candidates
     std::vector<std::unique_ptr<TunedConv>> tunables;         // convs of the step list with measured choices
-    std::map<int, ConvChoice> refined;                        // command -> choice measured in the network
+    // "cmd <index> <shape key>" -> choice measured in the network (the shape key
+    // keeps a cached choice from applying to the same command at another batch)
+    std::map<std::string, ConvChoice> refined;
     std::string tune_cache;                    // AEXRT_HIP_TUNE_CACHE file, empty: none
     hipStream_t lane_stream[kLanes] = {};      // capture-time streams of lanes 1..kLanes-1
     int n_lanes = 1;                           // lanes the schedule uses (measured at load)
@@ -763,9 +766,8 @@ void load_tune_cache(AexrtYoloModel* m) {
         if (std::sscanf(line.c_str() + tab + 1, "%d %d %d %d %d %d %d %d", &c.kind, &c.jn, &c.pw, &c.ksw, &c.tr,
                         &c.tc, &c.cc, &c.nw) != 8)
             continue;
-        int cmd = -1;
-        if (line.compare(0, 4, "cmd ") == 0 && std::sscanf(line.c_str() + 4, "%d", &cmd) == 1 && cmd >= 0)
-            m->refined[cmd] = c;  // a conv's choice measured in the network
+        if (line.compare(0, 4, "cmd ") == 0)
+            m->refined[line.substr(0, tab)] = c;  // a conv's choice measured in the network
         else
             m->tuned[line.substr(0, tab)] = c;
     }
@@ -780,7 +782,7 @@ void save_tune_cache(AexrtYoloModel* m) {
               << ' ' << c.cc << ' ' << c.nw << '\n';
         };
         for (const auto& [key, c] : m->tuned) put(key, c);
-        for (const auto& [cmd, c] : m->refined) put("cmd " + std::to_string(cmd), c);
+        for (const auto& [key, c] : m->refined) put(key, c);
         if (!f) return;
     }
     std::rename(tmp.c_str(), m->tune_cache.c_str());
@@ -1007,7 +1009,8 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                     tc->cmd = (int)ci;
                     tc->int8 = is_int8_algorithm(alg);
                     if (!tune_conv(m, p, tc->int8, &tc->cands)) return false;
-                    auto rf = m->refined.find((int)ci);
+                    tc->key = "cmd " + std::to_string(ci) + " " + tune_key(p, tc->int8);
+                    auto rf = m->refined.find(tc->key);
                     if (rf != m->refined.end()) {
                         for (const ConvChoice& k : tc->cands) tc->done = tc->done || same_choice(k, rf->second);
                         if (!tc->done) {
@@ -1213,15 +1216,21 @@ bool launch_steps_lanes(AexrtYoloModel* m, hipStream_t s) {
 
 bool run_network(AexrtYoloModel* m, hipStream_t s) {
     if (m->profile) {
+        // The steps are launched one by one with an event after each, twice
+        // in a row; the second pass is the one timed: by then the stream holds
+        // the first pass's work, so no step waits for the host to launch it.
         std::vector<hipEvent_t> ev(m->steps.size() + 1, nullptr);
         bool ok = true;
         for (auto& e : ev) ok = ok && check_hip(hipEventCreate(&e), "profile event create");
-        if (ok) ok = check_hip(hipEventRecord(ev[0], s), "profile event record");
         if (!ok) fail(m, last_error());
-        for (size_t i = 0; i < m->steps.size() && ok; ++i) {
-            hipError_t e = m->steps[i].launch(s);
-            if (e != hipSuccess) ok = fail(m, m->steps[i].label + ": " + hipGetErrorString(e));
-            else if (!check_hip(hipEventRecord(ev[i + 1], s), "profile event record")) ok = fail(m, last_error());
+        for (int pass = 0; pass < 2 && ok; ++pass) {
+            if (pass == 1) ok = check_hip(hipEventRecord(ev[0], s), "profile event record");
+            for (size_t i = 0; i < m->steps.size() && ok; ++i) {
+                hipError_t e = m->steps[i].launch(s);
+                if (e != hipSuccess) ok = fail(m, m->steps[i].label + ": " + hipGetErrorString(e));
+                else if (pass == 1 && !check_hip(hipEventRecord(ev[i + 1], s), "profile event record"))
+                    ok = fail(m, last_error());
+            }
         }
         if (ok && !check_hip(hipEventSynchronize(ev.back()), "profile sync")) ok = fail(m, last_error());
         m->prof_labels.clear();
@@ -1303,7 +1312,7 @@ bool refine_in_context(AexrtYoloModel* m) {
             if (ms[k][r] < ms[k][bi]) bi = r;
         t.p.choice = t.cands[bi];
         t.done = true;
-        m->refined[t.cmd] = t.p.choice;
+        m->refined[t.key] = t.p.choice;
         if (m->tune_log)
             std::fprintf(stderr, "aexrt in-network %s: candidate %zu of %zu  %.2f us (first %.2f us)\n",
                          m->steps[t.step].label.c_str(), bi, t.cands.size(), ms[k][bi] * 1000.0f, ms[k][0] * 1000.0f);
@@ -1877,7 +1886,9 @@ int aexrt_yolo_override_conv_algorithm(AexrtYoloModel* m, uint32_t engine_comman
         return 0;
     }
     drop_graph(m);
-    m->refined.erase((int)command_index);
+    const std::string prefix = "cmd " + std::to_string(command_index) + " ";
+    for (auto it = m->refined.begin(); it != m->refined.end();)
+        it = it->first.compare(0, prefix.size(), prefix) == 0 ? m->refined.erase(it) : std::next(it);
     mark_slot_readers(m);
     // placement does not depend on the kernel choice: rebuild the launch list
     if (!build_steps(m, m->copies)) return 0;
