@@ -364,12 +364,13 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_halo_kernel(HaloParams h) {
                 for (int q = 0; q < PW; ++q) B[hh][q] = *reinterpret_cast<const v4i*>(tb + bofs[q] + toff);
             }
         };
+        // every subtile runs, also past the conv's channels (zero weights there,
+        // never stored): no branches between the MFMAs
         auto mma = [&](const v4i (&A)[WQ][JN], const v4i (&B)[WQ][PW]) {
 #pragma unroll
             for (int hh = 0; hh < WQ; ++hh)
 #pragma unroll
                 for (int j = 0; j < JN; ++j) {
-                    if (j >= jmax) continue;
 #pragma unroll
                     for (int q = 0; q < PW; ++q) {
                         if constexpr (INT8)

@@ -518,9 +518,10 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvParams p) {
                 const v2i lo = quant8(af[q][0], s_q), hi = quant8(af[q][1], s_q);
                 bq[q] = v4i{lo[0], lo[1], hi[0], hi[1]};
             }
+            // every subtile runs, also past the conv's channels (zero weights
+            // there, never stored): no branches between the MFMAs
 #pragma unroll
             for (int j = 0; j < JN; ++j) {
-                if (j >= jmax) continue;
                 const v4i w = *reinterpret_cast<const v4i*>(wl + (j * 16 + col) * 64 + grp * 16);
 #pragma unroll
                 for (int q = 0; q < PW; ++q)
@@ -529,7 +530,6 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvParams p) {
         } else {
 #pragma unroll
             for (int j = 0; j < JN; ++j) {
-                if (j >= jmax) continue;
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const v8h w = *reinterpret_cast<const v8h*>(wl + (h * R + j * 16 + col) * 64 + grp * 16);
