@@ -90,6 +90,12 @@ struct ConvState {
     float* bias = nullptr;
     bool pg16 = false;            // int8 with per-16-input-channel scales (plan flag 16)
     uint32_t* strips = nullptr;   // pg16 at N > 1: the reference's strip amax of the input
+    uint64_t w_bytes = 0;         // bytes of w
+    // sibling pair (this conv first): weights and bias of both convs, rows of
+    // this conv then the sibling's, built from the w of each named here
+    void* w_pair = nullptr;
+    float* bias_pair = nullptr;
+    const void* pair_src[2] = {nullptr, nullptr};
 };
 
 struct Step {
@@ -152,6 +158,10 @@ struct AexrtYoloModel {
     std::vector<ValueInfo> vals;
     std::vector<Root> roots;
     std::vector<ConvState> convs;
+    // per command: the sibling conv whose output is placed right after this
+    // conv's output channels in one root (one launch computes both), or -1
+    std::vector<int> sibling;
+    bool merge_siblings = true;  // sibling pairs run as one launch (measured at load)
     std::vector<Step> steps;
     std::vector<CopyJob> copies;
     std::vector<void*> allocations;
@@ -452,6 +462,68 @@ bool try_place(AexrtYoloModel* m, int t, const Placement& pl) {
 
 AexrtConv2DDesc desc_of(const EngineCommand& c);
 
+// A conv that can share a launch with a sibling: fp16 direct kernels (every
+// plan id other than int8 and Winograd runs them from [OCp][Kp] weights), no
+// fused residual, its own output not placed yet (not a concat member, not
+// the network output), 16-channel aligned.
+bool sibling_candidate(AexrtYoloModel* m, size_t ci) {
+    const Engine& e = m->eng;
+    const ConvState& cs = m->convs[ci];
+    if (!cs.is_conv || cs.fused_residual || cs.pg16 || is_int8_algorithm(cs.algorithm) ||
+        is_winograd_algorithm(cs.algorithm))
+        return false;
+    const EngineCommand& c = e.commands[ci];
+    const ValueInfo& y = m->vals[c.output];
+    const ValueInfo& x = m->vals[c.inputs[0]];
+    return (c.kind == kCmdConv || c.kind == kCmdConvSilu) && !y.pl.valid && y.redirect < 0 && y.rank == 4 &&
+           c.output != e.manifest.output_value && !x.is_input && y.C % 16 == 0;
+}
+
+// Two fp16 convs of one input with the same geometry and epilogue (the box
+// and class branches of a detect head level) write adjacent channel ranges
+// of one root: a single launch with the output channels of both computes
+// them (every output channel is its own dot product, so the values are
+// those of two launches up to the kernel choice).
+void place_sibling_convs(AexrtYoloModel* m) {
+    const Engine& e = m->eng;
+    auto& V = m->vals;
+    m->sibling.assign(e.commands.size(), -1);
+    for (size_t ci = 0; ci < e.commands.size(); ++ci) {
+        if (!sibling_candidate(m, ci)) continue;
+        const EngineCommand& a = e.commands[ci];
+        const AexrtConv2DDesc da = desc_of(a);
+        for (size_t cj = ci + 1; cj < e.commands.size(); ++cj) {
+            const EngineCommand& b = e.commands[cj];
+            if (b.kind != a.kind || b.inputs[0] != a.inputs[0] || !sibling_candidate(m, cj)) continue;
+            AexrtConv2DDesc db = desc_of(b);
+            db.out_channels = da.out_channels;
+            if (std::memcmp(&da, &db, sizeof(da)) != 0) continue;
+            const ValueInfo& ya = V[a.output];
+            const int ca = ya.C, cb = V[b.output].C;
+            Root r;
+            r.C = ca + cb;
+            r.elements = int64_t(ya.N) * ya.H * ya.W * r.C;
+            if (r.C / 16 <= 128) {
+                r.slot_base = m->nslots;
+                m->nslots += r.C / 16;
+            }
+            m->roots.push_back(r);
+            const int root = (int)m->roots.size() - 1;
+            for (int k = 0; k < 2; ++k) {
+                ValueInfo& y = V[k ? b.output : a.output];
+                y.pl.valid = true;
+                y.pl.root = root;
+                y.pl.offset = k ? ca : 0;
+                y.pl.cstride = r.C;
+                y.pl.nstride = int64_t(y.H) * y.W * r.C;
+                y.pl.slot = r.slot_base >= 0 ? r.slot_base + (k ? ca / 16 : 0) : -1;
+            }
+            m->sibling[ci] = (int)cj;
+            break;
+        }
+    }
+}
+
 bool plan_memory(AexrtYoloModel* m, std::vector<CopyJob>& copies) {
     Engine& e = m->eng;
     auto& V = m->vals;
@@ -512,6 +584,7 @@ bool plan_memory(AexrtYoloModel* m, std::vector<CopyJob>& copies) {
             off += along_c ? x.C : x.H;
         }
     }
+    place_sibling_convs(m);
     // forward: views / aliases / everything else
     for (size_t ci = 0; ci < e.commands.size(); ++ci) {
         const EngineCommand& c = e.commands[ci];
@@ -676,6 +749,7 @@ bool prepare_conv_weights(AexrtYoloModel* m, size_t ci) {
     if (!constant_f32(m, bid, bias) || bias.size() != d.out_channels)
         return fail(m, "command " + std::to_string(ci) + ": conv bias is not a constant of out_channels values");
     cs.w = dev_alloc(m, host.size());
+    cs.w_bytes = host.size();
     cs.bias = static_cast<float*>(dev_alloc(m, bias.size() * 4));
     if (!cs.w || !cs.bias) return fail(m, "out of device memory for weights");
     if (!check_hip(hipMemcpy(cs.w, host.data(), host.size(), hipMemcpyHostToDevice), "weight upload") ||
@@ -688,6 +762,30 @@ bool prepare_conv_weights(AexrtYoloModel* m, size_t ci) {
                                     "scale upload"))
             return fail(m, "weight scale upload failed");
     }
+    return true;
+}
+
+// Weights and bias of a sibling pair (ci first): the packed rows of both
+// convs ([OCp][Kp], OCp = OC here) back to back, as one conv's would be.
+bool pair_conv_weights(AexrtYoloModel* m, size_t ci) {
+    ConvState& a = m->convs[ci];
+    const ConvState& b = m->convs[m->sibling[ci]];
+    const uint32_t ca = desc_of(m->eng.commands[ci]).out_channels;
+    const uint32_t cb = desc_of(m->eng.commands[m->sibling[ci]]).out_channels;
+    auto direct = [](uint32_t k) { return !is_int8_algorithm(k) && !is_winograd_algorithm(k); };
+    if (!direct(a.algorithm) || !direct(b.algorithm) || a.w_bytes % ca || b.w_bytes % cb || a.w_bytes / ca != b.w_bytes / cb)
+        return true;  // launched one by one
+    a.w_pair = dev_alloc(m, a.w_bytes + b.w_bytes);
+    a.bias_pair = static_cast<float*>(dev_alloc(m, (ca + cb) * 4u));
+    if (!a.w_pair || !a.bias_pair) return fail(m, "out of device memory for weights");
+    uint8_t* w = static_cast<uint8_t*>(a.w_pair);
+    if (!check_hip(hipMemcpy(w, a.w, a.w_bytes, hipMemcpyDeviceToDevice), "pair weights") ||
+        !check_hip(hipMemcpy(w + a.w_bytes, b.w, b.w_bytes, hipMemcpyDeviceToDevice), "pair weights") ||
+        !check_hip(hipMemcpy(a.bias_pair, a.bias, ca * 4u, hipMemcpyDeviceToDevice), "pair bias") ||
+        !check_hip(hipMemcpy(a.bias_pair + ca, b.bias, cb * 4u, hipMemcpyDeviceToDevice), "pair bias"))
+        return fail(m, last_error());
+    a.pair_src[0] = a.w;
+    a.pair_src[1] = b.w;
     return true;
 }
 
@@ -944,7 +1042,12 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
             case kCmdConvSilu: {
                 ConvState& cs = m->convs[ci];
                 const int xv = (int)c.inputs[0];
-                const AexrtConv2DDesc d = conv_desc_padded(m, ci);
+                AexrtConv2DDesc d = conv_desc_padded(m, ci);
+                // a sibling pair whose weights still are those the pair was built from
+                const int sib = m->sibling.empty() ? -1 : m->sibling[ci];
+                const bool pair = m->merge_siblings && sib >= 0 && !done[sib] && cs.w_pair && cs.pair_src[0] == cs.w &&
+                                  cs.pair_src[1] == m->convs[sib].w;
+                if (pair) d.out_channels += desc_of(e.commands[sib]).out_channels;
                 uint32_t flags = c.kind == kCmdConvSilu ? AEXRT_HIP_CONV_SILU : 0u;
                 AexrtHipTensorView xvw{};
                 if (m->vals[xv].is_input && m->input_nchw_direct) {
@@ -986,8 +1089,9 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                 }
                 ConvParams p{};
                 std::string why;
-                if (!build_conv_params(d, cs.algorithm, flags, xvw, cs.w, cs.scale, cs.bias,
-                                       cs.fused_residual ? &rvw : nullptr, yvw, nullptr, p, why))
+                if (!build_conv_params(d, cs.algorithm, flags, xvw, pair ? cs.w_pair : cs.w, cs.scale,
+                                       pair ? cs.bias_pair : cs.bias, cs.fused_residual ? &rvw : nullptr, yvw, nullptr,
+                                       p, why))
                     return fail(m, "command " + std::to_string(ci) + ": " + why);
                 const uint32_t alg = cs.algorithm;
                 if (cs.pg16) {
@@ -1038,6 +1142,10 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                 if (!(m->vals[xv].is_input && m->input_nchw_direct)) m->steps.back().reads.push_back(V[xv].pl.root);
                 if (cs.fused_residual) m->steps.back().reads.push_back(V[cs.residual_value].pl.root);
                 m->steps.back().writes = {V[yv].pl.root};
+                if (pair) {
+                    done[sib] = true;
+                    m->steps.back().label += " + cmd#" + std::to_string(e.src_cmd[sib]);
+                }
                 break;
             }
             case kCmdConcat: {
@@ -1324,40 +1432,53 @@ bool refine_in_context(AexrtYoloModel* m) {
 // Spreading independent steps over streams pays when kernels are long enough to
 // overlap (large batch) and costs cross-queue synchronization when they are not
 // (batch 1): both schedules are captured and timed at load, the faster one kept.
-bool choose_lanes(AexrtYoloModel* m) {
-    if (!m->use_graph) return true;
+// Time of 10 runs of the current schedule: the least of three such
+// measurements after the graph is captured and warmed up.
+bool time_schedule(AexrtYoloModel* m, float* ms_out) {
     hipEvent_t e0 = nullptr, e1 = nullptr;
-    if (!check_hip(hipEventCreate(&e0), "lanes event") || !check_hip(hipEventCreate(&e1), "lanes event")) {
+    if (!check_hip(hipEventCreate(&e0), "timing event") || !check_hip(hipEventCreate(&e1), "timing event")) {
         if (e0) (void)hipEventDestroy(e0);
         return fail(m, last_error());
     }
-    const int options[2] = {kLanes, 1};
-    float best_ms = 0.0f;
-    int best = 1;
+    drop_graph(m);
     bool ok = true;
-    for (int k = 0; k < 2 && ok; ++k) {
-        m->n_lanes = options[k];
-        schedule_steps(m);
-        drop_graph(m);
-        for (int r = 0; r < 3 && ok; ++r) ok = run_network(m, m->stream);  // capture + warm-up
-        ok = ok && check_hip(hipEventRecord(e0, m->stream), "lanes record");
+    for (int r = 0; r < 5 && ok; ++r) ok = run_network(m, m->stream);  // capture + warm-up
+    float best = 0.0f;
+    for (int rep = 0; rep < 3 && ok; ++rep) {
+        ok = check_hip(hipEventRecord(e0, m->stream), "timing record");
         for (int r = 0; r < 10 && ok; ++r) ok = run_network(m, m->stream);
-        ok = ok && check_hip(hipEventRecord(e1, m->stream), "lanes record") &&
-             check_hip(hipEventSynchronize(e1), "lanes sync");
+        ok = ok && check_hip(hipEventRecord(e1, m->stream), "timing record") &&
+             check_hip(hipEventSynchronize(e1), "timing sync");
         float ms = 0.0f;
-        ok = ok && check_hip(hipEventElapsedTime(&ms, e0, e1), "lanes elapsed");
-        if (ok && (k == 0 || ms < best_ms)) {
-            best_ms = ms;
-            best = options[k];
-        }
+        ok = ok && check_hip(hipEventElapsedTime(&ms, e0, e1), "timing elapsed");
+        if (ok && (rep == 0 || ms < best)) best = ms;
     }
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
-    if (!ok) return false;
+    *ms_out = best;
+    return ok;
+}
+
+// The faster of kLanes lanes and one (its time of 10 runs in *best_ms).
+bool choose_lanes(AexrtYoloModel* m, float* best_ms) {
+    *best_ms = 0.0f;
+    if (!m->use_graph) return true;
+    const int options[2] = {kLanes, 1};
+    int best = 1;
+    for (int k = 0; k < 2; ++k) {
+        m->n_lanes = options[k];
+        schedule_steps(m);
+        float ms = 0.0f;
+        if (!time_schedule(m, &ms)) return false;
+        if (k == 0 || ms < *best_ms) {
+            *best_ms = ms;
+            best = options[k];
+        }
+    }
     m->n_lanes = best;
     schedule_steps(m);
     drop_graph(m);
-    if (m->tune_log) std::fprintf(stderr, "aexrt lanes: %d (%.1f us per run)\n", best, best_ms * 100.0f);
+    if (m->tune_log) std::fprintf(stderr, "aexrt lanes: %d (%.1f us per run)\n", best, *best_ms * 100.0f);
     return true;
 }
 
@@ -1448,6 +1569,8 @@ bool build_model(AexrtYoloModel* m) {
         m->input_host = nullptr;
     for (size_t ci = 0; ci < e.commands.size(); ++ci)
         if (m->convs[ci].is_conv && !prepare_conv_weights(m, ci)) return false;
+    for (size_t ci = 0; ci < e.commands.size(); ++ci)
+        if (m->sibling[ci] >= 0 && !pair_conv_weights(m, ci)) return false;
     if (!check_hip(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking), "stream create"))
         return fail(m, last_error());
     for (int l = 1; l < kLanes; ++l)
@@ -1462,19 +1585,49 @@ bool build_model(AexrtYoloModel* m) {
         m->tune_cache = tcache;
         load_tune_cache(m);
     }
-    m->n_lanes = 1;
-    if (!build_steps(m, m->copies)) return false;
-    if (m->autotune && !refine_in_context(m)) return false;
     // AEXRT_HIP_LANES=<n>: fixed number of streams for the captured schedule
     // (1 = steps in launch order, e.g. for a per-kernel trace); otherwise the
-    // faster of kLanes and 1, measured
+    // faster of kLanes and 1, measured.  Sibling convs run as one launch or as
+    // two (which can overlap on separate lanes): with pairs in the plan, both
+    // schedules are measured and the faster kept.
     const char* lanes = std::getenv("AEXRT_HIP_LANES");
-    if (lanes && lanes[0] >= '1' && lanes[0] <= '9') {
-        m->n_lanes = std::min(kLanes, std::atoi(lanes));
-        schedule_steps(m);
-    } else if (m->autotune && !choose_lanes(m)) {
-        return false;
+    const bool fixed_lanes = lanes && lanes[0] >= '1' && lanes[0] <= '9';
+    const bool pairs = std::any_of(m->sibling.begin(), m->sibling.end(), [](int s) { return s >= 0; });
+    const int variants = pairs && m->autotune && m->use_graph ? 2 : 1;
+    float best_ms = 0.0f;
+    bool best_merge = true;
+    int best_lanes = 1;
+    for (int k = 0; k < variants; ++k) {
+        m->merge_siblings = k == 0;
+        m->n_lanes = 1;
+        if (!build_steps(m, m->copies)) return false;
+        if (m->autotune && !refine_in_context(m)) return false;
+        float ms = 0.0f;
+        if (fixed_lanes) {
+            m->n_lanes = std::min(kLanes, std::atoi(lanes));
+            schedule_steps(m);
+            if (variants > 1 && !time_schedule(m, &ms)) return false;
+        } else if (m->autotune && !choose_lanes(m, &ms)) {
+            return false;
+        }
+        if (k == 0 || ms < best_ms) {
+            best_ms = ms;
+            best_merge = m->merge_siblings;
+            best_lanes = m->n_lanes;
+        }
     }
+    if (best_merge != m->merge_siblings) {
+        // the choices of this build were measured with the first: cached in m->refined
+        m->merge_siblings = best_merge;
+        m->n_lanes = 1;
+        if (!build_steps(m, m->copies)) return false;
+        if (m->autotune && !refine_in_context(m)) return false;
+        m->n_lanes = best_lanes;
+        schedule_steps(m);
+        drop_graph(m);
+    }
+    if (m->tune_log && variants > 1)
+        std::fprintf(stderr, "aexrt sibling convs: %s\n", best_merge ? "one launch" : "two launches");
     if (!m->tune_cache.empty()) save_tune_cache(m);
     const char* prof = std::getenv("AEXRT_HIP_PROFILE");
     m->profile = prof && prof[0] == '1';
@@ -1885,6 +2038,12 @@ int aexrt_yolo_override_conv_algorithm(AexrtYoloModel* m, uint32_t engine_comman
         prepare_conv_weights(m, command_index);
         return 0;
     }
+    // a sibling pair with this conv gets its joint weights from the new ones
+    // (it runs as two launches while either conv is not an fp16 direct one)
+    for (size_t ci = 0; ci < m->sibling.size(); ++ci)
+        if ((ci == command_index || m->sibling[ci] == (int)command_index) && m->sibling[ci] >= 0 &&
+            !pair_conv_weights(m, ci))
+            return 0;
     drop_graph(m);
     const std::string prefix = "cmd " + std::to_string(command_index) + " ";
     for (auto it = m->refined.begin(); it != m->refined.end();)
