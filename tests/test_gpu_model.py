@@ -255,6 +255,45 @@ def test_yolov8n_160_w8a8_layers_and_end_to_end(cuda):
     assert err <= allowed, (err, allowed)
 
 
+def test_sibling_head_convs_one_launch_and_two(cuda, monkeypatch):
+    """The box and class branch convs of a detect level read one input: they run as one
+    launch into adjacent channel ranges of one buffer, and as two launches once an
+    override puts one of them on another kernel family; every conv matches the oracle
+    either way.  Without autotuning the runtime keeps the one-launch schedule, so both
+    paths run here whatever the load-time measurement would choose."""
+    monkeypatch.setenv("AEXRT_HIP_AUTOTUNE", "0")
+    g = build_yolov8n(batch=2, imgsz=160, seed=4)
+    algo = E.w8a8_algo_map(E.lower_graph(g), g.metadata["int8_convs"].split(","))
+    plan = E.compile_plan(g, precision="fp16", algo_overrides=algo)
+    data = E.build_aexrt_engine(g, precision="fp16", algo_overrides=algo, classes=80)
+    x = np.random.default_rng(5).random((2, 3, 160, 160)).astype(np.float32)
+
+    def paired_labels(m):
+        m.set_profiling(True)
+        m.run(x)
+        m.set_profiling(False)
+        return [lab for lab, _ in m.profile_events() if " + cmd#" in lab]
+
+    with NativeHipYoloModel(data) as m:
+        pairs = paired_labels(m)
+        assert len(pairs) == 3, pairs  # one per detect level
+        checked, _ = _layer_check(m, g, plan)
+        assert checked == 63
+        # the second conv of the first pair on Winograd: two launches there
+        second = int(pairs[0].rsplit("cmd#", 1)[1])
+        info = {i["command_index"]: i for i in m.conv_plan()}[second]
+        assert 40 in info["candidates"]
+        m.override_conv_algorithm(second, 40)
+        assert len(paired_labels(m)) == 2
+        checked, _ = _layer_check(m, g, plan)
+        assert checked == 63
+        # back on the direct kernel: one launch again
+        m.override_conv_algorithm(second, info["current_algorithm"])
+        assert len(paired_labels(m)) == 3
+        checked, _ = _layer_check(m, g, plan)
+        assert checked == 63
+
+
 def test_engine_file_roundtrip_and_fail_closed(cuda, tmp_path):
     g = _c2f_graph(batch=1, c=64, dim=8, seed=9)
     path = tmp_path / "c2f.aexrt"
