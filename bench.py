@@ -134,6 +134,14 @@ def roofline_for(prof: dict, replay, plans):
     cmd = replay["commands"][ci]
     int8 = "int8" in label
     ops, nbytes = conv_work(cmd["params"], int8)
+    # "+ cmd#N": a sibling conv of the same input computed by the same launch
+    # (its output channels appended); the input is read once for both
+    for sib in label.split(" + cmd#")[1:]:
+        p = replay["commands"][int(sib.split()[0])]["params"]
+        s_ops, s_bytes = conv_work(p, int8)
+        b, ic, ih, iw = (int(v) for v in p[:4])
+        ops += s_ops
+        nbytes += s_bytes - b * ic * ih * iw * (2 if ic > 3 else 4)
     secs = ms / 1e3
     peak_ops = PEAK_INT8_OPS if int8 else PEAK_FP16_FLOPS
     if ops / peak_ops >= nbytes / PEAK_HBM:
