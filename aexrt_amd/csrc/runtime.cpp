@@ -1459,13 +1459,14 @@ bool time_schedule(AexrtYoloModel* m, float* ms_out) {
     return ok;
 }
 
-// The faster of kLanes lanes and one (its time of 10 runs in *best_ms).
+// The fastest lane count of kLanes down to one (its time of 10 runs in *best_ms).
 bool choose_lanes(AexrtYoloModel* m, float* best_ms) {
     *best_ms = 0.0f;
     if (!m->use_graph) return true;
-    const int options[2] = {kLanes, 1};
+    int options[kLanes];
+    for (int k = 0; k < kLanes; ++k) options[k] = kLanes - k;
     int best = 1;
-    for (int k = 0; k < 2; ++k) {
+    for (int k = 0; k < kLanes; ++k) {
         m->n_lanes = options[k];
         schedule_steps(m);
         float ms = 0.0f;
@@ -1587,7 +1588,7 @@ bool build_model(AexrtYoloModel* m) {
     }
     // AEXRT_HIP_LANES=<n>: fixed number of streams for the captured schedule
     // (1 = steps in launch order, e.g. for a per-kernel trace); otherwise the
-    // faster of kLanes and 1, measured.  Sibling convs run as one launch or as
+    // fastest lane count from kLanes down to 1, measured.  Sibling convs run as one launch or as
     // two (which can overlap on separate lanes): with pairs in the plan, both
     // schedules are measured and the faster kept.
     const char* lanes = std::getenv("AEXRT_HIP_LANES");
