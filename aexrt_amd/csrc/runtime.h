@@ -17,8 +17,17 @@ struct EngineManifest {
     uint32_t precision = 0, layout = 0, has_objectness = 0, channels = 0, anchors = 0, classes = 0;
     uint32_t max_candidates = 0, max_detections = 0, graph_node_count = 0, value_count = 0;
     uint32_t constant_count = 0, command_count = 0, input_value = 0, output_value = 0;
-    uint64_t input_elements = 0;
+    uint64_t input_elements = 0, arena_nbytes = 0;
     float conf_threshold = 0.f, iou_threshold = 0.f;
+};
+
+// What the loader keeps of sections 7-9: the reference runtime's arena
+// description (validated, not used: this runtime plans its own NHWC memory),
+// the fusion groups (validated; their commands run one by one) and the
+// pipeline-cache record count (D3D12 shader/PSO blobs, nothing to use here).
+struct EngineExtras {
+    uint32_t memory_plan_version = 0, arena_pages = 0, fusion_groups = 0, cache_records = 0;
+    uint32_t physical_dispatch_plan = 0, barrier_plan = 0;
 };
 
 struct EngineValue {
@@ -59,6 +68,7 @@ struct Engine {
     std::vector<EngineCommand> commands;
     std::vector<EngineConstant> constants;  // indexed by value id
     std::vector<EnginePacked> packed;       // indexed by value id
+    EngineExtras extras;
     // after expand_fused_commands: the engine-file command each command came
     // from (the conv plan API speaks in engine-file indices)
     std::vector<uint32_t> src_cmd;

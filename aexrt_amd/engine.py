@@ -4,10 +4,11 @@
 What is kept byte-compatible with the reference, because it is the drop-in
 surface:
   * the container: 64-byte header, 32-byte TOC entries, 64-byte aligned
-    sections, CRC32 per section (engine.py:3952-3985);
-  * sections 1-6: manifest (engine.py:2556-2580), values (2583-2598),
-    commands (2601-2617), constants (2620-2647), kernel plan (2650-2662),
-    packed weights (2665-2690);
+    sections, CRC32 per section, sections 1-9 present (docs/AEXRT_ENGINE.md:54-104;
+    loader RT:17560-17599);
+  * the record formats of sections 1-9: manifest, values, commands, constants,
+    kernel plan, packed weights, Memory Plan V2, fusion plan, pipeline cache
+    (docs/AEXRT_ENGINE.md:106-538);
   * command kinds and their u32 params (yolo.py:701-927), kernel ids
     (runtime enum RT:8881-8940), plan flags (engine.py:85-96), packed layouts
     2/3/4/5/8 (engine.py:59-71);
@@ -15,10 +16,12 @@ surface:
     override (engine.py:1112-1222) and the int8 per-group flag loop
     (engine.py:192-210).
 
-What is not emitted: the D3D12 memory plan, barrier plan, fusion plan,
-physical dispatch plan and pipeline cache (sections 7-12).  The HIP runtime
-plans its own memory (one buffer per value, concat inputs placed as slices
-of their concat) and runs every command as its own kernel.
+The writer itself (_Section, the encoders, build_container) and the arena
+placement (plan_memory) are this compiler's own.  Not emitted: the optional
+physical dispatch and barrier plans (sections 10-11).  The fusion plan has no
+groups and the pipeline cache no records.  The HIP runtime plans its own
+NHWC memory at load (concat inputs placed as slices of their concat) and
+ignores section 7, which describes the reference runtime's fp32 NCHW arena.
 """
 from __future__ import annotations
 
@@ -46,6 +49,10 @@ SECTION_COMMANDS = 3
 SECTION_CONSTANTS = 4
 SECTION_KERNEL_PLAN = 5
 SECTION_PACKED_WEIGHTS = 6
+SECTION_MEMORY_PLAN = 7
+SECTION_FUSION_PLAN = 8
+SECTION_PIPELINE_CACHE = 9
+REQUIRED_SECTIONS = tuple(range(1, 10))
 
 PRECISION_FLOAT32 = 1
 PRECISION_FLOAT16 = 2
@@ -614,116 +621,286 @@ def build_packed_weights(replay: Dict[str, Any], plans: List[Dict[str, int]], pr
 
 
 # ---------------------------------------------------------------------------
-# sections and container
+# memory plan (section 7)
 # ---------------------------------------------------------------------------
 
 def _align(v: int, a: int) -> int:
-    return (int(v) + a - 1) // a * a
+    return -(-int(v) // a) * a
+
+
+STORAGE_DTYPE_FP32 = 1
+STORAGE_LAYOUT_LINEAR_NCHW = 1
+MEMORY_PLAN_V2 = 2
+ARENA_ALIGNMENT = 256
+
+
+def plan_memory(replay: Dict[str, Any], alignment: int = ARENA_ALIGNMENT) -> Dict[str, Any]:
+    """Arena placement described by the Memory Plan V2 section (docs/AEXRT_ENGINE.md:234-308; the
+    loader's checks RT:17891-17962).
+
+    Every non-constant value lives in fp32 linear-NCHW storage, the reference runtime's default
+    activation format (fp16 islands are a measured option there, ENG:211-246).  The placement
+    is this compiler's own:
+
+    * VIEW / ALIAS outputs take no storage of their own: they resolve to the allocation of their
+      source at the element offset in params[0] (nested views add up);
+    * pages are colours: the output of a command never shares a page with one of its inputs
+      (a D3D12 resource cannot be read and written by one dispatch), colours chosen greedily
+      in command order, smallest first;
+    * within a page, a value takes the lowest-offset slot whose previous occupant was last read
+      by an earlier command than the one that writes it (strictly earlier, so no command reads
+      and writes one slot), else a new slot at the end; the graph output is held to the end.
+
+    The alignment is halved until every alias offset is a multiple of it.
+    Returns {alignment, pages: [nbytes], records: {value_id: (flags, page, offset, nbytes)},
+    total_nbytes}.
+    """
+    values, commands = replay["values"], replay["commands"]
+    n = len(values)
+    root = list(range(n))
+    elem_offset = [0] * n
+    for c in commands:
+        if c["kind"] in ("VIEW", "ALIAS"):
+            src = int(c["inputs"][0])
+            out = int(c["output"])
+            root[out] = root[src]
+            elem_offset[out] = elem_offset[src] + int(c["params"][0])
+    is_const = [bool(v["flags"] & VALUE_CONSTANT) for v in values]
+    aliased = [i for i in range(n) if root[i] != i]
+    while alignment > 4 and any((elem_offset[i] * 4) % alignment for i in aliased):
+        alignment //= 2
+
+    born: Dict[int, int] = {}
+    last_read: Dict[int, int] = {}
+    for v in values:
+        if v["flags"] & VALUE_INPUT:
+            born[int(v["id"])] = -1
+    for step, c in enumerate(commands):
+        for i in c["inputs"]:
+            if not is_const[int(i)]:
+                r = root[int(i)]
+                last_read[r] = max(last_read.get(r, -1), step)
+        out = int(c["output"])
+        if root[out] == out:
+            born.setdefault(out, step)
+    out_root = root[int(replay["output_value"])]
+    last_read[out_root] = len(commands)
+
+    colour: Dict[int, int] = {}
+    for r, step in born.items():
+        if step < 0:
+            colour[r] = 0
+    for c in commands:
+        out = int(c["output"])
+        if root[out] != out or out in colour:
+            continue
+        taken = {colour[root[int(i)]] for i in c["inputs"] if not is_const[int(i)] and root[int(i)] in colour}
+        colour[out] = next(k for k in range(len(taken) + 1) if k not in taken)
+    page_ids = {k: p for p, k in enumerate(sorted(set(colour.values())))}
+    if len(page_ids) > 64:
+        raise ValueError("memory plan needs more than the loader's 64 pages")
+
+    slots: Dict[int, List[List[int]]] = {p: [] for p in page_ids.values()}  # [offset, size, free_after]
+    place: Dict[int, tuple] = {}
+    for r in sorted(born, key=lambda v: (born[v], v)):
+        page = page_ids[colour[r]]
+        nbytes = int(values[r]["elements"]) * 4
+        start, end = born[r], last_read.get(r, born[r])
+        size = _align(nbytes, alignment)
+        chosen = None
+        for slot in sorted(slots[page]):
+            if slot[2] < start and slot[1] >= size:
+                chosen = slot
+                break
+        if chosen is None:
+            top = max((s[0] + s[1] for s in slots[page]), default=0)
+            chosen = [top, size, end]
+            slots[page].append(chosen)
+        chosen[2] = end
+        place[r] = (page, chosen[0])
+    pages = [0] * len(page_ids)
+    for p, ss in slots.items():
+        pages[p] = max(s[0] + s[1] for s in ss)
+
+    records: Dict[int, tuple] = {}
+    for i in range(n):
+        if is_const[i] or root[i] not in place:
+            continue
+        page, base = place[root[i]]
+        flags = int(values[i]["flags"]) | VALUE_ARENA | (VALUE_ALIAS if root[i] != i else 0)
+        records[i] = (flags, page, base + elem_offset[i] * 4, int(values[i]["elements"]) * 4)
+    return dict(alignment=alignment, pages=pages, records=records, total_nbytes=sum(pages))
+
+
+# ---------------------------------------------------------------------------
+# sections and container
+# ---------------------------------------------------------------------------
+#
+# Every section is a fixed header, then records; constants and packed
+# weights end in a heap of 64-byte aligned payloads addressed by
+# section-relative offsets (docs/AEXRT_ENGINE.md:54-233).  _Section does the
+# layout for all of them; the functions below only list the fields.
+
+class _Section:
+    """One section payload: header fields, fixed- or variable-size records, then an optional
+    payload heap (each payload 64-byte aligned, its offset patched into its record)."""
+
+    def __init__(self, header_fmt: str, *header: Any) -> None:
+        self.head = struct.pack(header_fmt, *header)
+        self.records: List[tuple] = []   # (record_fmt, fields, payload or None, offset field index)
+
+    def record(self, fmt: str, *fields: Any, payload: Optional[bytes] = None, at: int = -1) -> None:
+        self.records.append((fmt, list(fields), payload, at))
+
+    def raw(self, data: bytes) -> None:
+        self.records.append((None, [data], None, -1))
+
+    def tobytes(self) -> bytes:
+        fixed = len(self.head) + sum(struct.calcsize(f) if f else len(v[0]) for f, v, _, _ in self.records)
+        heap = bytearray()
+        heap_base = _align(fixed, ENGINE_ALIGNMENT) if any(p is not None for *_, p, _ in self.records) else fixed
+        chunks = [self.head]
+        for fmt, fields, payload, at in self.records:
+            if fmt is None:
+                chunks.append(fields[0])
+                continue
+            if payload is not None:
+                heap.extend(bytes(_align(len(heap), ENGINE_ALIGNMENT) - len(heap)))
+                fields[at] = heap_base + len(heap)
+                heap.extend(payload)
+            chunks.append(struct.pack(fmt, *fields))
+        chunks.append(bytes(heap_base - fixed))
+        chunks.append(bytes(heap))
+        return b"".join(chunks)
+
+
+MANIFEST_U32_FIELDS = (
+    "manifest_version", "runtime_target", "precision", "mode", "layout", "has_objectness", "channels", "anchors",
+    "classes", "max_candidates", "max_detections", "graph_node_count", "value_count", "constant_count",
+    "command_count", "input_value", "output_value")
 
 
 def encode_manifest(**f: Any) -> bytes:
-    out = bytearray()
-    for v in (1, 1, f["precision"], 2, f["layout"], int(f["has_objectness"]), f["channels"], f["anchors"],
-              f["classes"], f["max_candidates"], f["max_detections"], f["graph_node_count"], f["value_count"],
-              f["constant_count"], f["command_count"], f["input_value"], f["output_value"]):
-        out += struct.pack("<I", int(v))
-    out += struct.pack("<QQff", f["input_elements"], f["arena_nbytes"], f["conf_threshold"], f["iou_threshold"])
-    out += bytes(f["source_hash"])
-    return bytes(out)
+    """Section 1 (docs/AEXRT_ENGINE.md:106-125): 17 u32, input_elements, arena_nbytes, thresholds, digest."""
+    f = dict(f, manifest_version=1, runtime_target=1, mode=2)
+    s = _Section("<17I", *(int(f[k]) for k in MANIFEST_U32_FIELDS))
+    s.record("<QQff32s", f["input_elements"], f["arena_nbytes"], f["conf_threshold"], f["iou_threshold"],
+             bytes(f["source_hash"]))
+    return s.tobytes()
 
 
-def encode_values(replay: Dict[str, Any]) -> bytes:
-    out = bytearray(struct.pack("<II", len(replay["values"]), 0))
+def encode_values(replay: Dict[str, Any], memory: Optional[Dict[str, Any]] = None) -> bytes:
+    """Section 2: <IIQ4IQQ> per value; arena values carry their memory-plan offset and size."""
+    recs = (memory or {}).get("records", {})
+    s = _Section("<II", len(replay["values"]), 0)
     for v in replay["values"]:
-        out += struct.pack("<IIQ4IQQ", v["id"], v["flags"], v["elements"], *v["shape4"], NO_OFFSET, 0)
-    return bytes(out)
+        flags, _, offset, nbytes = recs.get(int(v["id"]), (int(v["flags"]), 0, NO_OFFSET, 0))
+        s.record("<IIQ4IQQ", v["id"], flags, v["elements"], *v["shape4"], offset, nbytes)
+    return s.tobytes()
 
 
 def encode_commands(replay: Dict[str, Any], plans: List[Dict[str, int]]) -> bytes:
-    out = bytearray(struct.pack("<II", len(replay["commands"]), 0))
+    """Section 3: <6I> head (kind, output, #inputs, #params, kernel, precision), then the u32 lists."""
+    s = _Section("<II", len(replay["commands"]), 0)
     for c, p in zip(replay["commands"], plans):
-        out += struct.pack("<6I", c["kind_id"], c["output"], len(c["inputs"]), len(c["params"]),
-                           p["planned_kernel"], p["precision"])
-        if c["inputs"]:
-            out += struct.pack(f"<{len(c['inputs'])}I", *c["inputs"])
-        if c["params"]:
-            out += struct.pack(f"<{len(c['params'])}I", *c["params"])
-    return bytes(out)
+        words = [c["kind_id"], c["output"], len(c["inputs"]), len(c["params"]), p["planned_kernel"],
+                 p["precision"], *c["inputs"], *c["params"]]
+        s.raw(np.asarray(words, dtype="<u4").tobytes())
+    return s.tobytes()
+
+
+def fp16_constant_ids(replay: Dict[str, Any], precision: int) -> set:
+    """Constants an fp16 engine stores as fp16: conv weights and biases (ENG:1299-1304)."""
+    if precision != PRECISION_FLOAT16:
+        return set()
+    ids = set()
+    for c in replay["commands"]:
+        if c["kind"] in ("CONV", "CONV_SILU"):
+            ids.update(int(v) for v in c["inputs"][1:3])
+        elif c["kind"] == "CONCAT_CONV1X1":
+            ids.update(int(v) for v in c["inputs"][-2:])
+    return ids
 
 
 def encode_constants(replay: Dict[str, Any], precision: int) -> bytes:
+    """Section 4: <IIQQQ> (value, dtype, elements, offset, nbytes) per constant + payload heap."""
+    half = fp16_constant_ids(replay, precision)
     consts = [v for v in replay["values"] if v["flags"] & VALUE_CONSTANT]
-    fp16_ids = set()
-    if precision == PRECISION_FLOAT16:
-        for c in replay["commands"]:
-            if c["kind"] in ("CONV", "CONV_SILU") and len(c["inputs"]) >= 3:
-                fp16_ids.update(int(v) for v in c["inputs"][1:3])
-            elif c["kind"] == "CONCAT_CONV1X1" and len(c["inputs"]) >= 2:
-                fp16_ids.update(int(v) for v in c["inputs"][-2:])
-    rec = 32
-    data_offset = _align(8 + len(consts) * rec, ENGINE_ALIGNMENT)
-    out = bytearray(data_offset)
-    struct.pack_into("<II", out, 0, len(consts), 0)
-    cursor = data_offset
-    for i, v in enumerate(consts):
-        cursor = _align(cursor, ENGINE_ALIGNMENT)
-        if cursor > len(out):
-            out.extend(b"\0" * (cursor - len(out)))
-        raw = v["raw"]
-        prec = PRECISION_FLOAT16 if v["id"] in fp16_ids else PRECISION_FLOAT32
-        if prec == PRECISION_FLOAT16:
-            raw = np.frombuffer(raw, dtype="<f4").astype("<f2").tobytes()
-        struct.pack_into("<IIQQQ", out, 8 + i * rec, v["id"], prec, v["elements"], cursor, len(raw))
-        out.extend(raw)
-        cursor += len(raw)
-    return bytes(out)
+    s = _Section("<II", len(consts), 0)
+    for v in consts:
+        data = np.frombuffer(v["raw"], dtype="<f4")
+        dtype = PRECISION_FLOAT16 if v["id"] in half else PRECISION_FLOAT32
+        payload = (data.astype("<f2") if dtype == PRECISION_FLOAT16 else data).tobytes()
+        s.record("<IIQQQ", v["id"], dtype, v["elements"], 0, len(payload), payload=payload, at=3)
+    return s.tobytes()
 
 
 def encode_kernel_plan(plans: List[Dict[str, int]]) -> bytes:
-    out = bytearray(struct.pack("<II", len(plans), 1))
+    """Section 5: count, plan version 1, then <6I> per command (ENG:2650-2663 record fields)."""
+    s = _Section("<II", len(plans), 1)
     for p in plans:
-        out += struct.pack("<6I", p["command_index"], p["kind_id"], p["planned_kernel"], p["precision"],
-                           p["packed_value"], p["flags"])
-    return bytes(out)
+        s.record("<6I", *(p[k] for k in ("command_index", "kind_id", "planned_kernel", "precision",
+                                          "packed_value", "flags")))
+    return s.tobytes()
 
 
 def encode_packed_weights(packed: List[Dict[str, Any]]) -> bytes:
-    rec = 40
-    data_offset = _align(8 + len(packed) * rec, ENGINE_ALIGNMENT)
-    out = bytearray(data_offset)
-    struct.pack_into("<II", out, 0, len(packed), 0)
-    cursor = data_offset
-    for i, item in enumerate(packed):
-        cursor = _align(cursor, ENGINE_ALIGNMENT)
-        if cursor > len(out):
-            out.extend(b"\0" * (cursor - len(out)))
-        data = item["data"]
-        struct.pack_into("<4IQQQ", out, 8 + i * rec, item["value_id"], item["layout"], item["in_channels"],
-                         item["out_channels"], item["elements"], cursor, len(data))
-        out.extend(data)
-        cursor += len(data)
-    return bytes(out)
+    """Section 6: <4IQQQ> (value, layout, ic, oc, elements, offset, nbytes) per weight + heap."""
+    s = _Section("<II", len(packed), 0)
+    for w in packed:
+        s.record("<4IQQQ", w["value_id"], w["layout"], w["in_channels"], w["out_channels"], w["elements"], 0,
+                 len(w["data"]), payload=w["data"], at=5)
+    return s.tobytes()
+
+
+def encode_memory_plan(memory: Dict[str, Any]) -> bytes:
+    """Section 7, Memory Plan V2: <4IQII> header, <4IQ> per page, <6IQQ> per arena value."""
+    recs = memory["records"]
+    s = _Section("<4IQII", MEMORY_PLAN_V2, memory["alignment"], len(memory["pages"]), len(recs),
+                 memory["total_nbytes"], 1, 0)
+    for page, nbytes in enumerate(memory["pages"]):
+        s.record("<4IQ", page, STORAGE_DTYPE_FP32, STORAGE_LAYOUT_LINEAR_NCHW, 1, nbytes)
+    for vid in sorted(recs):
+        flags, page, offset, nbytes = recs[vid]
+        s.record("<6IQQ", vid, flags, page, STORAGE_DTYPE_FP32, STORAGE_LAYOUT_LINEAR_NCHW, 0, offset, nbytes)
+    return s.tobytes()
+
+
+def encode_fusion_plan(command_count: int) -> bytes:
+    """Section 8: version 1, no groups, authoritative (docs/AEXRT_ENGINE.md:321-360).  Concat +
+    1x1 fusion is a command kind (CONCAT_CONV1X1) here, not a group."""
+    return _Section("<4I", 1, 0, command_count, 1).tobytes()
+
+
+def encode_pipeline_cache() -> bytes:
+    """Section 9: version 1 and no shader or PSO records, the valid empty cache of
+    ``--no-pipeline-cache`` (docs/AEXRT_ENGINE.md:514-538).  HIP code objects live in the library."""
+    return _Section("<4I", 1, 0, 0, 0).tobytes()
+
+
+HEADER_FMT = "<8sIIIIQQQ16s"
+TOC_FMT = "<IIQQII"
+ENGINE_FLAG_VALID = 1
 
 
 def build_container(sections: Dict[int, bytes]) -> bytes:
-    ordered = sorted(sections.items())
-    toc_offset = ENGINE_HEADER_SIZE
-    toc_size = len(ordered) * ENGINE_TOC_ENTRY_SIZE
-    cursor = _align(toc_offset + toc_size, ENGINE_ALIGNMENT)
-    entries, payloads = [], []
-    for stype, payload in ordered:
-        cursor = _align(cursor, ENGINE_ALIGNMENT)
-        entries.append((stype, 0, cursor, len(payload), zlib.crc32(payload) & 0xFFFFFFFF, 0))
-        payloads.append((cursor, payload))
-        cursor += len(payload)
-    out = bytearray(cursor)
-    struct.pack_into("<8sIIIIQQQ16s", out, 0, ENGINE_MAGIC, ENGINE_VERSION, ENGINE_HEADER_SIZE, len(entries), 1,
-                     cursor, toc_offset, toc_size, b"\0" * 16)
-    for i, e in enumerate(entries):
-        struct.pack_into("<IIQQII", out, toc_offset + i * ENGINE_TOC_ENTRY_SIZE, *e)
-    for off, payload in payloads:
-        out[off:off + len(payload)] = payload
-    return bytes(out)
+    """Header, TOC, then each section 64-byte aligned in type order, CRC32 per section."""
+    items = sorted(sections.items())
+    toc_bytes = ENGINE_TOC_ENTRY_SIZE * len(items)
+    placed = []
+    pos = ENGINE_HEADER_SIZE + toc_bytes
+    for stype, payload in items:
+        pos = _align(pos, ENGINE_ALIGNMENT)
+        placed.append((stype, pos, payload))
+        pos += len(payload)
+    chunks = [struct.pack(HEADER_FMT, ENGINE_MAGIC, ENGINE_VERSION, ENGINE_HEADER_SIZE, len(items),
+                          ENGINE_FLAG_VALID, pos, ENGINE_HEADER_SIZE, toc_bytes, bytes(16))]
+    chunks += [struct.pack(TOC_FMT, t, 0, off, len(p), zlib.crc32(p) & 0xFFFFFFFF, 0) for t, off, p in placed]
+    at = ENGINE_HEADER_SIZE + toc_bytes
+    for _, off, p in placed:
+        chunks += [bytes(off - at), p]
+        at = off + len(p)
+    return b"".join(chunks)
 
 
 def _source_hash(replay: Dict[str, Any]) -> bytes:
@@ -764,11 +941,12 @@ def compile_plan(graph: Graph, *, precision: str = "fp16", algo_overrides: Optio
     return dict(replay=replay, plans=plans, packed=packed, precision=prec)
 
 
-def build_aexrt_engine(graph: Graph, *, precision: str = "fp16", classes: Optional[int] = None,
+def engine_sections(graph: Graph, *, precision: str = "fp16", classes: Optional[int] = None,
                        algo_overrides: Optional[Dict[int, int]] = None,
                        int8_pergroup: Optional[Sequence[int]] = None, max_candidates: int = 512,
                        max_detections: int = 100, conf_threshold: float = 0.25,
-                       iou_threshold: float = 0.45, fuse_concat_min_h: Optional[int] = None) -> bytes:
+                       iou_threshold: float = 0.45, fuse_concat_min_h: Optional[int] = None) -> Dict[int, bytes]:
+    """Payloads of sections 1-9 by section type (what build_container lays out)."""
     plan = compile_plan(graph, precision=precision, algo_overrides=algo_overrides, int8_pergroup=int8_pergroup,
                         fuse_concat_min_h=fuse_concat_min_h)
     replay, plans, packed, prec = plan["replay"], plan["plans"], plan["packed"], plan["precision"]
@@ -778,12 +956,16 @@ def build_aexrt_engine(graph: Graph, *, precision: str = "fp16", classes: Option
     channels = int(out_shape[-2]) if rank == 3 else int(out_shape[1])
     anchors = int(out_shape[-1]) if rank == 3 else int(out_shape[2] * out_shape[3])
     ncls = int(classes) if classes is not None else max(channels - 64, 1)
+    memory = plan_memory(replay)
     sections = {
-        SECTION_VALUES: encode_values(replay),
+        SECTION_VALUES: encode_values(replay, memory),
         SECTION_COMMANDS: encode_commands(replay, plans),
         SECTION_CONSTANTS: encode_constants(replay, prec),
         SECTION_KERNEL_PLAN: encode_kernel_plan(plans),
         SECTION_PACKED_WEIGHTS: encode_packed_weights(packed),
+        SECTION_MEMORY_PLAN: encode_memory_plan(memory),
+        SECTION_FUSION_PLAN: encode_fusion_plan(len(replay["commands"])),
+        SECTION_PIPELINE_CACHE: encode_pipeline_cache(),
     }
     sections[SECTION_MANIFEST] = encode_manifest(
         precision=prec, layout=1, has_objectness=False, channels=channels, anchors=anchors, classes=ncls,
@@ -792,9 +974,14 @@ def build_aexrt_engine(graph: Graph, *, precision: str = "fp16", classes: Option
         constant_count=sum(bool(v["flags"] & VALUE_CONSTANT) for v in replay["values"]),
         command_count=len(replay["commands"]), input_value=replay["input_value"],
         output_value=replay["output_value"], input_elements=replay["values"][replay["input_value"]]["elements"],
-        arena_nbytes=0, conf_threshold=conf_threshold, iou_threshold=iou_threshold,
+        arena_nbytes=memory["total_nbytes"], conf_threshold=conf_threshold, iou_threshold=iou_threshold,
         source_hash=_source_hash(replay))
-    return build_container(sections)
+    return sections
+
+
+def build_aexrt_engine(graph: Graph, **kwargs: Any) -> bytes:
+    """The .aexrt bytes of a graph (keyword arguments of engine_sections)."""
+    return build_container(engine_sections(graph, **kwargs))
 
 
 def save_aexrt_engine(graph: Graph, path, **kwargs) -> Dict[str, Any]:
@@ -808,41 +995,66 @@ def save_aexrt_engine(graph: Graph, path, **kwargs) -> Dict[str, Any]:
 
 
 def inspect_aexrt_engine(source) -> Dict[str, Any]:
-    """Header, TOC (with CRC check), manifest, kernel plan and packed-layout counts."""
+    """Header, TOC (CRC, duplicates, reserved fields, sections 1-9 present), manifest, kernel plan,
+    packed-layout counts, memory plan, fusion groups and pipeline-cache records; raises ValueError
+    on an engine the reference's inspector refuses (ENG:336-400)."""
     data = bytes(source) if not isinstance(source, (str, os.PathLike)) else Path(source).read_bytes()
     if len(data) < ENGINE_HEADER_SIZE:
         raise ValueError("truncated AEXRT engine header")
-    magic, version, hsize, count, flags, fsize, toc_off, toc_size, _ = struct.unpack_from("<8sIIIIQQQ16s", data, 0)
+    magic, version, hsize, count, flags, fsize, toc_off, toc_size, _ = struct.unpack_from(HEADER_FMT, data, 0)
     if magic != ENGINE_MAGIC or version != ENGINE_VERSION or hsize != ENGINE_HEADER_SIZE:
         raise ValueError("not an AEXRT engine")
-    if fsize != len(data) or toc_size != count * ENGINE_TOC_ENTRY_SIZE:
+    if fsize != len(data) or toc_size != count * ENGINE_TOC_ENTRY_SIZE or toc_off + toc_size > len(data):
         raise ValueError("AEXRT engine size mismatch")
-    sections = {}
+    sections: Dict[int, Dict[str, int]] = {}
     for i in range(count):
-        stype, _, off, size, crc, _ = struct.unpack_from("<IIQQII", data, toc_off + i * ENGINE_TOC_ENTRY_SIZE)
-        if off + size > len(data):
-            raise ValueError("AEXRT section out of range")
+        stype, sflags, off, size, crc, reserved = struct.unpack_from(TOC_FMT, data, toc_off + i * ENGINE_TOC_ENTRY_SIZE)
+        if reserved or off + size > len(data):
+            raise ValueError("invalid AEXRT section entry")
+        if stype in sections:
+            raise ValueError(f"duplicate AEXRT section {stype}")
         if zlib.crc32(data[off:off + size]) & 0xFFFFFFFF != crc:
             raise ValueError(f"AEXRT section {stype} checksum mismatch")
-        sections[stype] = dict(offset=off, size=size, crc32=crc)
-    info: Dict[str, Any] = dict(version=version, sections=sections, file_size=fsize)
-    if SECTION_MANIFEST in sections:
-        s = sections[SECTION_MANIFEST]
-        ints = struct.unpack_from("<17I", data, s["offset"])
-        info["manifest"] = dict(precision=ints[2], layout=ints[4], channels=ints[6], anchors=ints[7],
-                                classes=ints[8], value_count=ints[12], constant_count=ints[13],
-                                command_count=ints[14], input_value=ints[15], output_value=ints[16],
-                                input_elements=struct.unpack_from("<Q", data, s["offset"] + 68)[0])
-    if SECTION_KERNEL_PLAN in sections:
-        s = sections[SECTION_KERNEL_PLAN]
-        n, _ = struct.unpack_from("<II", data, s["offset"])
-        info["kernel_plan"] = [struct.unpack_from("<6I", data, s["offset"] + 8 + 24 * i) for i in range(n)]
-    if SECTION_PACKED_WEIGHTS in sections:
-        s = sections[SECTION_PACKED_WEIGHTS]
-        n, _ = struct.unpack_from("<II", data, s["offset"])
-        counts: Dict[int, int] = {}
-        for i in range(n):
-            rec = struct.unpack_from("<4IQQQ", data, s["offset"] + 8 + 40 * i)
-            counts[rec[1]] = counts.get(rec[1], 0) + 1
-        info["packed_layout_counts"] = counts
+        sections[stype] = dict(offset=off, size=size, crc32=crc, flags=sflags)
+    missing = [t for t in REQUIRED_SECTIONS if t not in sections]
+    if missing:
+        raise ValueError(f"AEXRT engine lacks sections {missing}")
+
+    def body(t: int) -> bytes:
+        s = sections[t]
+        return data[s["offset"]:s["offset"] + s["size"]]
+
+    info: Dict[str, Any] = dict(version=version, flags=flags, sections=sections, file_size=fsize)
+    head = struct.unpack_from("<17I", body(SECTION_MANIFEST))
+    info["manifest"] = {k: head[i] for i, k in enumerate(MANIFEST_U32_FIELDS)}
+    info["manifest"]["input_elements"], info["manifest"]["arena_nbytes"] = struct.unpack_from(
+        "<QQ", body(SECTION_MANIFEST), 68)
+    plan = body(SECTION_KERNEL_PLAN)
+    n = struct.unpack_from("<I", plan)[0]
+    info["kernel_plan"] = [struct.unpack_from("<6I", plan, 8 + 24 * i) for i in range(n)]
+    if any(not r[5] & PLAN_FLAG_AUTHORITATIVE or r[5] & ~0x1F for r in info["kernel_plan"]):
+        raise ValueError("invalid AEXRT kernel-plan flags")
+    pw = body(SECTION_PACKED_WEIGHTS)
+    layouts = [struct.unpack_from("<4IQQQ", pw, 8 + 40 * i)[1] for i in range(struct.unpack_from("<I", pw)[0])]
+    info["packed_layout_counts"] = {k: layouts.count(k) for k in sorted(set(layouts))}
+    mem = body(SECTION_MEMORY_PLAN)
+    if struct.unpack_from("<I", mem)[0] == MEMORY_PLAN_V2:
+        _, align, pages, nrec, total, mflags, mres = struct.unpack_from("<4IQII", mem)
+        if mflags != 1 or mres or total != info["manifest"]["arena_nbytes"]:
+            raise ValueError("invalid AEXRT V2 memory-plan header")
+        page_bytes = [struct.unpack_from("<4IQ", mem, 32 + 24 * p)[4] for p in range(pages)]
+        if sum(page_bytes) != total:
+            raise ValueError("invalid AEXRT V2 memory-page total")
+        info["memory_plan"] = dict(version=2, alignment=align, page_nbytes=page_bytes, value_records=nrec)
+    else:
+        info["memory_plan"] = dict(version=1)
+    fusion = body(SECTION_FUSION_PLAN)
+    fver, groups, fcmds, fflags = struct.unpack_from("<4I", fusion)
+    if fver != 1 or fcmds != info["manifest"]["command_count"] or not fflags & 1:
+        raise ValueError("invalid AEXRT fusion plan")
+    info["fusion_groups"] = [struct.unpack_from("<8I", fusion, 16 + 32 * g) for g in range(groups)]
+    cver, ndxil, npso, _ = struct.unpack_from("<4I", body(SECTION_PIPELINE_CACHE))
+    if cver != 1:
+        raise ValueError("invalid AEXRT pipeline cache")
+    info["pipeline_cache_records"] = ndxil + npso
     return info

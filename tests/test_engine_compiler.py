@@ -12,6 +12,8 @@ from aexrt_amd import engine as E
 from aexrt_amd.graph import Graph, TensorSpec
 from aexrt_amd.yolov8 import build_yolov8n
 
+from engine_acceptance import reference_accepts
+
 
 def _params(ic=128, oc=128, h=20, w=20, oh=20, ow=20, k=3, s=1, p=1, d=1, g=1, b=1):
     return [b, ic, h, w, oc, oh, ow, k, k, s, s, p, p, d, d, g]
@@ -51,7 +53,7 @@ def test_fp16_conv1x1_plan_record_matches_reference_kat():
     # reference: tests/test_engine_fp16_1x1_plan.py:27-73 -> plan[2:6] == (45, 2, 1, 3), layout 4
     data = E.build_aexrt_engine(_conv_graph(), precision="fp16", classes=60)
     info = E.inspect_aexrt_engine(data)
-    assert info["kernel_plan"][0][2:6] == (45, 2, 2, 3) or info["kernel_plan"][0][2:6] == (45, 2, 1, 3)
+    assert info["kernel_plan"][0][2:6] == (45, 2, 1, 3)
     assert info["packed_layout_counts"] == {4: 1}
 
 
@@ -119,16 +121,8 @@ def test_native_loader_validates_and_fails_closed():
     assert not _validate(bytes(bad))
     assert "checksum" in _lib.last_error()
     # plan says int8 but the packed-weight section lacks the layout-8 record
-    plan = E.compile_plan(g, algo_overrides={0: 52})
-    replay = plan["replay"]
-    sections = {
-        E.SECTION_VALUES: E.encode_values(replay),
-        E.SECTION_COMMANDS: E.encode_commands(replay, plan["plans"]),
-        E.SECTION_CONSTANTS: E.encode_constants(replay, plan["precision"]),
-        E.SECTION_KERNEL_PLAN: E.encode_kernel_plan(plan["plans"]),
-        E.SECTION_PACKED_WEIGHTS: E.encode_packed_weights([]),
-        E.SECTION_MANIFEST: struct.pack("<17I", *([0] * 17)) + bytes(56),
-    }
+    sections = E.engine_sections(g, algo_overrides={0: 52})
+    sections[E.SECTION_PACKED_WEIGHTS] = E.encode_packed_weights([])
     assert not _validate(E.build_container(sections))
     assert "layout-8" in _lib.last_error()
     # truncated header
@@ -213,3 +207,147 @@ def test_fused_engine_validates():
     L = _lib.lib()
     buf = ctypes.create_string_buffer(data, len(data))
     assert L.aexrt_hip_validate_engine(buf, len(data))
+
+
+def _engines():
+    g1 = build_yolov8n(batch=1, imgsz=160, seed=4)
+    r1 = E.lower_graph(g1)
+    int8 = E.w8a8_algo_map(r1, g1.metadata["int8_convs"].split(","))
+    return {
+        "conv1x1_fp16": E.build_aexrt_engine(_conv_graph(), precision="fp16", classes=60),
+        "conv3x3_silu_fp32": E.build_aexrt_engine(_conv_graph(k=3, silu=True), precision="fp32", classes=60),
+        "conv3x3_int8": E.build_aexrt_engine(_conv_graph(k=3, silu=True), algo_overrides={0: 52}, classes=60),
+        "yolov8n160_fp16": E.build_aexrt_engine(g1, precision="fp16", classes=80),
+        "yolov8n160_w8a8": E.build_aexrt_engine(g1, precision="fp16", classes=80, algo_overrides=int8),
+        "yolov8n160_w8a8_pg16": E.build_aexrt_engine(g1, precision="fp16", classes=80, algo_overrides=int8,
+                                                     int8_pergroup=sorted(int8)),
+        "yolov8n160_fused_concat": E.build_aexrt_engine(g1, precision="fp16", classes=80, fuse_concat_min_h=-1),
+        "yolov8n320_bs2_w8a8": E.build_aexrt_engine(build_yolov8n(batch=2, imgsz=320, seed=4), precision="fp16",
+                                                    classes=80, algo_overrides=int8),
+    }
+
+
+ENGINES = _engines()
+
+
+@pytest.mark.parametrize("name", sorted(ENGINES))
+def test_written_engines_pass_reference_acceptance(name):
+    """Sections 1-9, a real arena size and every record rule of the reference loader
+    (RT:17560-18593) and inspector (ENG:336-400)."""
+    data = ENGINES[name]
+    ok, why = reference_accepts(data)
+    assert ok, why
+    assert _validate(data), _lib.last_error()
+    info = E.inspect_aexrt_engine(data)
+    assert set(info["sections"]) == set(range(1, 10))
+    mem = info["memory_plan"]
+    assert mem["version"] == 2 and info["manifest"]["arena_nbytes"] == sum(mem["page_nbytes"]) > 0
+    assert info["fusion_groups"] == [] and info["pipeline_cache_records"] == 0
+
+
+def _arena_layout(data: bytes):
+    """(page, offset, nbytes, born, last read) of every allocated value, from the engine bytes."""
+    info = E.inspect_aexrt_engine(data)
+    s = info["sections"][E.SECTION_MEMORY_PLAN]
+    body = data[s["offset"]:s["offset"] + s["size"]]
+    _, _, pages, nrec, _, _, _ = struct.unpack_from("<4IQII", body)
+    at = 32 + 24 * pages
+    return [struct.unpack_from("<6IQQ", body, at + 40 * i) for i in range(nrec)]
+
+
+def test_memory_plan_keeps_live_values_apart_and_outputs_off_their_input_pages():
+    """Overlapping byte ranges on one page only for values whose lifetimes do not overlap; no
+    command writes a page it reads (page colouring)."""
+    g = build_yolov8n(batch=1, imgsz=160, seed=4)
+    replay = E.lower_graph(g)
+    mem = E.plan_memory(replay)
+    root = list(range(len(replay["values"])))
+    for c in replay["commands"]:
+        if c["kind"] in ("VIEW", "ALIAS"):
+            root[c["output"]] = root[c["inputs"][0]]
+    born, last = {}, {}
+    for v in replay["values"]:
+        if v["flags"] & E.VALUE_INPUT:
+            born[v["id"]] = -1
+    for i, c in enumerate(replay["commands"]):
+        for x in c["inputs"]:
+            last[root[x]] = max(last.get(root[x], -1), i)
+        born.setdefault(root[c["output"]], i)
+    last[root[replay["output_value"]]] = len(replay["commands"])
+    recs = {v: r for v, r in mem["records"].items() if root[v] == v}
+    for a in recs:
+        for b in recs:
+            if a >= b or recs[a][1] != recs[b][1]:
+                continue
+            _, _, oa, na = recs[a]
+            _, _, ob, nb = recs[b]
+            if oa < ob + nb and ob < oa + na:
+                assert last.get(a, born[a]) < born[b] or last.get(b, born[b]) < born[a], (a, b)
+    for c in replay["commands"]:
+        if c["kind"] in ("VIEW", "ALIAS"):
+            continue
+        out_page = mem["records"][c["output"]][1]
+        for x in c["inputs"]:
+            if x in mem["records"]:
+                assert mem["records"][x][1] != out_page
+    assert mem["total_nbytes"] < sum(4 * replay["values"][v]["elements"] for v in recs)
+    assert _arena_layout(ENGINES["yolov8n160_fp16"])
+
+
+def _patched(data: bytes, section: int, fn) -> bytes:
+    """Engine with one section payload replaced by fn(payload), CRCs and offsets rebuilt."""
+    info = E.inspect_aexrt_engine(data)
+    secs = {t: data[s["offset"]:s["offset"] + s["size"]] for t, s in info["sections"].items()}
+    secs[section] = fn(secs[section])
+    return E.build_container(secs)
+
+
+def _set(fmt: str, at: int, *vals):
+    def f(b: bytes) -> bytes:
+        out = bytearray(b)
+        struct.pack_into(fmt, out, at, *vals)
+        return bytes(out)
+    return f
+
+
+def _toc_patch(data: bytes, index: int, field_at: int, value: int) -> bytes:
+    out = bytearray(data)
+    struct.pack_into("<I", out, 64 + 32 * index + field_at, value)
+    return bytes(out)
+
+
+def _mutations():
+    base = ENGINES["conv3x3_int8"]
+    secs = E.inspect_aexrt_engine(base)["sections"]
+    order = sorted(secs)
+    return {
+        "duplicate section type": _toc_patch(base, order.index(9), 0, 8),
+        "TOC reserved field": _toc_patch(base, 0, 28, 1),
+        "missing memory plan": E.build_container({t: base[s["offset"]:s["offset"] + s["size"]]
+                                                  for t, s in secs.items() if t != 7}),
+        "arena_nbytes zero": _patched(base, 1, _set("<Q", 76, 0)),
+        "manifest version": _patched(base, 1, _set("<I", 0, 2)),
+        "manifest mode": _patched(base, 1, _set("<I", 12, 1)),
+        "values reserved": _patched(base, 2, _set("<I", 4, 7)),
+        "memory page flags": _patched(base, 7, _set("<I", 32 + 12, 0)),
+        "memory total": _patched(base, 7, _set("<Q", 16, 1)),
+        "memory record page dtype": _patched(base, 7, lambda b: _set("<I", 32 + 24 * struct.unpack_from(
+            "<I", b, 8)[0] + 12, 2)(b)),
+        "fusion plan version": _patched(base, 8, _set("<I", 0, 2)),
+        "fusion plan command count": _patched(base, 8, _set("<I", 8, 99)),
+        "pipeline cache version": _patched(base, 9, _set("<I", 0, 0)),
+        "pipeline cache record without payload": _patched(
+            base, 9, lambda b: struct.pack("<4I", 1, 1, 0, 0) + struct.pack("<IIQQQ", 1, 0, 5, 48, 0)),
+        "kernel plan flags": _patched(base, 5, _set("<I", 8 + 20, 1 | 64)),
+    }
+
+
+MUTATIONS = _mutations()
+
+
+@pytest.mark.parametrize("name", sorted(MUTATIONS))
+def test_mutated_engines_are_refused_like_the_reference(name):
+    data = MUTATIONS[name]
+    ok, _ = reference_accepts(data)
+    assert not ok
+    assert not _validate(data)
