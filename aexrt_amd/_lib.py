@@ -117,6 +117,7 @@ _SIGS = {
     "aexrt_hip_quant_fused_pg16": (c_int, [_vp, c_uint32, c_uint32, c_uint32, c_uint32, _vp, _vp, _vp]),
     "aexrt_hip_conv2d_int8_pg16": (c_int, [POINTER(ConvDesc), c_uint32, c_uint32, _vp, _vp, _vp, _vp, _vp, _vp,
                                            _vp]),
+    "aexrt_hip_conv2d_f32": (c_int, [POINTER(ConvDesc), c_uint32, _vp, _vp, _vp, _vp, _vp]),
     "aexrt_hip_conv_weight_bytes": (c_int, [POINTER(ConvDesc), c_uint32, POINTER(c_uint64)]),
     "aexrt_hip_pack_conv_weight": (c_int, [POINTER(ConvDesc), c_uint32, c_uint32, _vp, c_uint64, _vp,
                                            c_uint64, _vp]),
@@ -180,7 +181,34 @@ _MODEL_SIGS = {
     "aexrt_yolo_graph_node_count": (c_uint32, [_vp]),
     "aexrt_yolo_constant_count": (c_uint32, [_vp]),
     "aexrt_yolo_destroy": (None, [_vp]),
+    "aexrt_yolo_package_mode": (c_uint32, [_vp]),
+    "aexrt_yolo_flush_pipeline": (c_int, [_vp, POINTER(YoloDetection), c_uint32, POINTER(c_uint32)]),
+    "aexrt_yolo_pipeline_cache_size": (c_uint64, [_vp]),
+    "aexrt_yolo_export_pipeline_cache": (c_int, [_vp, _vp, c_uint64]),
+    "aexrt_yolo_debug_page": (c_int, [_vp, c_uint32, _vp, c_uint64]),
+    "aexrt_d3d12_probe": (c_int, []),
+    "aexrt_d3d12_create_device": (_vp, [c_uint32]),
+    "aexrt_d3d12_destroy_device": (None, [_vp]),
+    "aexrt_yolo_compile_from_package": (_vp, [_vp, ctypes.c_char_p]),
+    "aexrt_yolo_compile_from_onnx": (_vp, [_vp, ctypes.c_char_p]),
 }
+
+# The reference's prepared-plan counters (native/aexrt.h:313-385), all
+# uint32(model).
+PLAN_COUNTERS = (
+    "supported_prepared_command_count", "unsupported_prepared_command_count", "prepared_skipped_command_count",
+    "late_concat_conv1x1_fusion_count", "concat_residual_conv1x1_fusion_count", "paired_conv3x3_fusion_count",
+    "c2f_bottleneck_superblock_count", "c2f_tail_residual_fusion_count", "head_fusion_enabled",
+    "head_final_conv_fusion_enabled", "tileflow_conv1x1_count", "tileflow_3x3_spatial_count",
+    "tileflow_3x3_pack4_count", "tileflow_3x3_pack8_count", "tileflow_3x3_implicit_gemm_count",
+    "tileflow_3x3_implicit_gemm_40x40_count", "tileflow_3x3_implicit_gemm_20x20_count",
+    "tileflow_3x3_implicit_gemm_10x10_count", "tileflow_3x3_exact_40x40_64x64_count",
+    "tileflow_3x3_exact_20x20_64x64_count", "tileflow_3x3_exact_10x10_128x128_count",
+    "tileflow_3x3_exact_20x20_128x64_count", "tileflow_3x3_exact_10x10_256x64_count",
+    "tileflow_native_fp16_count", "dxil_cache_hit_count", "shader_cache_hit_count", "pso_cache_hit_count",
+)
+for _name in PLAN_COUNTERS:
+    _MODEL_SIGS["aexrt_yolo_" + _name] = (c_uint32, [_vp])
 
 
 def lib():

@@ -319,6 +319,38 @@ int aexrt_hip_conv2d(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t f
     return launch_conv(p, algorithm, static_cast<hipStream_t>(stream)) ? 1 : 0;
 }
 
+int aexrt_hip_conv2d_f32(const AexrtConv2DDesc* desc, uint32_t flags, const float* x, const float* weight,
+                         const float* bias, float* y, void* stream) {
+    if (!desc || !x || !weight || !bias || !y) {
+        set_error("conv2d_f32: null argument");
+        return 0;
+    }
+    const AexrtConv2DDesc& d = *desc;
+    if (d.batch == 0 || d.in_channels == 0 || d.out_channels == 0 || d.in_h == 0 || d.in_w == 0 || d.out_h == 0 ||
+        d.out_w == 0 || d.kernel_h == 0 || d.kernel_w == 0 || d.groups == 0 || d.stride_h == 0 || d.stride_w == 0 ||
+        d.dilation_h == 0 || d.dilation_w == 0 || d.in_channels % d.groups || d.out_channels % d.groups ||
+        (flags & ~AEXRT_HIP_CONV_SILU)) {
+        set_error("conv2d_f32: invalid descriptor or flags (SILU only)");
+        return 0;
+    }
+    const uint32_t dims[] = {d.batch, d.in_channels, d.in_h, d.in_w, d.out_channels, d.out_h, d.out_w,
+                             d.kernel_h, d.kernel_w, d.stride_h, d.stride_w, d.pad_top, d.pad_left,
+                             d.dilation_h, d.dilation_w, d.groups};
+    for (uint32_t v : dims)
+        if (v > 0x7FFFFFFu) {
+            set_error("conv2d_f32: descriptor value out of range");
+            return 0;
+        }
+    F32ConvParams p{};
+    p.x = x, p.w = weight, p.bias = bias, p.y = y;
+    p.N = (int)d.batch, p.C = (int)d.in_channels, p.H = (int)d.in_h, p.W = (int)d.in_w;
+    p.OC = (int)d.out_channels, p.OH = (int)d.out_h, p.OW = (int)d.out_w, p.KH = (int)d.kernel_h;
+    p.KW = (int)d.kernel_w, p.SH = (int)d.stride_h, p.SW = (int)d.stride_w, p.PT = (int)d.pad_top;
+    p.PL = (int)d.pad_left, p.DH = (int)d.dilation_h, p.DW = (int)d.dilation_w, p.G = (int)d.groups;
+    p.silu = (flags & AEXRT_HIP_CONV_SILU) ? 1 : 0;
+    return check_hip(launch_conv_f32(p, static_cast<hipStream_t>(stream)), "conv2d_f32") ? 1 : 0;
+}
+
 int aexrt_hip_conv2d_int8_pg16(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t flags,
                                const uint32_t* packed, const uint32_t* amax, const void* weight, const float* w_scale,
                                const float* bias, void* y, void* stream) {

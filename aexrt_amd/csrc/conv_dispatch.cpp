@@ -52,10 +52,18 @@ bool build_conv_params(const AexrtConv2DDesc& d, uint32_t algorithm, uint32_t fl
             why = "int8 kernel id does not match the stride";
             return false;
         }
-        if (!x.amax_slots || !w_scale) {
+        const bool dynamic = (flags & AEXRT_HIP_CONV_INT8_DYNAMIC) != 0;
+        if ((!dynamic && !x.amax_slots) || !w_scale) {
             why = "int8 conv needs the input amax slots and the weight scales";
             return false;
         }
+        if (dynamic && (acc_out || (flags & AEXRT_HIP_CONV_INT8_PG16) || nchw)) {
+            why = "dynamic int8 conv: no acc_out, not with pg16, NHWC input";
+            return false;
+        }
+    } else if (flags & AEXRT_HIP_CONV_INT8_DYNAMIC) {
+        why = "the dynamic int8 flag needs an int8 algorithm";
+        return false;
     }
     if (wino) {
         if (!winograd_shape_ok(d)) {
@@ -157,12 +165,35 @@ bool build_conv_params(const AexrtConv2DDesc& d, uint32_t algorithm, uint32_t fl
     p.M = (int)m;
     p.flags = (int)(flags & (AEXRT_HIP_CONV_SILU | AEXRT_HIP_CONV_RESIDUAL | AEXRT_HIP_CONV_OUT_F32));
     if (pg16) p.flags |= kConvPg16;
+    if (flags & AEXRT_HIP_CONV_INT8_DYNAMIC) p.flags |= kConvDynamic;
     return true;
+}
+
+DynConvParams dynamic_params(const ConvParams& p) {
+    DynConvParams q{};
+    q.x = static_cast<const __half*>(p.x);
+    q.x_nstride = p.x_nstride;
+    q.x_cstride = p.x_cstride;
+    q.w = static_cast<const int8_t*>(p.w);
+    q.Kp = p.Kp;
+    q.w_scale = p.w_scale;
+    q.bias = p.bias;
+    q.y = p.y;
+    q.y_nstride = p.y_nstride;
+    q.y_cstride = p.y_cstride;
+    q.res = p.res;
+    q.r_nstride = p.r_nstride;
+    q.r_cstride = p.r_cstride;
+    q.y_slots = p.y_slots;
+    q.N = p.N, q.H = p.H, q.W = p.W, q.C = p.C, q.OH = p.OH, q.OW = p.OW, q.OC = p.OC, q.K = p.KH, q.S = p.S;
+    q.flags = p.flags & (kConvSilu | kConvResidual | kConvOutF32);
+    return q;
 }
 
 bool launch_conv(const ConvParams& p, uint32_t algorithm, hipStream_t stream) {
     if (is_winograd_algorithm(algorithm)) return check_hip(launch_winograd_f2x2(p, stream), "winograd conv");
     if (p.flags & kConvPg16) return check_hip(launch_conv_int8_pg16(p, stream), "int8 pg16 conv");
+    if (p.flags & kConvDynamic) return check_hip(launch_conv_int8_dynamic(dynamic_params(p), stream), "int8 dynamic conv");
     return check_hip(launch_conv_igemm(p, is_int8_algorithm(algorithm), stream),
                      is_int8_algorithm(algorithm) ? "int8 conv" : "fp16 conv");
 }

@@ -4,6 +4,7 @@
 #include <atomic>
 #include <cmath>
 
+#include <cstdio>
 #include "conv_halo.h"
 
 namespace aexrt {
@@ -161,6 +162,11 @@ bool choose_halo_tile(HaloParams& h, bool int8, HaloTile& best) {
 
 hipError_t halo_launch(const HaloParams& h, bool int8, int epi, const HaloTile& t, hipStream_t s) {
     using halo::halo_launch_family;
+    if (LaunchProbe* pr = launch_probe()) {
+        std::snprintf(pr->name, sizeof(pr->name), "halo%s jn%d pw%d %dx%d cc%d nw%d",
+                      h.c.loader == kLoaderNchwF32 ? "-nchw" : "", t.jn, t.pw, t.TR, t.TC, t.CC, t.nw);
+        return hipSuccess;
+    }
     if (h.c.loader == kLoaderNchwF32) return halo::halo_launch_nchw(h, t.jn, t.pw, t.np, s);
     if (int8) {
         if (epi == 1) return halo_launch_family<true, 1>(h, t.jn, t.pw, t.np, t.nw, s);

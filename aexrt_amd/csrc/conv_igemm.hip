@@ -3,6 +3,7 @@
 #include <algorithm>
 #include <atomic>
 
+#include <cstdio>
 #include "conv_igemm.h"
 
 namespace aexrt {
@@ -15,6 +16,11 @@ namespace {
 
 hipError_t launch_variant(bool int8, bool mc, int epi, const ConvParams& p, const ConvTile& t, hipStream_t s) {
     using igemm::launch_family;
+    if (LaunchProbe* pr = launch_probe()) {
+        std::snprintf(pr->name, sizeof(pr->name), "igemm jn%d pw%d%s%s", t.jn, t.pw, t.ksw ? " ksw" : "",
+                      mc ? " mc" : "");
+        return hipSuccess;
+    }
     if (int8) {
         if (mc) {
             if (epi == 1) return launch_family<true, true, 1>(p, t, s);
@@ -42,6 +48,23 @@ uint64_t view_span(int N, int64_t nstride, int32_t cstride, int HW, int C, int e
 }
 
 }  // namespace
+
+namespace {
+thread_local LaunchProbe* g_probe = nullptr;
+}  // namespace
+
+void set_launch_probe(LaunchProbe* probe) { g_probe = probe; }
+LaunchProbe* launch_probe() { return g_probe; }
+
+void conv_kernel_name(const ConvParams& p, bool int8, char* out, size_t n) {
+    LaunchProbe pr{};
+    std::snprintf(pr.name, sizeof(pr.name), "none");
+    LaunchProbe* prev = g_probe;
+    g_probe = &pr;
+    const hipError_t e = launch_conv_igemm(p, int8, nullptr);
+    g_probe = prev;
+    std::snprintf(out, n, "%s", e == hipSuccess ? pr.name : "not launchable");
+}
 
 namespace {
 // jn * 100 + pw * 10 + ksw + 1, 0 = no override

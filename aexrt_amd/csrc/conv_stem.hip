@@ -19,6 +19,7 @@
 // block from the [OCp][Kp] (k = tap * C + c) layout the other fp16 kernels
 // use.  The general halo-tile kernel pads the input to 8 channels instead
 // (72 of 128 k, four MFMAs and a 16-byte LDS pixel per position).
+#include <cstdio>
 #include "conv_igemm.h"
 
 namespace aexrt {
@@ -344,6 +345,10 @@ hipError_t launch_conv_stem(const ConvParams& p, hipStream_t stream) {
     const int np = (h.npieces + 255) / 256;
     const int sw = ((h.npos + 15) / 16 + 3) / 4;
     const int jn = (p.OCp + 15) / 16;
+    if (LaunchProbe* pr = launch_probe()) {
+        std::snprintf(pr->name, sizeof(pr->name), "stem band tr%d%s", tr, one ? " one" : "");
+        return hipSuccess;
+    }
 #define AEXRT_STEM_CASE(J, N, W) \
     if (jn <= J && np <= N && sw <= W) return stem::stem_launch_cfg<J, N, W>(h, one, stream);
     AEXRT_STEM_CASE(1, 4, 4) AEXRT_STEM_CASE(1, 8, 8) AEXRT_STEM_CASE(1, 12, 12)

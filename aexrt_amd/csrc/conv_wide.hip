@@ -2,6 +2,7 @@
 // applicability, tile geometry, launch.
 #include <algorithm>
 
+#include <cstdio>
 #include "conv_wide.h"
 
 namespace aexrt {
@@ -119,6 +120,10 @@ hipError_t launch_conv_wide(const ConvParams& p, int epi, hipStream_t stream) {
     h.c = p;
     const ConvChoice& t = p.choice;
     if (!wide_geometry(h, t.jn, t.pw, t.tr, t.tc, t.cc)) return hipErrorInvalidValue;
+    if (LaunchProbe* pr = launch_probe()) {
+        std::snprintf(pr->name, sizeof(pr->name), "wide jn%d pw%d %dx%d cc%d", t.jn, t.pw, t.tr, t.tc, t.cc);
+        return hipSuccess;
+    }
 #define AEXRT_WIDE_CASE(J, P)                                                                    \
     if (t.jn == J && t.pw == P)                                                                  \
         return epi == igemm::kEpiSilu ? wide_launch_cfg<J, P, igemm::kEpiSilu>(h, stream)        \

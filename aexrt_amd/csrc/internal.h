@@ -47,5 +47,11 @@ bool build_conv_params(const AexrtConv2DDesc& d, uint32_t algorithm, uint32_t fl
                        const AexrtHipTensorView* residual, const AexrtHipTensorView& y, int32_t* acc_out,
                        ConvParams& p, std::string& why);
 bool launch_conv(const ConvParams& p, uint32_t algorithm, hipStream_t stream);
+// Kernel parameters of the dynamic int8 conv for a conv built with
+// AEXRT_HIP_CONV_INT8_DYNAMIC.
+DynConvParams dynamic_params(const ConvParams& p);
+// The reference dispatches int8 convs whose input has fewer than this many
+// elements to the dynamic kernel (native/aexrt_d3d12_runtime.cpp:21478-21479).
+constexpr uint64_t kInt8PrequantMinElements = 4096;
 
 }  // namespace aexrt

@@ -40,6 +40,7 @@ enum ConvFlags : int {
     kConvOutF32 = 4,    // store fp32 instead of fp16
     kConvPg16 = 16,     // int8 with per-16-input-channel activation scales (pg16)
     kConvOutNchw = 32,  // pg16 only: dense NCHW output (the reference's layout)
+    kConvDynamic = 64,  // int8 quantized per (position, 4 channels) in the kernel
 };
 
 // Views whose element (position m, channel c) sits at m * c_stride + c: the
@@ -116,6 +117,17 @@ ConvTile choose_conv_tile(int M, int OC, int Kp);
 // kernel instance.
 bool set_conv_tile_override(int jn, int pw, int ksw);
 
+// Kernel-name probe: while a probe is installed on the calling thread, the
+// conv launchers (implicit GEMM, halo, stem, wide) write the kernel and tile
+// they would launch into it and return hipSuccess without launching.
+struct LaunchProbe {
+    char name[96];
+};
+void set_launch_probe(LaunchProbe* probe);
+LaunchProbe* launch_probe();
+// Kernel and tile launch_conv_igemm(p, int8, ...) runs, as "family tile".
+void conv_kernel_name(const ConvParams& p, bool int8, char* out, size_t n);
+
 // Implicit-GEMM conv (int8 or fp16 MFMA).  Requires C % 8 == 0, OC % 4 == 0,
 // Kp % 64 == 0, OCp % 16 == 0 and 16-byte aligned views.
 hipError_t launch_conv_igemm(const ConvParams& p, bool int8, hipStream_t stream);
@@ -154,6 +166,44 @@ bool set_conv_stem(int mode, int tr);
 // channels zero-padded to a multiple of 8 (one 16-byte store per pixel and
 // 8 channels).  y has c_stride Cp = C rounded up to 8, dense.
 hipError_t launch_nchw_f32_to_nhwc8(const float* x, __half* y, int N, int C, int HW, hipStream_t stream);
+
+// Dynamic int8 conv (the reference's fallback for inputs of fewer than 4096
+// elements): per (position, 4-channel group) scale computed in the kernel,
+// v_dot4 int32 partials, fp32 dequant accumulation, + bias, SiLU (flags
+// kConvSilu), fp16 residual (kConvResidual), fp32 output (kConvOutF32).
+// w is the int8 [OCp][Kp] weight of the MFMA kernels (K = (ky, kx, c)).
+struct DynConvParams {
+    const __half* x;
+    int64_t x_nstride;
+    int32_t x_cstride;
+    const int8_t* w;
+    int32_t Kp;
+    const float* w_scale;
+    const float* bias;
+    void* y;
+    int64_t y_nstride;
+    int32_t y_cstride;
+    const __half* res;
+    int64_t r_nstride;
+    int32_t r_cstride;
+    SlotRef y_slots;
+    int N, H, W, C, OH, OW, OC, K, S;
+    int flags;
+};
+hipError_t launch_conv_int8_dynamic(const DynConvParams& p, hipStream_t stream);
+
+// fp32 direct conv on dense NCHW tensors (the reference's fp32 conv path):
+// w [OC][C/G][KH][KW], bias [OC], y [N][OC][OH][OW]; acc = bias, += x*w in
+// (channel, ky, kx) order without fused multiply-adds; silu: acc/(1+e^-acc).
+struct F32ConvParams {
+    const float* x;
+    const float* w;
+    const float* bias;
+    float* y;
+    int N, C, H, W, OC, OH, OW, KH, KW, SH, SW, PT, PL, DH, DW, G;
+    int silu;
+};
+hipError_t launch_conv_f32(const F32ConvParams& p, hipStream_t stream);
 
 // Winograd F(2x2,3x3), fp16 MFMA.  U is [16][OCp][Cp] fp16 (Cp = C rounded up
 // to 32).  Same views/flags as ConvParams (w = U, Kp = Cp).

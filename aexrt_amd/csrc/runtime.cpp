@@ -75,6 +75,10 @@ struct Root {
     // an int8 conv reads a value of this root: its producers keep its amax
     // slots (slot updates of roots no int8 conv reads are skipped)
     bool slots_read = true;
+    // every channel of the root is covered by a producer that folds into its
+    // slots (false when a slice was placed at a channel offset or size that
+    // is not a multiple of 16: int8 readers then take their own amax pass)
+    bool slots_complete = true;
     size_t byte_offset = 0;
 };
 
@@ -89,7 +93,9 @@ struct ConvState {
     float* scale = nullptr;
     float* bias = nullptr;
     bool pg16 = false;            // int8 with per-16-input-channel scales (plan flag 16)
+    bool dynamic = false;         // int8 on an input of < 4096 elements: quantized per (position, 4 ch)
     uint32_t* strips = nullptr;   // pg16 at N > 1: the reference's strip amax of the input
+    uint32_t* own_slots = nullptr;  // per-tensor int8 whose input slots are incomplete: its own amax pass
     uint64_t w_bytes = 0;         // bytes of w
     // sibling pair (this conv first): weights and bias of both convs, rows of
     // this conv then the sibling's, built from the w of each named here
@@ -109,6 +115,10 @@ struct Step {
     std::vector<int> deps;
     int lane = 0;
     bool signal = false;  // a later step on another lane waits for this one
+    // conv steps: label = head + " kernel=" + family() + tail (the kernel that
+    // runs can change after the step is built: measured tile choices)
+    std::string head, tail;
+    std::function<std::string()> family;
 };
 
 // A conv whose kernel choice is measured: its launch reads p (the choice
@@ -125,6 +135,21 @@ struct TunedConv {
 
 // Streams a captured graph spreads independent steps over.
 constexpr int kLanes = 4;
+
+// What the prepared step list does with the engine's commands, in the terms
+// of the reference's counters (native/aexrt.h:307-385): commands folded into
+// another launch, fusions, and convs per kernel family.
+struct PlanStats {
+    uint32_t skipped = 0;               // engine commands with no launch of their own
+    uint32_t late_concat_conv1x1 = 0;   // concats placed in place and read whole by a 1x1 conv
+    uint32_t paired_conv3x3 = 0;        // two 3x3 convs of one input computed by one launch
+    uint32_t tail_residual = 0;         // residual adds in a conv epilogue
+    uint32_t conv1x1 = 0, spatial3x3 = 0, pack4_3x3 = 0, igemm3x3 = 0, igemm3x3_40 = 0, igemm3x3_20 = 0,
+             igemm3x3_10 = 0;
+    uint32_t exact_40_64x64 = 0, exact_20_64x64 = 0, exact_10_128x128 = 0, exact_20_128x64 = 0,
+             exact_10_256x64 = 0;
+    uint32_t native_fp16 = 0;
+};
 
 // A CONCAT input that could not be placed inside its concat: copied there.
 struct CopyJob {
@@ -195,6 +220,7 @@ struct AexrtYoloModel {
     std::vector<std::string> prof_labels;
     std::vector<double> prof_ms;
     AexrtYoloRunTiming timing{};
+    aexrt::PlanStats stats{};
     std::string last_error;
     bool executable = false;
     // YOLO postprocess of output0 (decode + filter, NMS, top-k)
@@ -330,14 +356,25 @@ bool infer_dims(AexrtYoloModel* m) {
                 if (!x || p.size() < 13 || p[6] != p[7] || p[8] != p[9] || p[10] != p[11] || p[12] != 1)
                     return fail(m, "command " + std::to_string(ci) + ": unsupported MAXPOOL");
                 o.N = (int)p[0], o.C = (int)p[1], o.H = (int)p[4], o.W = (int)p[5];
-                if (x->C != o.C || x->H != (int)p[2] || x->W != (int)p[3])
+                if (x->rank != 4 || x->N != o.N || x->C != o.C || x->H != (int)p[2] || x->W != (int)p[3])
                     return fail(m, "command " + std::to_string(ci) + ": MAXPOOL input mismatch");
+                // the output is what the pooling window yields (floor mode), so
+                // the kernel never writes past the output root
+                const int64_t k = p[6], st = p[8], pad = p[10];
+                if (k < 1 || st < 1 || 2 * pad > k || (int64_t)x->H + 2 * pad < k || (int64_t)x->W + 2 * pad < k ||
+                    o.H != ((int64_t)x->H + 2 * pad - k) / st + 1 || o.W != ((int64_t)x->W + 2 * pad - k) / st + 1)
+                    return fail(m, "command " + std::to_string(ci) + ": MAXPOOL output dims do not follow the window");
                 break;
             }
             case kCmdResize: {
                 ValueInfo* x = need_in(0);
                 if (!x || p.size() < 6) return fail(m, "command " + std::to_string(ci) + ": bad RESIZE");
                 o.N = (int)p[0], o.C = (int)p[1], o.H = (int)p[4], o.W = (int)p[5];
+                // the kernel runs over the input's images and channels into an
+                // output root sized from these params: they must agree
+                if (x->rank != 4 || (int)p[0] != x->N || (int)p[1] != x->C || (int)p[2] != x->H || (int)p[3] != x->W ||
+                    o.H < 1 || o.W < 1)
+                    return fail(m, "command " + std::to_string(ci) + ": RESIZE params do not match its input");
                 break;
             }
             case kCmdBinary: {
@@ -407,7 +444,7 @@ void mark_slot_readers(AexrtYoloModel* m) {
     for (Root& r : m->roots) r.slots_read = false;
     for (size_t ci = 0; ci < m->eng.commands.size(); ++ci) {
         const ConvState& cs = m->convs[ci];
-        if (!cs.is_conv || !is_int8_algorithm(cs.algorithm)) continue;
+        if (!cs.is_conv || !is_int8_algorithm(cs.algorithm) || cs.dynamic) continue;
         const ValueInfo& x = m->vals[m->eng.commands[ci].inputs[0]];
         if (x.pl.valid && x.pl.root >= 0) m->roots[x.pl.root].slots_read = true;
     }
@@ -557,6 +594,9 @@ bool plan_memory(AexrtYoloModel* m, std::vector<CopyJob>& copies) {
             if (along_c) {
                 slice.offset += off;
                 slice.slot = (base.slot >= 0 && off % 16 == 0) ? base.slot + off / 16 : -1;
+                // a slice off the 16-channel grid: its producer cannot fold into
+                // the root's slots, and a neighbour's group would miss it
+                if (base.slot >= 0 && (off % 16 || x.C % 16)) m->roots[base.root].slots_complete = false;
             } else {
                 slice.offset += int64_t(off) * x.W * base.cstride;
             }
@@ -660,6 +700,21 @@ AexrtConv2DDesc conv_desc_padded(AexrtYoloModel* m, size_t ci) {
     const ValueInfo& x = m->vals[c.inputs[0]];
     if (x.cpad > x.C) d.in_channels = (uint32_t)x.cpad;
     return d;
+}
+
+// How an int8 conv quantizes its input (RT:23935-24318): an input of fewer
+// than 4096 elements is quantized per (position, 4 channels) in the conv
+// (RT:21478-21479, the dynamic kernel, pg16 or not); otherwise plan flag 16
+// (engine.py:85-96) selects per-16-input-channel scales (RT:4770-4923), else
+// one per-tensor scale.
+void set_int8_mode(AexrtYoloModel* m, size_t ci) {
+    ConvState& cs = m->convs[ci];
+    const EngineCommand& c = m->eng.commands[ci];
+    const AexrtConv2DDesc d = desc_of(c);
+    const bool int8 = is_int8_algorithm(cs.algorithm);
+    const uint64_t elems = uint64_t(d.batch) * d.in_channels * d.in_h * d.in_w;
+    cs.dynamic = int8 && elems < kInt8PrequantMinElements;
+    cs.pg16 = int8 && !cs.dynamic && (c.plan_flags & kPlanFlagInt8PerGroup) != 0;
 }
 
 uint32_t resolve_algorithm(AexrtYoloModel* m, size_t ci, uint32_t wanted) {
@@ -1000,6 +1055,20 @@ void schedule_steps(AexrtYoloModel* m) {
     }
 }
 
+// Labels of the conv steps name the kernel and tile that runs (it changes as
+// the tile choices are measured): "<command> alg=<plan family> kernel=<kernel>".
+void label_steps(AexrtYoloModel* m) {
+    for (Step& st : m->steps)
+        if (st.family) st.label = st.head + " kernel=" + st.family() + st.tail;
+}
+
+// Key of a conv's choice measured in the network: the command, its algorithm
+// and its shape.  Overriding a conv's algorithm and restoring it finds the
+// first measurement again, so the restored model runs the same kernels.
+std::string refined_key(size_t ci, uint32_t alg, const ConvParams& p, bool int8) {
+    return "cmd " + std::to_string(ci) + " alg " + std::to_string(alg) + " " + tune_key(p, int8);
+}
+
 bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
     Engine& e = m->eng;
     auto& V = m->vals;
@@ -1087,6 +1156,24 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                         xvw.amax_stripe_stride = 0;
                     }
                 }
+                // a9: the reference quantizes an int8 conv's input per (position,
+                // 4 channels) in the kernel when the input has fewer than 4096
+                // elements (RT:21478-21479); otherwise a per-tensor int8 conv whose
+                // input slots do not cover every channel takes its own amax pass
+                const bool int8 = is_int8_algorithm(cs.algorithm);
+                AexrtHipTensorView own_src{};
+                bool own_pass = false;
+                if (int8 && cs.dynamic) {
+                    flags |= AEXRT_HIP_CONV_INT8_DYNAMIC;
+                } else if (int8 && !cs.pg16 && (!xvw.amax_slots || !m->roots[V[xv].pl.root].slots_complete)) {
+                    if (!cs.own_slots) cs.own_slots = static_cast<uint32_t*>(dev_alloc(m, d.in_channels / 16 * 4));
+                    if (!cs.own_slots) return fail(m, "out of device memory for conv amax slots");
+                    own_src = xvw;
+                    xvw.amax_slots = cs.own_slots;
+                    xvw.amax_stripes = 1;
+                    xvw.amax_stripe_stride = 0;
+                    own_pass = true;
+                }
                 ConvParams p{};
                 std::string why;
                 if (!build_conv_params(d, cs.algorithm, flags, xvw, pair ? cs.w_pair : cs.w, cs.scale,
@@ -1094,9 +1181,23 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                                        p, why))
                     return fail(m, "command " + std::to_string(ci) + ": " + why);
                 const uint32_t alg = cs.algorithm;
+                std::function<hipError_t(hipStream_t)> pre;
+                if (own_pass) {
+                    uint32_t* own = cs.own_slots;
+                    const int on = (int)d.batch, ohw = (int)(d.in_h * d.in_w), oc_in = (int)d.in_channels;
+                    pre = [=](hipStream_t s) {
+                        hipError_t e = launch_fill_u32(own, oc_in / 16, 0u, s);
+                        if (e == hipSuccess)
+                            e = launch_amax_slots_nhwc(static_cast<const __half*>(own_src.data), own_src.n_stride,
+                                                       own_src.c_stride, on, ohw, oc_in, SlotRef{own, 1u, 0u}, s);
+                        return e;
+                    };
+                }
+                std::string head = conv_label(c, e.src_cmd[ci], alg);
+                std::function<std::string()> family;
                 if (cs.pg16) {
                     uint32_t* strips = cs.strips;
-                    m->steps.push_back(Step{(int)ci, conv_label(c, e.src_cmd[ci], alg) + " pg16", [=](hipStream_t s) {
+                    m->steps.push_back(Step{(int)ci, "", [=](hipStream_t s) {
                                                 if (strips) {
                                                     hipError_t e = launch_fill_u32(strips, strip_c / 16, 0u, s);
                                                     if (e == hipSuccess)
@@ -1108,12 +1209,19 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                                                 }
                                                 return launch_conv_int8_pg16(p, s);
                                             }});
+                    head += " pg16";
+                    family = [] { return std::string("int8 pg16 mfma"); };
+                } else if (int8 && cs.dynamic) {
+                    const DynConvParams dp = dynamic_params(p);
+                    m->steps.push_back(Step{(int)ci, "", [dp](hipStream_t s) { return launch_conv_int8_dynamic(dp, s); }});
+                    head += " dynamic";
+                    family = [] { return std::string("int8 dynamic dot4"); };
                 } else if (m->autotune && !is_winograd_algorithm(alg)) {
                     auto tc = std::make_unique<TunedConv>();
                     tc->cmd = (int)ci;
-                    tc->int8 = is_int8_algorithm(alg);
+                    tc->int8 = int8;
                     if (!tune_conv(m, p, tc->int8, &tc->cands)) return false;
-                    tc->key = "cmd " + std::to_string(ci) + " " + tune_key(p, tc->int8);
+                    tc->key = refined_key(ci, alg, p, tc->int8);
                     auto rf = m->refined.find(tc->key);
                     if (rf != m->refined.end()) {
                         for (const ConvChoice& k : tc->cands) tc->done = tc->done || same_choice(k, rf->second);
@@ -1130,21 +1238,47 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                     tc->step = m->steps.size();
                     TunedConv* t = tc.get();
                     m->tunables.push_back(std::move(tc));
-                    m->steps.push_back(Step{(int)ci, conv_label(c, e.src_cmd[ci], alg), [t](hipStream_t s) {
+                    m->steps.push_back(Step{(int)ci, "", [t, pre](hipStream_t s) {
+                                                if (pre) {
+                                                    const hipError_t e = pre(s);
+                                                    if (e != hipSuccess) return e;
+                                                }
                                                 return launch_conv_igemm(t->p, t->int8, s);
                                             }});
+                    family = [t] {
+                        char name[96];
+                        conv_kernel_name(t->p, t->int8, name, sizeof(name));
+                        return std::string(name);
+                    };
                 } else {
-                    m->steps.push_back(Step{(int)ci, conv_label(c, e.src_cmd[ci], alg), [p, alg](hipStream_t s) {
+                    m->steps.push_back(Step{(int)ci, "", [p, alg, pre](hipStream_t s) {
+                                                if (pre) {
+                                                    const hipError_t e = pre(s);
+                                                    if (e != hipSuccess) return e;
+                                                }
                                                 if (is_winograd_algorithm(alg)) return launch_winograd_f2x2(p, s);
                                                 return launch_conv_igemm(p, is_int8_algorithm(alg), s);
                                             }});
+                    if (is_winograd_algorithm(alg)) {
+                        family = [] { return std::string("winograd f2x2 mfma"); };
+                    } else {
+                        family = [p, int8] {
+                            char name[96];
+                            conv_kernel_name(p, int8, name, sizeof(name));
+                            return std::string(name);
+                        };
+                    }
                 }
-                if (!(m->vals[xv].is_input && m->input_nchw_direct)) m->steps.back().reads.push_back(V[xv].pl.root);
-                if (cs.fused_residual) m->steps.back().reads.push_back(V[cs.residual_value].pl.root);
-                m->steps.back().writes = {V[yv].pl.root};
+                if (own_pass) head += " own-amax";
+                Step& st = m->steps.back();
+                st.head = head;
+                st.family = family;
+                if (!(m->vals[xv].is_input && m->input_nchw_direct)) st.reads.push_back(V[xv].pl.root);
+                if (cs.fused_residual) st.reads.push_back(V[cs.residual_value].pl.root);
+                st.writes = {V[yv].pl.root};
                 if (pair) {
                     done[sib] = true;
-                    m->steps.back().label += " + cmd#" + std::to_string(e.src_cmd[sib]);
+                    st.tail = " + cmd#" + std::to_string(e.src_cmd[sib]);
                 }
                 break;
             }
@@ -1253,6 +1387,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                 break;  // VIEW / ALIAS: placement only
         }
     }
+    label_steps(m);
     schedule_steps(m);
     return true;
 }
@@ -1425,6 +1560,7 @@ bool refine_in_context(AexrtYoloModel* m) {
             std::fprintf(stderr, "aexrt in-network %s: candidate %zu of %zu  %.2f us (first %.2f us)\n",
                          m->steps[t.step].label.c_str(), bi, t.cands.size(), ms[k][bi] * 1000.0f, ms[k][0] * 1000.0f);
     }
+    label_steps(m);
     drop_graph(m);
     return true;
 }
@@ -1532,6 +1668,74 @@ bool launch_postprocess(AexrtYoloModel* m, hipStream_t s) {
                      "yolo postprocess");
 }
 
+// The reference's prepared-plan counters (RT:29204-29285, 22913-23110) for this
+// step list: engine commands without a launch of their own, the fusions
+// performed, and the convs by the kernel family that runs them (the
+// reference's "tileflow" buckets: 1x1 convs; 3x3 convs on a spatial tile
+// kernel (halo window, wide, band); 3x3 dot4 convs (pack4: the dynamic int8
+// kernel); 3x3 implicit-GEMM convs (igemm, pg16, Winograd) with their
+// 40x40/20x20/10x10 and exact-shape sub-counts; fp16 MFMA convs).
+void compute_stats(AexrtYoloModel* m) {
+    PlanStats st{};
+    const Engine& e = m->eng;
+    std::vector<uint8_t> launched(e.manifest.command_count, 0);
+    std::vector<uint8_t> conv_kind(e.commands.size(), 0);  // 1 igemm, 2 spatial, 3 dot4
+    for (const Step& x : m->steps) {
+        if (x.cmd < 0) continue;
+        if (e.src_cmd[x.cmd] < launched.size()) launched[e.src_cmd[x.cmd]] = 1;
+        if (!x.family) continue;
+        const std::string f = x.family();
+        const uint8_t k = f.rfind("int8 dynamic", 0) == 0 ? 3
+                          : (f.rfind("halo", 0) == 0 || f.rfind("wide", 0) == 0 || f.rfind("stem", 0) == 0) ? 2
+                                                                                                          : 1;
+        conv_kind[x.cmd] = k;
+        if (!x.tail.empty()) {
+            st.paired_conv3x3 += desc_of(e.commands[x.cmd]).kernel_h == 3;
+            if (m->sibling[x.cmd] >= 0) conv_kind[m->sibling[x.cmd]] = k;
+        }
+    }
+    for (uint8_t v : launched) st.skipped += v ? 0u : 1u;
+    for (size_t ci = 0; ci < e.commands.size(); ++ci) {
+        const EngineCommand& c = e.commands[ci];
+        if (c.kind == kCmdConcat) {
+            bool copied = false;
+            for (const CopyJob& j : m->copies) copied = copied || j.cmd == (int)ci;
+            bool feeds_1x1 = false;
+            for (int u : m->vals[c.output].consumers)
+                feeds_1x1 = feeds_1x1 || (m->convs[u].is_conv && desc_of(e.commands[u]).kernel_h == 1);
+            st.late_concat_conv1x1 += !copied && feeds_1x1;
+        }
+        const ConvState& cs = m->convs[ci];
+        if (!cs.is_conv) continue;
+        st.tail_residual += cs.fused_residual;
+        st.native_fp16 += !is_int8_algorithm(cs.algorithm);
+        const AexrtConv2DDesc d = desc_of(c);
+        if (d.kernel_h == 1) {
+            ++st.conv1x1;
+            continue;
+        }
+        if (conv_kind[ci] == 2) {
+            ++st.spatial3x3;
+            continue;
+        }
+        if (conv_kind[ci] == 3) {
+            ++st.pack4_3x3;
+            continue;
+        }
+        ++st.igemm3x3;
+        st.igemm3x3_40 += d.out_h == 40;
+        st.igemm3x3_20 += d.out_h == 20;
+        st.igemm3x3_10 += d.out_h == 10;
+        const uint32_t ic = d.in_channels, oc = d.out_channels;
+        st.exact_40_64x64 += d.out_h == 40 && ic == 64 && oc == 64;
+        st.exact_20_64x64 += d.out_h == 20 && ic == 64 && oc == 64;
+        st.exact_10_128x128 += d.out_h == 10 && ic == 128 && oc == 128;
+        st.exact_20_128x64 += d.out_h == 20 && ic == 128 && oc == 64;
+        st.exact_10_256x64 += d.out_h == 10 && ic == 256 && oc == 64;
+    }
+    m->stats = st;
+}
+
 bool build_model(AexrtYoloModel* m) {
     if (!infer_dims(m)) return false;
     fuse_residuals(m);
@@ -1546,9 +1750,7 @@ bool build_model(AexrtYoloModel* m) {
             return fail(m, "command " + std::to_string(ci) + ": conv geometry not supported (groups/dilation)");
         cs.planned = (c.plan_flags & 1u) ? c.plan_kernel : c.planned_kernel;
         cs.algorithm = resolve_algorithm(m, ci, cs.planned);
-        // plan flag 16 (engine.py:85-96): the reference packs and convolves
-        // with per-16-input-channel scales (RT:4770-4923)
-        cs.pg16 = (c.plan_flags & kPlanFlagInt8PerGroup) != 0 && is_int8_algorithm(cs.algorithm);
+        set_int8_mode(m, ci);
     }
     if (!plan_memory(m, m->copies)) return false;
     mark_slot_readers(m);
@@ -1633,6 +1835,8 @@ bool build_model(AexrtYoloModel* m) {
     const char* prof = std::getenv("AEXRT_HIP_PROFILE");
     m->profile = prof && prof[0] == '1';
     setup_postprocess(m);
+    label_steps(m);
+    compute_stats(m);
     m->executable = true;
     return true;
 }
@@ -1741,6 +1945,42 @@ AexrtDevice* aexrt_hip_create_device(uint32_t device_index) {
 
 void aexrt_hip_destroy_device(AexrtDevice* device) { delete device; }
 
+// The reference's device entry points (native/aexrt.h:129-140) under their
+// own names, so that its ctypes binding loads this library unchanged.
+int aexrt_d3d12_probe(void) {
+    int count = 0;
+    return hipGetDeviceCount(&count) == hipSuccess && count > 0 ? 1 : 0;
+}
+AexrtDevice* aexrt_d3d12_create_device(uint32_t adapter_index) { return aexrt_hip_create_device(adapter_index); }
+void aexrt_d3d12_destroy_device(AexrtDevice* device) { aexrt_hip_destroy_device(device); }
+int aexrt_d3d12_get_capabilities(AexrtDevice* device, AexrtD3D12Capabilities* caps) {
+    if (!device || !caps || caps->struct_size < sizeof(AexrtD3D12Capabilities)) {
+        set_error("get_capabilities: bad arguments");
+        return 0;
+    }
+    const bool gfx950 = std::strncmp(device->props.gcnArchName, "gfx950", 6) == 0;
+    caps->struct_size = sizeof(AexrtD3D12Capabilities);
+    caps->highest_shader_model = 0;  // no D3D shader model: HIP code objects
+    caps->native_fp16_supported = 1;
+    caps->wave_mma_tier = gfx950 ? 1u : 0u;  // matrix cores (MFMA)
+    caps->dxc_available = 0;
+    caps->reserved[0] = caps->reserved[1] = caps->reserved[2] = 0;
+    return 1;
+}
+
+// Building from an ONNX file or a package directory is the compiler's job
+// (aexrt_amd.engine writes the .aexrt engine); the runtime loads engines.
+AexrtYoloModel* aexrt_yolo_compile_from_package(AexrtDevice* device, const char* package_path) {
+    (void)device, (void)package_path;
+    set_error("compile_from_package: not supported; build a .aexrt engine and call aexrt_yolo_load_engine");
+    return nullptr;
+}
+AexrtYoloModel* aexrt_yolo_compile_from_onnx(AexrtDevice* device, const char* onnx_path) {
+    (void)device, (void)onnx_path;
+    set_error("compile_from_onnx: not supported; build a .aexrt engine and call aexrt_yolo_load_engine");
+    return nullptr;
+}
+
 int aexrt_hip_get_capabilities(AexrtDevice* device, AexrtHipCapabilities* caps) {
     if (!device || !caps || caps->struct_size < sizeof(AexrtHipCapabilities)) {
         set_error("get_capabilities: bad arguments");
@@ -1764,13 +2004,15 @@ int aexrt_hip_validate_engine(const void* data, uint64_t nbytes) {
         set_error("validate_engine: null data");
         return 0;
     }
-    Engine e;
+    // the container rules, then the shape inference of the load (host only)
+    AexrtYoloModel m;
     std::string err;
-    if (!parse_engine(static_cast<const uint8_t*>(data), (size_t)nbytes, e, err)) {
+    if (!parse_engine(static_cast<const uint8_t*>(data), (size_t)nbytes, m.eng, err) ||
+        !expand_fused_commands(m.eng, err)) {
         set_error(err);
         return 0;
     }
-    return 1;
+    return infer_dims(&m) ? 1 : 0;
 }
 
 AexrtYoloModel* aexrt_yolo_load_engine_memory(AexrtDevice* device, const void* data, uint64_t nbytes) {
@@ -1815,8 +2057,62 @@ uint32_t aexrt_yolo_has_objectness(AexrtYoloModel* m) { return m ? m->eng.manife
 uint32_t aexrt_yolo_graph_node_count(AexrtYoloModel* m) { return m ? m->eng.manifest.graph_node_count : 0; }
 uint32_t aexrt_yolo_graph_value_count(AexrtYoloModel* m) { return m ? (uint32_t)m->eng.values.size() : 0; }
 uint32_t aexrt_yolo_constant_count(AexrtYoloModel* m) { return m ? m->eng.manifest.constant_count : 0; }
-uint32_t aexrt_yolo_prepared_command_count(AexrtYoloModel* m) { return m ? (uint32_t)m->eng.commands.size() : 0; }
+uint32_t aexrt_yolo_prepared_command_count(AexrtYoloModel* m) { return m ? m->eng.manifest.command_count : 0; }
 int aexrt_yolo_is_executable(AexrtYoloModel* m) { return m && m->executable ? 1 : 0; }
+
+// A model loaded from an .aexrt engine is a native graph with the YOLO
+// postprocess (AEXRT_YOLO_PACKAGE_NATIVE_D3D12_GRAPH, native/aexrt.h:53-57).
+uint32_t aexrt_yolo_package_mode(AexrtYoloModel* m) { return m ? 2u : 0u; }
+// Every command of an accepted engine runs (the loader refuses the others).
+uint32_t aexrt_yolo_supported_prepared_command_count(AexrtYoloModel* m) { return m ? m->eng.manifest.command_count : 0; }
+uint32_t aexrt_yolo_unsupported_prepared_command_count(AexrtYoloModel* m) { (void)m; return 0; }
+uint32_t aexrt_yolo_prepared_skipped_command_count(AexrtYoloModel* m) { return m ? m->stats.skipped : 0; }
+uint32_t aexrt_yolo_late_concat_conv1x1_fusion_count(AexrtYoloModel* m) { return m ? m->stats.late_concat_conv1x1 : 0; }
+// D3D12-only fusions this backend does not form: 0.
+uint32_t aexrt_yolo_concat_residual_conv1x1_fusion_count(AexrtYoloModel* m) { (void)m; return 0; }
+uint32_t aexrt_yolo_paired_conv3x3_fusion_count(AexrtYoloModel* m) { return m ? m->stats.paired_conv3x3 : 0; }
+uint32_t aexrt_yolo_c2f_bottleneck_superblock_count(AexrtYoloModel* m) { (void)m; return 0; }
+uint32_t aexrt_yolo_c2f_tail_residual_fusion_count(AexrtYoloModel* m) { return m ? m->stats.tail_residual : 0; }
+uint32_t aexrt_yolo_head_fusion_enabled(AexrtYoloModel* m) { (void)m; return 0; }
+uint32_t aexrt_yolo_head_final_conv_fusion_enabled(AexrtYoloModel* m) { (void)m; return 0; }
+uint32_t aexrt_yolo_tileflow_conv1x1_count(AexrtYoloModel* m) { return m ? m->stats.conv1x1 : 0; }
+uint32_t aexrt_yolo_tileflow_3x3_spatial_count(AexrtYoloModel* m) { return m ? m->stats.spatial3x3 : 0; }
+uint32_t aexrt_yolo_tileflow_3x3_pack4_count(AexrtYoloModel* m) { return m ? m->stats.pack4_3x3 : 0; }
+uint32_t aexrt_yolo_tileflow_3x3_pack8_count(AexrtYoloModel* m) { (void)m; return 0; }
+uint32_t aexrt_yolo_tileflow_3x3_implicit_gemm_count(AexrtYoloModel* m) { return m ? m->stats.igemm3x3 : 0; }
+uint32_t aexrt_yolo_tileflow_3x3_implicit_gemm_40x40_count(AexrtYoloModel* m) { return m ? m->stats.igemm3x3_40 : 0; }
+uint32_t aexrt_yolo_tileflow_3x3_implicit_gemm_20x20_count(AexrtYoloModel* m) { return m ? m->stats.igemm3x3_20 : 0; }
+uint32_t aexrt_yolo_tileflow_3x3_implicit_gemm_10x10_count(AexrtYoloModel* m) { return m ? m->stats.igemm3x3_10 : 0; }
+uint32_t aexrt_yolo_tileflow_3x3_exact_40x40_64x64_count(AexrtYoloModel* m) { return m ? m->stats.exact_40_64x64 : 0; }
+uint32_t aexrt_yolo_tileflow_3x3_exact_20x20_64x64_count(AexrtYoloModel* m) { return m ? m->stats.exact_20_64x64 : 0; }
+uint32_t aexrt_yolo_tileflow_3x3_exact_10x10_128x128_count(AexrtYoloModel* m) { return m ? m->stats.exact_10_128x128 : 0; }
+uint32_t aexrt_yolo_tileflow_3x3_exact_20x20_128x64_count(AexrtYoloModel* m) { return m ? m->stats.exact_20_128x64 : 0; }
+uint32_t aexrt_yolo_tileflow_3x3_exact_10x10_256x64_count(AexrtYoloModel* m) { return m ? m->stats.exact_10_256x64 : 0; }
+uint32_t aexrt_yolo_tileflow_native_fp16_count(AexrtYoloModel* m) { return m ? m->stats.native_fp16 : 0; }
+
+// Runs are synchronous (no frames in flight): like the reference with one
+// pipeline frame (native/aexrt.h:412-416), flushing yields 0 detections.
+int aexrt_yolo_flush_pipeline(AexrtYoloModel* m, AexrtYoloDetection* detections, uint32_t max_detections,
+                              uint32_t* out_detection_count) {
+    if (!m || !detections || !out_detection_count || max_detections == 0) return 0;
+    *out_detection_count = 0;
+    return 1;
+}
+
+// No shader or pipeline objects are compiled at load (the HIP code objects
+// are part of the library): the exported cache is the valid empty one, a
+// 16-byte header (version 1, no shader or PSO records, flags 1), as the
+// reference builds it with no entries (RT:31062-31101).
+uint64_t aexrt_yolo_pipeline_cache_size(AexrtYoloModel* m) { return m ? 16u : 0u; }
+int aexrt_yolo_export_pipeline_cache(AexrtYoloModel* m, void* output, uint64_t output_nbytes) {
+    if (!m || !output || output_nbytes < 16) return 0;
+    const uint32_t header[4] = {1u, 0u, 0u, 1u};
+    std::memcpy(output, header, sizeof(header));
+    return 1;
+}
+uint32_t aexrt_yolo_dxil_cache_hit_count(AexrtYoloModel* m) { (void)m; return 0; }
+uint32_t aexrt_yolo_shader_cache_hit_count(AexrtYoloModel* m) { (void)m; return 0; }
+uint32_t aexrt_yolo_pso_cache_hit_count(AexrtYoloModel* m) { (void)m; return 0; }
 
 void* aexrt_yolo_input_device_ptr(AexrtYoloModel* m) { return m ? m->input_dev : nullptr; }
 
@@ -1940,6 +2236,15 @@ int aexrt_yolo_debug_value(AexrtYoloModel* m, uint32_t value_id, float* out, uin
     return copy_value_to_host(m, v, out, elements) ? 1 : 0;
 }
 
+// The reference reads back a D3D12 arena page (native/aexrt.h:403); values
+// here live in roots of one NHWC arena, read through aexrt_yolo_debug_value.
+int aexrt_yolo_debug_page(AexrtYoloModel* m, uint32_t page_id, float* out, uint64_t elements) {
+    (void)page_id, (void)out, (void)elements;
+    if (m) m->last_error = "debug_page: no arena pages in this runtime; use aexrt_yolo_debug_value";
+    set_error("debug_page: no arena pages in this runtime; use aexrt_yolo_debug_value");
+    return 0;
+}
+
 int aexrt_yolo_value_info(AexrtYoloModel* m, uint32_t value_id, uint32_t* out4) {
     if (!m || !out4 || value_id >= m->vals.size()) return 0;
     const auto& x = m->vals[value_id];
@@ -2032,27 +2337,45 @@ int aexrt_yolo_override_conv_algorithm(AexrtYoloModel* m, uint32_t engine_comman
     }
     if (!ok) return fail(m, "override: algorithm not applicable to this command") ? 1 : 0;
     if (!check_hip(hipStreamSynchronize(m->stream), "override sync")) return fail(m, last_error()) ? 1 : 0;
-    const uint32_t previous = m->convs[command_index].algorithm;
-    m->convs[command_index].algorithm = kernel;
-    if (!prepare_conv_weights(m, command_index)) {
-        m->convs[command_index].algorithm = previous;
-        prepare_conv_weights(m, command_index);
+    // Everything an override changes is kept so that a failure restores the
+    // model as it was (weights stay allocated until the model is freed).
+    const ConvState saved = m->convs[command_index];
+    std::vector<std::pair<size_t, ConvState>> saved_pairs;
+    for (size_t ci = 0; ci < m->sibling.size(); ++ci)
+        if (m->sibling[ci] >= 0 && (ci == command_index || m->sibling[ci] == (int)command_index))
+            saved_pairs.emplace_back(ci, m->convs[ci]);
+    auto restore = [&](const std::string& why) {
+        const std::string msg = "override: " + why;
+        m->convs[command_index] = saved;
+        for (const auto& [ci, cs] : saved_pairs) m->convs[ci] = cs;
+        drop_graph(m);
+        mark_slot_readers(m);
+        if (!build_steps(m, m->copies) || (m->autotune && !refine_in_context(m))) {
+            m->executable = false;
+            fail(m, msg + "; the model could not be restored and is no longer executable");
+            return 0;
+        }
+        compute_stats(m);
+        fail(m, msg);
         return 0;
-    }
+    };
+    ConvState& cs = m->convs[command_index];
+    cs.algorithm = kernel;
+    set_int8_mode(m, command_index);
+    if (!prepare_conv_weights(m, command_index)) return restore(m->last_error);
     // a sibling pair with this conv gets its joint weights from the new ones
     // (it runs as two launches while either conv is not an fp16 direct one)
-    for (size_t ci = 0; ci < m->sibling.size(); ++ci)
-        if ((ci == command_index || m->sibling[ci] == (int)command_index) && m->sibling[ci] >= 0 &&
-            !pair_conv_weights(m, ci))
-            return 0;
+    for (const auto& sp : saved_pairs)
+        if (!pair_conv_weights(m, sp.first)) return restore(m->last_error);
     drop_graph(m);
-    const std::string prefix = "cmd " + std::to_string(command_index) + " ";
-    for (auto it = m->refined.begin(); it != m->refined.end();)
-        it = it->first.compare(0, prefix.size(), prefix) == 0 ? m->refined.erase(it) : std::next(it);
     mark_slot_readers(m);
-    // placement does not depend on the kernel choice: rebuild the launch list
-    if (!build_steps(m, m->copies)) return 0;
-    return !m->autotune || refine_in_context(m) ? 1 : 0;
+    // placement does not depend on the kernel choice: rebuild the launch list;
+    // the other convs keep their measured choices (keyed by command, algorithm
+    // and shape), and so does this one when it returns to an earlier algorithm
+    if (!build_steps(m, m->copies)) return restore(m->last_error);
+    if (m->autotune && !refine_in_context(m)) return restore(m->last_error);
+    compute_stats(m);
+    return 1;
 }
 
 void aexrt_yolo_destroy(AexrtYoloModel* m) { free_model(m); }

@@ -21,6 +21,7 @@ RESIDUAL = 2
 OUT_F32 = 4
 IN_NCHW_F32 = 8
 INT8_PG16 = 16
+INT8_DYNAMIC = 32
 
 SRC_RAW_F32 = 0
 SRC_RAW_F16 = 1

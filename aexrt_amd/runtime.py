@@ -79,6 +79,34 @@ class NativeHipYoloModel:
         return int(self.lib.aexrt_yolo_prepared_command_count(self.model))
 
     @property
+    def package_mode(self) -> int:
+        return int(self.lib.aexrt_yolo_package_mode(self.model))
+
+    def counter(self, name: str) -> int:
+        """One of the reference's prepared-plan counters (native/aexrt.h:313-385), by the name
+        after ``aexrt_yolo_`` (e.g. ``"tileflow_conv1x1_count"``)."""
+        if name not in _lib.PLAN_COUNTERS:
+            raise KeyError(name)
+        return int(getattr(self.lib, "aexrt_yolo_" + name)(self.model))
+
+    def counters(self) -> dict:
+        return {name: self.counter(name) for name in _lib.PLAN_COUNTERS}
+
+    def flush_pipeline(self, max_detections: int = 100) -> list:
+        dets = (YoloDetection * max(1, max_detections))()
+        count = ctypes.c_uint32(0)
+        if not self.lib.aexrt_yolo_flush_pipeline(self.model, dets, max(1, max_detections), ctypes.byref(count)):
+            raise RuntimeError(f"flush_pipeline failed: {self.last_error()}")
+        return [(d.x1, d.y1, d.x2, d.y2, d.score, int(d.class_id)) for d in dets[: count.value]]
+
+    def pipeline_cache(self) -> bytes:
+        n = int(self.lib.aexrt_yolo_pipeline_cache_size(self.model))
+        buf = ctypes.create_string_buffer(max(n, 1))
+        if n and not self.lib.aexrt_yolo_export_pipeline_cache(self.model, buf, n):
+            raise RuntimeError(f"export_pipeline_cache failed: {self.last_error()}")
+        return buf.raw[:n]
+
+    @property
     def capabilities(self) -> dict:
         caps = DeviceCapabilities()
         caps.struct_size = ctypes.sizeof(DeviceCapabilities)

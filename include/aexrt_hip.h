@@ -92,6 +92,12 @@ typedef struct AexrtHipTensorView {
                                        * (plan flag 16, native/aexrt_d3d12_runtime.cpp:
                                        * 4770-4923): slot g of x->amax_slots is group g's
                                        * amax (the reference's amax[1 + g]); no acc_out */
+#define AEXRT_HIP_CONV_INT8_DYNAMIC 32u /* int8 with the scale computed in the kernel per output
+                                         * position and 4-channel input group (the reference's
+                                         * fallback int8 conv, native/aexrt_d3d12_runtime.cpp:
+                                         * 2952-3115, dispatched for inputs of fewer than 4096
+                                         * elements, RT:21478-21479); x->amax_slots is not read;
+                                         * no acc_out, not with PG16 */
 
 /* Weight source layouts accepted by aexrt_hip_pack_conv_weight: the
  * reference's packed layouts (src/aexrt/engine.py:59-71) plus raw constants. */
@@ -185,6 +191,18 @@ int aexrt_hip_conv2d(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t f
                      const AexrtHipTensorView* x, const void* weight, const float* w_scale,
                      const float* bias, const AexrtHipTensorView* residual,
                      const AexrtHipTensorView* y, int32_t* acc_out, void* stream);
+
+/* a15 on the GPU: fp32 direct convolution of dense NCHW tensors, the
+ * reference's aexrt_d3d12_conv2d_float32 / aexrt_d3d12_conv2d_silu_float32
+ * (native/aexrt.h:175-189; shader native/aexrt_d3d12_runtime.cpp:1554-1622)
+ * with the arithmetic of its CPU path cpu_conv2d (RT:20552-20580): acc =
+ * bias[oc], then += x*w over (input channel of the group, ky, kx), taps
+ * outside the input skipped, each multiply and add rounded on its own;
+ * flags AEXRT_HIP_CONV_SILU: acc / (1 + exp(-acc)).  weight [OC][C/groups]
+ * [KH][KW] fp32; x [N][C][H][W]; y [N][OC][OH][OW]; any stride, padding,
+ * dilation and groups. */
+int aexrt_hip_conv2d_f32(const AexrtConv2DDesc* desc, uint32_t flags, const float* x, const float* weight,
+                         const float* bias, float* y, void* stream);
 
 /* a6, reference form: the pg16 int8 conv on the reference's own operands,
  * native/aexrt_d3d12_runtime.cpp:4770-4923 (dispatch 24152-24258): packed =
@@ -339,11 +357,40 @@ AexrtDevice* aexrt_hip_create_device(uint32_t device_index);
 void aexrt_hip_destroy_device(AexrtDevice* device);
 int aexrt_hip_get_capabilities(AexrtDevice* device, AexrtHipCapabilities* caps);
 
-/* native/aexrt.h:275: load a .aexrt engine (sections 1-6; CRC-checked, plan
- * and packed weights cross-checked, fail closed).  The _memory variant takes
- * the engine bytes directly. */
+/* native/aexrt.h:29-37, the struct the reference's wrapper passes. */
+typedef struct AexrtD3D12Capabilities {
+    uint32_t struct_size;
+    uint32_t highest_shader_model; /* 0: no D3D shader model (HIP code objects)   */
+    uint32_t native_fp16_supported; /* 1                                          */
+    uint32_t wave_mma_tier;         /* 1 with matrix cores (gfx950 MFMA), else 0  */
+    uint32_t dxc_available;         /* 0                                          */
+    uint32_t reserved[3];
+} AexrtD3D12Capabilities;
+
+/* The reference's device entry points under their own names
+ * (native/aexrt.h:129-140; bound by src/aexrt/cpp_runtime.py:543-548), so
+ * its ctypes wrapper loads this library with only the path changed:
+ * probe = 1 when a HIP device exists; create/destroy = the aexrt_hip_ ones
+ * (adapter_index = HIP device index). */
+int aexrt_d3d12_probe(void);
+AexrtDevice* aexrt_d3d12_create_device(uint32_t adapter_index);
+void aexrt_d3d12_destroy_device(AexrtDevice* device);
+int aexrt_d3d12_get_capabilities(AexrtDevice* device, AexrtD3D12Capabilities* capabilities);
+
+/* native/aexrt.h:271-281: building from a package directory or an ONNX file
+ * is the compiler's job here (aexrt_amd.engine writes the .aexrt engine):
+ * both return NULL with a diagnostic; load engines with
+ * aexrt_yolo_load_engine. */
+AexrtYoloModel* aexrt_yolo_compile_from_package(AexrtDevice* device, const char* package_path);
+AexrtYoloModel* aexrt_yolo_compile_from_onnx(AexrtDevice* device, const char* onnx_path);
+
+/* native/aexrt.h:275: load a .aexrt engine (sections 1-9 required, 10-11
+ * accepted; the reference loader's record rules, RT:17560-18593, CRC per
+ * section; fail closed).  The _memory variant takes the engine bytes
+ * directly. */
 AexrtYoloModel* aexrt_yolo_load_engine(AexrtDevice* device, const char* engine_path);
-/* Parses and validates engine bytes without a device (1 = loadable). */
+/* Parses and validates engine bytes without a device, including the shape
+ * checks of the load (1 = loadable). */
 int aexrt_hip_validate_engine(const void* data, uint64_t nbytes);
 AexrtYoloModel* aexrt_yolo_load_engine_memory(AexrtDevice* device, const void* data, uint64_t nbytes);
 
@@ -358,8 +405,70 @@ uint32_t aexrt_yolo_has_objectness(AexrtYoloModel* model);
 uint32_t aexrt_yolo_graph_node_count(AexrtYoloModel* model);
 uint32_t aexrt_yolo_graph_value_count(AexrtYoloModel* model);
 uint32_t aexrt_yolo_constant_count(AexrtYoloModel* model);
-uint32_t aexrt_yolo_prepared_command_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_prepared_command_count(AexrtYoloModel* model);  /* engine-file commands */
 int aexrt_yolo_is_executable(AexrtYoloModel* model);
+
+/* native/aexrt.h:301: 2 (AEXRT_YOLO_PACKAGE_NATIVE_D3D12_GRAPH) for an
+ * engine, the reference's value for .aexrt models (RT:17627). */
+uint32_t aexrt_yolo_package_mode(AexrtYoloModel* model);
+/* native/aexrt.h:313-385, the prepared-plan counters (RT:29204-29285,
+ * 22913-23110), for what this runtime does with the engine's commands:
+ *   supported = every command (the loader refuses engines it cannot run),
+ *   unsupported = 0;
+ *   skipped = engine commands with no launch of their own (views, aliases,
+ *   concats placed in place, residual adds in a conv epilogue, the 2nd/3rd
+ *   SPPF pools, the second conv of a paired launch);
+ *   late_concat_conv1x1 = concats placed in place whose output a 1x1 conv
+ *   reads whole; paired_conv3x3 = pairs of 3x3 convs of one input computed
+ *   by one launch; c2f_tail_residual = residual adds done in a conv
+ *   epilogue; concat_residual_conv1x1, c2f_bottleneck_superblock and the
+ *   head fusions = 0 (D3D12 fusions this backend does not form);
+ *   tileflow_* = convs by the kernel family that runs them: conv1x1 = 1x1
+ *   convs; 3x3_spatial = 3x3 convs on a spatial tile kernel (halo window,
+ *   wide, band); 3x3_pack4 = 3x3 convs on the dynamic int8 dot4 kernel;
+ *   3x3_pack8 = 0; 3x3_implicit_gemm = 3x3 convs on the implicit-GEMM,
+ *   pg16 or Winograd kernels, with 40x40 / 20x20 / 10x10 and exact-shape
+ *   sub-counts; native_fp16 = convs on fp16 MFMA kernels. */
+uint32_t aexrt_yolo_supported_prepared_command_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_unsupported_prepared_command_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_prepared_skipped_command_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_late_concat_conv1x1_fusion_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_concat_residual_conv1x1_fusion_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_paired_conv3x3_fusion_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_c2f_bottleneck_superblock_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_c2f_tail_residual_fusion_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_head_fusion_enabled(AexrtYoloModel* model);
+uint32_t aexrt_yolo_head_final_conv_fusion_enabled(AexrtYoloModel* model);
+uint32_t aexrt_yolo_tileflow_conv1x1_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_tileflow_3x3_spatial_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_tileflow_3x3_pack4_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_tileflow_3x3_pack8_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_tileflow_3x3_implicit_gemm_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_tileflow_3x3_implicit_gemm_40x40_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_tileflow_3x3_implicit_gemm_20x20_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_tileflow_3x3_implicit_gemm_10x10_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_tileflow_3x3_exact_40x40_64x64_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_tileflow_3x3_exact_20x20_64x64_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_tileflow_3x3_exact_10x10_128x128_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_tileflow_3x3_exact_20x20_128x64_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_tileflow_3x3_exact_10x10_256x64_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_tileflow_native_fp16_count(AexrtYoloModel* model);
+
+/* native/aexrt.h:412-421: runs are synchronous (no frame in flight), so a
+ * flush returns 1 with 0 detections, as the reference does with one
+ * pipeline frame; 0 on a null argument or max_detections == 0. */
+int aexrt_yolo_flush_pipeline(AexrtYoloModel* model, AexrtYoloDetection* detections, uint32_t max_detections,
+                              uint32_t* out_detection_count);
+
+/* native/aexrt.h:469-484: no shader or pipeline objects are compiled at
+ * load, so the exported cache is the valid empty one (16 bytes: version 1,
+ * 0 shader and 0 PSO records, flags 1, as RT:31062-31101 writes it with no
+ * entries) and the hit counts are 0. */
+uint64_t aexrt_yolo_pipeline_cache_size(AexrtYoloModel* model);
+int aexrt_yolo_export_pipeline_cache(AexrtYoloModel* model, void* output, uint64_t output_nbytes);
+uint32_t aexrt_yolo_dxil_cache_hit_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_shader_cache_hit_count(AexrtYoloModel* model);
+uint32_t aexrt_yolo_pso_cache_hit_count(AexrtYoloModel* model);
 
 /* native/aexrt.h:391-398: one inference from a host fp32 CHW input.  The
  * network and the YOLO postprocess of output0 (decode + confidence filter,
@@ -393,6 +502,9 @@ void* aexrt_yolo_input_ptr(AexrtYoloModel* model, uint64_t* out_elements);
  * logical NCHW (or [N, C, A]) order. */
 int aexrt_yolo_debug_output(AexrtYoloModel* model, float* out, uint64_t elements);
 int aexrt_yolo_debug_value(AexrtYoloModel* model, uint32_t value_id, float* out, uint64_t elements);
+/* native/aexrt.h:403 reads a D3D12 arena page; values here live in one NHWC
+ * arena read through debug_value: returns 0 with a diagnostic. */
+int aexrt_yolo_debug_page(AexrtYoloModel* model, uint32_t page_id, float* out, uint64_t elements);
 /* Logical dims of a value: out4 = {N, C, H, W} ({N, C, A, 1} for rank 3);
  * returns the rank, 0 when the value has no device storage. */
 int aexrt_yolo_value_info(AexrtYoloModel* model, uint32_t value_id, uint32_t* out4);

@@ -5,7 +5,9 @@ direct convolution on the rest, storing every intermediate tensor as fp16
 like the device path (the network output stays fp32).  Each int8 conv is
 the reference chain on the fp16-stored input: per-tensor amax over the whole
 tensor (all images), RNE quantization with 127/amax, exact int32
-accumulation, dequant float(acc)*amax/127*w_scale + bias, SiLU.
+accumulation, dequant float(acc)*amax/127*w_scale + bias, SiLU -- or, for
+an input of fewer than 4096 elements, the reference's dynamic fallback
+(per position and 4-channel group scales computed in the conv).
 """
 from __future__ import annotations
 
@@ -13,8 +15,12 @@ from typing import Dict, Iterable, Optional
 
 import numpy as np
 
-from . import (amax, amax_slots, conv_desc, conv_int8_acc, conv_int8_epilogue, conv_int8_pg, cpu_conv2d, maxpool,
-               quant_pack, quantize, resize_nearest, round_f16, weight_quant)
+from . import (amax, amax_slots, conv_desc, conv_int8_acc, conv_int8_dynamic, conv_int8_epilogue, conv_int8_pg,
+               cpu_conv2d, maxpool, quant_pack, quantize, resize_nearest, round_f16, weight_quant)
+
+# The reference prequantizes (amax + pack) only inputs of at least this many
+# elements (RT:21478-21479); smaller int8 inputs take the dynamic kernel.
+PREQUANT_MIN_ELEMENTS = 4096
 
 
 def _silu_map(graph):
@@ -50,6 +56,12 @@ def conv_layer(x: np.ndarray, w: np.ndarray, b: np.ndarray, attrs: dict, *, int8
     p = int(attrs.get("pads", [0, 0, 0, 0])[0])
     desc = conv_desc(n, c, h, wd, int(w.shape[0]), k, s, p)
     bias = round_f16(b)
+    if int8 and x.size < PREQUANT_MIN_ELEMENTS:
+        # RT:21478-21479: an input of fewer than 4096 elements is not
+        # prequantized; the conv quantizes per (position, 4 channels) itself
+        # (RT:2952-3115), pg16 or not
+        qw, ws = weight_quant(w, fp16_round=True)
+        return conv_int8_dynamic(x, qw, desc, ws, bias, silu)
     if int8 and pg16:
         slots = amax_slots(x)
         packed = quant_pack(x, slots, per_group=True)

@@ -351,3 +351,50 @@ def test_mutated_engines_are_refused_like_the_reference(name):
     ok, _ = reference_accepts(data)
     assert not ok
     assert not _validate(data)
+
+
+def _yolo_engine_sections(imgsz=160):
+    g = build_yolov8n(batch=1, imgsz=imgsz, seed=4)
+    return E.engine_sections(g, precision="fp16", classes=80)
+
+
+def _mutate_command(sections, kind: str, fn):
+    """Sections with the params of the first command of `kind` rewritten by fn(params) (same count)."""
+    body = bytearray(sections[E.SECTION_COMMANDS])
+    n = struct.unpack_from("<I", body, 0)[0]
+    at = 8
+    for _ in range(n):
+        k, _, ni, npar, _, _ = struct.unpack_from("<6I", body, at)
+        p_at = at + 24 + 4 * ni
+        if k == E.COMMAND_KIND[kind]:
+            params = list(struct.unpack_from(f"<{npar}I", body, p_at))
+            struct.pack_into(f"<{npar}I", body, p_at, *fn(params))
+            out = dict(sections)
+            out[E.SECTION_COMMANDS] = bytes(body)
+            return out
+        at = p_at + 4 * npar
+    raise AssertionError(f"no {kind} command")
+
+
+def _with(params, **changes):
+    out = list(params)
+    for idx, v in changes.items():
+        out[int(idx[1:])] = v
+    return out
+
+
+@pytest.mark.parametrize("kind,change", [
+    ("RESIZE", dict(i1=64)),       # more channels than its input: the kernel would overrun the output root
+    ("RESIZE", dict(i0=3)),        # more images than its input
+    ("RESIZE", dict(i2=7)),        # input height that is not the input's
+    ("MAXPOOL", dict(i0=2)),       # batch that is not the input's
+    ("MAXPOOL", dict(i4=9)),       # output rows the 5x5/s1/p2 window does not produce
+])
+def test_loader_refuses_resize_and_maxpool_params_that_disagree_with_their_input(kind, change):
+    """infer_dims checks RESIZE / MAXPOOL params against the input before anything is sized from
+    them (aexrt_hip_validate_engine runs the same host-side shape inference as a load)."""
+    base = _yolo_engine_sections()
+    assert _validate(E.build_container(base)), _lib.last_error()
+    bad = _mutate_command(base, kind, lambda p: _with(p, **change))
+    assert not _validate(E.build_container(bad))
+    assert kind in _lib.last_error()

@@ -263,6 +263,86 @@ def test_dynamic_fallback_exact_when_inputs_are_grid_values():
     np.testing.assert_allclose(y, ref, rtol=1e-6)
 
 
+def _unpack_nc4(packed, n, c, h, w):
+    """NC/4HW4 uint32 words -> int8 NCHW (channel 4*icg + j in byte j of word (n, icg, pos))."""
+    b = np.asarray(packed, np.uint32).reshape(n, c // 4, h * w).view(np.uint8).reshape(n, c // 4, h * w, 4)
+    return b.transpose(0, 1, 3, 2).reshape(n, c, h, w).view(np.int8)
+
+
+@pytest.mark.parametrize("k,s", [(1, 1), (3, 1), (3, 2)])
+def test_pg16_equals_float64_group_dequant_with_distinct_group_amax(k, s):
+    """or_conv_int8_pg against the closed form of per-16-channel activation scales: each channel's
+    quantized value times amax[1 + c/16]/127, each weight times its scale, a float64 convolution.
+    The four groups have distinct maxima, so a wrong group index (c/4, c/16 + 1, ...) fails."""
+    rng = np.random.default_rng(21)
+    n, c, h, w, oc = 2, 64, 7, 6, 16
+    x = rng.standard_normal((n, c, h, w)).astype(np.float32)
+    for g, m in enumerate((0.25, 3.0, 1.0, 9.5)):
+        x[:, 16 * g:16 * (g + 1)] *= m / np.abs(x[:, 16 * g:16 * (g + 1)]).max()
+    wt = rng.standard_normal((oc, c, k, k)).astype(np.float32)
+    b = rng.uniform(-0.1, 0.1, oc).astype(np.float32)
+    desc = O.conv_desc(n, c, h, w, oc, k, s, k // 2)
+    qw, ws = O.weight_quant(wt, fp16_round=False)
+    slots = O.amax_slots(x)
+    group_amax = slots.view(np.float32)[1:]
+    assert len(set(group_amax.tolist())) == 4
+    packed = O.quant_pack(x, slots, per_group=True)
+    y = O.conv_int8_pg(packed, qw, desc, slots, ws, b, silu=False)
+    qa = _unpack_nc4(packed, n, c, h, w).astype(np.float64)
+    xa = qa * (np.repeat(group_amax.astype(np.float64), 16) / 127.0)[None, :, None, None]
+    wa = qw.astype(np.float64) * ws.astype(np.float64)[:, None, None, None]
+    import torch
+    ref = torch.nn.functional.conv2d(torch.from_numpy(xa), torch.from_numpy(wa), torch.from_numpy(b.astype(np.float64)),
+                                     stride=s, padding=k // 2).numpy()
+    np.testing.assert_allclose(y, ref, rtol=2e-5, atol=2e-5 * np.abs(ref).max())
+    # the per-tensor scale for every group is far off (planted mistake)
+    xt = qa * (float(group_amax.max()) / 127.0)
+    wrong = torch.nn.functional.conv2d(torch.from_numpy(xt), torch.from_numpy(wa), stride=s, padding=k // 2).numpy()
+    assert np.abs(wrong - ref).max() > 100 * np.abs(y - ref).max()
+
+
+@pytest.mark.parametrize("k,s", [(1, 1), (3, 1), (3, 2)])
+def test_dynamic_fallback_exact_with_power_of_two_group_scales(k, s):
+    """Every 4-channel group holds integers times a group-specific 2^-e with 127 * 2^-e present in
+    each of its windows (one pixel for 1x1, the 3x3 taps otherwise): 127/amax and amax/127 are
+    exact powers of two, quantization is exact, and the dynamic conv equals the float64
+    convolution of x.  A scale shared across groups, or taken over the wrong taps, is inexact."""
+    rng = np.random.default_rng(22)
+    n, c, h, w, oc = 1, 16, 6, 5, 8
+    e = np.array([0, 3, 1, 5])  # group g values are ints * 2^-e[g]
+    q = rng.integers(-126, 127, (n, c, h, w)).astype(np.float64)
+    q[:, 0::4] = 127.0  # channel 4g holds the group's maximum at every position
+    x = (q * (2.0 ** -np.repeat(e, 4))[None, :, None, None]).astype(np.float32)
+    qw = rng.integers(-127, 128, (oc, c, k, k), dtype=np.int8)
+    ws = np.full(oc, 0.5, np.float32)
+    b = np.zeros(oc, np.float32)
+    desc = O.conv_desc(n, c, h, w, oc, k, s, k // 2)
+    y = O.conv_int8_dynamic(x, qw, desc, ws, b, silu=False)
+    import torch
+    ref = 0.5 * torch.nn.functional.conv2d(torch.from_numpy(x.astype(np.float64)),
+                                           torch.from_numpy(qw.astype(np.float64)), stride=s, padding=k // 2).numpy()
+    np.testing.assert_allclose(y, ref, rtol=1e-6, atol=1e-6)
+
+
+def test_network_int8_convs_below_4096_elements_take_the_dynamic_path():
+    """oracle.network follows RT:21478-21479: an int8 conv whose input has fewer than 4096 elements
+    is the dynamic conv, at 4096 and above the per-tensor chain."""
+    from oracle import network as ON
+    rng = np.random.default_rng(23)
+    w = rng.standard_normal((16, 32, 3, 3)).astype(np.float32)
+    b = rng.uniform(-0.1, 0.1, 16).astype(np.float32)
+    attrs = dict(strides=[1, 1], pads=[1, 1, 1, 1])
+    for shape, dynamic in (((1, 32, 11, 11), True), ((1, 32, 8, 16), False), ((2, 32, 8, 8), False)):
+        x = O.round_f16(rng.standard_normal(shape).astype(np.float32))
+        y = ON.conv_layer(x, w, b, attrs, int8=True, silu=True)
+        desc = O.conv_desc(*shape, 16, 3, 1, 1)
+        qw, ws = O.weight_quant(w, fp16_round=True)
+        dyn = O.conv_int8_dynamic(x, qw, desc, ws, O.round_f16(b), True)
+        pt = O.w8a8_conv(x, w, b, desc, silu=True, fp16_engine=True)[-1]
+        assert np.array_equal(y, dyn if dynamic else pt), shape
+        assert not np.array_equal(dyn, pt)
+
+
 # ---------------------------------------------------------------- a15 cpu conv
 @pytest.mark.parametrize("k,s,p", [(1, 1, 0), (3, 1, 1), (3, 2, 1), (6, 2, 2)])
 def test_cpu_conv2d_against_torch(k, s, p):

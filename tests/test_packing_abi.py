@@ -30,6 +30,36 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
 
 
+def test_library_exports_every_symbol_the_reference_wrapper_binds():
+    """NativeCppYoloModel._configure (src/aexrt/cpp_runtime.py:543-662) binds these names; a
+    missing one makes the reference's own wrapper fail on load."""
+    names = (GOLDEN / "reference_ffi_symbols.txt").read_text().split()
+    assert len(names) == 54
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_reference_compile_entry_points_refuse_with_a_diagnostic():
+    L = _lib.lib()
+    assert L.aexrt_yolo_compile_from_onnx(None, b"model.onnx") is None
+    assert "not supported" in _lib.last_error()
+    assert L.aexrt_yolo_compile_from_package(None, b"pkg") is None
+    assert "aexrt_yolo_load_engine" in _lib.last_error()
+
+
+def test_model_queries_on_null_model_are_zero():
+    """Every counter the reference's wrapper reads answers 0 for a null model, as in RT:30676-30810."""
+    L = _lib.lib()
+    for name in _lib.PLAN_COUNTERS:
+        assert getattr(L, "aexrt_yolo_" + name)(None) == 0, name
+    assert L.aexrt_yolo_package_mode(None) == 0
+    assert L.aexrt_yolo_pipeline_cache_size(None) == 0
+    det = (_lib.YoloDetection * 4)()
+    cnt = ctypes.c_uint32(7)
+    assert L.aexrt_yolo_flush_pipeline(None, det, 4, ctypes.byref(cnt)) == 0
+
+
 def test_library_loads_and_reports_abi():
     assert _lib.lib().aexrt_hip_abi_version() == 2
 
