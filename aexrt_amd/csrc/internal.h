@@ -54,4 +54,13 @@ DynConvParams dynamic_params(const ConvParams& p);
 // elements to the dynamic kernel (native/aexrt_d3d12_runtime.cpp:21478-21479).
 constexpr uint64_t kInt8PrequantMinElements = 4096;
 
+// The reference's int8 conv command on a plain fp16 NHWC input (dynamic
+// below 4096 elements, else amax into `scratch` + pg16 or per-tensor conv);
+// scratch holds int8_command_scratch_words(C) uint32 (unused by the dynamic
+// kernel).
+uint64_t int8_command_scratch_words(uint32_t in_channels);
+bool run_int8_command(const AexrtConv2DDesc& d, uint32_t algorithm, uint32_t flags, const AexrtHipTensorView& x,
+                      const void* weight, const float* w_scale, const float* bias, const AexrtHipTensorView* residual,
+                      const AexrtHipTensorView& y, uint32_t* scratch, uint64_t scratch_words, hipStream_t stream);
+
 }  // namespace aexrt

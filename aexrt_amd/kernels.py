@@ -281,6 +281,18 @@ def conv2d(pc: PreparedConv, x, y, *, flags: int = SILU, x_slots=None, y_slots=N
         _ptr(acc_out), _stream(stream)), "conv2d")
 
 
+def conv2d_int8(pc: PreparedConv, x, y, *, flags: int = SILU, residual=None, stream=None) -> None:
+    """The reference's int8 conv command on a plain fp16 NHWC input: dynamic below 4096 input
+    elements, else the input's amax (strips with INT8_PG16) then the int8 conv."""
+    d = ConvDesc.from_params(pc.params)
+    xv, yv = view(x), view(y)
+    rv = view(residual) if residual is not None else None
+    check(_lib.lib().aexrt_hip_conv2d_int8(
+        ctypes.byref(d), pc.algorithm, flags, ctypes.byref(xv), pc.weight.data_ptr(), _ptr(pc.w_scale),
+        pc.bias.data_ptr(), None if rv is None else ctypes.byref(rv), ctypes.byref(yv), _stream(stream)),
+        "conv2d_int8")
+
+
 def fill_u32(t, value: int = 0, stream=None) -> None:
     check(_lib.lib().aexrt_hip_fill_u32(t.data_ptr(), t.numel(), value, _stream(stream)), "fill_u32")
 

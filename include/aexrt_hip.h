@@ -204,6 +204,24 @@ int aexrt_hip_conv2d(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t f
 int aexrt_hip_conv2d_f32(const AexrtConv2DDesc* desc, uint32_t flags, const float* x, const float* weight,
                          const float* bias, float* y, void* stream);
 
+/* a14 for int8 commands: the reference's whole int8 conv command (the int8
+ * block of record_replay_conv, native/aexrt_d3d12_runtime.cpp:23935-24318)
+ * on a plain fp16 NHWC input view (x->amax_slots is ignored):
+ *   - an input of fewer than 4096 elements (RT:21478-21479) runs the dynamic
+ *     kernel (per position and 4-channel group scales, RT:2952-3115);
+ *   - with AEXRT_HIP_CONV_INT8_PG16 the reference's strip amax of the input
+ *     (RT:3219-3259) then the pg16 conv (RT:4770-4923);
+ *   - otherwise the per-tensor amax of the input, then the prequantized conv
+ *     (RT:3314-3346, 4614-4762) quantizing on load.
+ * algorithm 51/52/53; flags SILU / RESIDUAL / OUT_F32 / INT8_PG16; in_channels
+ * % 16 == 0.  The amax words live in a scratch buffer the library allocates
+ * on the current device at first use (16 x C/16 uint32, grown when a conv
+ * needs more) and keeps until the process ends; every call clears what it
+ * uses first.  Calls that overlap on one device share that scratch and race. */
+int aexrt_hip_conv2d_int8(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t flags, const AexrtHipTensorView* x,
+                          const void* weight, const float* w_scale, const float* bias,
+                          const AexrtHipTensorView* residual, const AexrtHipTensorView* y, void* stream);
+
 /* a6, reference form: the pg16 int8 conv on the reference's own operands,
  * native/aexrt_d3d12_runtime.cpp:4770-4923 (dispatch 24152-24258): packed =
  * NC/4HW4 int8 words (aexrt_hip_quant_pack_nchw with per_group = 1, or

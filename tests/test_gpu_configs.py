@@ -216,3 +216,63 @@ def test_dynamic_int8_fp16_silu_residual_and_slots(cuda, case, residual):
         assert ok, worst
     want = [np.float32(np.abs(got[:, g * 16:(g + 1) * 16]).max()).view(np.uint32) for g in range(oc // 16)]
     np.testing.assert_array_equal(slots, want)
+
+
+def _cmd_case(cuda, x, wt, b, k, s, *, pg16=False, silu=True):
+    import torch
+
+    n, c, h, w = x.shape
+    oc = wt.shape[0]
+    desc = O.conv_desc(n, c, h, w, oc, k, s, k // 2)
+    alg = 51 if k == 1 else (53 if s == 2 else 52)
+    pc = K.prepare_conv(desc, alg, K.SRC_LAYOUT_INT8, packing.pack_conv_int8(wt, fp16_engine=True), b, device=cuda)
+    xd = torch.from_numpy(nchw_to_nhwc(x.astype(np.float16))).to(cuda)
+    _, _, oh, ow = O.out_shape(desc)
+    y = torch.empty((n, oh, ow, oc), dtype=torch.float16, device=cuda)
+    K.conv2d_int8(pc, xd, y, flags=(K.SILU if silu else 0) | (K.INT8_PG16 if pg16 else 0))
+    torch.cuda.synchronize()
+    return desc, nhwc_to_nchw(y.float().cpu().numpy())
+
+
+def test_int8_command_c2_per_tensor(cuda):
+    """C2 (1x128x40x40 fp16 with 1% outliers x8, 1x1 128->256, per-16-output-channel weight scales)
+    through the int8 command: the input's amax, quantize-on-load, int32 MFMA, dequant + bias + SiLU,
+    within one fp16 ulp of the oracle's chain."""
+    from tests.helpers import c2_input, group16_weight
+
+    rng = np.random.default_rng(1)
+    x = c2_input(seed=1)
+    wt = group16_weight(rng, 256, 128, 1)
+    b = packing.fp16_round(rng.uniform(-0.1, 0.1, 256).astype(np.float32))
+    desc, got = _cmd_case(cuda, x, wt, b, 1, 1)
+    y_ref = O.w8a8_conv(x, wt, b, desc, silu=True, fp16_engine=True)[-1]
+    ok, worst = _within_ulp16(y_ref, got)
+    assert ok, worst
+
+
+def test_int8_command_pg16_strips_at_batch_two(cuda):
+    """Plan flag 16 through the command: the reference's memory-strip amax (images mixed at N > 1),
+    per-group pack scales, pg16 conv; within 1e-3 of the range of the oracle's pg16 chain."""
+    from oracle import network as ON
+
+    rng = np.random.default_rng(41)
+    x = O.round_f16(rng.standard_normal((2, 64, 12, 12)).astype(np.float32))
+    x[:, 16:32] *= 6.0
+    x = O.round_f16(x)
+    wt = he_weight(rng, 32, 64, 3)
+    b = rng.uniform(-0.1, 0.1, 32).astype(np.float32)
+    desc, got = _cmd_case(cuda, x, wt, packing.fp16_round(b), 3, 1, pg16=True)
+    ref = ON.conv_layer(x, wt, b, dict(strides=[1, 1], pads=[1, 1, 1, 1]), int8=True, silu=True, pg16=True)
+    err, allowed = tol_range(ref, got, 1e-3)
+    assert err <= allowed, (err, allowed)
+
+
+def test_int8_command_below_4096_elements_is_the_dynamic_conv(cuda):
+    rng = np.random.default_rng(42)
+    x = O.round_f16(rng.standard_normal((1, 128, 5, 5)).astype(np.float32))
+    wt = he_weight(rng, 128, 128, 3)
+    b = packing.fp16_round(rng.uniform(-0.1, 0.1, 128).astype(np.float32))
+    desc, got = _cmd_case(cuda, x, wt, b, 3, 1, pg16=True)
+    qw, ws = O.weight_quant(wt, fp16_round=True)
+    ok, worst = _within_ulp16(O.conv_int8_dynamic(x, qw, desc, ws, b, True), got)
+    assert ok, worst

@@ -538,16 +538,24 @@ def test_plan_counters_describe_the_prepared_step_list(cuda):
 
 
 def test_inference_session_hip_backend_matches_the_oracle(cuda):
-    """InferenceSession(graph, backend="hip") (the reference's session factory, session.py:33-79)
-    compiles the graph to an engine and runs it on this backend."""
+    """InferenceSession(graph, backend="hip") (the reference's session factory, session.py:10-125)
+    compiles the graph to an engine and runs it on this backend: fp16 against the oracle's fp16
+    network, and W8A8 (the backend's default: every int8-eligible conv) against the oracle with
+    those convs on the W8A8 chain."""
     from aexrt_amd.session import InferenceSession
 
     g = _c2f_graph(batch=1, c=64, dim=20, seed=11)
+    name = next(iter(g.inputs))
     x = np.random.default_rng(11).standard_normal((1, 64, 20, 20)).astype(np.float32)
-    sess = InferenceSession(g, backend="hip")
-    assert sess.info().name == "hip"
-    out = sess.run({next(iter(g.inputs)): x})
+    fp16 = InferenceSession(g, backend="hip", w8a8=False)
+    assert fp16.info().name == "hip"
     ref = ON.run_graph(g, x)[g.outputs[0]]
-    got = np.asarray(out[g.outputs[0]]).reshape(ref.shape)
+    got = np.asarray(fp16.run({name: x})[g.outputs[0]]).reshape(ref.shape)
     err, allowed = tol_range(ref, got, 1e-2)
+    assert err <= allowed, (err, allowed)
+    w8a8 = InferenceSession(g, backend="hip")
+    convs = [n.name for n in g.nodes if n.op == "Conv"]
+    ref8 = ON.run_graph(g, x, int8_convs=convs)[g.outputs[0]]
+    got8 = np.asarray(w8a8.run({name: x})[g.outputs[0]]).reshape(ref8.shape)
+    err, allowed = tol_range(ref8, got8, 1e-2)
     assert err <= allowed, (err, allowed)
