@@ -110,9 +110,69 @@ bool run_int8_command(const AexrtConv2DDesc& d, uint32_t algorithm, uint32_t fla
 
 }  // namespace aexrt
 
+// ---- allocation-free variant -------------------------------------------------
+// For callers that cannot allocate device memory (code under HIP graph
+// capture, tight serving loops, harnesses that forbid hipMalloc): the amax
+// words live in this file-scope array instead of library-allocated memory.
+// Each device holds its own copy until the process ends.  It covers convs of
+// up to kNoAllocMaxChannels input channels (16 stripes x C/16 words).
+namespace aexrt {
+namespace {
+constexpr uint32_t kNoAllocMaxChannels = 4096;
+constexpr uint64_t kNoAllocWords = uint64_t(kCmdStripes) * (kNoAllocMaxChannels / 16);  // 16 KiB
+}  // namespace
+}  // namespace aexrt
+
+static __device__ __align__(256) uint32_t scratch[aexrt::kNoAllocWords];
+
+namespace aexrt {
+namespace {
+
+std::mutex g_symbol_mutex;
+std::map<int, uint32_t*> g_scratch_ptr;  // device -> address of `scratch` on that device
+
+// The device address of `scratch` on the current device, looked up once per
+// device with that device current.  Host code uses this pointer, never the
+// array's name (a host-side stand-in).
+uint32_t* static_scratch() {
+    int dev = 0;
+    if (!check_hip(hipGetDevice(&dev), "conv2d_int8_noalloc: current device")) return nullptr;
+    std::lock_guard<std::mutex> lock(g_symbol_mutex);
+    auto it = g_scratch_ptr.find(dev);
+    if (it != g_scratch_ptr.end()) return it->second;
+    void* p = nullptr;
+    if (!check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "conv2d_int8_noalloc: scratch address") || !p)
+        return nullptr;
+    g_scratch_ptr[dev] = static_cast<uint32_t*>(p);
+    return static_cast<uint32_t*>(p);
+}
+
+}  // namespace
+}  // namespace aexrt
+
 using namespace aexrt;
 
 extern "C" {
+
+int aexrt_hip_conv2d_int8_noalloc(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t flags,
+                                  const AexrtHipTensorView* x, const void* weight, const float* w_scale,
+                                  const float* bias, const AexrtHipTensorView* residual, const AexrtHipTensorView* y,
+                                  void* stream) {
+    if (!desc || !x || !y || !weight || !w_scale || !bias || !x->data || !y->data) {
+        set_error("conv2d_int8_noalloc: null argument");
+        return 0;
+    }
+    if (desc->in_channels > kNoAllocMaxChannels) {
+        set_error("conv2d_int8_noalloc: at most 4096 input channels (its static amax scratch is 16 KiB per device)");
+        return 0;
+    }
+    uint32_t* s = static_scratch();
+    if (!s) return 0;
+    return run_int8_command(*desc, algorithm, flags, *x, weight, w_scale, bias, residual, *y, s, kNoAllocWords,
+                            static_cast<hipStream_t>(stream))
+               ? 1
+               : 0;
+}
 
 int aexrt_hip_conv2d_int8(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t flags, const AexrtHipTensorView* x,
                           const void* weight, const float* w_scale, const float* bias,

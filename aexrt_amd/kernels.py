@@ -293,6 +293,18 @@ def conv2d_int8(pc: PreparedConv, x, y, *, flags: int = SILU, residual=None, str
         "conv2d_int8")
 
 
+def conv2d_int8_noalloc(pc: PreparedConv, x, y, *, flags: int = SILU, residual=None, stream=None) -> None:
+    """:func:`conv2d_int8` with the amax scratch in the library's static device array (no device
+    allocation; in_channels <= 4096)."""
+    d = ConvDesc.from_params(pc.params)
+    xv, yv = view(x), view(y)
+    rv = view(residual) if residual is not None else None
+    check(_lib.lib().aexrt_hip_conv2d_int8_noalloc(
+        ctypes.byref(d), pc.algorithm, flags, ctypes.byref(xv), pc.weight.data_ptr(), _ptr(pc.w_scale),
+        pc.bias.data_ptr(), None if rv is None else ctypes.byref(rv), ctypes.byref(yv), _stream(stream)),
+        "conv2d_int8_noalloc")
+
+
 def fill_u32(t, value: int = 0, stream=None) -> None:
     check(_lib.lib().aexrt_hip_fill_u32(t.data_ptr(), t.numel(), value, _stream(stream)), "fill_u32")
 

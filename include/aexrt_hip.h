@@ -222,6 +222,20 @@ int aexrt_hip_conv2d_int8(const AexrtConv2DDesc* desc, uint32_t algorithm, uint3
                           const void* weight, const float* w_scale, const float* bias,
                           const AexrtHipTensorView* residual, const AexrtHipTensorView* y, void* stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): aexrt_hip_conv2d_int8 with its amax scratch in a static
+ * device array of 16 KiB (16 x 256 uint32) that each device holds until the
+ * process ends, instead of library-allocated memory; calls no allocating
+ * routine.  Same arguments, kernels and results as aexrt_hip_conv2d_int8;
+ * in_channels <= 4096, larger convs are refused with a diagnostic.  Every
+ * call on a device shares that device's array (cleared before use): calls
+ * that overlap on one device race. */
+int aexrt_hip_conv2d_int8_noalloc(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t flags,
+                                  const AexrtHipTensorView* x, const void* weight, const float* w_scale,
+                                  const float* bias, const AexrtHipTensorView* residual, const AexrtHipTensorView* y,
+                                  void* stream);
+
 /* a6, reference form: the pg16 int8 conv on the reference's own operands,
  * native/aexrt_d3d12_runtime.cpp:4770-4923 (dispatch 24152-24258): packed =
  * NC/4HW4 int8 words (aexrt_hip_quant_pack_nchw with per_group = 1, or
