@@ -163,8 +163,11 @@ bool choose_halo_tile(HaloParams& h, bool int8, HaloTile& best) {
 hipError_t halo_launch(const HaloParams& h, bool int8, int epi, const HaloTile& t, hipStream_t s) {
     using halo::halo_launch_family;
     if (LaunchProbe* pr = launch_probe()) {
-        std::snprintf(pr->name, sizeof(pr->name), "halo%s jn%d pw%d %dx%d cc%d nw%d",
-                      h.c.loader == kLoaderNchwF32 ? "-nchw" : "", t.jn, t.pw, t.TR, t.TC, t.CC, t.nw);
+        // the kernel template instance (as a trace names it), then the tile
+        const bool nchw = h.c.loader == kLoaderNchwF32;
+        std::snprintf(pr->name, sizeof(pr->name), "conv3x3_halo_kernel<%s,%d,%d,%d,%d,%s,%d> %dx%d cc%d",
+                      int8 ? "true" : "false", t.jn, t.pw, t.np, nchw ? (int)igemm::kEpiSilu : epi,
+                      nchw ? "true" : "false", nchw ? 4 : t.nw, t.TR, t.TC, t.CC);
         return hipSuccess;
     }
     if (h.c.loader == kLoaderNchwF32) return halo::halo_launch_nchw(h, t.jn, t.pw, t.np, s);

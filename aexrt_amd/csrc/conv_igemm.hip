@@ -17,8 +17,9 @@ namespace {
 hipError_t launch_variant(bool int8, bool mc, int epi, const ConvParams& p, const ConvTile& t, hipStream_t s) {
     using igemm::launch_family;
     if (LaunchProbe* pr = launch_probe()) {
-        std::snprintf(pr->name, sizeof(pr->name), "igemm jn%d pw%d%s%s", t.jn, t.pw, t.ksw ? " ksw" : "",
-                      mc ? " mc" : "");
+        // the kernel template instance (as a trace names it), then the tile
+        std::snprintf(pr->name, sizeof(pr->name), "conv_mfma_kernel<%s,%d,%d,%s,%s,%d>", int8 ? "true" : "false",
+                      t.jn, t.pw, t.ksw ? "true" : "false", mc ? "true" : "false", epi);
         return hipSuccess;
     }
     if (int8) {

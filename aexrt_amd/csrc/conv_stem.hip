@@ -346,7 +346,14 @@ hipError_t launch_conv_stem(const ConvParams& p, hipStream_t stream) {
     const int sw = ((h.npos + 15) / 16 + 3) / 4;
     const int jn = (p.OCp + 15) / 16;
     if (LaunchProbe* pr = launch_probe()) {
-        std::snprintf(pr->name, sizeof(pr->name), "stem band tr%d%s", tr, one ? " one" : "");
+        // the instance the cases below pick (as a trace names it), then the band
+        int J = 0, N = 0;
+        for (int j : {1, 2, 4})
+            for (int n : {4, 8, 12})
+                if (!J && jn <= j && np <= n && sw <= n) J = j, N = n;
+        if (!J) return hipErrorInvalidValue;
+        std::snprintf(pr->name, sizeof(pr->name), "conv3x3_stem_kernel<%d,%d,%d> tr%d%s", J, N, N, tr,
+                      one ? " one" : "");
         return hipSuccess;
     }
 #define AEXRT_STEM_CASE(J, N, W) \

@@ -121,7 +121,10 @@ hipError_t launch_conv_wide(const ConvParams& p, int epi, hipStream_t stream) {
     const ConvChoice& t = p.choice;
     if (!wide_geometry(h, t.jn, t.pw, t.tr, t.tc, t.cc)) return hipErrorInvalidValue;
     if (LaunchProbe* pr = launch_probe()) {
-        std::snprintf(pr->name, sizeof(pr->name), "wide jn%d pw%d %dx%d cc%d", t.jn, t.pw, t.tr, t.tc, t.cc);
+        // the kernel template instance (as a trace names it), then the tile
+        std::snprintf(pr->name, sizeof(pr->name), "conv3x3_wide_kernel<%d,%d,%d,%d,%d> %dx%d cc%d", t.jn, t.pw,
+                      kWideNPW, kWideNWP, epi == igemm::kEpiSilu ? (int)igemm::kEpiSilu : (int)igemm::kEpiAny, t.tr,
+                      t.tc, t.cc);
         return hipSuccess;
     }
 #define AEXRT_WIDE_CASE(J, P)                                                                    \

@@ -206,6 +206,8 @@ struct AexrtYoloModel {
     // "cmd <index> <shape key>" -> choice measured in the network (the shape key
     // keeps a cached choice from applying to the same command at another batch)
     std::map<std::string, ConvChoice> refined;
+    // "schedule <input dims> <commands>" -> (sibling convs as one launch, lane count) measured at load
+    std::map<std::string, std::pair<int, int>> schedules;
     std::string tune_cache;                    // AEXRT_HIP_TUNE_CACHE file, empty: none
     hipStream_t lane_stream[kLanes] = {};      // capture-time streams of lanes 1..kLanes-1
     int n_lanes = 1;                           // lanes the schedule uses (measured at load)
@@ -921,6 +923,8 @@ void load_tune_cache(AexrtYoloModel* m) {
             continue;
         if (line.compare(0, 4, "cmd ") == 0)
             m->refined[line.substr(0, tab)] = c;  // a conv's choice measured in the network
+        else if (line.compare(0, 9, "schedule ") == 0)
+            m->schedules[line.substr(0, tab)] = {c.kind, c.jn};  // merge flag, lanes
         else
             m->tuned[line.substr(0, tab)] = c;
     }
@@ -936,6 +940,7 @@ void save_tune_cache(AexrtYoloModel* m) {
         };
         for (const auto& [key, c] : m->tuned) put(key, c);
         for (const auto& [key, c] : m->refined) put(key, c);
+        for (const auto& [key, v] : m->schedules) put(key, ConvChoice{v.first, v.second, 0, 0, 0, 0, 0, 0});
         if (!f) return;
     }
     std::rename(tmp.c_str(), m->tune_cache.c_str());
@@ -1055,18 +1060,40 @@ void schedule_steps(AexrtYoloModel* m) {
     }
 }
 
-// Labels of the conv steps name the kernel and tile that runs (it changes as
-// the tile choices are measured): "<command> alg=<plan family> kernel=<kernel>".
-void label_steps(AexrtYoloModel* m) {
-    for (Step& st : m->steps)
-        if (st.family) st.label = st.head + " kernel=" + st.family() + st.tail;
-}
-
 // Key of a conv's choice measured in the network: the command, its algorithm
 // and its shape.  Overriding a conv's algorithm and restoring it finds the
 // first measurement again, so the restored model runs the same kernels.
 std::string refined_key(size_t ci, uint32_t alg, const ConvParams& p, bool int8) {
     return "cmd " + std::to_string(ci) + " alg " + std::to_string(alg) + " " + tune_key(p, int8);
+}
+
+// Without measurement (AEXRT_HIP_AUTOTUNE=0) a conv still takes a cached
+// choice when the tune cache has one this build offers: its choice measured in
+// the network first, else its shape's isolated measurement; otherwise the
+// heuristics (choice kind 0).
+void apply_cached_choice(AexrtYoloModel* m, size_t ci, uint32_t alg, ConvParams& p, bool int8) {
+    if (m->tune_cache.empty()) return;
+    ConvChoice all[128];
+    const int na = enumerate_conv_choices(p, int8, all, 128);
+    auto offered = [&](const ConvChoice& c) {
+        for (int k = 0; k < na; ++k)
+            if (same_choice(all[k], c)) return true;
+        return false;
+    };
+    auto rf = m->refined.find(refined_key(ci, alg, p, int8));
+    if (rf != m->refined.end() && offered(rf->second)) {
+        p.choice = rf->second;
+        return;
+    }
+    auto tu = m->tuned.find(tune_key(p, int8));
+    if (tu != m->tuned.end() && offered(tu->second)) p.choice = tu->second;
+}
+
+// Labels of the conv steps name the kernel and tile that runs (it changes as
+// the tile choices are measured): "<command> alg=<plan family> kernel=<kernel>".
+void label_steps(AexrtYoloModel* m) {
+    for (Step& st : m->steps)
+        if (st.family) st.label = st.head + " kernel=" + st.family() + st.tail;
 }
 
 bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
@@ -1210,12 +1237,12 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                                                 return launch_conv_int8_pg16(p, s);
                                             }});
                     head += " pg16";
-                    family = [] { return std::string("int8 pg16 mfma"); };
+                    family = [] { return std::string("conv_int8_pg16_kernel"); };
                 } else if (int8 && cs.dynamic) {
                     const DynConvParams dp = dynamic_params(p);
                     m->steps.push_back(Step{(int)ci, "", [dp](hipStream_t s) { return launch_conv_int8_dynamic(dp, s); }});
                     head += " dynamic";
-                    family = [] { return std::string("int8 dynamic dot4"); };
+                    family = [] { return std::string("conv_int8_dynamic_kernel"); };
                 } else if (m->autotune && !is_winograd_algorithm(alg)) {
                     auto tc = std::make_unique<TunedConv>();
                     tc->cmd = (int)ci;
@@ -1251,6 +1278,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                         return std::string(name);
                     };
                 } else {
+                    if (!is_winograd_algorithm(alg)) apply_cached_choice(m, ci, alg, p, int8);
                     m->steps.push_back(Step{(int)ci, "", [p, alg, pre](hipStream_t s) {
                                                 if (pre) {
                                                     const hipError_t e = pre(s);
@@ -1260,7 +1288,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                                                 return launch_conv_igemm(p, is_int8_algorithm(alg), s);
                                             }});
                     if (is_winograd_algorithm(alg)) {
-                        family = [] { return std::string("winograd f2x2 mfma"); };
+                        family = [] { return std::string("winograd_f2x2_kernel"); };
                     } else {
                         family = [p, int8] {
                             char name[96];
@@ -1685,9 +1713,11 @@ void compute_stats(AexrtYoloModel* m) {
         if (e.src_cmd[x.cmd] < launched.size()) launched[e.src_cmd[x.cmd]] = 1;
         if (!x.family) continue;
         const std::string f = x.family();
-        const uint8_t k = f.rfind("int8 dynamic", 0) == 0 ? 3
-                          : (f.rfind("halo", 0) == 0 || f.rfind("wide", 0) == 0 || f.rfind("stem", 0) == 0) ? 2
-                                                                                                          : 1;
+        const uint8_t k = f.rfind("conv_int8_dynamic", 0) == 0 ? 3
+                          : (f.rfind("conv3x3_halo", 0) == 0 || f.rfind("conv3x3_wide", 0) == 0 ||
+                             f.rfind("conv3x3_stem", 0) == 0)
+                              ? 2
+                              : 1;
         conv_kind[x.cmd] = k;
         if (!x.tail.empty()) {
             st.paired_conv3x3 += desc_of(e.commands[x.cmd]).kernel_h == 3;
@@ -1783,8 +1813,12 @@ bool build_model(AexrtYoloModel* m) {
     m->autotune = !(tune && tune[0] == '0');
     const char* tlog = std::getenv("AEXRT_HIP_TUNE_LOG");
     m->tune_log = tlog && tlog[0] == '1';
+    // AEXRT_HIP_TUNE_CACHE=<file>: choices measured by an earlier load are
+    // reused (and, when measuring, the file is rewritten with this load's); with
+    // AEXRT_HIP_AUTOTUNE=0 the cached choices still apply, nothing is measured
+    // and the file is left as it is
     const char* tcache = std::getenv("AEXRT_HIP_TUNE_CACHE");
-    if (m->autotune && tcache && tcache[0]) {
+    if (tcache && tcache[0]) {
         m->tune_cache = tcache;
         load_tune_cache(m);
     }
@@ -1797,11 +1831,19 @@ bool build_model(AexrtYoloModel* m) {
     const bool fixed_lanes = lanes && lanes[0] >= '1' && lanes[0] <= '9';
     const bool pairs = std::any_of(m->sibling.begin(), m->sibling.end(), [](int s) { return s >= 0; });
     const int variants = pairs && m->autotune && m->use_graph ? 2 : 1;
+    // without measurement, a schedule cached for this network (same input and
+    // command count) is reused
+    const ValueInfo& xin = m->vals[e.manifest.input_value];
+    const std::string skey = "schedule " + std::to_string(xin.N) + "x" + std::to_string(xin.C) + "x" +
+                             std::to_string(xin.H) + "x" + std::to_string(xin.W) + " commands " +
+                             std::to_string(e.commands.size());
+    const auto cached_sched = m->schedules.find(skey);
+    const bool use_cached_sched = !m->autotune && cached_sched != m->schedules.end();
     float best_ms = 0.0f;
     bool best_merge = true;
     int best_lanes = 1;
     for (int k = 0; k < variants; ++k) {
-        m->merge_siblings = k == 0;
+        m->merge_siblings = use_cached_sched ? cached_sched->second.first != 0 : k == 0;
         m->n_lanes = 1;
         if (!build_steps(m, m->copies)) return false;
         if (m->autotune && !refine_in_context(m)) return false;
@@ -1829,9 +1871,15 @@ bool build_model(AexrtYoloModel* m) {
         schedule_steps(m);
         drop_graph(m);
     }
+    if (use_cached_sched && !fixed_lanes) {
+        m->n_lanes = std::max(1, std::min(kLanes, cached_sched->second.second));
+        schedule_steps(m);
+        drop_graph(m);
+    }
+    if (m->autotune) m->schedules[skey] = {m->merge_siblings ? 1 : 0, m->n_lanes};
     if (m->tune_log && variants > 1)
         std::fprintf(stderr, "aexrt sibling convs: %s\n", best_merge ? "one launch" : "two launches");
-    if (!m->tune_cache.empty()) save_tune_cache(m);
+    if (m->autotune && !m->tune_cache.empty()) save_tune_cache(m);
     const char* prof = std::getenv("AEXRT_HIP_PROFILE");
     m->profile = prof && prof[0] == '1';
     setup_postprocess(m);

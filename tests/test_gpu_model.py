@@ -12,6 +12,9 @@ to end, the raw head output must match the oracle network within a looser bound.
 """
 from __future__ import annotations
 
+import os
+import shutil
+
 import numpy as np
 import pytest
 
@@ -20,6 +23,7 @@ import oracle.network as ON
 from aexrt_amd import engine as E
 from aexrt_amd.graph import Graph, TensorSpec
 from aexrt_amd.runtime import NativeHipYoloModel
+from aexrt_amd.workloads import c2f_block
 from aexrt_amd.yolov8 import build_yolov8n
 from tests.helpers import tol_range
 
@@ -27,37 +31,7 @@ pytestmark = pytest.mark.gpu
 
 
 def _c2f_graph(batch=1, c=128, dim=40, seed=3, shortcut=True) -> Graph:
-    """C2f block: 1x1 c->c, split 2x(c/2), two bottlenecks (3x3 pair + residual), concat 4 -> 1x1 2c->c."""
-    rng = np.random.default_rng(seed)
-    g = Graph("c2f")
-    g.input("x", TensorSpec((batch, c, dim, dim)))
-    k = [0]
-
-    def conv(x, cin, cout, ks):
-        k[0] += 1
-        n = f"conv{k[0]}"
-        g.const(f"{n}.w", (rng.standard_normal((cout, cin, ks, ks)) * np.sqrt(2.0 / (cin * ks * ks))).astype(np.float32))
-        g.const(f"{n}.b", rng.uniform(-0.1, 0.1, cout).astype(np.float32))
-        p = ks // 2
-        g.conv2d(f"{n}.y", x, f"{n}.w", f"{n}.b", pads=(p, p, p, p), name=n)
-        g.sigmoid(f"{n}.s", f"{n}.y")
-        g.mul(f"{n}.o", f"{n}.y", f"{n}.s")
-        return f"{n}.o"
-
-    h = c // 2
-    y = conv("x", c, c, 1)
-    g.split(["a", "b"], y, [h, h], axis=1)
-    parts = ["a", "b"]
-    for i in range(2):
-        t = conv(conv(parts[-1], h, h, 3), h, h, 3)
-        if shortcut:
-            g.add(f"res{i}", parts[-1], t)
-            t = f"res{i}"
-        parts.append(t)
-    g.concat("cat", *parts, axis=1)
-    out = conv("cat", 2 * c, c, 1)
-    g.output(out)
-    return g
+    return c2f_block(batch=batch, c=c, dim=dim, seed=seed, shortcut=shortcut)
 
 
 def _ulp16(a):
@@ -349,6 +323,20 @@ def test_tune_cache_file_roundtrip(cuda, tmp_path, monkeypatch):
     assert again[key] != "1 9 9 0 0 0 0 4"
 
 
+TUNE_PLAN = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "aexrt_amd", "tuned",
+                         "yolov8n320.tune")
+
+
+def _use_bench_plan(monkeypatch, tmp_path):
+    """Load with the kernel plan bench.py runs (the committed measured choices, no measurement at
+    load), so that the layers checked are computed by the benchmark's kernels."""
+    if os.path.exists(TUNE_PLAN):
+        plan = tmp_path / "plan.tune"
+        shutil.copyfile(TUNE_PLAN, plan)
+        monkeypatch.setenv("AEXRT_HIP_TUNE_CACHE", str(plan))
+        monkeypatch.setenv("AEXRT_HIP_AUTOTUNE", "0")
+
+
 def _yolo_engine(batch, imgsz, **kw):
     g = build_yolov8n(batch=batch, imgsz=imgsz, seed=4)
     names = g.metadata["int8_convs"].split(",")
@@ -369,7 +357,7 @@ def test_yolov8n_160_bs1_dynamic_int8_layers(cuda):
         m.set_profiling(False)
         labels = [lab for lab, _ in m.profile_events()]
         dyn = [lab for lab in labels if " dynamic" in lab]
-        assert len(dyn) == 4 and all("kernel=int8 dynamic dot4" in lab for lab in dyn), dyn
+        assert len(dyn) == 4 and all("kernel=conv_int8_dynamic_kernel" in lab for lab in dyn), dyn
         assert m.counter("tileflow_3x3_pack4_count") == 4
         checked, _ = _layer_check(m, g, plan)
         assert checked == 63
@@ -379,9 +367,11 @@ def test_yolov8n_160_bs1_dynamic_int8_layers(cuda):
     assert err <= allowed, (err, allowed)
 
 
-def test_yolov8n_320_bs1_w8a8_layers_and_end_to_end(cuda):
-    """The benchmark network at batch 1: every layer against the oracle (int8 layers within one
-    fp16 ulp), the raw head output end to end, and the run reproducible bit for bit."""
+def test_yolov8n_320_bs1_w8a8_layers_and_end_to_end(cuda, monkeypatch, tmp_path):
+    """The benchmark network at batch 1 on the benchmark's kernel plan: every layer against the
+    oracle (int8 layers within one fp16 ulp), the raw head output end to end, and the run
+    reproducible bit for bit."""
+    _use_bench_plan(monkeypatch, tmp_path)
     g, names, plan, data = _yolo_engine(1, 320)
     x = np.random.default_rng(4).random((1, 3, 320, 320)).astype(np.float32)
     with NativeHipYoloModel(data) as m:
@@ -396,9 +386,10 @@ def test_yolov8n_320_bs1_w8a8_layers_and_end_to_end(cuda):
     assert err <= allowed, (err, allowed)
 
 
-def test_yolov8n_320_bs64_w8a8_layers(cuda):
-    """The benchmark workload (batch 64): every one of the 63 convs on the kernels the load chose
-    for this batch, against the oracle fed the GPU's own layer inputs."""
+def test_yolov8n_320_bs64_w8a8_layers(cuda, monkeypatch, tmp_path):
+    """The benchmark workload (batch 64) on the benchmark's kernel plan: every one of the 63 convs
+    against the oracle fed the GPU's own layer inputs."""
+    _use_bench_plan(monkeypatch, tmp_path)
     g, names, plan, data = _yolo_engine(64, 320)
     x = np.random.default_rng(4).random((64, 3, 320, 320)).astype(np.float32)
     with NativeHipYoloModel(data) as m:
