@@ -16,6 +16,10 @@ calibration kernel, so that the reported MB are HBM bytes.
 ``python -m aexrt_amd.profiling --fetch DIR --write DIR --pass-log FILE [--trace DIR]``
 prints a markdown table: step label, kernel, MB read, MB written, and, with a
 kernel trace, the mean dispatch duration of that kernel instance and grid.
+``--stats --trace DIR --pass-log FILE`` summarises a kernel trace of
+``bench.py --trace-pass`` per kernel instance and per step; ``--mfma DIR
+--pass-log FILE [--trace DIR --trace-log FILE]`` prints the executed MFMA
+operations of a pmc pass per step and, with the trace, the MFMA rate.
 """
 from __future__ import annotations
 
@@ -101,13 +105,132 @@ def traffic_table(fetch_dir: str, write_dir: str, pass_log: str, trace_dir: Opti
     return [dict(f_scale=f_scale, w_scale=w_scale)] + rows
 
 
+def trace_pass_info(log: str) -> dict:
+    for line in Path(log).read_text().splitlines():
+        line = line.strip()
+        if line.startswith("{") and "trace_pass" in line:
+            return json.loads(line)["trace_pass"]
+    raise ValueError(f"no trace_pass line in {log}")
+
+
+def kernel_stats(trace_dir: str, pass_log: str) -> dict:
+    """Per-step kernel durations of a ``bench.py --trace-pass`` kernel trace.
+
+    The trace ends with the pass's graph replays (one stream, steps in launch
+    order): the last replays x steps dispatches are matched to the step
+    labels in order.  Returns per-step mean duration, per-instance totals per
+    replay, and the replays' wall time (first dispatch start to last end)."""
+    info = trace_pass_info(pass_log)
+    labels, reps = info["steps"], int(info["replays"])
+    rows = []
+    with open(_csv_in(trace_dir, "kernel_trace.csv"), newline="") as f:
+        for r in csv.DictReader(f):
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+    rows.sort()
+    n = len(labels)
+    tail = rows[-reps * n:]
+    if len(tail) != reps * n:
+        raise ValueError("fewer dispatches than replays x steps")
+    per_step = []
+    for i, lab in enumerate(labels):
+        ds = [(tail[r * n + i][1] - tail[r * n + i][0]) / 1e3 for r in range(reps)]
+        per_step.append(dict(step=lab, kernel=short_name(tail[i][2]), mean_us=statistics.mean(ds),
+                             min_us=min(ds)))
+    walls = [(tail[(r + 1) * n - 1][1] - tail[r * n][0]) / 1e3 for r in range(reps)]
+    inst: Dict[str, dict] = {}
+    for s in per_step:
+        e = inst.setdefault(s["kernel"], dict(n=0, us=0.0))
+        e["n"] += 1
+        e["us"] += s["mean_us"]
+    return dict(per_step=per_step, instances=inst, wall_us=statistics.median(walls),
+                busy_us=sum(s["mean_us"] for s in per_step), replays=reps, batch=info["batch"])
+
+
+def mfma_table(pmc_dir: str, pass_log: str) -> List[dict]:
+    """Per-step executed MFMA operations of a ``bench.py --pmc-pass`` run with
+    SQ_INSTS_VALU_MFMA_MOPS_I8 and SQ_INSTS_VALU_MFMA_MOPS_F16 (ops = MOPS x 512)."""
+    info = pass_info(pass_log)
+    labels = info["steps"]
+    disp = load_dispatches(pmc_dir)
+    _, steps = _steps_after_calibration(disp, len(labels))
+    out = []
+    for lab, d in zip(labels, steps):
+        c = d["counters"]
+        out.append(dict(step=lab, kernel=short_name(d["name"]),
+                        ops_i8=c.get("SQ_INSTS_VALU_MFMA_MOPS_I8", 0.0) * 512,
+                        ops_f16=c.get("SQ_INSTS_VALU_MFMA_MOPS_F16", 0.0) * 512))
+    return out
+
+
+def _print_stats(a) -> int:
+    st = kernel_stats(a.trace, a.pass_log)
+    print(f"{st['replays']} graph replays at batch {st['batch']} on one stream; replay wall time (first dispatch "
+          f"start to last end, median) {st['wall_us']:.1f} us; sum of kernel durations {st['busy_us']:.1f} us\n")
+    print("| kernel instance | launches per step | us per step | mean us per launch |")
+    print("|---|---|---|---|")
+    for k, e in sorted(st["instances"].items(), key=lambda kv: -kv[1]["us"]):
+        print(f"| `{k}` | {e['n']} | {e['us']:.2f} | {e['us'] / e['n']:.2f} |")
+    print("\n| step | kernel | mean us | min us |")
+    print("|---|---|---|---|")
+    for s in st["per_step"]:
+        print(f"| {s['step']} | `{s['kernel'][:70]}` | {s['mean_us']:.2f} | {s['min_us']:.2f} |")
+    return 0
+
+
+PEAK_INT8_OPS = 5.0e15   # MI355X dense int8 MFMA, op/s
+PEAK_FP16_FLOPS = 2.5e15  # MI355X dense fp16 MFMA, flop/s
+
+
+def _print_mfma(a) -> int:
+    """Executed MFMA ops per step with the step's mean duration from a
+    ``--trace-pass`` kernel trace (``--trace DIR --trace-log FILE``): MFMA rate
+    = executed ops / duration, as a fraction of the dense peak of its type."""
+    rows = mfma_table(a.mfma, a.pass_log)
+    dur = {}
+    if a.trace and a.trace_log:
+        for s in kernel_stats(a.trace, a.trace_log)["per_step"]:
+            dur[s["step"]] = s["mean_us"]
+    print("| step | kernel | int8 MFMA Gop | fp16 MFMA Gflop | trace mean us | MFMA rate T/s | of peak |")
+    print("|---|---|---|---|---|---|---|")
+    fam = {}
+    for r in rows:
+        us = dur.get(r["step"])
+        key = "int8" if r["ops_i8"] else ("fp16" if r["ops_f16"] else "other")
+        ops = r["ops_i8"] + r["ops_f16"]
+        peak = PEAK_INT8_OPS if key == "int8" else PEAK_FP16_FLOPS
+        rate = ops / (us * 1e-6) if us else None
+        rc = f"{rate / 1e12:.1f}" if rate is not None else ""
+        fc = f"{rate / peak:.4f}" if rate is not None and key != "other" else ""
+        uc = f"{us:.2f}" if us is not None else ""
+        print(f"| {r['step']} | `{r['kernel'][:60]}` | {r['ops_i8'] / 1e9:.3f} | {r['ops_f16'] / 1e9:.3f} | {uc} | {rc} | {fc} |")
+        f = fam.setdefault(key, dict(ops=0.0, us=0.0, n=0))
+        f["ops"] += ops
+        f["us"] += us or 0.0
+        f["n"] += 1
+    print("\n| launches | count | executed MFMA Gop | trace us per step | MFMA rate T/s | of peak |")
+    print("|---|---|---|---|---|---|")
+    for k, f in fam.items():
+        peak = PEAK_INT8_OPS if k == "int8" else PEAK_FP16_FLOPS
+        rate = f["ops"] / (f["us"] * 1e-6) if f["us"] else 0.0
+        fc = f"{rate / peak:.4f}" if k != "other" else ""
+        print(f"| {k} | {f['n']} | {f['ops'] / 1e9:.2f} | {f['us']:.1f} | {rate / 1e12:.1f} | {fc} |")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--fetch", required=True)
-    ap.add_argument("--write", required=True)
+    ap.add_argument("--fetch")
+    ap.add_argument("--write")
     ap.add_argument("--pass-log", required=True)
     ap.add_argument("--trace")
+    ap.add_argument("--stats", action="store_true", help="kernel statistics of a bench.py --trace-pass trace")
+    ap.add_argument("--mfma", help="MFMA counter run of bench.py --pmc-pass")
+    ap.add_argument("--trace-log", help="log of the bench.py --trace-pass run the --trace directory holds")
     a = ap.parse_args()
+    if a.stats:
+        return _print_stats(a)
+    if a.mfma:
+        return _print_mfma(a)
     t = traffic_table(a.fetch, a.write, a.pass_log, a.trace)
     print(f"counter scale (calibration bytes / counter bytes): FETCH_SIZE {t[0]['f_scale']:.4f}, "
           f"WRITE_SIZE {t[0]['w_scale']:.4f}\n")
