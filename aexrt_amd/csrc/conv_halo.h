@@ -48,7 +48,7 @@ struct HaloParams {
     int ntile;       // N * tpi
     int wbytes;      // LDS bytes of the resident weights
     int tbytes;      // LDS bytes of one window buffer
-    int pstride;     // LDS bytes per window pixel (CC * element size)
+    int pstride;     // LDS bytes per window pixel: CC * element size, + 16 when that is an even multiple of 16
     FastDiv fd_cc8, fd_icol, fd_tc, fd_ntc, fd_tpi, fd_cc, fd_spc;
     int icol4;                // NCHW: column quads of a window row: (ICOL + 3 + 3) / 4
     FastDiv fd_icol4, fd_rq;  // NCHW: / icol4, / (IR * icol4)
@@ -70,6 +70,7 @@ using igemm::quant8;
 using igemm::rsrc_t;
 using igemm::v2i;
 using igemm::xcd_remap;
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 template <bool INT8, int JN, int PW, int NP, int EPI, bool NCHW = false, int NW = 4>
 __global__ __launch_bounds__(NW * 64) void conv3x3_halo_kernel(HaloParams h) {
@@ -93,9 +94,10 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_halo_kernel(HaloParams h) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15;
     const int grp = lane >> 4;
+    const int gsw = grp ^ ((col >> 2) & 3);  // LDS slot of k group grp in weight row col (mod 16)
 
     const int b = xcd_remap(blockIdx.x, gridDim.x);
     const int pg = (int)fdiv((uint32_t)b, p.fd_ntn);
@@ -119,26 +121,6 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_halo_kernel(HaloParams h) {
     float scale_v = 0.0f;
     if constexpr (INT8) scale_v = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsc, cofs, 0, 0));
 
-    // ---- weights: [chunk * spc + s][h][row][grp * 16 B], gathered ----------
-    // 16-byte piece e: grp = e & 3, row = (e >> 2) % R, (gs, h) from the rest;
-    // chunk-local k = g * 16 + h * 8 = tap * CC + c.  At most NT *
-    // kHaloWeightRounds pieces: one round of loads per thread.
-    const int wpieces = h.wbytes >> 4;
-    auto wload = [&](int e) {
-        const int g4 = e & 3;
-        const int row = (e >> 2) % R;
-        const int gsh = (e >> 2) / R;
-        const int gs = gsh / WQ, hh = gsh - (gsh / WQ) * WQ;
-        const int ch = (int)fdiv((uint32_t)gs, h.fd_spc);
-        const int kk = ((gs - ch * h.spc) * 4 + g4) * 16 + hh * 8;
-        const int tap = (int)fdiv((uint32_t)kk, h.fd_cc);
-        const int k = tap * p.C + ch * h.CC + (kk - tap * h.CC);
-        const bool ok = e < wpieces && tap < 9 && n0 + row < p.OCp;
-        return bload16(rw, ok ? (uint32_t)((n0 + row) * p.Kp + k) * ESZ : kOob);
-    };
-    v4i wst[kHaloWeightRounds];
-#pragma unroll
-    for (int r = 0; r < kHaloWeightRounds; ++r) wst[r] = wload(tid + r * NT);
 
     // ---- input windows -----------------------------------------------------
     // Piece k of this thread: e = tid + k * NT -> window pixel (ir, ic) and
@@ -209,6 +191,35 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_halo_kernel(HaloParams h) {
     };
     window_loads(0, 0, true);
 
+    // ---- weights: [chunk * spc + s][h][row][64 B], gathered ----------------
+    // 16-byte piece e: LDS slot e & 3 of row (e >> 2) % R, (gs, h) from the
+    // rest.  Slot g' of a row holds k group g = g' ^ ((row >> 2) & 3) (chunk-
+    // local k = g * 16 + h * 8 = tap * CC + c): the 16 rows an MFMA operand
+    // read covers then spread one k group over all LDS banks.  The loads write LDS
+    // directly (buffer_load ... lds: lane l of a wave's 64 pieces lands at
+    // the wave's base + 16 l), so the weights take no registers and no LDS
+    // store instructions; rounds past the image (a multiple of 64 pieces)
+    // are skipped whole.
+    const int wpieces = h.wbytes >> 4;
+#pragma unroll
+    for (int r = 0; r < kHaloWeightRounds; ++r) {
+        const int e0 = r * NT + wave * 64;  // wave-uniform
+        if (e0 < wpieces) {
+            const uint32_t e = (uint32_t)(e0 + lane);
+            const int row = (int)((e >> 2) % (uint32_t)R);
+            const int g4 = (int)(e & 3u) ^ ((row >> 2) & 3);
+            const int gsh = (int)((e >> 2) / (uint32_t)R);
+            const int gs = gsh / WQ, hh = gsh - (gsh / WQ) * WQ;
+            const int ch = (int)fdiv((uint32_t)gs, h.fd_spc);
+            const int kk = ((gs - ch * h.spc) * 4 + g4) * 16 + hh * 8;
+            const int tap = (int)fdiv((uint32_t)kk, h.fd_cc);
+            const int k = tap * p.C + ch * h.CC + (kk - tap * h.CC);
+            const bool ok = tap < 9 && n0 + row < p.OCp;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(lds + e0 * 16), 16,
+                                                      ok ? (uint32_t)((n0 + row) * p.Kp + k) * ESZ : kOob, 0, 0, 0);
+        }
+    }
+
     // ---- output side -------------------------------------------------------
     const bool out_f32 = EPI == igemm::kEpiAny && (p.flags & kConvOutF32);
     const bool do_res = igemm::epi_res<EPI>(p);
@@ -237,6 +248,15 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_halo_kernel(HaloParams h) {
         }
         l_toff[e] = off;
     }
+    // tap offsets of this lane's k groups at k step 0 (the table's first row)
+    int t0[WQ];
+#pragma unroll
+    for (int hh = 0; hh < WQ; ++hh) {
+        const int kk = grp * 16 + hh * 8;
+        const int tap = (int)fdiv((uint32_t)kk, h.fd_cc);
+        const int ky = tap / 3, kx = tap - (tap / 3) * 3;
+        t0[hh] = (ky * h.ICOL + kx) * h.pstride + (kk - tap * h.CC) * ESZ;
+    }
     // window byte offset of each position subtile's output position; output
     // position (r, c) of the tile, or -1 past the tile
     int bofs[PW], prc_out[PW];
@@ -256,11 +276,6 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_halo_kernel(HaloParams h) {
     if (tid < R) {
         l_bias[tid] = bias_v;
         if constexpr (INT8) l_scale[tid] = in_scale * scale_v;
-    }
-#pragma unroll
-    for (int r = 0; r < kHaloWeightRounds; ++r) {
-        const int e = tid + r * NT;
-        if (e < wpieces) *reinterpret_cast<v4i*>(lds + e * 16) = wst[r];
     }
     if constexpr (NCHW) {
         // the padding channels of the window pixels are never written
@@ -297,6 +312,10 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_halo_kernel(HaloParams h) {
     // packed outputs of the last finished tile (fp16: .xy; fp32: all four)
     v4i ov[JN][PW];
 
+    // the weight loads into LDS complete before any wave passes the first
+    // barrier (a wave with no window piece to store would not otherwise wait
+    // for them); every load issued so far is needed by the first iteration
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     const int wstep = WQ * R * 64;  // LDS bytes of one k step's weights
     uint8_t* const win = lds + h.wbytes;
     const int total = ntl * h.nch;
@@ -353,13 +372,20 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_halo_kernel(HaloParams h) {
         // s + 1 are read before the MFMAs of step s (scheduling barriers keep
         // the compiler from sinking the reads next to their MFMAs)
         const uint8_t* const wb = lds + ch * h.spc * wstep;
+        // tap offsets of the step being fetched are in tn; the fetch reads
+        // those of the next step from the table, one step ahead of their use
+        int tn[WQ];
+#pragma unroll
+        for (int hh = 0; hh < WQ; ++hh) tn[hh] = t0[hh];
         auto fetch = [&](int s, v4i (&A)[WQ][JN], v4i (&B)[WQ][PW]) {
+            const int sn = min(s + 1, h.spc - 1);
 #pragma unroll
             for (int hh = 0; hh < WQ; ++hh) {
-                const int toff = l_toff[(s * 4 + grp) * WQ + hh];
+                const int toff = tn[hh];
+                tn[hh] = l_toff[(sn * 4 + grp) * WQ + hh];
 #pragma unroll
                 for (int j = 0; j < JN; ++j)
-                    A[hh][j] = *reinterpret_cast<const v4i*>(wb + s * wstep + (hh * R + j * 16 + col) * 64 + grp * 16);
+                    A[hh][j] = *reinterpret_cast<const v4i*>(wb + s * wstep + (hh * R + j * 16 + col) * 64 + gsw * 16);
 #pragma unroll
                 for (int q = 0; q < PW; ++q) B[hh][q] = *reinterpret_cast<const v4i*>(tb + bofs[q] + toff);
             }

@@ -70,10 +70,11 @@ bool halo_geometry(HaloParams& h, const HaloTile& t, bool int8) {
     if (ntile > INT32_MAX / 2) return false;
     h.ntile = (int)ntile;
     h.wbytes = h.nch * h.spc * wq * t.jn * 16 * 64;
-    // unpadded: padding the pixel stride to an odd multiple of 16 bytes (no
-    // bank conflicts between the 16 lanes of a quarter-wave) measured slower
-    // on the network, its larger windows cost occupancy
+    // an MFMA operand read takes 16 bytes of 16 consecutive window pixels: a
+    // pixel stride that is an odd multiple of 16 bytes spreads them over all
+    // LDS banks, an even one folds them onto a quarter or half of the banks
     h.pstride = t.CC * esz;
+    if ((h.pstride / 16) % 2 == 0) h.pstride += 16;
     h.tbytes = (h.IR * h.ICOL * h.pstride + 15) & ~15;
     if (h.wbytes + 2 * h.tbytes > (t.nw == 8 ? kLdsBudget8 : kLdsBudget) ||
         h.wbytes > 64 * t.nw * kHaloWeightRounds * 16)

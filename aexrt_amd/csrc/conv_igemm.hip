@@ -139,6 +139,7 @@ int enumerate_conv_choices(const ConvParams& p, bool int8, ConvChoice* out, int 
         }
     }
     if (n < cap && nchw && !int8) n += enumerate_stem_choices(p, out + n, cap - n);
+    if (n < cap && !nchw) n += enumerate_m32_choices(p, int8, out + n, cap - n);
     if (n < cap && !nchw && !int8) n += enumerate_wide_choices(p, out + n, cap - n);
     if (n < cap) n += enumerate_halo_choices(p, int8, out + n, cap - n);
     return n;
@@ -212,6 +213,20 @@ hipError_t launch_conv_igemm(const ConvParams& p0, bool int8, hipStream_t stream
         p.fd_c = make_fastdiv((uint32_t)p.C);
         p.fd_kw = make_fastdiv((uint32_t)p.KW);
         hipError_t e = hipErrorNotSupported;
+        if (p.choice.kind == 0 && !nchw) {
+            ConvChoice forced;
+            if (forced_m32_choice(forced) && p.KH == 3 && p.KW == 3) {
+                p.choice = forced;  // a forced tile that does not fit is an error
+                e = launch_conv_m32(p, int8, epi, stream);
+                if (e != hipSuccess) return e;
+                continue;
+            }
+        }
+        if (p.choice.kind == 5) {
+            e = launch_conv_m32(p, int8, epi, stream);
+            if (e != hipSuccess) return e;
+            continue;
+        }
         if (p.choice.kind == 0 && !int8 && !nchw) {
             ConvChoice forced;
             if (forced_wide_choice(forced)) {

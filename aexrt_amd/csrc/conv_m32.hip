@@ -1,0 +1,203 @@
+// Host side of the 32x32-MFMA 3x3 conv (kernel in conv_m32.h): geometry,
+// candidate tiles, forced tiles, launch.
+#include <algorithm>
+#include <atomic>
+#include <cstdio>
+
+#include "conv_m32.h"
+
+namespace aexrt {
+
+namespace m32 {
+AEXRT_M32_FAMILIES(AEXRT_M32_EXTERN)
+}  // namespace m32
+
+namespace {
+
+// dynamic LDS of one block (its static tables aside)
+constexpr int kM32LdsBudget = 156 * 1024;
+
+struct M32Tile {
+    int mq, nq, np, TR, TC, CC;
+    int nw = 4;  // waves per block
+};
+
+bool m32_shape_ok(const ConvParams& p) {
+    return p.KH == 3 && p.KW == 3 && p.P == 1 && (p.S == 1 || p.S == 2) && p.OH == (p.H - 1) / p.S + 1 &&
+           p.OW == (p.W - 1) / p.S + 1 && p.H < 8192 && p.W < 8192 && p.loader == kLoaderNhwc && p.C % 16 == 0 &&
+           p.x_cstride % 8 == 0;
+}
+
+// Fills the geometry of tile t into h; false when it does not fit the kernel.
+bool m32_geometry(M32Params& h, const M32Tile& t, bool int8) {
+    const ConvParams& p = h.c;
+    const int cpp = int8 ? 16 : 8;
+    const int ksub = int8 ? 32 : 16;
+    if (t.CC < 16 || t.CC % 16 || p.C % t.CC || t.TR < 1 || t.TC < 1 || t.mq < 1 || t.nq < 1) return false;
+    if (t.TR * t.TC > t.nw * 32 * t.mq) return false;
+    h.TR = t.TR;
+    h.TC = t.TC;
+    h.IR = (t.TR - 1) * p.S + 3;
+    h.ICOL = (t.TC - 1) * p.S + 3;
+    h.NPIX = h.IR * h.ICOL;
+    h.CC = t.CC;
+    h.nch = p.C / t.CC;
+    h.nks = (9 * t.CC + ksub - 1) / ksub;
+    if (h.nks > kM32MaxSteps) return false;
+    h.npiece = (t.CC / cpp) * h.NPIX;
+    if (h.npiece > 64 * t.nw * t.np) return false;
+    h.ntc = (p.OW + t.TC - 1) / t.TC;
+    h.tpi = ((p.OH + t.TR - 1) / t.TR) * h.ntc;
+    const int64_t ntile = (int64_t)p.N * h.tpi;
+    if (ntile > INT32_MAX / 2) return false;
+    h.ntile = (int)ntile;
+    const int nocb = t.nq * 32;
+    h.wbytes = h.nch * h.nks * 2 * nocb * 16;
+    h.tbytes = h.npiece * 16;
+    if ((int64_t)h.wbytes + 2 * h.tbytes > kM32LdsBudget) return false;
+    h.c.ntn = (p.OCp + nocb - 1) / nocb;
+    h.fd_npix = make_fastdiv((uint32_t)h.NPIX);
+    h.fd_icol = make_fastdiv((uint32_t)h.ICOL);
+    h.fd_tc = make_fastdiv((uint32_t)t.TC);
+    h.fd_ntc = make_fastdiv((uint32_t)h.ntc);
+    h.fd_tpi = make_fastdiv((uint32_t)h.tpi);
+    h.fd_cc = make_fastdiv((uint32_t)t.CC);
+    h.fd_nks = make_fastdiv((uint32_t)h.nks);
+    h.fd_nocb = make_fastdiv((uint32_t)nocb);
+    h.c.fd_ntn = make_fastdiv((uint32_t)h.c.ntn);
+    return true;
+}
+
+// (mq, nq) tiles of 8 subtiles have no 8-round window instance (registers);
+// 8-wave blocks exist for tiles of at most 4 subtiles
+bool m32_instantiated(int mq, int nq, int np, int nw) {
+    if (np != 4 && np != 8) return false;
+    if (nw == 8) {
+        if (np == 8) return (mq == 1 && nq <= 2) || (mq == 2 && nq == 1);
+        return (mq == 1 && nq <= 3) || (mq == 2 && nq <= 2);
+    }
+    if (nw != 4) return false;
+    if (np == 8 && mq * nq == 8) return false;
+    if (mq == 4) return nq == 1 || nq == 2;
+    return (mq == 1 || mq == 2) && nq >= 1 && nq <= 4;
+}
+
+// Smallest instantiated piece count that holds the window.
+bool m32_fit(M32Params& h, M32Tile& t, bool int8) {
+    for (int np : {4, 8}) {
+        if (!m32_instantiated(t.mq, t.nq, np, t.nw)) continue;
+        t.np = np;
+        M32Params hh = h;
+        if (m32_geometry(hh, t, int8)) {
+            h = hh;
+            return true;
+        }
+    }
+    return false;
+}
+
+std::atomic<bool> g_m32_forced{false};
+std::atomic<uint64_t> g_m32_force{0};  // mq | nq << 8 | tr << 16 | tc << 32 | cc << 48
+std::atomic<int> g_m32_force_nw{4};
+
+hipError_t m32_launch(const M32Params& h, bool int8, int epi, const M32Tile& t, hipStream_t s) {
+    using m32::m32_launch_family;
+    if (LaunchProbe* pr = launch_probe()) {
+        std::snprintf(pr->name, sizeof(pr->name), "conv3x3_m32_kernel<%s,%d,%d,%d,%d,%d> %dx%d cc%d",
+                      int8 ? "true" : "false", t.mq, t.nq, t.np, epi, t.nw, t.TR, t.TC, t.CC);
+        return hipSuccess;
+    }
+    if (int8) {
+        if (epi == 1) return m32_launch_family<true, 1>(h, t.mq, t.nq, t.np, t.nw, s);
+        if (epi == 2) return m32_launch_family<true, 2>(h, t.mq, t.nq, t.np, t.nw, s);
+        return m32_launch_family<true, 0>(h, t.mq, t.nq, t.np, t.nw, s);
+    }
+    if (epi == 1) return m32_launch_family<false, 1>(h, t.mq, t.nq, t.np, t.nw, s);
+    return m32_launch_family<false, 0>(h, t.mq, t.nq, t.np, t.nw, s);
+}
+
+}  // namespace
+
+int enumerate_m32_choices(const ConvParams& p, bool int8, ConvChoice* out, int cap) {
+    if (!m32_shape_ok(p)) return 0;
+    int n = 0;
+    const int oc32 = (p.OCp + 31) / 32;
+    for (int div = 1; div <= 8 && n < cap; div <<= 1) {
+        if (p.C % div) break;
+        const int CC = p.C / div;
+        if (CC % 16) continue;
+        for (int nq = 1; nq <= 4 && n < cap; ++nq) {
+            if (nq > oc32 || (nq == 3 && oc32 != 3)) continue;  // 3 subtiles only for 65..96 channels
+            for (int nw : {4, 8})
+            for (int mq : {1, 2, 4}) {
+                if (n >= cap) break;
+                if (!m32_instantiated(mq, nq, 4, nw)) continue;
+                const int npos = nw * 32 * mq;
+                const int tcs[4] = {p.OW, 32, 16, 8};
+                for (int i = 0; i < 4 && n < cap; ++i) {
+                    const int tc = tcs[i];
+                    bool dup = false;
+                    for (int k = 0; k < i; ++k) dup = dup || tcs[k] == tc;
+                    if (dup || tc > p.OW || tc > npos || (tc < p.OW && i > 0 && p.OW <= npos)) continue;
+                    const int TR = std::min(p.OH, npos / tc);
+                    if (TR < 1) continue;
+                    M32Params h{};
+                    h.c = p;
+                    M32Tile t{mq, nq, 4, TR, tc, CC, nw};
+                    if (!m32_fit(h, t, int8)) continue;
+                    ConvChoice c;
+                    c.kind = 5;
+                    c.jn = nq;
+                    c.pw = mq;
+                    c.tr = TR;
+                    c.tc = tc;
+                    c.cc = CC;
+                    c.nw = nw;
+                    out[n++] = c;
+                }
+            }
+        }
+    }
+    return n;
+}
+
+bool set_conv3x3_m32(bool on, int mq, int nq, int tr, int tc, int cc, int nw) {
+    if (!on) {
+        g_m32_forced.store(false);
+        return true;
+    }
+    if (!m32_instantiated(mq, nq, 4, nw) || tr < 1 || tr > 0xFFFF || tc < 1 || tc > 0xFFFF || cc < 16 || cc > 0xFFFF)
+        return false;
+    g_m32_force_nw.store(nw);
+    g_m32_force.store((uint64_t)mq | ((uint64_t)nq << 8) | ((uint64_t)tr << 16) | ((uint64_t)tc << 32) |
+                      ((uint64_t)cc << 48));
+    g_m32_forced.store(true);
+    return true;
+}
+
+bool forced_m32_choice(ConvChoice& c) {
+    if (!g_m32_forced.load(std::memory_order_relaxed)) return false;
+    const uint64_t f = g_m32_force.load(std::memory_order_relaxed);
+    c = ConvChoice{};
+    c.kind = 5;
+    c.pw = (int)(f & 0xFF);
+    c.jn = (int)((f >> 8) & 0xFF);
+    c.tr = (int)((f >> 16) & 0xFFFF);
+    c.tc = (int)((f >> 32) & 0xFFFF);
+    c.cc = (int)((f >> 48) & 0xFFFF);
+    c.nw = g_m32_force_nw.load(std::memory_order_relaxed);
+    return true;
+}
+
+// One batch slice of a conv with a kind-5 choice (views already inside
+// 32-bit spans).  A choice that does not fit the conv is an error.
+hipError_t launch_conv_m32(const ConvParams& p, bool int8, int epi, hipStream_t stream) {
+    if (!m32_shape_ok(p) || p.choice.kind != 5) return hipErrorInvalidValue;
+    M32Params h{};
+    h.c = p;
+    M32Tile t{p.choice.pw, p.choice.jn, 4, p.choice.tr, p.choice.tc, p.choice.cc, p.choice.nw};
+    if (!m32_instantiated(t.mq, t.nq, 4, t.nw) || !m32_fit(h, t, int8)) return hipErrorInvalidValue;
+    return m32_launch(h, int8, epi, t, stream);
+}
+
+}  // namespace aexrt

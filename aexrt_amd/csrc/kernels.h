@@ -152,6 +152,18 @@ int enumerate_wide_choices(const ConvParams& p, ConvChoice* out, int cap);
 hipError_t launch_conv_wide(const ConvParams& p, int epi, hipStream_t stream);
 // The tile forced by set_conv3x3_halo mode 4 (false: none).
 bool forced_wide_choice(ConvChoice& c);
+// 32x32-MFMA 3x3 conv (choice kind 5: jn = NQ 32-channel subtiles of the
+// block, pw = MQ 32-position subtiles per wave, tr x tc positions per tile,
+// cc channels per chunk; C % 16 == 0, weights of all chunks resident in LDS).
+// epi as for the halo kernel.  hipErrorInvalidValue when the choice does not
+// fit the conv.
+int enumerate_m32_choices(const ConvParams& p, bool int8, ConvChoice* out, int cap);
+hipError_t launch_conv_m32(const ConvParams& p, bool int8, int epi, hipStream_t stream);
+// Forces every 3x3 conv the kind-0 heuristics would run onto one m32 tile
+// of nw (4 or 8) waves per block (on = false: off).  False for a tile
+// without a kernel instance.
+bool set_conv3x3_m32(bool on, int mq, int nq, int tr, int tc, int cc, int nw);
+bool forced_m32_choice(ConvChoice& c);
 // Band kernel of the network's first conv (3x3 pad 1, stride 1/2, fp32 NCHW
 // input of at most 3 channels read directly, fp16 SiLU output, OCp <= 64,
 // W % 4 == 0): whole output rows per tile, one fp16 MFMA per 16 positions and

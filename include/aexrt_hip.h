@@ -300,6 +300,13 @@ int aexrt_hip_set_conv_tile(int32_t jn, int32_t pw, int32_t ksw);
  * channels) exists with 8 waves.  mode 4 = force the wide-tile fp16 kernel on
  * fp16 convs (every output channel, 49..80, in each wave; jn 4 or 5, pw 2 or
  * 4, tr * tc <= 64 * pw, cc channels per chunk with weights streamed).
+ * mode 5 = force the 32x32-MFMA kernel on 3x3 convs (int8 and fp16, C % 16 ==
+ * 0) with 4 waves per block: jn 32-channel subtiles per block (1..4; 1..2
+ * with pw 4), pw 32-position subtiles per wave (1/2/4), tr x tc output
+ * positions (tr * tc <= 128 * pw), cc input channels per chunk (C % cc == 0,
+ * cc % 16 == 0; the weights of all chunks stay in LDS); mode 6 = the same
+ * with 8 waves per block (pw 1 with jn 1..3, pw 2 with jn 1..2; tr * tc <=
+ * 256 * pw).  Any other mode switches modes 5 and 6 off.
  * Returns 0 for a bad request. */
 int aexrt_hip_set_conv3x3_halo(int32_t mode, int32_t jn, int32_t pw, int32_t tr, int32_t tc, int32_t cc);
 
