@@ -327,6 +327,48 @@ int aexrt_hip_conv2d(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t f
     return launch_conv(p, algorithm, static_cast<hipStream_t>(stream)) ? 1 : 0;
 }
 
+int aexrt_hip_conv2d_fused_1x1(const AexrtConv2DDesc* desc, uint32_t flags, const AexrtHipTensorView* x,
+                               const void* weight, const float* bias, const AexrtConv2DDesc* desc2, uint32_t flags2,
+                               const void* weight2, const float* bias2, const AexrtHipTensorView* y2, void* stream) {
+    if (!desc || !desc2 || !x || !y2 || !weight || !bias || !weight2 || !bias2 || !x->data || !y2->data) {
+        set_error("conv2d_fused_1x1: null argument");
+        return 0;
+    }
+    const AexrtConv2DDesc& d = *desc;
+    const AexrtConv2DDesc& d2 = *desc2;
+    if (flags != AEXRT_HIP_CONV_SILU || (flags2 & ~AEXRT_HIP_CONV_SILU) || d2.kernel_h != 1 || d2.kernel_w != 1 ||
+        d2.stride_h != 1 || d2.pad_top != 0 || d2.batch != d.batch || d2.in_channels != d.out_channels ||
+        d2.in_h != d.out_h || d2.in_w != d.out_w) {
+        set_error("conv2d_fused_1x1: an fp16 SiLU conv followed by a 1x1 s1 conv of its output (SILU or no flags)");
+        return 0;
+    }
+    // the intermediate is never stored: a dense view of its shape over y2's
+    // memory stands in for it in the parameter checks
+    AexrtHipTensorView mid{};
+    mid.data = y2->data;
+    mid.c_stride = (int32_t)d.out_channels;
+    mid.n_stride = int64_t(d.out_h) * d.out_w * d.out_channels;
+    std::string why;
+    ConvParams p{}, p2{};
+    if (!build_conv_params(d, 5u, flags, *x, weight, nullptr, bias, nullptr, mid, nullptr, p, why) ||
+        !build_conv_params(d2, 5u, flags2, mid, weight2, nullptr, bias2, nullptr, *y2, nullptr, p2, why)) {
+        set_error("conv2d_fused_1x1: " + why);
+        return 0;
+    }
+    p.fuse_1x1 = &p2;
+    ConvChoice c{};
+    if (!forced_m32_choice(c)) {
+        ConvChoice all[64];
+        if (enumerate_m32_choices(p, false, all, 64) < 1) {
+            set_error("conv2d_fused_1x1: no 32x32-MFMA tile covers every output channel of this conv");
+            return 0;
+        }
+        c = all[0];
+    }
+    p.choice = c;
+    return check_hip(launch_conv_igemm(p, false, static_cast<hipStream_t>(stream)), "conv2d_fused_1x1") ? 1 : 0;
+}
+
 int aexrt_hip_conv2d_f32(const AexrtConv2DDesc* desc, uint32_t flags, const float* x, const float* weight,
                          const float* bias, float* y, void* stream) {
     if (!desc || !x || !weight || !bias || !y) {

@@ -119,6 +119,8 @@ ConvTile choose_conv_tile(int M, int OC, int Kp) {
 }
 
 int enumerate_conv_choices(const ConvParams& p, bool int8, ConvChoice* out, int cap) {
+    // a fused 1x1 runs only in the 32x32-MFMA kernel's epilogue
+    if (p.fuse_1x1) return p.loader == kLoaderNhwc ? enumerate_m32_choices(p, int8, out, cap) : 0;
     int n = 0;
     const bool nchw = p.loader == kLoaderNchwF32;
     if (!nchw && p.Kp / 64 <= igemm::kMaxSteps) {
@@ -162,7 +164,8 @@ hipError_t launch_conv_igemm(const ConvParams& p0, bool int8, hipStream_t stream
                                 : std::max((uint64_t)p0.x_nstride * 2, (uint64_t)HWi * p0.x_cstride * 2);
     const uint64_t per_img = std::max({x_img, (uint64_t)p0.y_nstride * (out_f32 ? 4 : 2),
                                        p0.res ? (uint64_t)p0.r_nstride * 2 : 0,
-                                       p0.acc_out ? (uint64_t)HWo * p0.OC * 4 : 0});
+                                       p0.acc_out ? (uint64_t)HWo * p0.OC * 4 : 0,
+                                       p0.fuse_1x1 ? (uint64_t)p0.fuse_1x1->y_nstride * 2 : 0});
     if ((uint64_t)p0.OCp * p0.Kp * 2 > kMaxViewBytes || per_img == 0) return hipErrorInvalidValue;
     const int per_launch = (int)std::min<uint64_t>((uint64_t)p0.N, kMaxViewBytes / per_img);
     if (per_launch < 1) return hipErrorInvalidValue;
@@ -178,8 +181,20 @@ hipError_t launch_conv_igemm(const ConvParams& p0, bool int8, hipStream_t stream
     const int epi = p0.acc_out ? igemm::kEpiAny
                     : f == kConvSilu ? igemm::kEpiSilu
                     : (int8 && f == (kConvSilu | kConvResidual) ? igemm::kEpiSiluRes : igemm::kEpiAny);
+    if (p0.fuse_1x1 && (p0.choice.kind != 5 || int8)) return hipErrorInvalidValue;
     for (int nb = 0; nb < p0.N; nb += per_launch) {
         ConvParams p = p0;
+        ConvParams f2;  // the fused 1x1 on this slice of the batch
+        if (p0.fuse_1x1) {
+            f2 = *p0.fuse_1x1;
+            f2.N = std::min(per_launch, p0.N - nb);
+            f2.M = f2.N * HWo;
+            f2.y = static_cast<char*>(f2.y) + (int64_t)nb * f2.y_nstride * 2;
+            f2.y_bytes = (uint32_t)view_span(f2.N, f2.y_nstride, f2.y_cstride, HWo, f2.OC, 2);
+            if ((uint64_t)f2.OCp * f2.Kp * 2 > kMaxViewBytes || (uint64_t)f2.y_nstride * 2 > kMaxViewBytes)
+                return hipErrorInvalidValue;
+            p.fuse_1x1 = &f2;
+        }
         p.N = std::min(per_launch, p0.N - nb);
         p.M = p.N * HWo;
         p.x = nchw ? static_cast<const void*>(static_cast<const float*>(p0.x) + (int64_t)nb * p0.x_nstride)

@@ -45,6 +45,10 @@ struct M32Params {
     int wbytes;            // LDS bytes of the resident weights (all chunks)
     int tbytes;            // LDS bytes of one window buffer
     FastDiv fd_npix, fd_icol, fd_tc, fd_ntc, fd_tpi, fd_cc, fd_nks, fd_nocb;
+    // fused 1x1 conv (F2 instances): fp16 weights [OCp][Kp] over this conv's
+    // output channels, bias, flags, output view and slots; its input is this
+    // conv's fp16 output, which is not stored
+    ConvParams c2;
 };
 
 namespace m32 {
@@ -60,8 +64,9 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-template <bool INT8, int MQ, int NQ, int NP, int EPI, int NW>
+template <bool INT8, int MQ, int NQ, int NP, int EPI, int NW, bool F2 = false>
 __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
+    static_assert(!F2 || (!INT8 && EPI == igemm::kEpiSilu), "the fused 1x1 follows an fp16 SiLU conv");
     constexpr int NT = NW * 64;           // threads of the block
     constexpr int ESZ = INT8 ? 1 : 2;
     constexpr int KSUB = INT8 ? 32 : 16;  // k of one MFMA
@@ -78,6 +83,8 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
     __shared__ int l_toff[2 * kM32MaxSteps];
     __shared__ float l_bias[NOCB], l_scale[NOCB];
     __shared__ uint32_t l_slots[NOCB / 16];
+    __shared__ float l_bias2[F2 ? NOCB : 1];
+    __shared__ uint32_t l_slots2[F2 ? NOCB / 16 : 1];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -144,6 +151,12 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
     const float bias_v = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, cofs, 0, 0));
     float scale_v = 0.0f;
     if constexpr (INT8) scale_v = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsc, cofs, 0, 0));
+    float bias2_v = 0.0f;
+    if constexpr (F2) {
+        const rsrc_t rb2 = make_rsrc(h.c2.bias, (uint32_t)h.c2.OC * 4u);
+        bias2_v = __uint_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(rb2, tid < NOCB && tid < h.c2.OC ? (uint32_t)tid * 4u : kOob, 0, 0));
+    }
 
     // ---- weights: piece (chunk, k step, half, oc row) at LDS byte
     // (((ch * nks + ks) * 2 + half) * NOCB + row) * 16, written by the loads
@@ -201,6 +214,10 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
     }
     const int abase = (hi * NOCB + l32) * 16;  // this lane's A piece in a k step's [half][oc] block
     if (tid < NOCB / 16) l_slots[tid] = 0u;
+    if constexpr (F2) {
+        if (tid < NOCB / 16) l_slots2[tid] = 0u;
+        if (tid < NOCB) l_bias2[tid] = bias2_v;
+    }
     float s_q = 0.0f, in_scale = 0.0f;
     if constexpr (INT8) igemm::in_slot_scale(slot_raw, s_q, in_scale);
     if (tid < NOCB) {
@@ -212,10 +229,12 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 
     const int jmax = min(NQ * 2, (p.OCp - n0) >> 4);  // 16-channel groups of the block with channels
-    float gmax[NQ * 2];
+    float gmax[NQ * 2], gmax2[F2 ? NQ * 2 : 1];
 #pragma unroll
     for (int g = 0; g < NQ * 2; ++g) gmax[g] = 0.0f;
-    int yo[MQ], ro[MQ], mo[MQ];
+#pragma unroll
+    for (int g = 0; g < (F2 ? NQ * 2 : 1); ++g) gmax2[g] = 0.0f;
+    int yo[MQ], ro[MQ], mo[MQ], yo2[F2 ? MQ : 1];
     auto out_pos = [&](int tl, bool valid) {
         int n, oh0, ow0;
         tile_pos(tl, n, oh0, ow0);
@@ -227,6 +246,7 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
             yo[q] = ok ? n * (int)p.y_nstride + pos * p.y_cstride : -1;
             ro[q] = n * (int)p.r_nstride + pos * p.r_cstride;
             mo[q] = n * p.OH * p.OW + pos;
+            if constexpr (F2) yo2[q] = ok ? n * (int)h.c2.y_nstride + pos * h.c2.y_cstride : -1;
         }
     };
 
@@ -235,6 +255,9 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
     const rsrc_t ry = make_rsrc(p.y, p.y_bytes);
     const rsrc_t rr = make_rsrc(p.res, p.r_bytes);
     const rsrc_t racc = make_rsrc(p.acc_out, p.acc_out ? (uint32_t)p.M * (uint32_t)p.OC * 4u : 0u);
+    const rsrc_t rw2 = make_rsrc(F2 ? h.c2.w : nullptr, F2 ? (uint32_t)h.c2.OCp * (uint32_t)h.c2.Kp * 2u : 0u);
+    const rsrc_t ry2 = make_rsrc(F2 ? h.c2.y : nullptr, F2 ? h.c2.y_bytes : 0u);
+    const bool silu2 = F2 && (h.c2.flags & kConvSilu);
 
     acc_t acc[MQ][NQ];
 #pragma unroll
@@ -337,7 +360,75 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
         // ---- epilogue at a tile's end: lane l holds, for position subtile q
         // and channel subtile j, channels 8 j4 + 4 hi + r (r < 4) of position
         // (wave * MQ + q) * 32 + l % 32 in acc[q][j][4 j4 + r] ----
-        if (tile_end) {
+        if (F2 && tile_end) {
+            // fused 1x1: y1 = fp16(silu(acc + bias)) is the B operand of a
+            // second product over the block's channels, out = W2 y1 + bias2.
+            // k step k2 of that product takes channels 16 k2 + 8 hi .. + 7 of
+            // y1 in a lane: four of them the lane holds (rows 8 j4 + 4 hi + r
+            // of subtile k2 / 2, j4 = 2 (k2 % 2) + hi), four its partner lane
+            // (lane ^ 32) does.
+#pragma unroll
+            for (int q = 0; q < MQ; ++q) {
+                v4i b2[NQ * 2];
+#pragma unroll
+                for (int j = 0; j < NQ; ++j) {
+                    uint32_t h2[4][2];
+#pragma unroll
+                    for (int j4 = 0; j4 < 4; ++j4) {
+                        const int lc = j * 32 + j4 * 8 + hi * 4;
+                        float v[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) v[r] = silu(acc[q][j][4 * j4 + r] + l_bias[lc + r]);
+                        const __half2 a = __floats2half2_rn(v[0], v[1]), c = __floats2half2_rn(v[2], v[3]);
+                        __builtin_memcpy(&h2[j4][0], &a, 4);
+                        __builtin_memcpy(&h2[j4][1], &c, 4);
+                    }
+#pragma unroll
+                    for (int m = 0; m < 2; ++m) {
+                        const uint32_t s0 = hi ? h2[2 * m][0] : h2[2 * m + 1][0];
+                        const uint32_t s1 = hi ? h2[2 * m][1] : h2[2 * m + 1][1];
+                        const uint32_t r0 = (uint32_t)__shfl_xor((int)s0, 32, 64);
+                        const uint32_t r1 = (uint32_t)__shfl_xor((int)s1, 32, 64);
+                        b2[2 * j + m] = hi ? v4i{(int)r0, (int)r1, (int)h2[2 * m + 1][0], (int)h2[2 * m + 1][1]}
+                                           : v4i{(int)h2[2 * m][0], (int)h2[2 * m][1], (int)r0, (int)r1};
+                    }
+                }
+#pragma unroll
+                for (int j2 = 0; j2 < NQ; ++j2) {
+                    const int row2 = j2 * 32 + l32;
+                    v4i a2[NQ * 2];
+#pragma unroll
+                    for (int k2 = 0; k2 < NQ * 2; ++k2)
+                        a2[k2] = bload16(rw2, row2 < h.c2.OCp ? (uint32_t)(row2 * h.c2.Kp + k2 * 16 + hi * 8) * 2u : kOob);
+                    v16f acc2{};
+#pragma unroll
+                    for (int k2 = 0; k2 < NQ * 2; ++k2)
+                        acc2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a2[k2]),
+                                                                      __builtin_bit_cast(v8h, b2[k2]), acc2, 0, 0, 0);
+#pragma unroll
+                    for (int j4 = 0; j4 < 4; ++j4) {
+                        const int oc0 = j2 * 32 + j4 * 8 + hi * 4;
+                        float v[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            v[r] = acc2[4 * j4 + r] + l_bias2[oc0 + r];
+                            if (silu2) v[r] = silu(v[r]);
+                        }
+                        const bool ok = oc0 < h.c2.OC && yo2[q] >= 0;
+                        const float m4 = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+                        gmax2[j2 * 2 + (j4 >> 1)] = fmaxf(gmax2[j2 * 2 + (j4 >> 1)], ok ? m4 : 0.0f);
+                        const __half2 oh[2] = {__floats2half2_rn(v[0], v[1]), __floats2half2_rn(v[2], v[3])};
+                        v2i o;
+                        __builtin_memcpy(&o, oh, 8);
+                        __builtin_amdgcn_raw_buffer_store_b64(o, ry2, ok ? (uint32_t)(yo2[q] + oc0) * 2u : kOob, 0, 0);
+                    }
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < MQ; ++q)
+#pragma unroll
+                for (int j = 0; j < NQ; ++j) acc[q][j] = acc_t{};
+        } else if (tile_end) {
 #pragma unroll
             for (int q = 0; q < MQ; ++q)
 #pragma unroll
@@ -388,15 +479,20 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
         ch = nch_;
     }
 
-    igemm::flush_slots<NQ * 2>(p, gmax, n0, jmax, 0xFFFFFFFFu, out_f32, l_slots);
+    if constexpr (F2) {
+        const int jmax2 = min(NQ * 2, h.c2.OCp >> 4);
+        igemm::flush_slots<NQ * 2>(h.c2, gmax2, 0, jmax2, 0xFFFFFFFFu, false, l_slots2);
+    } else {
+        igemm::flush_slots<NQ * 2>(p, gmax, n0, jmax, 0xFFFFFFFFu, out_f32, l_slots);
+    }
 }
 
 // Blocks of one instance the GPU holds at once with lds_bytes of dynamic LDS.
-template <bool INT8, int MQ, int NQ, int NP, int EPI, int NW>
+template <bool INT8, int MQ, int NQ, int NP, int EPI, int NW, bool F2>
 int m32_resident_blocks(int lds_bytes) {
     int per_cu = 0, cus = 0, dev = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv3x3_m32_kernel<INT8, MQ, NQ, NP, EPI, NW>, NW * 64,
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv3x3_m32_kernel<INT8, MQ, NQ, NP, EPI, NW, F2>, NW * 64,
                                                      (size_t)lds_bytes) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu < 1 ||
         cus < 1)
@@ -406,17 +502,17 @@ int m32_resident_blocks(int lds_bytes) {
 
 // Persistent grid: every resident block slot gets one contiguous run of
 // position tiles of one channel tile.
-template <bool INT8, int MQ, int NQ, int NP, int EPI, int NW>
+template <bool INT8, int MQ, int NQ, int NP, int EPI, int NW, bool F2 = false>
 hipError_t m32_launch_cfg(M32Params h, hipStream_t stream) {
     const int lds_bytes = h.wbytes + 2 * h.tbytes;
-    const int cap = m32_resident_blocks<INT8, MQ, NQ, NP, EPI, NW>(lds_bytes);
+    const int cap = m32_resident_blocks<INT8, MQ, NQ, NP, EPI, NW, F2>(lds_bytes);
     int groups = h.ntile;
     if ((int64_t)h.ntile * h.c.ntn > cap) groups = std::max(1, cap / h.c.ntn);
     h.c.per = (h.ntile + groups - 1) / groups;
     groups = (h.ntile + h.c.per - 1) / h.c.per;
     const int64_t blocks = (int64_t)groups * h.c.ntn;
     if (blocks > INT32_MAX) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((conv3x3_m32_kernel<INT8, MQ, NQ, NP, EPI, NW>), dim3((unsigned)blocks), dim3(NW * 64),
+    hipLaunchKernelGGL((conv3x3_m32_kernel<INT8, MQ, NQ, NP, EPI, NW, F2>), dim3((unsigned)blocks), dim3(NW * 64),
                        (size_t)lds_bytes, stream, h);
     return hipGetLastError();
 }
@@ -441,6 +537,10 @@ hipError_t m32_launch_family(const M32Params& h, int mq, int nq, int np, int nw,
 #undef AEXRT_M32_CASE8
     return hipErrorInvalidValue;
 }
+
+// fp16 SiLU 3x3 convs with a fused 1x1 (F2): tiles whose block covers
+// every output channel (nq 2 or 3: up to 64 / 96 channels).
+hipError_t m32_launch_f2(const M32Params& h, int mq, int nq, int np, int nw, hipStream_t stream);
 
 #define AEXRT_M32_FAMILIES(X) X(true, 0) X(true, 1) X(true, 2) X(false, 0) X(false, 1)
 #define AEXRT_M32_EXTERN(I, E) \

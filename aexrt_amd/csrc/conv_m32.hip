@@ -82,10 +82,37 @@ bool m32_instantiated(int mq, int nq, int np, int nw) {
     return (mq == 1 || mq == 2) && nq >= 1 && nq <= 4;
 }
 
+// Tiles with a fused-1x1 instance (conv_m32_f16_f2.hip).
+bool m32_f2_instantiated(int mq, int nq, int np, int nw) {
+    if (nw == 4) {
+        if (np == 4) return (mq == 1 || mq == 2) && (nq == 2 || nq == 3);
+        return np == 8 && ((mq <= 2 && nq == 2) || (mq == 1 && nq == 3));
+    }
+    if (nw == 8) {
+        if (np == 4) return (mq == 1 && (nq == 2 || nq == 3)) || (mq == 2 && nq == 2);
+        return np == 8 && mq == 1 && nq == 2;
+    }
+    return false;
+}
+
+// The fused 1x1 fits a tile of nq channel subtiles: its input is every output
+// channel of the block (one channel tile), it reads k < 32 nq of its padded
+// rows, and its output channels fit the block's second product.
+bool m32_f2_ok(const ConvParams& p, int nq) {
+    const ConvParams* f = p.fuse_1x1;
+    if (!f) return true;
+    const int nocb = nq * 32;
+    return p.OCp <= nocb && f->C == p.OC && f->KH == 1 && f->KW == 1 && f->S == 1 && f->P == 0 && f->N == p.N &&
+           f->H == p.OH && f->W == p.OW && f->OCp <= nocb && f->Kp >= nocb && f->OC % 4 == 0 && f->w && f->bias &&
+           f->y && !(f->flags & ~kConvSilu) && !(p.flags & (kConvResidual | kConvOutF32)) && (p.flags & kConvSilu);
+}
+
 // Smallest instantiated piece count that holds the window.
 bool m32_fit(M32Params& h, M32Tile& t, bool int8) {
+    const bool f2 = h.c.fuse_1x1 != nullptr;
+    if (f2 && (int8 || !m32_f2_ok(h.c, t.nq))) return false;
     for (int np : {4, 8}) {
-        if (!m32_instantiated(t.mq, t.nq, np, t.nw)) continue;
+        if (f2 ? !m32_f2_instantiated(t.mq, t.nq, np, t.nw) : !m32_instantiated(t.mq, t.nq, np, t.nw)) continue;
         t.np = np;
         M32Params hh = h;
         if (m32_geometry(hh, t, int8)) {
@@ -102,10 +129,17 @@ std::atomic<int> g_m32_force_nw{4};
 
 hipError_t m32_launch(const M32Params& h, bool int8, int epi, const M32Tile& t, hipStream_t s) {
     using m32::m32_launch_family;
+    const bool f2 = h.c.fuse_1x1 != nullptr;
     if (LaunchProbe* pr = launch_probe()) {
-        std::snprintf(pr->name, sizeof(pr->name), "conv3x3_m32_kernel<%s,%d,%d,%d,%d,%d> %dx%d cc%d",
-                      int8 ? "true" : "false", t.mq, t.nq, t.np, epi, t.nw, t.TR, t.TC, t.CC);
+        std::snprintf(pr->name, sizeof(pr->name), "conv3x3_m32_kernel<%s,%d,%d,%d,%d,%d%s> %dx%d cc%d",
+                      int8 ? "true" : "false", t.mq, t.nq, t.np, epi, t.nw, f2 ? ",true" : "", t.TR, t.TC, t.CC);
         return hipSuccess;
+    }
+    if (f2) {
+        if (int8 || epi != 1) return hipErrorInvalidValue;
+        M32Params hf = h;
+        hf.c2 = *h.c.fuse_1x1;
+        return m32::m32_launch_f2(hf, t.mq, t.nq, t.np, t.nw, s);
     }
     if (int8) {
         if (epi == 1) return m32_launch_family<true, 1>(h, t.mq, t.nq, t.np, t.nw, s);
@@ -131,7 +165,7 @@ int enumerate_m32_choices(const ConvParams& p, bool int8, ConvChoice* out, int c
             for (int nw : {4, 8})
             for (int mq : {1, 2, 4}) {
                 if (n >= cap) break;
-                if (!m32_instantiated(mq, nq, 4, nw)) continue;
+                if (p.fuse_1x1 ? !m32_f2_instantiated(mq, nq, 4, nw) : !m32_instantiated(mq, nq, 4, nw)) continue;
                 const int npos = nw * 32 * mq;
                 const int tcs[4] = {p.OW, 32, 16, 8};
                 for (int i = 0; i < 4 && n < cap; ++i) {
@@ -196,7 +230,7 @@ hipError_t launch_conv_m32(const ConvParams& p, bool int8, int epi, hipStream_t 
     M32Params h{};
     h.c = p;
     M32Tile t{p.choice.pw, p.choice.jn, 4, p.choice.tr, p.choice.tc, p.choice.cc, p.choice.nw};
-    if (!m32_instantiated(t.mq, t.nq, 4, t.nw) || !m32_fit(h, t, int8)) return hipErrorInvalidValue;
+    if (!m32_fit(h, t, int8)) return hipErrorInvalidValue;
     return m32_launch(h, int8, epi, t, stream);
 }
 

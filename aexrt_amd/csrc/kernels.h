@@ -95,6 +95,10 @@ struct ConvParams {
     ConvChoice choice{};      // kernel / tile (kind 0: heuristics)
     int K, M;
     int flags;
+    // host side only: a 1x1 fp16 conv applied to this conv's fp16 output in
+    // the epilogue (its weights, bias, flags and output view; the input view
+    // is this conv's output, which is then not stored).  Null: none.
+    const struct ConvParams* fuse_1x1 = nullptr;
     // filled in by the igemm launcher
     uint32_t x_bytes = 0, y_bytes = 0, r_bytes = 0;  // byte spans of the views
     uint32_t x_slot_bytes = 0;                       // byte span of the input slots

@@ -283,6 +283,17 @@ def conv2d(pc: PreparedConv, x, y, *, flags: int = SILU, x_slots=None, y_slots=N
         _ptr(acc_out), _stream(stream)), "conv2d")
 
 
+def conv2d_fused_1x1(pc: PreparedConv, pc2: PreparedConv, x, y2, *, flags2: int = 0, y2_slots=None,
+                     stream=None) -> None:
+    """fp16 3x3 SiLU conv ``pc`` with the 1x1 conv ``pc2`` of its output fused into its epilogue:
+    y2 = conv1x1(fp16(silu(conv3x3(x)))) (SiLU too with flags2 = SILU); the 3x3 output is not stored."""
+    d, d2 = ConvDesc.from_params(pc.params), ConvDesc.from_params(pc2.params)
+    xv, yv = view(x), view(y2, y2_slots)
+    check(_lib.lib().aexrt_hip_conv2d_fused_1x1(
+        ctypes.byref(d), SILU, ctypes.byref(xv), pc.weight.data_ptr(), pc.bias.data_ptr(), ctypes.byref(d2), flags2,
+        pc2.weight.data_ptr(), pc2.bias.data_ptr(), ctypes.byref(yv), _stream(stream)), "conv2d_fused_1x1")
+
+
 def conv2d_int8(pc: PreparedConv, x, y, *, flags: int = SILU, residual=None, stream=None) -> None:
     """The reference's int8 conv command on a plain fp16 NHWC input: dynamic below 4096 input
     elements, else the input's amax (strips with INT8_PG16) then the int8 conv."""

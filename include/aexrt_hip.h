@@ -310,6 +310,19 @@ int aexrt_hip_set_conv_tile(int32_t jn, int32_t pw, int32_t ksw);
  * Returns 0 for a bad request. */
 int aexrt_hip_set_conv3x3_halo(int32_t mode, int32_t jn, int32_t pw, int32_t tr, int32_t tc, int32_t cc);
 
+/* fp16 3x3 SiLU conv (algorithm 5 weights) with a 1x1 conv of its output fused
+ * into the epilogue: y2 = conv1x1(fp16(silu(conv3x3(x) + bias)), weight2) +
+ * bias2 (SiLU when flags2 has it); the 3x3 output is never stored.  The
+ * YOLOv8 head's last two convs of each branch (the reference fuses its head
+ * into one replay group, fusion kinds 4/5 of src/aexrt/engine.py:78-79).
+ * Runs on the 32x32-MFMA kernel with a tile covering every 3x3 output channel
+ * (<= 96): the one forced by aexrt_hip_set_conv3x3_halo mode 5/6, else the
+ * first that fits.  flags = SILU; y2 gets amax slots when its view has them.
+ * Returns 0 and sets the error otherwise. */
+int aexrt_hip_conv2d_fused_1x1(const AexrtConv2DDesc* desc, uint32_t flags, const AexrtHipTensorView* x,
+                               const void* weight, const float* bias, const AexrtConv2DDesc* desc2, uint32_t flags2,
+                               const void* weight2, const float* bias2, const AexrtHipTensorView* y2, void* stream);
+
 /* Kernel of the network's first conv (3x3 pad 1, stride 1/2, the fp32 NCHW
  * input with at most 3 channels read directly, SiLU, fp16 output; a kernel
  * choice of the reference's replay_conv_algorithm, RT:9424-9500): mode 0

@@ -193,3 +193,66 @@ def test_m32_forced_tile_that_does_not_fit_fails(cuda):
         K.set_conv3x3_halo(K.HALO_AUTO)
     with pytest.raises(RuntimeError):  # no instance: 4 position subtiles x 3 channel subtiles
         K.set_conv3x3_halo(K.HALO_FORCE_M32, 3, 4, 4, 16, 16)
+
+
+# (n, c, h, w, oc, oc2, tile (mode, jn, pw, tr, tc, cc) or None, silu2, slice of a wider output)
+FUSED = [
+    (2, 64, 40, 40, 64, 64, (5, 2, 2, 6, 40, 32), False, None),   # the head's 40x40 box branch
+    (1, 64, 40, 40, 64, 64, None, False, None),                   # the first tile that fits
+    (2, 80, 20, 20, 80, 80, (5, 3, 1, 3, 20, 16), False, None),   # class branch: 80 channels, 96-channel block
+    (2, 64, 10, 10, 64, 64, (6, 2, 1, 10, 10, 64), True, (16, 80, 96)),  # 8 waves, SiLU, into a channel slice
+    (1, 80, 13, 11, 80, 64, (5, 3, 2, 13, 11, 16), False, None),  # ragged map, 1x1 to fewer channels
+]
+
+
+@pytest.mark.parametrize("case", FUSED, ids=[f"c{t[1]}_{t[2]}x{t[3]}_oc{t[4]}_to{t[5]}_{'forced' if t[6] else 'auto'}"
+                                             f"{'_silu' if t[7] else ''}{'_slice' if t[8] else ''}" for t in FUSED])
+def test_m32_fused_1x1(cuda, case):
+    """A 3x3 SiLU conv with the following 1x1 conv in its epilogue: against the oracle's two convs
+    with the 3x3 output rounded to fp16 in between (what the unfused pair stores and reads)."""
+    import torch
+
+    n, c, h, w, oc, oc2, tile, silu2, sl = case
+    rng = np.random.default_rng(501 + c + h + oc2)
+    x = O.round_f16(rng.standard_normal((n, c, h, w)).astype(np.float32))
+    wt = he_weight(rng, oc, c, 3)
+    b = packing.fp16_round(rng.uniform(-0.1, 0.1, oc).astype(np.float32))
+    w2 = he_weight(rng, oc2, oc, 1)
+    b2 = packing.fp16_round(rng.uniform(-0.1, 0.1, oc2).astype(np.float32))
+    desc = O.conv_desc(n, c, h, w, oc, 3, 1, 1)
+    desc2 = O.conv_desc(n, oc, h, w, oc2, 1, 1, 0)
+    pc = K.prepare_conv(desc, 5, K.SRC_RAW_F32, wt, b, device=cuda)
+    pc2 = K.prepare_conv(desc2, 5, K.SRC_RAW_F32, w2, b2, device=cuda)
+    lo, hi, width = sl if sl else (0, oc2, oc2)
+    big = torch.zeros((n, h, w, width), dtype=torch.float16, device=cuda)
+    slots = K.new_slots(width, cuda)
+    if tile:
+        K.set_conv3x3_halo(*tile)
+    try:
+        K.conv2d_fused_1x1(pc, pc2, _dev_nhwc(x, cuda), big[..., lo:hi], flags2=K.SILU if silu2 else 0,
+                           y2_slots=slots[lo // 16:hi // 16])
+    finally:
+        K.set_conv3x3_halo(K.HALO_AUTO)
+    torch.cuda.synchronize()
+    got = nhwc_to_nchw(big.float().cpu().numpy())
+    y1 = O.round_f16(O.cpu_conv2d(x, O.round_f16(wt), b, desc, silu=True))
+    y2 = O.cpu_conv2d(y1, O.round_f16(w2), b2, desc2, silu=silu2)
+    assert np.isfinite(got).all()
+    err, allowed = tol_range(y2, got[:, lo:hi], FP16_TOL)
+    assert err <= allowed, (err, allowed)
+    assert not got[:, :lo].any() and not got[:, hi:].any()
+    np.testing.assert_array_equal(_u32(slots)[lo // 16:hi // 16], _slots_of(got[:, lo:hi], oc2))
+
+
+def test_m32_fused_1x1_refuses_what_it_cannot_fuse(cuda):
+    import torch
+
+    rng = np.random.default_rng(7)
+    desc = O.conv_desc(1, 64, 8, 8, 128, 3, 1, 1)  # 128 channels: no tile covers them all
+    desc2 = O.conv_desc(1, 128, 8, 8, 64, 1, 1, 0)
+    pc = K.prepare_conv(desc, 5, K.SRC_RAW_F32, he_weight(rng, 128, 64, 3), np.zeros(128, np.float32), device=cuda)
+    pc2 = K.prepare_conv(desc2, 5, K.SRC_RAW_F32, he_weight(rng, 64, 128, 1), np.zeros(64, np.float32), device=cuda)
+    x = torch.zeros((1, 8, 8, 64), dtype=torch.float16, device=cuda)
+    y = torch.zeros((1, 8, 8, 64), dtype=torch.float16, device=cuda)
+    with pytest.raises(RuntimeError):
+        K.conv2d_fused_1x1(pc, pc2, x, y)
