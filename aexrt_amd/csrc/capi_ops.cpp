@@ -336,10 +336,12 @@ int aexrt_hip_conv2d_fused_1x1(const AexrtConv2DDesc* desc, uint32_t flags, cons
     }
     const AexrtConv2DDesc& d = *desc;
     const AexrtConv2DDesc& d2 = *desc2;
-    if (flags != AEXRT_HIP_CONV_SILU || (flags2 & ~AEXRT_HIP_CONV_SILU) || d2.kernel_h != 1 || d2.kernel_w != 1 ||
+    if (flags != AEXRT_HIP_CONV_SILU || (flags2 & ~(AEXRT_HIP_CONV_SILU | AEXRT_HIP_CONV_OUT_F32)) ||
+        d2.kernel_h != 1 || d2.kernel_w != 1 ||
         d2.stride_h != 1 || d2.pad_top != 0 || d2.batch != d.batch || d2.in_channels != d.out_channels ||
         d2.in_h != d.out_h || d2.in_w != d.out_w) {
-        set_error("conv2d_fused_1x1: an fp16 SiLU conv followed by a 1x1 s1 conv of its output (SILU or no flags)");
+        set_error("conv2d_fused_1x1: an fp16 SiLU conv followed by a 1x1 s1 conv of its output (flags2: SILU, "
+                  "OUT_F32)");
         return 0;
     }
     // the intermediate is never stored: a dense view of its shape over y2's

@@ -165,7 +165,9 @@ hipError_t launch_conv_igemm(const ConvParams& p0, bool int8, hipStream_t stream
     const uint64_t per_img = std::max({x_img, (uint64_t)p0.y_nstride * (out_f32 ? 4 : 2),
                                        p0.res ? (uint64_t)p0.r_nstride * 2 : 0,
                                        p0.acc_out ? (uint64_t)HWo * p0.OC * 4 : 0,
-                                       p0.fuse_1x1 ? (uint64_t)p0.fuse_1x1->y_nstride * 2 : 0});
+                                       p0.fuse_1x1 ? (uint64_t)p0.fuse_1x1->y_nstride *
+                                                         ((p0.fuse_1x1->flags & kConvOutF32) ? 4 : 2)
+                                                   : 0});
     if ((uint64_t)p0.OCp * p0.Kp * 2 > kMaxViewBytes || per_img == 0) return hipErrorInvalidValue;
     const int per_launch = (int)std::min<uint64_t>((uint64_t)p0.N, kMaxViewBytes / per_img);
     if (per_launch < 1) return hipErrorInvalidValue;
@@ -189,9 +191,10 @@ hipError_t launch_conv_igemm(const ConvParams& p0, bool int8, hipStream_t stream
             f2 = *p0.fuse_1x1;
             f2.N = std::min(per_launch, p0.N - nb);
             f2.M = f2.N * HWo;
-            f2.y = static_cast<char*>(f2.y) + (int64_t)nb * f2.y_nstride * 2;
-            f2.y_bytes = (uint32_t)view_span(f2.N, f2.y_nstride, f2.y_cstride, HWo, f2.OC, 2);
-            if ((uint64_t)f2.OCp * f2.Kp * 2 > kMaxViewBytes || (uint64_t)f2.y_nstride * 2 > kMaxViewBytes)
+            const int esz2 = (f2.flags & kConvOutF32) ? 4 : 2;
+            f2.y = static_cast<char*>(f2.y) + (int64_t)nb * f2.y_nstride * esz2;
+            f2.y_bytes = (uint32_t)view_span(f2.N, f2.y_nstride, f2.y_cstride, HWo, f2.OC, esz2);
+            if ((uint64_t)f2.OCp * f2.Kp * 2 > kMaxViewBytes || (uint64_t)f2.y_nstride * esz2 > kMaxViewBytes)
                 return hipErrorInvalidValue;
             p.fuse_1x1 = &f2;
         }

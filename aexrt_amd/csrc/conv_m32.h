@@ -258,6 +258,7 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
     const rsrc_t rw2 = make_rsrc(F2 ? h.c2.w : nullptr, F2 ? (uint32_t)h.c2.OCp * (uint32_t)h.c2.Kp * 2u : 0u);
     const rsrc_t ry2 = make_rsrc(F2 ? h.c2.y : nullptr, F2 ? h.c2.y_bytes : 0u);
     const bool silu2 = F2 && (h.c2.flags & kConvSilu);
+    const bool out2_f32 = F2 && (h.c2.flags & kConvOutF32);
 
     acc_t acc[MQ][NQ];
 #pragma unroll
@@ -417,10 +418,18 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
                         const bool ok = oc0 < h.c2.OC && yo2[q] >= 0;
                         const float m4 = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
                         gmax2[j2 * 2 + (j4 >> 1)] = fmaxf(gmax2[j2 * 2 + (j4 >> 1)], ok ? m4 : 0.0f);
-                        const __half2 oh[2] = {__floats2half2_rn(v[0], v[1]), __floats2half2_rn(v[2], v[3])};
-                        v2i o;
-                        __builtin_memcpy(&o, oh, 8);
-                        __builtin_amdgcn_raw_buffer_store_b64(o, ry2, ok ? (uint32_t)(yo2[q] + oc0) * 2u : kOob, 0, 0);
+                        if (out2_f32) {
+                            const v4i o{__float_as_int(v[0]), __float_as_int(v[1]), __float_as_int(v[2]),
+                                        __float_as_int(v[3])};
+                            __builtin_amdgcn_raw_buffer_store_b128(o, ry2, ok ? (uint32_t)(yo2[q] + oc0) * 4u : kOob,
+                                                                   0, 0);
+                        } else {
+                            const __half2 oh[2] = {__floats2half2_rn(v[0], v[1]), __floats2half2_rn(v[2], v[3])};
+                            v2i o;
+                            __builtin_memcpy(&o, oh, 8);
+                            __builtin_amdgcn_raw_buffer_store_b64(o, ry2, ok ? (uint32_t)(yo2[q] + oc0) * 2u : kOob,
+                                                                  0, 0);
+                        }
                     }
                 }
             }
@@ -481,7 +490,7 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
 
     if constexpr (F2) {
         const int jmax2 = min(NQ * 2, h.c2.OCp >> 4);
-        igemm::flush_slots<NQ * 2>(h.c2, gmax2, 0, jmax2, 0xFFFFFFFFu, false, l_slots2);
+        igemm::flush_slots<NQ * 2>(h.c2, gmax2, 0, jmax2, 0xFFFFFFFFu, out2_f32, l_slots2);
     } else {
         igemm::flush_slots<NQ * 2>(p, gmax, n0, jmax, 0xFFFFFFFFu, out_f32, l_slots);
     }

@@ -104,7 +104,8 @@ bool m32_f2_ok(const ConvParams& p, int nq) {
     const int nocb = nq * 32;
     return p.OCp <= nocb && f->C == p.OC && f->KH == 1 && f->KW == 1 && f->S == 1 && f->P == 0 && f->N == p.N &&
            f->H == p.OH && f->W == p.OW && f->OCp <= nocb && f->Kp >= nocb && f->OC % 4 == 0 && f->w && f->bias &&
-           f->y && !(f->flags & ~kConvSilu) && !(p.flags & (kConvResidual | kConvOutF32)) && (p.flags & kConvSilu);
+           f->y && !(f->flags & ~(kConvSilu | kConvOutF32)) && !(p.flags & (kConvResidual | kConvOutF32)) &&
+           (p.flags & kConvSilu);
 }
 
 // Smallest instantiated piece count that holds the window.
@@ -156,10 +157,11 @@ int enumerate_m32_choices(const ConvParams& p, bool int8, ConvChoice* out, int c
     if (!m32_shape_ok(p)) return 0;
     int n = 0;
     const int oc32 = (p.OCp + 31) / 32;
-    for (int div = 1; div <= 8 && n < cap; div <<= 1) {
-        if (p.C % div) break;
+    // channel chunks: every CC = C / div (CC % 16 == 0) from the whole input down to 16 channels
+    for (int div = 1; div <= p.C / 16 && n < cap; ++div) {
+        if (p.C % div) continue;
         const int CC = p.C / div;
-        if (CC % 16) continue;
+        if (CC % 16 || (div > 8 && CC != 16)) continue;
         for (int nq = 1; nq <= 4 && n < cap; ++nq) {
             if (nq > oc32 || (nq == 3 && oc32 != 3)) continue;  // 3 subtiles only for 65..96 channels
             for (int nw : {4, 8})

@@ -65,6 +65,7 @@ struct ValueInfo {
     Placement pl;
     int redirect = -1;   // conv output fused into this value (residual add output)
     int cpad = 0;        // physical channels when zero-padded (network input)
+    bool elided = false; // an fp16 conv output consumed only inside its producer's launch (never stored)
 };
 
 struct Root {
@@ -97,6 +98,11 @@ struct ConvState {
     uint32_t* strips = nullptr;   // pg16 at N > 1: the reference's strip amax of the input
     uint32_t* own_slots = nullptr;  // per-tensor int8 whose input slots are incomplete: its own amax pass
     uint64_t w_bytes = 0;         // bytes of w
+    // a 1x1 fp16 conv applied in this 3x3 conv's epilogue (command index), or
+    // the 3x3 conv this 1x1 conv is applied in; f2p: that 1x1's launch
+    // parameters (its input is this conv's output, which is not stored)
+    int fused_1x1 = -1, fused_into = -1;
+    ConvParams f2p{};
     // sibling pair (this conv first): weights and bias of both convs, rows of
     // this conv then the sibling's, built from the w of each named here
     void* w_pair = nullptr;
@@ -119,6 +125,14 @@ struct Step {
     // runs can change after the step is built: measured tile choices)
     std::string head, tail;
     std::function<std::string()> family;
+};
+
+// Schedule of a network measured at load: sibling convs as one launch, lane
+// count, head 1x1 convs fused into their 3x3 producers.
+struct Schedule {
+    int first = 1;   // sibling pairs in one launch
+    int second = 1;  // lanes
+    int fuse = 0;    // head 3x3 + 1x1 pairs in one launch
 };
 
 // A conv whose kernel choice is measured: its launch reads p (the choice
@@ -144,6 +158,7 @@ struct PlanStats {
     uint32_t late_concat_conv1x1 = 0;   // concats placed in place and read whole by a 1x1 conv
     uint32_t paired_conv3x3 = 0;        // two 3x3 convs of one input computed by one launch
     uint32_t tail_residual = 0;         // residual adds in a conv epilogue
+    uint32_t head_final_conv = 0;       // 1x1 convs applied in the preceding 3x3 conv's epilogue
     uint32_t conv1x1 = 0, spatial3x3 = 0, pack4_3x3 = 0, igemm3x3 = 0, igemm3x3_40 = 0, igemm3x3_20 = 0,
              igemm3x3_10 = 0;
     uint32_t exact_40_64x64 = 0, exact_20_64x64 = 0, exact_10_128x128 = 0, exact_20_128x64 = 0,
@@ -187,6 +202,8 @@ struct AexrtYoloModel {
     // conv's output channels in one root (one launch computes both), or -1
     std::vector<int> sibling;
     bool merge_siblings = true;  // sibling pairs run as one launch (measured at load)
+    bool fuse_1x1 = false;       // head 3x3 + 1x1 pairs run as one launch (measured at load)
+    int fusable_1x1 = 0;         // such pairs in the plan
     std::vector<Step> steps;
     std::vector<CopyJob> copies;
     std::vector<void*> allocations;
@@ -206,8 +223,8 @@ struct AexrtYoloModel {
     // "cmd <index> <shape key>" -> choice measured in the network (the shape key
     // keeps a cached choice from applying to the same command at another batch)
     std::map<std::string, ConvChoice> refined;
-    // "schedule <input dims> <commands>" -> (sibling convs as one launch, lane count) measured at load
-    std::map<std::string, std::pair<int, int>> schedules;
+    // "schedule <input dims> <commands>" -> schedule measured at load
+    std::map<std::string, Schedule> schedules;
     std::string tune_cache;                    // AEXRT_HIP_TUNE_CACHE file, empty: none
     hipStream_t lane_stream[kLanes] = {};      // capture-time streams of lanes 1..kLanes-1
     int n_lanes = 1;                           // lanes the schedule uses (measured at load)
@@ -429,6 +446,59 @@ void fuse_residuals(AexrtYoloModel* m) {
             break;
         }
     }
+}
+
+bool is_f32(AexrtYoloModel* m, int v);
+AexrtConv2DDesc desc_of(const EngineCommand& c);
+
+// The last two convs of each YOLO head branch, 3x3 SiLU then a 1x1 of its
+// output (its only consumer), both fp16: the 1x1 runs in the 3x3 conv's
+// epilogue on the 32x32-MFMA kernel (every 3x3 output channel of a position
+// in one block, so at most 96), and the 3x3 output is never stored.
+// Sets the pairs for m->fuse_1x1 (clears them when off); returns the number of
+// pairs the plan has with fusion on.
+int fuse_head_1x1(AexrtYoloModel* m) {
+    const Engine& e = m->eng;
+    auto& V = m->vals;
+    for (size_t ci = 0; ci < e.commands.size(); ++ci) {
+        ConvState& cs = m->convs[ci];
+        if (cs.fused_1x1 >= 0) V[e.commands[ci].output].elided = false;
+        cs.fused_1x1 = cs.fused_into = -1;
+    }
+    int pairs = 0;
+    for (size_t ci = 0; ci < e.commands.size(); ++ci) {
+        ConvState& cs = m->convs[ci];
+        const EngineCommand& c = e.commands[ci];
+        if (!cs.is_conv || c.kind != kCmdConvSilu || cs.fused_residual || cs.pg16 || cs.fused_into >= 0 ||
+            is_int8_algorithm(cs.algorithm) || is_winograd_algorithm(cs.algorithm) || m->sibling[ci] >= 0)
+            continue;
+        const AexrtConv2DDesc d = desc_of(c);
+        const ValueInfo& x = V[c.inputs[0]];
+        const ValueInfo& y = V[c.output];
+        if (d.kernel_h != 3 || d.kernel_w != 3 || d.stride_h != 1 || d.pad_top != 1 || d.in_channels % 16 ||
+            d.out_channels > 96 || x.is_input || y.consumers.size() != 1 || y.redirect >= 0 || y.rank != 4 ||
+            c.output == e.manifest.output_value)
+            continue;
+        bool paired = false;
+        for (int s2 : m->sibling) paired = paired || s2 == (int)ci;
+        if (paired) continue;
+        const int cj = y.consumers[0];
+        const ConvState& cn = m->convs[cj];
+        const EngineCommand& n = e.commands[cj];
+        if (!cn.is_conv || cn.fused_residual || cn.pg16 || is_int8_algorithm(cn.algorithm) ||
+            is_winograd_algorithm(cn.algorithm) || n.inputs[0] != c.output || m->sibling[cj] >= 0)
+            continue;
+        const AexrtConv2DDesc d2 = desc_of(n);
+        if (d2.kernel_h != 1 || d2.kernel_w != 1 || d2.stride_h != 1 || d2.pad_top != 0 || d2.out_channels > 96 ||
+            d2.out_channels % 8)
+            continue;
+        ++pairs;
+        if (!m->fuse_1x1) continue;
+        cs.fused_1x1 = cj;
+        m->convs[cj].fused_into = (int)ci;
+        V[c.output].elided = true;
+    }
+    return pairs;
 }
 
 bool is_fused_add(AexrtYoloModel* m, size_t ci) {
@@ -898,7 +968,14 @@ std::string tune_key(const ConvParams& p, bool int8) {
                   p.flags, p.loader, p.N, p.H, p.W, p.C, p.OC, p.KH, p.KW, p.S, p.P, p.OH, p.OW,
                   (long long)p.x_nstride, p.x_cstride, (long long)p.y_nstride, p.y_cstride, p.res ? 1 : 0,
                   p.acc_out ? 1 : 0, p.x_slots.stripes);
-    return buf;
+    std::string k = buf;
+    if (p.fuse_1x1) {
+        // the fused 1x1: its output channels, flags and output view
+        std::snprintf(buf, sizeof(buf), "|f%d,%d,%lld,%d", p.fuse_1x1->OC, p.fuse_1x1->flags,
+                      (long long)p.fuse_1x1->y_nstride, p.fuse_1x1->y_cstride);
+        k += buf;
+    }
+    return k;
 }
 
 bool same_choice(const ConvChoice& a, const ConvChoice& b) {
@@ -924,7 +1001,7 @@ void load_tune_cache(AexrtYoloModel* m) {
         if (line.compare(0, 4, "cmd ") == 0)
             m->refined[line.substr(0, tab)] = c;  // a conv's choice measured in the network
         else if (line.compare(0, 9, "schedule ") == 0)
-            m->schedules[line.substr(0, tab)] = {c.kind, c.jn};  // merge flag, lanes
+            m->schedules[line.substr(0, tab)] = Schedule{c.kind, c.jn, c.pw};  // merge flag, lanes, fusion
         else
             m->tuned[line.substr(0, tab)] = c;
     }
@@ -940,7 +1017,7 @@ void save_tune_cache(AexrtYoloModel* m) {
         };
         for (const auto& [key, c] : m->tuned) put(key, c);
         for (const auto& [key, c] : m->refined) put(key, c);
-        for (const auto& [key, v] : m->schedules) put(key, ConvChoice{v.first, v.second, 0, 0, 0, 0, 0, 0});
+        for (const auto& [key, v] : m->schedules) put(key, ConvChoice{v.first, v.second, v.fuse, 0, 0, 0, 0, 0});
         if (!f) return;
     }
     std::rename(tmp.c_str(), m->tune_cache.c_str());
@@ -1072,9 +1149,12 @@ std::string refined_key(size_t ci, uint32_t alg, const ConvParams& p, bool int8)
 // the network first, else its shape's isolated measurement; otherwise the
 // heuristics (choice kind 0).
 void apply_cached_choice(AexrtYoloModel* m, size_t ci, uint32_t alg, ConvParams& p, bool int8) {
-    if (m->tune_cache.empty()) return;
     ConvChoice all[128];
     const int na = enumerate_conv_choices(p, int8, all, 128);
+    // a fused 1x1 runs on the 32x32-MFMA kernel only: without a measured
+    // choice, the first tile that fits
+    if (p.fuse_1x1 && na > 0) p.choice = all[0];
+    if (m->tune_cache.empty()) return;
     auto offered = [&](const ConvChoice& c) {
         for (int k = 0; k < na; ++k)
             if (same_choice(all[k], c)) return true;
@@ -1207,6 +1287,44 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                                        pair ? cs.bias_pair : cs.bias, cs.fused_residual ? &rvw : nullptr, yvw, nullptr,
                                        p, why))
                     return fail(m, "command " + std::to_string(ci) + ": " + why);
+                int f2v = -1;  // output value of a 1x1 conv fused into this conv's epilogue
+                if (cs.fused_1x1 >= 0) {
+                    // fused only where a 32x32-MFMA tile holds every output channel of the
+                    // 3x3 conv (its resident weights and windows fit LDS); otherwise both
+                    // convs run on their own and the 3x3 output is stored
+                    ConvParams probe = p;
+                    ConvParams probe2 = p;
+                    probe2.C = (int)d.out_channels;
+                    probe2.OC = (int)desc_of(e.commands[cs.fused_1x1]).out_channels;
+                    probe2.OCp = (probe2.OC + 15) / 16 * 16;
+                    probe2.Kp = (probe2.C + 63) / 64 * 64;
+                    probe2.KH = probe2.KW = 1;
+                    probe2.S = 1;
+                    probe2.P = 0;
+                    probe2.H = p.OH;
+                    probe2.W = p.OW;
+                    probe2.flags = 0;
+                    probe.fuse_1x1 = &probe2;
+                    ConvChoice none[4];
+                    if (enumerate_m32_choices(probe, false, none, 4) == 0) {
+                        m->convs[cs.fused_1x1].fused_into = -1;
+                        cs.fused_1x1 = -1;
+                        V[c.output].elided = false;
+                    }
+                }
+                if (cs.fused_1x1 >= 0) {
+                    const int cj = cs.fused_1x1;
+                    const ConvState& cn = m->convs[cj];
+                    const EngineCommand& n = e.commands[cj];
+                    const uint32_t flags2 = (n.kind == kCmdConvSilu ? AEXRT_HIP_CONV_SILU : 0u) |
+                                            (is_f32(m, cn.out_value) ? AEXRT_HIP_CONV_OUT_F32 : 0u);
+                    if (!build_conv_params(conv_desc_padded(m, cj), cn.algorithm, flags2, yvw, cn.w, nullptr, cn.bias,
+                                           nullptr, view_of(m, cn.out_value), nullptr, cs.f2p, why))
+                        return fail(m, "command " + std::to_string(cj) + " (fused 1x1): " + why);
+                    p.fuse_1x1 = &cs.f2p;
+                    f2v = cn.out_value;
+                    done[cj] = true;
+                }
                 const uint32_t alg = cs.algorithm;
                 std::function<hipError_t(hipStream_t)> pre;
                 if (own_pass) {
@@ -1303,7 +1421,8 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                 st.family = family;
                 if (!(m->vals[xv].is_input && m->input_nchw_direct)) st.reads.push_back(V[xv].pl.root);
                 if (cs.fused_residual) st.reads.push_back(V[cs.residual_value].pl.root);
-                st.writes = {V[yv].pl.root};
+                st.writes = {V[f2v >= 0 ? f2v : yv].pl.root};
+                if (f2v >= 0) st.tail = " then 1x1 cmd#" + std::to_string(e.src_cmd[cs.fused_1x1]);
                 if (pair) {
                     done[sib] = true;
                     st.tail = " + cmd#" + std::to_string(e.src_cmd[sib]);
@@ -1715,11 +1834,11 @@ void compute_stats(AexrtYoloModel* m) {
         const std::string f = x.family();
         const uint8_t k = f.rfind("conv_int8_dynamic", 0) == 0 ? 3
                           : (f.rfind("conv3x3_halo", 0) == 0 || f.rfind("conv3x3_wide", 0) == 0 ||
-                             f.rfind("conv3x3_stem", 0) == 0)
+                             f.rfind("conv3x3_stem", 0) == 0 || f.rfind("conv3x3_m32", 0) == 0)
                               ? 2
                               : 1;
         conv_kind[x.cmd] = k;
-        if (!x.tail.empty()) {
+        if (x.tail.rfind(" + cmd#", 0) == 0) {  // a sibling pair in one launch
             st.paired_conv3x3 += desc_of(e.commands[x.cmd]).kernel_h == 3;
             if (m->sibling[x.cmd] >= 0) conv_kind[m->sibling[x.cmd]] = k;
         }
@@ -1738,6 +1857,7 @@ void compute_stats(AexrtYoloModel* m) {
         const ConvState& cs = m->convs[ci];
         if (!cs.is_conv) continue;
         st.tail_residual += cs.fused_residual;
+        st.head_final_conv += cs.fused_1x1 >= 0;
         st.native_fp16 += !is_int8_algorithm(cs.algorithm);
         const AexrtConv2DDesc d = desc_of(c);
         if (d.kernel_h == 1) {
@@ -1783,6 +1903,8 @@ bool build_model(AexrtYoloModel* m) {
         set_int8_mode(m, ci);
     }
     if (!plan_memory(m, m->copies)) return false;
+    m->fuse_1x1 = false;
+    m->fusable_1x1 = fuse_head_1x1(m);
     mark_slot_readers(m);
     // arena
     size_t total = 0;
@@ -1830,7 +1952,13 @@ bool build_model(AexrtYoloModel* m) {
     const char* lanes = std::getenv("AEXRT_HIP_LANES");
     const bool fixed_lanes = lanes && lanes[0] >= '1' && lanes[0] <= '9';
     const bool pairs = std::any_of(m->sibling.begin(), m->sibling.end(), [](int s) { return s >= 0; });
-    const int variants = pairs && m->autotune && m->use_graph ? 2 : 1;
+    // AEXRT_HIP_FUSE_1X1=0 / 1: head 3x3 + 1x1 pairs never / always in one launch; otherwise
+    // both are measured (with autotuning) or the cached schedule's choice is taken
+    const char* f1 = std::getenv("AEXRT_HIP_FUSE_1X1");
+    const int fuse_forced = f1 && (f1[0] == '0' || f1[0] == '1') ? f1[0] - '0' : -1;
+    const bool fuse_choice = m->fusable_1x1 > 0 && fuse_forced < 0 && m->autotune && m->use_graph;
+    const int merge_variants = pairs && m->autotune && m->use_graph ? 2 : 1;
+    const int variants = merge_variants * (fuse_choice ? 2 : 1);
     // without measurement, a schedule cached for this network (same input and
     // command count) is reused
     const ValueInfo& xin = m->vals[e.manifest.input_value];
@@ -1840,10 +1968,18 @@ bool build_model(AexrtYoloModel* m) {
     const auto cached_sched = m->schedules.find(skey);
     const bool use_cached_sched = !m->autotune && cached_sched != m->schedules.end();
     float best_ms = 0.0f;
-    bool best_merge = true;
+    bool best_merge = true, best_fuse = false;
     int best_lanes = 1;
+    // the schedule cache keeps (merge, lanes, fuse) in a choice's (kind, jn, pw)
+    auto fuse_for = [&](int k) {
+        if (fuse_forced >= 0) return fuse_forced != 0;
+        if (use_cached_sched) return cached_sched->second.fuse != 0;
+        return fuse_choice ? k / merge_variants == 0 : false;
+    };
     for (int k = 0; k < variants; ++k) {
-        m->merge_siblings = use_cached_sched ? cached_sched->second.first != 0 : k == 0;
+        m->merge_siblings = use_cached_sched ? cached_sched->second.first != 0 : k % merge_variants == 0;
+        m->fuse_1x1 = fuse_for(k);
+        fuse_head_1x1(m);
         m->n_lanes = 1;
         if (!build_steps(m, m->copies)) return false;
         if (m->autotune && !refine_in_context(m)) return false;
@@ -1858,12 +1994,15 @@ bool build_model(AexrtYoloModel* m) {
         if (k == 0 || ms < best_ms) {
             best_ms = ms;
             best_merge = m->merge_siblings;
+            best_fuse = m->fuse_1x1;
             best_lanes = m->n_lanes;
         }
     }
-    if (best_merge != m->merge_siblings) {
+    if (best_merge != m->merge_siblings || best_fuse != m->fuse_1x1) {
         // the choices of this build were measured with the first: cached in m->refined
         m->merge_siblings = best_merge;
+        m->fuse_1x1 = best_fuse;
+        fuse_head_1x1(m);
         m->n_lanes = 1;
         if (!build_steps(m, m->copies)) return false;
         if (m->autotune && !refine_in_context(m)) return false;
@@ -1876,9 +2015,10 @@ bool build_model(AexrtYoloModel* m) {
         schedule_steps(m);
         drop_graph(m);
     }
-    if (m->autotune) m->schedules[skey] = {m->merge_siblings ? 1 : 0, m->n_lanes};
+    if (m->autotune) m->schedules[skey] = Schedule{m->merge_siblings ? 1 : 0, m->n_lanes, m->fuse_1x1 ? 1 : 0};
     if (m->tune_log && variants > 1)
-        std::fprintf(stderr, "aexrt sibling convs: %s\n", best_merge ? "one launch" : "two launches");
+        std::fprintf(stderr, "aexrt sibling convs: %s, head 1x1 convs: %s\n", best_merge ? "one launch" : "two launches",
+                     best_fuse ? "fused" : "on their own");
     if (m->autotune && !m->tune_cache.empty()) save_tune_cache(m);
     const char* prof = std::getenv("AEXRT_HIP_PROFILE");
     m->profile = prof && prof[0] == '1';
@@ -2122,7 +2262,7 @@ uint32_t aexrt_yolo_paired_conv3x3_fusion_count(AexrtYoloModel* m) { return m ? 
 uint32_t aexrt_yolo_c2f_bottleneck_superblock_count(AexrtYoloModel* m) { (void)m; return 0; }
 uint32_t aexrt_yolo_c2f_tail_residual_fusion_count(AexrtYoloModel* m) { return m ? m->stats.tail_residual : 0; }
 uint32_t aexrt_yolo_head_fusion_enabled(AexrtYoloModel* m) { (void)m; return 0; }
-uint32_t aexrt_yolo_head_final_conv_fusion_enabled(AexrtYoloModel* m) { (void)m; return 0; }
+uint32_t aexrt_yolo_head_final_conv_fusion_enabled(AexrtYoloModel* m) { return m && m->stats.head_final_conv ? 1u : 0u; }
 uint32_t aexrt_yolo_tileflow_conv1x1_count(AexrtYoloModel* m) { return m ? m->stats.conv1x1 : 0; }
 uint32_t aexrt_yolo_tileflow_3x3_spatial_count(AexrtYoloModel* m) { return m ? m->stats.spatial3x3 : 0; }
 uint32_t aexrt_yolo_tileflow_3x3_pack4_count(AexrtYoloModel* m) { return m ? m->stats.pack4_3x3 : 0; }
@@ -2300,7 +2440,7 @@ int aexrt_yolo_value_info(AexrtYoloModel* m, uint32_t value_id, uint32_t* out4) 
     out4[1] = (uint32_t)x.C;
     out4[2] = (uint32_t)x.H;
     out4[3] = (uint32_t)x.W;
-    if (x.is_const || x.redirect >= 0 || !(x.pl.valid || x.is_input)) return 0;
+    if (x.is_const || x.redirect >= 0 || x.elided || !(x.pl.valid || x.is_input)) return 0;
     return x.rank;
 }
 

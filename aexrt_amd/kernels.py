@@ -286,7 +286,8 @@ def conv2d(pc: PreparedConv, x, y, *, flags: int = SILU, x_slots=None, y_slots=N
 def conv2d_fused_1x1(pc: PreparedConv, pc2: PreparedConv, x, y2, *, flags2: int = 0, y2_slots=None,
                      stream=None) -> None:
     """fp16 3x3 SiLU conv ``pc`` with the 1x1 conv ``pc2`` of its output fused into its epilogue:
-    y2 = conv1x1(fp16(silu(conv3x3(x)))) (SiLU too with flags2 = SILU); the 3x3 output is not stored."""
+    y2 = conv1x1(fp16(silu(conv3x3(x)))) (SiLU too with flags2 SILU, fp32 y2 with OUT_F32); the 3x3
+    output is not stored."""
     d, d2 = ConvDesc.from_params(pc.params), ConvDesc.from_params(pc2.params)
     xv, yv = view(x), view(y2, y2_slots)
     check(_lib.lib().aexrt_hip_conv2d_fused_1x1(

@@ -123,21 +123,24 @@ def conv_work(params, int8: bool):
 
 
 def parse_label(label: str):
-    """(engine command index, kernel instance, int8, sibling command indices) of a conv step
-    label "cmd#N KIND ... alg=... kernel=<instance> <tile>[ + cmd#M]"; None for other steps."""
+    """(engine command index, kernel instance, int8, sibling command indices, fused 1x1 command
+    indices) of a conv step label "cmd#N KIND ... alg=... kernel=<instance> <tile>[ + cmd#M]
+    [ then 1x1 cmd#K]"; None for other steps."""
     if not label.startswith("cmd#") or " kernel=" not in label:
         return None
     ci = int(label.split()[0][4:])
     head, rest = label.split(" kernel=", 1)
+    rest, *fused = rest.split(" then 1x1 cmd#")
     parts = rest.split(" + cmd#")
     instance = parts[0].split(" ")[0]
     sibs = [int(p.split()[0]) for p in parts[1:]]
-    return ci, instance, "alg=int8" in head, sibs
+    return ci, instance, "alg=int8" in head, sibs, [int(f.split()[0]) for f in fused]
 
 
 def launch_work(label: str, replay):
-    """(ops, algorithmic bytes) of one conv launch (a sibling pair reads its input once)."""
-    ci, _, int8, sibs = parse_label(label)
+    """(ops, algorithmic bytes) of one conv launch (a sibling pair reads its input once; a fused
+    1x1 reads the 3x3 output in registers, so neither that output nor its read is HBM traffic)."""
+    ci, _, int8, sibs, fused = parse_label(label)
     cmds = replay["commands"]
     ops, nbytes = conv_work(cmds[ci]["params"], int8)
     for s in sibs:
@@ -146,6 +149,12 @@ def launch_work(label: str, replay):
         b, ic, ih, iw = (int(v) for v in p[:4])
         ops += s_ops
         nbytes += s_bytes - b * ic * ih * iw * (2 if ic > 3 else 4)
+    for f in fused:
+        p = cmds[f]["params"]
+        f_ops, f_bytes = conv_work(p, False)
+        b, ic, ih, iw = (int(v) for v in p[:4])
+        ops += f_ops
+        nbytes += f_bytes - 2 * b * ic * ih * iw * 2  # the 3x3 output, written and read, is neither
     return ops, nbytes
 
 
@@ -203,7 +212,7 @@ def analyse(steps, replay, batch: int):
         p = parse_label(label)
         if p is None:
             continue
-        _, inst, int8, _ = p
+        _, inst, int8, _, _ = p
         ops, nbytes = launch_work(label, replay)
         e = by_inst.setdefault(inst, dict(ms=0.0, ops=0, bytes=0, labels=[], int8=int8))
         e["ms"] += ms

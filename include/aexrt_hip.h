@@ -312,7 +312,8 @@ int aexrt_hip_set_conv3x3_halo(int32_t mode, int32_t jn, int32_t pw, int32_t tr,
 
 /* fp16 3x3 SiLU conv (algorithm 5 weights) with a 1x1 conv of its output fused
  * into the epilogue: y2 = conv1x1(fp16(silu(conv3x3(x) + bias)), weight2) +
- * bias2 (SiLU when flags2 has it); the 3x3 output is never stored.  The
+ * bias2 (SiLU when flags2 has it, fp32 y2 with OUT_F32); the 3x3 output is
+ * never stored.  The
  * YOLOv8 head's last two convs of each branch (the reference fuses its head
  * into one replay group, fusion kinds 4/5 of src/aexrt/engine.py:78-79).
  * Runs on the 32x32-MFMA kernel with a tile covering every 3x3 output channel

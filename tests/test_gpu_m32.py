@@ -202,11 +202,13 @@ FUSED = [
     (2, 80, 20, 20, 80, 80, (5, 3, 1, 3, 20, 16), False, None),   # class branch: 80 channels, 96-channel block
     (2, 64, 10, 10, 64, 64, (6, 2, 1, 10, 10, 64), True, (16, 80, 96)),  # 8 waves, SiLU, into a channel slice
     (1, 80, 13, 11, 80, 64, (5, 3, 2, 13, 11, 16), False, None),  # ragged map, 1x1 to fewer channels
+    (2, 80, 20, 20, 80, 80, (5, 3, 1, 3, 20, 16), "f32", None),   # fp32 output (the head's raw output)
 ]
 
 
 @pytest.mark.parametrize("case", FUSED, ids=[f"c{t[1]}_{t[2]}x{t[3]}_oc{t[4]}_to{t[5]}_{'forced' if t[6] else 'auto'}"
-                                             f"{'_silu' if t[7] else ''}{'_slice' if t[8] else ''}" for t in FUSED])
+                                             f"{'_' + (t[7] if isinstance(t[7], str) else 'silu') if t[7] else ''}"
+                                             f"{'_slice' if t[8] else ''}" for t in FUSED])
 def test_m32_fused_1x1(cuda, case):
     """A 3x3 SiLU conv with the following 1x1 conv in its epilogue: against the oracle's two convs
     with the 3x3 output rounded to fp16 in between (what the unfused pair stores and reads)."""
@@ -224,13 +226,15 @@ def test_m32_fused_1x1(cuda, case):
     pc = K.prepare_conv(desc, 5, K.SRC_RAW_F32, wt, b, device=cuda)
     pc2 = K.prepare_conv(desc2, 5, K.SRC_RAW_F32, w2, b2, device=cuda)
     lo, hi, width = sl if sl else (0, oc2, oc2)
-    big = torch.zeros((n, h, w, width), dtype=torch.float16, device=cuda)
+    f32 = silu2 == "f32"
+    silu2 = silu2 is True
+    big = torch.zeros((n, h, w, width), dtype=torch.float32 if f32 else torch.float16, device=cuda)
     slots = K.new_slots(width, cuda)
     if tile:
         K.set_conv3x3_halo(*tile)
     try:
-        K.conv2d_fused_1x1(pc, pc2, _dev_nhwc(x, cuda), big[..., lo:hi], flags2=K.SILU if silu2 else 0,
-                           y2_slots=slots[lo // 16:hi // 16])
+        K.conv2d_fused_1x1(pc, pc2, _dev_nhwc(x, cuda), big[..., lo:hi],
+                           flags2=(K.SILU if silu2 else 0) | (K.OUT_F32 if f32 else 0), y2_slots=slots[lo // 16:hi // 16])
     finally:
         K.set_conv3x3_halo(K.HALO_AUTO)
     torch.cuda.synchronize()
@@ -238,7 +242,7 @@ def test_m32_fused_1x1(cuda, case):
     y1 = O.round_f16(O.cpu_conv2d(x, O.round_f16(wt), b, desc, silu=True))
     y2 = O.cpu_conv2d(y1, O.round_f16(w2), b2, desc2, silu=silu2)
     assert np.isfinite(got).all()
-    err, allowed = tol_range(y2, got[:, lo:hi], FP16_TOL)
+    err, allowed = tol_range(y2, got[:, lo:hi], FP32_TOL if f32 else FP16_TOL)
     assert err <= allowed, (err, allowed)
     assert not got[:, :lo].any() and not got[:, hi:].any()
     np.testing.assert_array_equal(_u32(slots)[lo // 16:hi // 16], _slots_of(got[:, lo:hi], oc2))

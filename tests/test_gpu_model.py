@@ -72,6 +72,8 @@ def _layer_check(model: NativeHipYoloModel, graph: Graph, plan: dict, tol=1e-2, 
         else:
             xin, wid, bid = c["inputs"]
             rank_x, _ = model.value_info(xin)
+            if rank_x == 0:  # a 1x1 conv fused into its producer's launch: checked with the producer
+                continue
             x = model.value(xin)
             if x.ndim == 3:
                 continue
@@ -86,7 +88,19 @@ def _layer_check(model: NativeHipYoloModel, graph: Graph, plan: dict, tol=1e-2, 
         rank_y, _ = model.value_info(out)
         conv_ref = y_ref
         fused = rank_y == 0
-        if fused:  # fused into the residual add that consumes it
+        nxt = cmds[consumers[out][0]] if fused else None
+        convs_in_check = 1
+        if fused and nxt["kind"] in ("CONV", "CONV_SILU"):
+            # a 1x1 conv applied in this conv's epilogue: the pair against the oracle's two convs
+            # with this conv's output rounded to fp16 in between
+            w2 = names[nxt["inputs"][1]]
+            node2 = convs[w2.rsplit(".w", 1)[0]]
+            y_ref = ON.conv_layer(O.round_f16(y_ref), graph.constants[w2], graph.constants[names[nxt["inputs"][2]]],
+                                  node2.attrs, int8=False, silu=nxt["kind"] == "CONV_SILU", threads=threads)
+            out = nxt["output"]
+            fused = False
+            convs_in_check = 2
+        elif fused:  # fused into the residual add that consumes it
             add = cmds[consumers[out][0]]
             other = [v for v in add["inputs"] if v != out][0]
             conv_ref = O.round_f16(y_ref)
@@ -106,7 +120,7 @@ def _layer_check(model: NativeHipYoloModel, graph: Graph, plan: dict, tol=1e-2, 
             ratio = err / max(allowed, 1e-30)
             assert ratio <= 1.0, (i, names[out], current[i], err, allowed)
         worst = max(worst, ratio)
-        checked += 1
+        checked += convs_in_check
     return checked, worst
 
 
@@ -503,9 +517,11 @@ def test_int8_conv_on_a_concat_with_a_misaligned_slice(cuda):
         assert checked == 3
 
 
-def test_plan_counters_describe_the_prepared_step_list(cuda):
+def test_plan_counters_describe_the_prepared_step_list(cuda, monkeypatch):
     """The reference's counters (native/aexrt.h:313-385) for YOLOv8n-320 at batch 2: every command
-    supported, the fused residual adds, the paired head convs, convs per kernel family adding up."""
+    supported, the fused residual adds, the paired head convs, the head's 1x1 convs in their 3x3
+    producers' epilogues, convs per kernel family adding up."""
+    monkeypatch.setenv("AEXRT_HIP_FUSE_1X1", "1")
     g, names, plan, data = _yolo_engine(2, 320)
     with NativeHipYoloModel(data) as m:
         c = m.counter
@@ -516,6 +532,7 @@ def test_plan_counters_describe_the_prepared_step_list(cuda):
         n_add = sum(1 for cmd in plan["replay"]["commands"] if cmd["kind"] == "BINARY")
         assert c("c2f_tail_residual_fusion_count") == n_add == 6
         assert c("paired_conv3x3_fusion_count") in (0, 3)
+        assert c("head_final_conv_fusion_enabled") == 1
         n_conv = sum(1 for cmd in plan["replay"]["commands"] if cmd["kind"] in ("CONV", "CONV_SILU"))
         assert c("tileflow_conv1x1_count") + c("tileflow_3x3_spatial_count") + c("tileflow_3x3_pack4_count") + \
             c("tileflow_3x3_implicit_gemm_count") == n_conv == 63
@@ -549,4 +566,33 @@ def test_inference_session_hip_backend_matches_the_oracle(cuda):
     ref8 = ON.run_graph(g, x, int8_convs=convs)[g.outputs[0]]
     got8 = np.asarray(w8a8.run({name: x})[g.outputs[0]]).reshape(ref8.shape)
     err, allowed = tol_range(ref8, got8, 1e-2)
+    assert err <= allowed, (err, allowed)
+
+
+def test_head_1x1_convs_fused_and_on_their_own(cuda, monkeypatch):
+    """Each head branch's last two convs (3x3 SiLU, then a 1x1 of its output) run as one launch
+    (the 1x1 in the 3x3 kernel's epilogue, the 3x3 output never stored) or as two; every conv
+    matches the oracle either way (a fused pair against the oracle's two convs with the 3x3
+    output rounded to fp16 in between), and the raw head outputs of the two agree."""
+    g = build_yolov8n(batch=2, imgsz=160, seed=4)
+    algo = E.w8a8_algo_map(E.lower_graph(g), g.metadata["int8_convs"].split(","))
+    plan = E.compile_plan(g, precision="fp16", algo_overrides=algo)
+    data = E.build_aexrt_engine(g, precision="fp16", algo_overrides=algo, classes=80)
+    x = np.random.default_rng(6).random((2, 3, 160, 160)).astype(np.float32)
+    outs = {}
+    for fuse in ("1", "0"):
+        monkeypatch.setenv("AEXRT_HIP_FUSE_1X1", fuse)
+        with NativeHipYoloModel(data) as m:
+            m.set_profiling(True)
+            m.run(x)
+            m.set_profiling(False)
+            fused = [lab for lab, _ in m.profile_events() if " then 1x1 cmd#" in lab]
+            assert len(fused) == (6 if fuse == "1" else 0), fused
+            assert all("conv3x3_m32_kernel<false," in lab and ",true>" in lab for lab in fused), fused
+            assert m.counter("head_final_conv_fusion_enabled") == (1 if fuse == "1" else 0)
+            checked, _ = _layer_check(m, g, plan)
+            assert checked == 63
+            m.run(x)
+            outs[fuse] = m.output()
+    err, allowed = tol_range(outs["0"], outs["1"], 1e-2)
     assert err <= allowed, (err, allowed)
