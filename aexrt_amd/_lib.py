@@ -133,6 +133,7 @@ _SIGS = {
     "aexrt_hip_set_conv_tile": (c_int, [c_int32, c_int32, c_int32]),
     "aexrt_hip_set_conv3x3_halo": (c_int, [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32]),
     "aexrt_hip_set_conv_stem": (c_int, [c_int32, c_int32]),
+    "aexrt_hip_set_conv1x1_stream": (c_int, [c_int32, c_int32, c_int32]),
     "aexrt_hip_fill_u32": (c_int, [_vp, c_uint64, c_uint32, _vp]),
     "aexrt_hip_nchw_f32_to_nhwc": (c_int, [_vp, c_uint32, c_uint32, c_uint32, POINTER(TensorView), _vp]),
     "aexrt_hip_nhwc_to_nchw_f32": (c_int, [POINTER(TensorView), c_uint32, c_uint32, c_uint32, c_uint32, _vp,

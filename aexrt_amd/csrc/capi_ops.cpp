@@ -204,6 +204,14 @@ int aexrt_hip_set_conv_stem(int32_t mode, int32_t tr) {
     return 1;
 }
 
+int aexrt_hip_set_conv1x1_stream(int32_t mode, int32_t jq, int32_t pq) {
+    if (!set_conv1x1_stream(mode != 0, jq, pq)) {
+        set_error("set_conv1x1_stream: no kernel instance for this tile");
+        return 0;
+    }
+    return 1;
+}
+
 int aexrt_hip_conv_weight_bytes(const AexrtConv2DDesc* desc, uint32_t algorithm, uint64_t* out_nbytes) {
     if (!desc || !out_nbytes) {
         set_error("conv_weight_bytes: null argument");

@@ -231,6 +231,20 @@ hipError_t launch_conv_igemm(const ConvParams& p0, bool int8, hipStream_t stream
         p.fd_c = make_fastdiv((uint32_t)p.C);
         p.fd_kw = make_fastdiv((uint32_t)p.KW);
         hipError_t e = hipErrorNotSupported;
+        if (p.choice.kind == 0 && int8 && p.KH == 1 && p.KW == 1) {
+            ConvChoice forced;
+            if (forced_s1x1_choice(forced)) {
+                p.choice = forced;  // a forced tile that does not fit is an error
+                e = launch_conv_s1x1(p, int8, epi, stream);
+                if (e != hipSuccess) return e;
+                continue;
+            }
+        }
+        if (p.choice.kind == 6) {
+            e = launch_conv_s1x1(p, int8, epi, stream);
+            if (e != hipSuccess) return e;
+            continue;
+        }
         if (p.choice.kind == 0 && !nchw) {
             ConvChoice forced;
             if (forced_m32_choice(forced) && p.KH == 3 && p.KW == 3) {

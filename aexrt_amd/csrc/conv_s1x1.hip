@@ -1,0 +1,111 @@
+// Host side of the streaming 1x1 int8 conv (kernel in conv_s1x1.h): geometry,
+// the forced tile, launch.
+#include <algorithm>
+#include <atomic>
+#include <cstdio>
+
+#include "conv_s1x1.h"
+
+namespace aexrt {
+
+namespace s1x1 {
+AEXRT_S1X1_EXTERN(0)
+AEXRT_S1X1_EXTERN(1)
+}  // namespace s1x1
+
+namespace {
+
+// dynamic LDS of one block (its static arrays aside)
+constexpr int kS1x1LdsBudget = 152 * 1024;
+
+struct S1x1Tile {
+    int jq, pq, np;
+};
+
+// int8 1x1 stride-1 convs on views whose positions are evenly strided, with
+// the SiLU or run-time-flag epilogue and no residual.
+bool s1x1_shape_ok(const ConvParams& p, bool int8) {
+    return int8 && p.loader == kLoaderNhwc && p.KH == 1 && p.KW == 1 && p.S == 1 && p.P == 0 && p.OH == p.H &&
+           p.OW == p.W && p.C % 16 == 0 && p.x_cstride % 8 == 0 && (p.lin & kLinX) && (p.lin & kLinY) &&
+           !(p.flags & kConvResidual) && p.res == nullptr && p.fuse_1x1 == nullptr && p.M < (1 << 24);
+}
+
+bool s1x1_instantiated(int jq, int pq, int np) {
+    if (jq != 1 && jq != 2 && jq != 4 && jq != 8) return false;
+    if (np != 1 && np != 2 && np != 4 && np != 8) return false;
+    if (pq == 1) return true;
+    return pq == 2 && jq <= 4 && np <= 4;
+}
+
+// Fills the geometry of tile (jq, pq) into h and the piece count into t.np;
+// false when it does not fit a kernel instance or the LDS.
+bool s1x1_geometry(S1x1Params& h, S1x1Tile& t) {
+    const ConvParams& p = h.c;
+    h.TP = 64 * t.pq;
+    h.nks = p.Kp / 64;
+    h.c16 = p.C / 16;
+    h.npiece = h.TP * h.c16;
+    const int need = (h.npiece + 255) / 256;
+    t.np = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : need <= 8 ? 8 : 0;
+    if (!t.np || !s1x1_instantiated(t.jq, t.pq, t.np)) return false;
+    const int64_t ntile = ((int64_t)p.M + h.TP - 1) / h.TP;
+    if (ntile > INT32_MAX / 2) return false;
+    h.ntile = (int)ntile;
+    const int ocb = 16 * t.jq;
+    h.wbytes = h.nks * ocb * 64;
+    h.tbytes = h.nks * h.TP * 64;
+    if ((int64_t)h.wbytes + 2 * h.tbytes > kS1x1LdsBudget) return false;
+    h.c.ntn = (p.OCp + ocb - 1) / ocb;
+    h.c.fd_ntn = make_fastdiv((uint32_t)h.c.ntn);
+    h.fd_c16 = make_fastdiv((uint32_t)h.c16);
+    return true;
+}
+
+std::atomic<int> g_s1x1_force{0};  // jq | pq << 8, 0 = off
+
+hipError_t s1x1_launch(const S1x1Params& h, int epi, const S1x1Tile& t, hipStream_t s) {
+    if (LaunchProbe* pr = launch_probe()) {
+        std::snprintf(pr->name, sizeof(pr->name), "conv1x1_stream_kernel<%d,%d,%d,%d>", t.jq, t.pq, t.np, epi);
+        return hipSuccess;
+    }
+    if (epi == igemm::kEpiSilu) return s1x1::s1x1_launch_family<igemm::kEpiSilu>(h, t.jq, t.pq, t.np, s);
+    if (epi == igemm::kEpiAny) return s1x1::s1x1_launch_family<igemm::kEpiAny>(h, t.jq, t.pq, t.np, s);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+bool set_conv1x1_stream(bool on, int jq, int pq) {
+    if (!on) {
+        g_s1x1_force.store(0);
+        return true;
+    }
+    if (!s1x1_instantiated(jq, pq, 1)) return false;
+    g_s1x1_force.store(jq | (pq << 8));
+    return true;
+}
+
+bool forced_s1x1_choice(ConvChoice& c) {
+    const int f = g_s1x1_force.load(std::memory_order_relaxed);
+    if (!f) return false;
+    c = ConvChoice{};
+    c.kind = 6;
+    c.jn = f & 0xFF;
+    c.pw = (f >> 8) & 0xFF;
+    return true;
+}
+
+// One batch slice of a conv with a kind-6 choice (views already inside
+// 32-bit spans, p.lin set).  A choice that does not fit the conv is an error.
+hipError_t launch_conv_s1x1(const ConvParams& p, bool int8, int epi, hipStream_t stream) {
+    if (!s1x1_shape_ok(p, int8) || p.choice.kind != 6) return hipErrorInvalidValue;
+    if (int8 && (p.x_slots.p == nullptr || (int64_t)p.x_slots.stripes * p.x_nslots > igemm::kMaxSlotReads))
+        return hipErrorInvalidValue;
+    S1x1Params h{};
+    h.c = p;
+    S1x1Tile t{p.choice.jn, p.choice.pw, 0};
+    if (!s1x1_geometry(h, t)) return hipErrorInvalidValue;
+    return s1x1_launch(h, epi, t, stream);
+}
+
+}  // namespace aexrt

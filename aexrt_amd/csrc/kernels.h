@@ -168,6 +168,20 @@ hipError_t launch_conv_m32(const ConvParams& p, bool int8, int epi, hipStream_t 
 // without a kernel instance.
 bool set_conv3x3_m32(bool on, int mq, int nq, int tr, int tc, int cc, int nw);
 bool forced_m32_choice(ConvChoice& c);
+// Streaming 1x1 int8 conv (choice kind 6: jn = JQ 16-channel subtiles of the
+// block, pw = PQ 16-position subtiles per wave; C % 16 == 0, positions evenly
+// strided in both views, no residual): weights resident in LDS, every tile's
+// input loaded at once and quantized once into an int8 LDS tile, the next
+// tile in flight during the current one's MFMAs.  epi 0 any flags / 1 SiLU.
+// hipErrorInvalidValue when the choice does not fit the conv.  Not among the
+// load-time candidates (enumerate_conv_choices): the one load that measured it
+// there ended in a host segmentation fault whose cause is not found; it runs
+// only when forced (set_conv1x1_stream).
+hipError_t launch_conv_s1x1(const ConvParams& p, bool int8, int epi, hipStream_t stream);
+// Forces every int8 1x1 conv the kind-0 heuristics would run onto one
+// streaming tile (on = false: off).  False for a tile without an instance.
+bool set_conv1x1_stream(bool on, int jq, int pq);
+bool forced_s1x1_choice(ConvChoice& c);
 // Band kernel of the network's first conv (3x3 pad 1, stride 1/2, fp32 NCHW
 // input of at most 3 channels read directly, fp16 SiLU output, OCp <= 64,
 // W % 4 == 0): whole output rows per tile, one fp16 MFMA per 16 positions and

@@ -223,6 +223,13 @@ def set_conv_stem(mode: int = STEM_AUTO, tr: int = 0) -> None:
     check(_lib.lib().aexrt_hip_set_conv_stem(mode, tr), "set_conv_stem")
 
 
+def set_conv1x1_stream(on: bool = False, jq: int = 0, pq: int = 0) -> None:
+    """Force the streaming 1x1 int8 kernel (jq 16-channel subtiles per block, pq 16-position
+    subtiles per wave) onto every int8 1x1 conv launched without a measured choice; off restores
+    the automatic choice."""
+    check(_lib.lib().aexrt_hip_set_conv1x1_stream(1 if on else 0, jq, pq), "set_conv1x1_stream")
+
+
 def conv_weight_bytes(params: Sequence[int], algorithm: int) -> int:
     d = ConvDesc.from_params(params)
     n = ctypes.c_uint64()

@@ -324,6 +324,15 @@ int aexrt_hip_conv2d_fused_1x1(const AexrtConv2DDesc* desc, uint32_t flags, cons
                                const void* weight, const float* bias, const AexrtConv2DDesc* desc2, uint32_t flags2,
                                const void* weight2, const float* bias2, const AexrtHipTensorView* y2, void* stream);
 
+/* Tuning/test hook, no reference counterpart: mode 1 runs every int8 1x1
+ * stride-1 conv launched without a measured kernel choice on the streaming
+ * 1x1 kernel (weights resident in LDS, each tile's input loaded at once and
+ * quantized once into an int8 LDS tile) with jq 16-channel subtiles per block
+ * (1/2/4/8) and pq 16-position subtiles per wave (1, or 2 with jq <= 4); a
+ * conv that tile does not fit (LDS, views not evenly strided, residual) then
+ * fails.  mode 0 switches it off.  Returns 0 for a tile without an instance. */
+int aexrt_hip_set_conv1x1_stream(int32_t mode, int32_t jq, int32_t pq);
+
 /* Kernel of the network's first conv (3x3 pad 1, stride 1/2, the fp32 NCHW
  * input with at most 3 channels read directly, SiLU, fp16 output; a kernel
  * choice of the reference's replay_conv_algorithm, RT:9424-9500): mode 0

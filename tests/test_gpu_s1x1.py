@@ -1,0 +1,121 @@
+"""Parity of the streaming 1x1 int8 conv kernel on forced tiles, through the op-level C ABI.
+
+The int32 accumulators must equal the oracle's exactly (exact sums of int8 products whatever
+the tile), the stored fp16 outputs must be within one fp16 ulp of the W8A8 oracle, and the
+output amax slots must hold the max |y| of what was stored.  Cases cover ragged position
+tails, channel counts that leave a padded k step (C = 16, 48), several channel blocks with an
+empty half (OC 80 on 64-channel blocks), 1 to 8 input pieces per thread, two position subtiles
+per wave, runs of several tiles per block (the double-buffered LDS tiles), fp32 output without
+SiLU, the SiLU-only instance, and channel-slice input and output views (a concat root's
+layout: positions evenly strided, channel stride wider than the conv).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+from aexrt_amd import kernels as K
+from aexrt_amd import packing
+from tests.helpers import group16_weight, nchw_to_nhwc, nhwc_to_nchw, tol_range
+from tests.test_gpu_ops import FP32_TOL, _run_int8, _u32
+
+pytestmark = pytest.mark.gpu
+
+
+def _ulp16(a):
+    return np.spacing(np.abs(a).astype(np.float16)).astype(np.float64)
+
+
+def _slots_of(y, oc):
+    g = (oc + 15) // 16
+    return np.array([np.float32(np.abs(y[:, k * 16:(k + 1) * 16]).max()).view(np.uint32) for k in range(g)],
+                    dtype=np.uint32)
+
+
+# (n, c, h, w, oc, jq, pq, seed)
+S1X1_CASES = [
+    (2, 32, 7, 9, 32, 2, 1, 401),       # ragged tail: 126 positions in two 64-position tiles
+    (2, 48, 7, 9, 32, 2, 2, 402),       # C = 48: the k step's last 16 channels padded; 2 subtiles per wave
+    (3, 16, 11, 13, 16, 1, 1, 403),     # C = 16, one 16-channel subtile
+    (1, 96, 10, 10, 80, 4, 1, 404),     # OC 80 on 64-channel blocks: the second block is 3/4 empty
+    (2, 192, 20, 20, 64, 4, 1, 405),    # three k steps, 3 of 4 piece rounds per thread
+    (2, 128, 20, 20, 64, 4, 2, 409),    # 2 subtiles per wave, 4 pieces per thread
+    (1, 384, 10, 10, 256, 8, 1, 406),   # six k steps, 8 pieces per thread, two channel blocks
+    (48, 512, 20, 20, 128, 8, 1, 407),  # 128 KB of LDS: one block per CU, runs of 2 tiles per block
+    (24, 32, 80, 80, 32, 2, 1, 408),    # 2400 tiles on at most 2048 resident blocks: runs of 2 tiles
+]
+
+
+@pytest.mark.parametrize("case", S1X1_CASES,
+                         ids=[f"n{t[0]}_c{t[1]}_{t[2]}x{t[3]}_oc{t[4]}_jq{t[5]}_pq{t[6]}" for t in S1X1_CASES])
+def test_s1x1_int8_conv(cuda, case):
+    n, c, h, w, oc, jq, pq, seed = case
+    K.set_conv1x1_stream(True, jq, pq)
+    try:
+        r = _run_int8(cuda, n, c, h, w, oc, 1, 1, seed)
+        np.testing.assert_array_equal(r["acc"], r["acc_ref"])
+        err = np.abs(r["y"].astype(np.float64) - r["y_ref"])
+        assert (err <= _ulp16(r["y_ref"])).all(), float(err.max())
+        np.testing.assert_array_equal(r["slots"], _slots_of(r["y"], oc))
+        # fp32 output without activation
+        r = _run_int8(cuda, n, c, h, w, oc, 1, 1, seed + 50, silu=False, out_f32=True)
+        np.testing.assert_array_equal(r["acc"], r["acc_ref"])
+        err, allowed = tol_range(r["y_ref"], r["y"], FP32_TOL)
+        assert err <= allowed, (err, allowed)
+    finally:
+        K.set_conv1x1_stream(False)
+
+
+# (n, c, h, w, oc, input root width, input channel offset, output root width, output offset, jq, pq, seed)
+S1X1_SLICES = [
+    (2, 64, 20, 20, 64, 128, 64, 192, 64, 4, 1, 421),    # second half of a root -> middle of a concat root
+    (4, 128, 10, 10, 128, 384, 128, 256, 0, 8, 1, 422),  # middle third -> first half
+    (3, 32, 9, 11, 48, 64, 0, 96, 48, 2, 2, 423),        # ragged tail, 48 of 96 output channels
+]
+
+
+@pytest.mark.parametrize("case", S1X1_SLICES,
+                         ids=[f"c{t[1]}of{t[5]}_oc{t[4]}of{t[7]}_jq{t[9]}_pq{t[10]}" for t in S1X1_SLICES])
+def test_s1x1_int8_silu_channel_slices(cuda, case):
+    """The SiLU instance (no accumulator output) reading a channel slice of one root and writing
+    a channel slice of another: the other channels of the output root stay untouched."""
+    import torch
+
+    n, c, h, w, oc, cw, c0, ow_, o0, jq, pq, seed = case
+    rng = np.random.default_rng(seed)
+    xr = rng.standard_normal((n, cw, h, w)).astype(np.float16).astype(np.float32)
+    x = xr[:, c0:c0 + c]
+    wt = group16_weight(rng, oc, c, 1)
+    b = packing.fp16_round(rng.uniform(-0.1, 0.1, oc).astype(np.float32))
+    desc = O.conv_desc(n, c, h, w, oc, 1, 1, 0)
+    pc = K.prepare_conv(desc, 51, K.SRC_LAYOUT_INT8, packing.pack_conv_int8(wt, fp16_engine=True), b, device=cuda)
+    xroot = torch.from_numpy(nchw_to_nhwc(xr.astype(np.float16))).to(cuda)
+    xv = xroot[..., c0:c0 + c]
+    xs = K.new_slots(c, cuda)
+    K.amax_slots(xv, xs)
+    yroot = torch.full((n, h, w, ow_), 7.0, dtype=torch.float16, device=cuda)
+    yv = yroot[..., o0:o0 + oc]
+    ys = K.new_slots(oc, cuda)
+    K.set_conv1x1_stream(True, jq, pq)
+    try:
+        K.conv2d(pc, xv, yv, flags=K.SILU, x_slots=xs, y_slots=ys)
+        torch.cuda.synchronize()
+    finally:
+        K.set_conv1x1_stream(False)
+    _, _, _, _, _, y_ref = O.w8a8_conv(x, wt, b, desc, silu=True, fp16_engine=True)
+    got_root = yroot.float().cpu().numpy()
+    got = nhwc_to_nchw(got_root[..., o0:o0 + oc])
+    err = np.abs(got.astype(np.float64) - y_ref)
+    assert (err <= _ulp16(y_ref)).all(), float(err.max())
+    np.testing.assert_array_equal(_u32(ys), _slots_of(got, oc))
+    rest = np.concatenate([got_root[..., :o0], got_root[..., o0 + oc:]], axis=3)
+    assert (rest == 7.0).all()
+
+
+def test_s1x1_rejects_tiles_without_instance(cuda):
+    with pytest.raises(RuntimeError, match="set_conv1x1_stream"):
+        K.set_conv1x1_stream(True, 3, 1)
+    with pytest.raises(RuntimeError, match="set_conv1x1_stream"):
+        K.set_conv1x1_stream(True, 8, 2)
+    K.set_conv1x1_stream(False)
