@@ -181,14 +181,14 @@ int aexrt_hip_set_conv_tile(int32_t jn, int32_t pw, int32_t ksw) {
 }
 
 int aexrt_hip_set_conv3x3_halo(int32_t mode, int32_t jn, int32_t pw, int32_t tr, int32_t tc, int32_t cc) {
-    if (mode == 5 || mode == 6) {
-        if (!set_conv3x3_m32(true, pw, jn, tr, tc, cc, mode == 6 ? 8 : 4)) {
+    if (mode == 5 || mode == 6 || mode == 7) {
+        if (!set_conv3x3_m32(true, pw, jn, tr, tc, cc, mode == 5 ? 4 : 8, mode == 7 ? 2 : 1)) {
             set_error("set_conv3x3_halo: no 32x32-MFMA kernel instance for this tile");
             return 0;
         }
         return 1;
     }
-    set_conv3x3_m32(false, 0, 0, 0, 0, 0, 4);
+    set_conv3x3_m32(false, 0, 0, 0, 0, 0, 4, 1);
     if (!set_conv3x3_halo(mode, jn, pw, tr, tc, cc)) {
         set_error("set_conv3x3_halo: bad mode or no kernel instance for this tile");
         return 0;

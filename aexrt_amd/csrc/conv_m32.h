@@ -26,6 +26,14 @@
 // one barrier per iteration.  The NW (4 or 8) waves split the tile's
 // positions (MQ 32-position subtiles each) and share the block's NQ
 // 32-channel subtiles.
+//
+// NG = 2 (8 waves): the waves form two groups of 4 with a window
+// double-buffer each and a barrier of their own (a counter in LDS), sharing
+// the block's resident weights; group g takes tiles g, g + 2, ... of the
+// block's run.  With one barrier per block all waves are in the same phase
+// (MFMAs, then the epilogue's VALU, then staging), so the matrix cores idle
+// during the epilogue; two groups drift apart and one group's MFMAs run
+// beside the other's epilogue and staging.
 #pragma once
 #include "conv_igemm.h"
 
@@ -64,10 +72,26 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-template <bool INT8, int MQ, int NQ, int NP, int EPI, int NW, bool F2 = false>
+// Barrier of the waves of one group: each wave adds one to the group's LDS
+// counter after its LDS writes and waits until the counter reaches target.
+// The wait is bounded (about a second), so a wave can never spin forever.
+__device__ __forceinline__ void group_barrier(uint32_t* ctr, uint32_t target) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    for (uint32_t it = 0; it < (1u << 22); ++it) {
+        if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+template <bool INT8, int MQ, int NQ, int NP, int EPI, int NW, bool F2 = false, int NG = 1>
 __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
     static_assert(!F2 || (!INT8 && EPI == igemm::kEpiSilu), "the fused 1x1 follows an fp16 SiLU conv");
+    static_assert(NG == 1 || (NG == 2 && NW == 8), "two wave groups of 4");
     constexpr int NT = NW * 64;           // threads of the block
+    constexpr int NWG = NW / NG;          // waves of a group
+    constexpr int NTG = NWG * 64;         // threads of a group
     constexpr int ESZ = INT8 ? 1 : 2;
     constexpr int KSUB = INT8 ? 32 : 16;  // k of one MFMA
     constexpr int CPP = 16 / ESZ;         // channels of one 16-byte piece
@@ -85,12 +109,16 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
     __shared__ uint32_t l_slots[NOCB / 16];
     __shared__ float l_bias2[F2 ? NOCB : 1];
     __shared__ uint32_t l_slots2[F2 ? NOCB / 16 : 1];
+    __shared__ uint32_t l_gbar[NG];  // group barrier counters
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31;
     const int hi = lane >> 5;
+    const int grp_id = NG == 1 ? 0 : wave / NWG;  // wave-uniform
+    const int gwave = wave - grp_id * NWG;         // wave within its group
+    const int gtid = tid - grp_id * NTG;           // thread within its group
 
     const int b = xcd_remap(blockIdx.x, gridDim.x);
     const int pg = (int)fdiv((uint32_t)b, p.fd_ntn);
@@ -101,12 +129,13 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
     const rsrc_t rx = make_rsrc(p.x, p.x_bytes);
     const rsrc_t rw = make_rsrc(p.w, (uint32_t)p.OCp * (uint32_t)p.Kp * ESZ);
 
-    // ---- window pieces of this thread: e = tid + k * NT -> plane e / NPIX,
-    // pixel (ir, ic); LDS place e * 16 (the same for every tile and chunk) ----
+    // ---- window pieces of this thread: e = gtid + k * NTG -> plane e / NPIX,
+    // pixel (ir, ic); LDS place e * 16 of its group's buffers (the same for
+    // every tile and chunk) ----
     int prc[NP], prel[NP];
 #pragma unroll
     for (int k = 0; k < NP; ++k) {
-        const int e = tid + k * NT;
+        const int e = gtid + k * NTG;
         const int pl = (int)fdiv((uint32_t)e, h.fd_npix);
         const int pix = e - pl * h.NPIX;
         const int ir = (int)fdiv((uint32_t)pix, h.fd_icol);
@@ -114,8 +143,10 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
         prc[k] = e < h.npiece ? (ir | (ic << 16)) : 0x7FFF;  // row 0x7FFF fails every bounds test
         prel[k] = (ir * p.W + ic) * p.x_cstride + pl * CPP;
     }
-    auto tile_pos = [&](int tl, int& n, int& oh0, int& ow0) {
-        const int ti = pt0 + tl;
+    // this group's tiles: lt-th of the group -> tl = grp_id + lt * NG of the block's run
+    const int ntl_g = NG == 1 ? ntl : (ntl - grp_id + NG - 1) / NG;
+    auto tile_pos = [&](int lt, int& n, int& oh0, int& ow0) {
+        const int ti = pt0 + grp_id + lt * NG;
         n = (int)fdiv((uint32_t)ti, h.fd_tpi);
         const int rem = ti - n * h.tpi;
         const int tr = (int)fdiv((uint32_t)rem, h.fd_ntc);
@@ -140,7 +171,7 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
             for (int u = 0; u < NL; ++u) pf[k][u] = bload16(rx, ok ? off + 16u * u : kOob);
         }
     };
-    window_loads(0, 0, true);
+    window_loads(0, 0, ntl_g > 0);
 
     // ---- input scale, per-channel constants --------------------------------
     uint32_t slot_raw[igemm::kMaxSlotReads / 64];
@@ -205,7 +236,7 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
     const int tpos = h.TR * h.TC;
 #pragma unroll
     for (int q = 0; q < MQ; ++q) {
-        const int pl = (wave * MQ + q) * 32 + l32;
+        const int pl = (gwave * MQ + q) * 32 + l32;
         const int pc = min(pl, tpos - 1);
         const int r = (int)fdiv((uint32_t)pc, h.fd_tc);
         const int c = pc - r * h.TC;
@@ -214,6 +245,7 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
     }
     const int abase = (hi * NOCB + l32) * 16;  // this lane's A piece in a k step's [half][oc] block
     if (tid < NOCB / 16) l_slots[tid] = 0u;
+    if (tid < NG) l_gbar[tid] = 0u;
     if constexpr (F2) {
         if (tid < NOCB / 16) l_slots2[tid] = 0u;
         if (tid < NOCB) l_bias2[tid] = bias2_v;
@@ -227,6 +259,10 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
     // the weight loads into LDS complete before any wave passes the first
     // barrier; every load issued so far is needed by the first iteration
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    // two groups: the weights and tables written by all waves are complete
+    // before either group reads them (one group's barrier does not cover
+    // the other's loads)
+    if constexpr (NG == 2) __syncthreads();
 
     const int jmax = min(NQ * 2, (p.OCp - n0) >> 4);  // 16-channel groups of the block with channels
     float gmax[NQ * 2], gmax2[F2 ? NQ * 2 : 1];
@@ -268,15 +304,15 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
     v2i rv[MQ][NQ][4];
 
     const int wstep = 2 * NOCB * 16;  // LDS bytes of one k step's weights
-    uint8_t* const win = lds + h.wbytes;
-    const int total = ntl * h.nch;
+    uint8_t* const win = lds + h.wbytes + grp_id * 2 * h.tbytes;
+    const int total = ntl_g * h.nch;
     int tl = 0, ch = 0;
     for (int i = 0; i < total; ++i) {
         uint8_t* const tb = win + (i & 1) * h.tbytes;
         // this iteration's window -> LDS (int8: quantized once here)
 #pragma unroll
         for (int k = 0; k < NP; ++k) {
-            const int e = tid + k * NT;
+            const int e = gtid + k * NTG;
             if (e < h.npiece) {
                 if constexpr (INT8) {
                     const v2i lo = quant8(pf[k][0], s_q), hq = quant8(pf[k][1], s_q);
@@ -306,8 +342,9 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
             nch_ = 0;
             ++ntl_;
         }
-        window_loads(min(ntl_, ntl - 1), nch_, ntl_ < ntl);
-        __syncthreads();
+        window_loads(min(ntl_, ntl_g - 1), nch_, ntl_ < ntl_g);
+        if constexpr (NG == 1) __syncthreads();
+        else group_barrier(&l_gbar[grp_id], (uint32_t)(i + 1) * NWG);
 
         // k steps of the chunk, software-pipelined two steps deep: the LDS
         // operands of step s + 2 are read before the MFMAs of step s (every
@@ -497,11 +534,11 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
 }
 
 // Blocks of one instance the GPU holds at once with lds_bytes of dynamic LDS.
-template <bool INT8, int MQ, int NQ, int NP, int EPI, int NW, bool F2>
+template <bool INT8, int MQ, int NQ, int NP, int EPI, int NW, bool F2, int NG>
 int m32_resident_blocks(int lds_bytes) {
     int per_cu = 0, cus = 0, dev = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv3x3_m32_kernel<INT8, MQ, NQ, NP, EPI, NW, F2>, NW * 64,
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv3x3_m32_kernel<INT8, MQ, NQ, NP, EPI, NW, F2, NG>, NW * 64,
                                                      (size_t)lds_bytes) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu < 1 ||
         cus < 1)
@@ -511,24 +548,31 @@ int m32_resident_blocks(int lds_bytes) {
 
 // Persistent grid: every resident block slot gets one contiguous run of
 // position tiles of one channel tile.
-template <bool INT8, int MQ, int NQ, int NP, int EPI, int NW, bool F2 = false>
+template <bool INT8, int MQ, int NQ, int NP, int EPI, int NW, bool F2 = false, int NG = 1>
 hipError_t m32_launch_cfg(M32Params h, hipStream_t stream) {
-    const int lds_bytes = h.wbytes + 2 * h.tbytes;
-    const int cap = m32_resident_blocks<INT8, MQ, NQ, NP, EPI, NW, F2>(lds_bytes);
+    const int lds_bytes = h.wbytes + NG * 2 * h.tbytes;
+    const int cap = m32_resident_blocks<INT8, MQ, NQ, NP, EPI, NW, F2, NG>(lds_bytes);
     int groups = h.ntile;
     if ((int64_t)h.ntile * h.c.ntn > cap) groups = std::max(1, cap / h.c.ntn);
     h.c.per = (h.ntile + groups - 1) / groups;
     groups = (h.ntile + h.c.per - 1) / h.c.per;
     const int64_t blocks = (int64_t)groups * h.c.ntn;
     if (blocks > INT32_MAX) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((conv3x3_m32_kernel<INT8, MQ, NQ, NP, EPI, NW, F2>), dim3((unsigned)blocks), dim3(NW * 64),
+    hipLaunchKernelGGL((conv3x3_m32_kernel<INT8, MQ, NQ, NP, EPI, NW, F2, NG>), dim3((unsigned)blocks), dim3(NW * 64),
                        (size_t)lds_bytes, stream, h);
     return hipGetLastError();
 }
 
-// Every (MQ, NQ, NP, NW) of one (INT8, EPI) family.
+// Every (MQ, NQ, NP, NW, NG) of one (INT8, EPI) family.
 template <bool INT8, int EPI>
-hipError_t m32_launch_family(const M32Params& h, int mq, int nq, int np, int nw, hipStream_t stream) {
+hipError_t m32_launch_family(const M32Params& h, int mq, int nq, int np, int nw, int ng, hipStream_t stream) {
+    // 8 waves in two groups of 4 (their own window buffers and barriers)
+#define AEXRT_M32_CASE2G(M, N, P) \
+    if (nw == 8 && ng == 2 && mq == M && nq == N && np == P) return m32_launch_cfg<INT8, M, N, P, EPI, 8, false, 2>(h, stream);
+    AEXRT_M32_CASE2G(1, 1, 4) AEXRT_M32_CASE2G(1, 2, 4) AEXRT_M32_CASE2G(1, 3, 4) AEXRT_M32_CASE2G(2, 1, 4)
+    AEXRT_M32_CASE2G(2, 2, 4) AEXRT_M32_CASE2G(1, 1, 8) AEXRT_M32_CASE2G(1, 2, 8) AEXRT_M32_CASE2G(2, 1, 8)
+#undef AEXRT_M32_CASE2G
+    if (ng != 1) return hipErrorInvalidValue;
 #define AEXRT_M32_CASE(M, N, P) \
     if (nw == 4 && mq == M && nq == N && np == P) return m32_launch_cfg<INT8, M, N, P, EPI, 4>(h, stream);
     AEXRT_M32_CASE(1, 1, 4) AEXRT_M32_CASE(1, 2, 4) AEXRT_M32_CASE(1, 3, 4) AEXRT_M32_CASE(1, 4, 4)
@@ -549,13 +593,13 @@ hipError_t m32_launch_family(const M32Params& h, int mq, int nq, int np, int nw,
 
 // fp16 SiLU 3x3 convs with a fused 1x1 (F2): tiles whose block covers
 // every output channel (nq 2 or 3: up to 64 / 96 channels).
-hipError_t m32_launch_f2(const M32Params& h, int mq, int nq, int np, int nw, hipStream_t stream);
+hipError_t m32_launch_f2(const M32Params& h, int mq, int nq, int np, int nw, int ng, hipStream_t stream);
 
 #define AEXRT_M32_FAMILIES(X) X(true, 0) X(true, 1) X(true, 2) X(false, 0) X(false, 1)
 #define AEXRT_M32_EXTERN(I, E) \
-    extern template hipError_t m32_launch_family<I, E>(const M32Params&, int, int, int, int, hipStream_t);
+    extern template hipError_t m32_launch_family<I, E>(const M32Params&, int, int, int, int, int, hipStream_t);
 #define AEXRT_M32_INSTANCE(I, E) \
-    template hipError_t m32_launch_family<I, E>(const M32Params&, int, int, int, int, hipStream_t);
+    template hipError_t m32_launch_family<I, E>(const M32Params&, int, int, int, int, int, hipStream_t);
 
 }  // namespace m32
 }  // namespace aexrt

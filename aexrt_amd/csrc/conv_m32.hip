@@ -20,6 +20,7 @@ constexpr int kM32LdsBudget = 156 * 1024;
 struct M32Tile {
     int mq, nq, np, TR, TC, CC;
     int nw = 4;  // waves per block
+    int ng = 1;  // wave groups (2: two groups of 4 with their own windows and barriers)
 };
 
 bool m32_shape_ok(const ConvParams& p) {
@@ -34,7 +35,7 @@ bool m32_geometry(M32Params& h, const M32Tile& t, bool int8) {
     const int cpp = int8 ? 16 : 8;
     const int ksub = int8 ? 32 : 16;
     if (t.CC < 16 || t.CC % 16 || p.C % t.CC || t.TR < 1 || t.TC < 1 || t.mq < 1 || t.nq < 1) return false;
-    if (t.TR * t.TC > t.nw * 32 * t.mq) return false;
+    if (t.ng < 1 || t.nw % t.ng || t.TR * t.TC > t.nw / t.ng * 32 * t.mq) return false;
     h.TR = t.TR;
     h.TC = t.TC;
     h.IR = (t.TR - 1) * p.S + 3;
@@ -45,7 +46,7 @@ bool m32_geometry(M32Params& h, const M32Tile& t, bool int8) {
     h.nks = (9 * t.CC + ksub - 1) / ksub;
     if (h.nks > kM32MaxSteps) return false;
     h.npiece = (t.CC / cpp) * h.NPIX;
-    if (h.npiece > 64 * t.nw * t.np) return false;
+    if (h.npiece > 64 * (t.nw / t.ng) * t.np) return false;
     h.ntc = (p.OW + t.TC - 1) / t.TC;
     h.tpi = ((p.OH + t.TR - 1) / t.TR) * h.ntc;
     const int64_t ntile = (int64_t)p.N * h.tpi;
@@ -54,7 +55,7 @@ bool m32_geometry(M32Params& h, const M32Tile& t, bool int8) {
     const int nocb = t.nq * 32;
     h.wbytes = h.nch * h.nks * 2 * nocb * 16;
     h.tbytes = h.npiece * 16;
-    if ((int64_t)h.wbytes + 2 * h.tbytes > kM32LdsBudget) return false;
+    if ((int64_t)h.wbytes + t.ng * 2 * h.tbytes > kM32LdsBudget) return false;
     h.c.ntn = (p.OCp + nocb - 1) / nocb;
     h.fd_npix = make_fastdiv((uint32_t)h.NPIX);
     h.fd_icol = make_fastdiv((uint32_t)h.ICOL);
@@ -70,8 +71,14 @@ bool m32_geometry(M32Params& h, const M32Tile& t, bool int8) {
 
 // (mq, nq) tiles of 8 subtiles have no 8-round window instance (registers);
 // 8-wave blocks exist for tiles of at most 4 subtiles
-bool m32_instantiated(int mq, int nq, int np, int nw) {
+bool m32_instantiated(int mq, int nq, int np, int nw, int ng = 1) {
     if (np != 4 && np != 8) return false;
+    if (ng == 2) {
+        if (nw != 8) return false;
+        if (np == 8) return (mq == 1 && nq <= 2) || (mq == 2 && nq == 1);
+        return (mq == 1 && nq <= 3) || (mq == 2 && nq <= 2);
+    }
+    if (ng != 1) return false;
     if (nw == 8) {
         if (np == 8) return (mq == 1 && nq <= 2) || (mq == 2 && nq == 1);
         return (mq == 1 && nq <= 3) || (mq == 2 && nq <= 2);
@@ -83,7 +90,9 @@ bool m32_instantiated(int mq, int nq, int np, int nw) {
 }
 
 // Tiles with a fused-1x1 instance (conv_m32_f16_f2.hip).
-bool m32_f2_instantiated(int mq, int nq, int np, int nw) {
+bool m32_f2_instantiated(int mq, int nq, int np, int nw, int ng = 1) {
+    if (ng == 2) return nw == 8 && mq == 1 && (nq == 2 || nq == 3) && (np == 4 || np == 8);
+    if (ng != 1) return false;
     if (nw == 4) {
         if (np == 4) return (mq == 1 || mq == 2) && (nq == 2 || nq == 3);
         return np == 8 && ((mq <= 2 && nq == 2) || (mq == 1 && nq == 3));
@@ -113,7 +122,8 @@ bool m32_fit(M32Params& h, M32Tile& t, bool int8) {
     const bool f2 = h.c.fuse_1x1 != nullptr;
     if (f2 && (int8 || !m32_f2_ok(h.c, t.nq))) return false;
     for (int np : {4, 8}) {
-        if (f2 ? !m32_f2_instantiated(t.mq, t.nq, np, t.nw) : !m32_instantiated(t.mq, t.nq, np, t.nw)) continue;
+        if (f2 ? !m32_f2_instantiated(t.mq, t.nq, np, t.nw, t.ng) : !m32_instantiated(t.mq, t.nq, np, t.nw, t.ng))
+            continue;
         t.np = np;
         M32Params hh = h;
         if (m32_geometry(hh, t, int8)) {
@@ -127,28 +137,30 @@ bool m32_fit(M32Params& h, M32Tile& t, bool int8) {
 std::atomic<bool> g_m32_forced{false};
 std::atomic<uint64_t> g_m32_force{0};  // mq | nq << 8 | tr << 16 | tc << 32 | cc << 48
 std::atomic<int> g_m32_force_nw{4};
+std::atomic<int> g_m32_force_ng{1};
 
 hipError_t m32_launch(const M32Params& h, bool int8, int epi, const M32Tile& t, hipStream_t s) {
     using m32::m32_launch_family;
     const bool f2 = h.c.fuse_1x1 != nullptr;
     if (LaunchProbe* pr = launch_probe()) {
         std::snprintf(pr->name, sizeof(pr->name), "conv3x3_m32_kernel<%s,%d,%d,%d,%d,%d%s> %dx%d cc%d",
-                      int8 ? "true" : "false", t.mq, t.nq, t.np, epi, t.nw, f2 ? ",true" : "", t.TR, t.TC, t.CC);
+                      int8 ? "true" : "false", t.mq, t.nq, t.np, epi, t.nw,
+                      t.ng == 2 ? (f2 ? ",true,2" : ",false,2") : (f2 ? ",true" : ""), t.TR, t.TC, t.CC);
         return hipSuccess;
     }
     if (f2) {
         if (int8 || epi != 1) return hipErrorInvalidValue;
         M32Params hf = h;
         hf.c2 = *h.c.fuse_1x1;
-        return m32::m32_launch_f2(hf, t.mq, t.nq, t.np, t.nw, s);
+        return m32::m32_launch_f2(hf, t.mq, t.nq, t.np, t.nw, t.ng, s);
     }
     if (int8) {
-        if (epi == 1) return m32_launch_family<true, 1>(h, t.mq, t.nq, t.np, t.nw, s);
-        if (epi == 2) return m32_launch_family<true, 2>(h, t.mq, t.nq, t.np, t.nw, s);
-        return m32_launch_family<true, 0>(h, t.mq, t.nq, t.np, t.nw, s);
+        if (epi == 1) return m32_launch_family<true, 1>(h, t.mq, t.nq, t.np, t.nw, t.ng, s);
+        if (epi == 2) return m32_launch_family<true, 2>(h, t.mq, t.nq, t.np, t.nw, t.ng, s);
+        return m32_launch_family<true, 0>(h, t.mq, t.nq, t.np, t.nw, t.ng, s);
     }
-    if (epi == 1) return m32_launch_family<false, 1>(h, t.mq, t.nq, t.np, t.nw, s);
-    return m32_launch_family<false, 0>(h, t.mq, t.nq, t.np, t.nw, s);
+    if (epi == 1) return m32_launch_family<false, 1>(h, t.mq, t.nq, t.np, t.nw, t.ng, s);
+    return m32_launch_family<false, 0>(h, t.mq, t.nq, t.np, t.nw, t.ng, s);
 }
 
 }  // namespace
@@ -164,11 +176,12 @@ int enumerate_m32_choices(const ConvParams& p, bool int8, ConvChoice* out, int c
         if (CC % 16 || (div > 8 && CC != 16)) continue;
         for (int nq = 1; nq <= 4 && n < cap; ++nq) {
             if (nq > oc32 || (nq == 3 && oc32 != 3)) continue;  // 3 subtiles only for 65..96 channels
-            for (int nw : {4, 8})
+            for (int nwg : {4, 8, 16})  // waves per block x groups: 4 x 1, 8 x 1, 8 x 2
             for (int mq : {1, 2, 4}) {
                 if (n >= cap) break;
-                if (p.fuse_1x1 ? !m32_f2_instantiated(mq, nq, 4, nw) : !m32_instantiated(mq, nq, 4, nw)) continue;
-                const int npos = nw * 32 * mq;
+                const int nw = nwg == 16 ? 8 : nwg, ng = nwg == 16 ? 2 : 1;
+                if (p.fuse_1x1 ? !m32_f2_instantiated(mq, nq, 4, nw, ng) : !m32_instantiated(mq, nq, 4, nw, ng)) continue;
+                const int npos = nw / ng * 32 * mq;
                 const int tcs[4] = {p.OW, 32, 16, 8};
                 for (int i = 0; i < 4 && n < cap; ++i) {
                     const int tc = tcs[i];
@@ -179,7 +192,7 @@ int enumerate_m32_choices(const ConvParams& p, bool int8, ConvChoice* out, int c
                     if (TR < 1) continue;
                     M32Params h{};
                     h.c = p;
-                    M32Tile t{mq, nq, 4, TR, tc, CC, nw};
+                    M32Tile t{mq, nq, 4, TR, tc, CC, nw, ng};
                     if (!m32_fit(h, t, int8)) continue;
                     ConvChoice c;
                     c.kind = 5;
@@ -189,6 +202,7 @@ int enumerate_m32_choices(const ConvParams& p, bool int8, ConvChoice* out, int c
                     c.tc = tc;
                     c.cc = CC;
                     c.nw = nw;
+                    c.ksw = ng - 1;  // kind 5 keeps its wave groups (minus one) here
                     out[n++] = c;
                 }
             }
@@ -197,14 +211,15 @@ int enumerate_m32_choices(const ConvParams& p, bool int8, ConvChoice* out, int c
     return n;
 }
 
-bool set_conv3x3_m32(bool on, int mq, int nq, int tr, int tc, int cc, int nw) {
+bool set_conv3x3_m32(bool on, int mq, int nq, int tr, int tc, int cc, int nw, int ng) {
     if (!on) {
         g_m32_forced.store(false);
         return true;
     }
-    if (!m32_instantiated(mq, nq, 4, nw) || tr < 1 || tr > 0xFFFF || tc < 1 || tc > 0xFFFF || cc < 16 || cc > 0xFFFF)
+    if (!m32_instantiated(mq, nq, 4, nw, ng) || tr < 1 || tr > 0xFFFF || tc < 1 || tc > 0xFFFF || cc < 16 || cc > 0xFFFF)
         return false;
     g_m32_force_nw.store(nw);
+    g_m32_force_ng.store(ng);
     g_m32_force.store((uint64_t)mq | ((uint64_t)nq << 8) | ((uint64_t)tr << 16) | ((uint64_t)tc << 32) |
                       ((uint64_t)cc << 48));
     g_m32_forced.store(true);
@@ -222,6 +237,7 @@ bool forced_m32_choice(ConvChoice& c) {
     c.tc = (int)((f >> 32) & 0xFFFF);
     c.cc = (int)((f >> 48) & 0xFFFF);
     c.nw = g_m32_force_nw.load(std::memory_order_relaxed);
+    c.ksw = g_m32_force_ng.load(std::memory_order_relaxed) - 1;
     return true;
 }
 
@@ -231,7 +247,7 @@ hipError_t launch_conv_m32(const ConvParams& p, bool int8, int epi, hipStream_t 
     if (!m32_shape_ok(p) || p.choice.kind != 5) return hipErrorInvalidValue;
     M32Params h{};
     h.c = p;
-    M32Tile t{p.choice.pw, p.choice.jn, 4, p.choice.tr, p.choice.tc, p.choice.cc, p.choice.nw};
+    M32Tile t{p.choice.pw, p.choice.jn, 4, p.choice.tr, p.choice.tc, p.choice.cc, p.choice.nw, p.choice.ksw + 1};
     if (!m32_fit(h, t, int8)) return hipErrorInvalidValue;
     return m32_launch(h, int8, epi, t, stream);
 }

@@ -164,9 +164,9 @@ bool forced_wide_choice(ConvChoice& c);
 int enumerate_m32_choices(const ConvParams& p, bool int8, ConvChoice* out, int cap);
 hipError_t launch_conv_m32(const ConvParams& p, bool int8, int epi, hipStream_t stream);
 // Forces every 3x3 conv the kind-0 heuristics would run onto one m32 tile
-// of nw (4 or 8) waves per block (on = false: off).  False for a tile
-// without a kernel instance.
-bool set_conv3x3_m32(bool on, int mq, int nq, int tr, int tc, int cc, int nw);
+// of nw (4 or 8) waves per block in ng (1, or 2 with 8 waves) wave groups
+// (on = false: off).  False for a tile without a kernel instance.
+bool set_conv3x3_m32(bool on, int mq, int nq, int tr, int tc, int cc, int nw, int ng);
 bool forced_m32_choice(ConvChoice& c);
 // Streaming 1x1 int8 conv (choice kind 6: jn = JQ 16-channel subtiles of the
 // block, pw = PQ 16-position subtiles per wave; C % 16 == 0, positions evenly

@@ -203,12 +203,14 @@ def set_conv_tile(jn: int = 0, pw: int = 0, ksw: bool = False) -> None:
 
 
 HALO_AUTO, HALO_OFF, HALO_FORCE, HALO_FORCE8, HALO_FORCE_WIDE, HALO_FORCE_M32, HALO_FORCE_M32_8 = 0, 1, 2, 3, 4, 5, 6
+HALO_FORCE_M32_2G = 7
 
 
 def set_conv3x3_halo(mode: int = HALO_AUTO, jn: int = 0, pw: int = 0, tr: int = 0, tc: int = 0, cc: int = 0) -> None:
     """Select the halo-tile kernel for 3x3 convs: automatic, off (implicit GEMM), or a forced tile
     (HALO_FORCE: 4 waves per block, HALO_FORCE8: 8 waves; HALO_FORCE_WIDE: the wide-tile fp16 kernel;
-    HALO_FORCE_M32 / HALO_FORCE_M32_8: the 32x32-MFMA kernel with 4 / 8 waves per block, jn 32-channel
+    HALO_FORCE_M32 / HALO_FORCE_M32_8: the 32x32-MFMA kernel with 4 / 8 waves per block (HALO_FORCE_M32_2G:
+    8 waves in two groups of 4 with their own windows and barriers), jn 32-channel
     subtiles and pw 32-position subtiles)."""
     check(_lib.lib().aexrt_hip_set_conv3x3_halo(mode, jn, pw, tr, tc, cc), "set_conv3x3_halo")
 

@@ -306,7 +306,10 @@ int aexrt_hip_set_conv_tile(int32_t jn, int32_t pw, int32_t ksw);
  * positions (tr * tc <= 128 * pw), cc input channels per chunk (C % cc == 0,
  * cc % 16 == 0; the weights of all chunks stay in LDS); mode 6 = the same
  * with 8 waves per block (pw 1 with jn 1..3, pw 2 with jn 1..2; tr * tc <=
- * 256 * pw).  Any other mode switches modes 5 and 6 off.
+ * 256 * pw); mode 7 = 8 waves in two groups of 4, each group with its own
+ * input windows and barrier and its own tiles of the block's run (pw 1 with
+ * jn 1..3, pw 2 with jn 1..2; tr * tc <= 128 * pw).  Any other mode
+ * switches modes 5, 6 and 7 off.
  * Returns 0 for a bad request. */
 int aexrt_hip_set_conv3x3_halo(int32_t mode, int32_t jn, int32_t pw, int32_t tr, int32_t tc, int32_t cc);
 

@@ -27,7 +27,9 @@ def _ulp16(a):
 
 
 def _force(mq, nq, tr, tc, cc, nw=4):
-    K.set_conv3x3_halo(K.HALO_FORCE_M32 if nw == 4 else K.HALO_FORCE_M32_8, nq, mq, tr, tc, cc)
+    """nw 4 or 8 waves per block; 16: 8 waves in two groups of 4."""
+    mode = {4: K.HALO_FORCE_M32, 8: K.HALO_FORCE_M32_8, 16: K.HALO_FORCE_M32_2G}[nw]
+    K.set_conv3x3_halo(mode, nq, mq, tr, tc, cc)
 
 
 def _slots_of(y, oc):
@@ -47,6 +49,9 @@ INT8_M32 = [
     (1, 48, 9, 7, 32, 1, 2, 1, 9, 7, 3, 307),        # C = 48: three 16-channel chunks, padded k steps
     (2, 64, 20, 20, 64, 1, 2, 2, 20, 20, 2, 308, 8),  # 8 waves: one 20x20 image per tile
     (1, 32, 17, 15, 96, 2, 1, 3, 9, 8, 1, 309, 8),    # 8 waves, stride 2, 96 channels
+    (2, 64, 20, 20, 64, 1, 2, 2, 10, 20, 2, 310, 16),   # two wave groups, each with its own tiles
+    (3, 32, 17, 15, 96, 2, 1, 3, 4, 8, 1, 312, 16),     # two groups, stride 2, ragged tiles
+    (1, 64, 8, 8, 64, 1, 1, 2, 8, 8, 1, 313, 16),       # one tile: the second group has none
 ]
 
 
@@ -132,6 +137,8 @@ FP16_M32 = [
     (2, 64, 40, 40, 64, 1, 2, 2, 10, 40, 2, True, False, 8),  # 8 waves: the head's 40x40 shape
     (1, 64, 40, 40, 80, 1, 1, 3, 6, 40, 4, True, False, 8),   # 8 waves, 96-channel block
     (1, 48, 13, 11, 64, 2, 2, 1, 7, 11, 3, False, True, 8),   # 8 waves, stride 2, fp32 output
+    (2, 64, 40, 40, 144, 1, 1, 3, 3, 40, 4, True, False, 16),  # two groups: the head's 144-channel sibling pair
+    (1, 64, 40, 40, 64, 1, 2, 2, 6, 40, 4, True, False, 16),   # two groups, two subtiles per wave
 ]
 
 
@@ -203,6 +210,8 @@ FUSED = [
     (2, 64, 10, 10, 64, 64, (6, 2, 1, 10, 10, 64), True, (16, 80, 96)),  # 8 waves, SiLU, into a channel slice
     (1, 80, 13, 11, 80, 64, (5, 3, 2, 13, 11, 16), False, None),  # ragged map, 1x1 to fewer channels
     (2, 80, 20, 20, 80, 80, (5, 3, 1, 3, 20, 16), "f32", None),   # fp32 output (the head's raw output)
+    (2, 64, 40, 40, 64, 64, (7, 2, 1, 3, 40, 32), False, None),   # two wave groups
+    (2, 80, 20, 20, 80, 80, (7, 3, 1, 3, 20, 16), "f32", None),   # two groups, fp32 output
 ]
 
 
