@@ -217,6 +217,54 @@ def _print_mfma(a) -> int:
     return 0
 
 
+# Issue cycles of one wave64 VALU instruction on a SIMD (gfx950 measured with
+# 8 waves per SIMD: fp32 add 2.5, most others 4.2, exp/rcp 8.2; 4 is the
+# figure for the mix) and the part's SIMDs and clock, for the VALU-time column.
+VALU_CYCLES = 4.0
+SIMDS = 1024
+CLOCK_HZ = 2.4e9
+INSTS_COUNTERS = ("SQ_WAVES", "SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_INSTS_VMEM_RD",
+                  "SQ_INSTS_VMEM_WR")
+
+
+def insts_table(pmc_dir: str, pass_log: str) -> List[dict]:
+    """Per-step instruction counts of a ``bench.py --pmc-pass`` run with the INSTS_COUNTERS:
+    per wave, and the VALU issue time if the step's VALU instructions were spread evenly
+    over every SIMD (VALU_CYCLES each)."""
+    info = pass_info(pass_log)
+    labels = info["steps"]
+    disp = load_dispatches(pmc_dir)
+    _, steps = _steps_after_calibration(disp, len(labels))
+    out = []
+    for lab, d in zip(labels, steps):
+        c = d["counters"]
+        w = max(c.get("SQ_WAVES", 0.0), 1.0)
+        valu = c.get("SQ_INSTS_VALU", 0.0)
+        out.append(dict(step=lab, kernel=short_name(d["name"]), waves=w, valu=valu / w,
+                        salu=c.get("SQ_INSTS_SALU", 0.0) / w, lds=c.get("SQ_INSTS_LDS", 0.0) / w,
+                        vmem_rd=c.get("SQ_INSTS_VMEM_RD", 0.0) / w, vmem_wr=c.get("SQ_INSTS_VMEM_WR", 0.0) / w,
+                        valu_us=valu * VALU_CYCLES / SIMDS / CLOCK_HZ * 1e6))
+    return out
+
+
+def _print_insts(a) -> int:
+    rows = insts_table(a.insts, a.pass_log)
+    print("| step | kernel | waves | VALU / wave | SALU / wave | LDS / wave | VMEM rd / wave | VMEM wr / wave "
+          "| VALU issue us |")
+    print("|---|---|---|---|---|---|---|---|---|")
+    fam = {}
+    for r in rows:
+        print(f"| {r['step']} | `{r['kernel'][:60]}` | {r['waves']:.0f} | {r['valu']:.0f} | {r['salu']:.0f} | "
+              f"{r['lds']:.0f} | {r['vmem_rd']:.0f} | {r['vmem_wr']:.0f} | {r['valu_us']:.2f} |")
+        key = "int8" if "alg=int8" in r["step"] else ("fp16" if " alg=" in r["step"] else "other")
+        fam[key] = fam.get(key, 0.0) + r["valu_us"]
+    print("\n| launches | VALU issue us per step |")
+    print("|---|---|")
+    for k, v in fam.items():
+        print(f"| {k} | {v:.1f} |")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--fetch")
@@ -226,9 +274,12 @@ def main() -> int:
     ap.add_argument("--stats", action="store_true", help="kernel statistics of a bench.py --trace-pass trace")
     ap.add_argument("--mfma", help="MFMA counter run of bench.py --pmc-pass")
     ap.add_argument("--trace-log", help="log of the bench.py --trace-pass run the --trace directory holds")
+    ap.add_argument("--insts", help="instruction counter run of bench.py --pmc-pass (INSTS_COUNTERS)")
     a = ap.parse_args()
     if a.stats:
         return _print_stats(a)
+    if a.insts:
+        return _print_insts(a)
     if a.mfma:
         return _print_mfma(a)
     t = traffic_table(a.fetch, a.write, a.pass_log, a.trace)

@@ -81,3 +81,24 @@ def test_mfma_table_counts_ops(tmp_path):
     _counters(tmp_path / "m", [("neg", 1, "SQ_INSTS_VALU_MFMA_MOPS_I8", 0.0), ("k", 1, "SQ_INSTS_VALU_MFMA_MOPS_I8", 4.0)])
     (row,) = profiling.mfma_table(str(tmp_path / "m"), str(log))
     assert row["ops_i8"] == 4 * 512 and row["ops_f16"] == 0
+
+
+def test_insts_table_per_wave_and_valu_time(tmp_path):
+    log = tmp_path / "i.log"
+    log.write_text(json.dumps({"pmc_pass": {"steps": ["cmd#3 CONV_SILU x alg=int8_mfma_1x1 kernel=k"],
+                                            "calibration_bytes": 1024}}))
+    rows = [("neg", 1, "SQ_WAVES", 4.0), ("k", 1, "SQ_WAVES", 8.0), ("k", 1, "SQ_INSTS_VALU", 800.0),
+            ("k", 1, "SQ_INSTS_LDS", 80.0)]
+    # one dispatch per kernel: the loader sums a dispatch's rows, so give each row its own dispatch id
+    d = tmp_path / "i"
+    d.mkdir(parents=True)
+    with open(d / "run_counter_collection.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, ["Dispatch_Id", "Kernel_Name", "Grid_Size", "Counter_Name", "Counter_Value"])
+        w.writeheader()
+        for name, grid, counter, value in rows:
+            w.writerow(dict(Dispatch_Id=0 if name == "neg" else 1, Kernel_Name=name, Grid_Size=grid,
+                            Counter_Name=counter, Counter_Value=value))
+    (row,) = profiling.insts_table(str(d), str(log))
+    assert row["waves"] == 8 and row["valu"] == 100 and row["lds"] == 10
+    # 800 VALU instructions x 4 cycles over 1024 SIMDs at 2.4 GHz
+    assert row["valu_us"] == pytest.approx(800 * 4 / 1024 / 2.4e9 * 1e6)
