@@ -76,4 +76,13 @@ __device__ __forceinline__ void slot_max(uint32_t* slot, float v) {
     if (b > seen) atomicMax(slot, b);
 }
 
+// XCD-aware block order: workgroups are dealt round-robin over the 8 XCDs,
+// so block b runs on XCD b % 8.  Give each XCD a contiguous range of logical
+// blocks so the lines that neighbouring blocks share are fetched into one L2.
+__device__ __forceinline__ int xcd_remap(int b, int nb) {
+    const int full = (nb / 8) * 8;
+    if (b >= full) return b;
+    return (b % 8) * (nb / 8) + b / 8;
+}
+
 }  // namespace aexrt

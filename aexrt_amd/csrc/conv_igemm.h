@@ -64,14 +64,7 @@ __device__ __forceinline__ v4i bload16(rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
 }
 
-// XCD-aware block order: workgroups are dealt round-robin over the 8 XCDs,
-// so block b runs on XCD b % 8.  Give each XCD a contiguous range of runs so
-// the input rows shared by neighbouring runs are fetched into one L2.
-__device__ __forceinline__ int xcd_remap(int b, int nb) {
-    const int full = (nb / 8) * 8;
-    if (b >= full) return b;
-    return (b % 8) * (nb / 8) + b / 8;
-}
+using ::aexrt::xcd_remap;
 
 // fp32 product of the fp16 in the low / high half of h2 and s, rounded once:
 // v_fma_mix with a -0 addend is exactly RN(x * s) (x converted exactly).

@@ -374,7 +374,10 @@ __global__ __launch_bounds__(kThreads) void sppf_maxpool_nhwc_kernel(
     __shared__ uint32_t lm[3];
     const int HW = H * W;
     const int CC = C / 8;
-    const int n = blockIdx.x / CC, cc = blockIdx.x - n * CC;
+    // the CC blocks of one image on one XCD: each reads 16 bytes of every
+    // pixel's channels, so the others' parts of the lines hit its L2
+    const int b = xcd_remap(blockIdx.x, gridDim.x);
+    const int n = b / CC, cc = b - n * CC;
     const int tid = threadIdx.x;
     if (tid < 3) lm[tid] = 0u;
     const __half* xb = x + n * x_nstride + cc * 8;
@@ -429,7 +432,7 @@ __global__ __launch_bounds__(kThreads) void sppf_maxpool_nhwc_kernel(
     __syncthreads();
     if (tid < 3) {
         const SlotRef& sr = tid == 0 ? s1 : (tid == 1 ? s2 : s3);
-        if (sr.p && lm[tid]) slot_max(slot_copy(sr, blockIdx.x) + (cc >> 1), u2f(lm[tid]));
+        if (sr.p && lm[tid]) slot_max(slot_copy(sr, b) + (cc >> 1), u2f(lm[tid]));
     }
 }
 

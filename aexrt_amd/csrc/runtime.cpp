@@ -130,10 +130,14 @@ struct Step {
 // Schedule of a network measured at load: sibling convs as one launch, lane
 // count, head 1x1 convs fused into their 3x3 producers.
 struct Schedule {
-    int first = 1;   // sibling pairs in one launch
-    int second = 1;  // lanes
-    int fuse = 0;    // head 3x3 + 1x1 pairs in one launch
+    int first = 1;      // sibling pairs in one launch
+    int second = 1;     // lanes
+    int fuse = 0;       // head 3x3 + 1x1 pairs in one launch: 0 none, else the pairs of mask
+    uint32_t mask = 0;  // bit k: the k-th pair in command order (0 with fuse set: every pair)
 };
+
+// Pairs a schedule fuses (bit k: the k-th head pair in command order).
+uint32_t schedule_fuse_mask(const Schedule& s) { return s.fuse == 0 ? 0u : s.mask ? s.mask : ~0u; }
 
 // A conv whose kernel choice is measured: its launch reads p (the choice
 // can change after the step list is built).
@@ -202,8 +206,10 @@ struct AexrtYoloModel {
     // conv's output channels in one root (one launch computes both), or -1
     std::vector<int> sibling;
     bool merge_siblings = true;  // sibling pairs run as one launch (measured at load)
-    bool fuse_1x1 = false;       // head 3x3 + 1x1 pairs run as one launch (measured at load)
-    int fusable_1x1 = 0;         // such pairs in the plan
+    // head 3x3 + 1x1 pairs that run as one launch (bit k: the k-th pair in command
+    // order; measured at load), and every such pair of the plan (3x3, 1x1 command)
+    uint32_t fuse_mask = 0;
+    std::vector<std::pair<int, int>> fuse_pairs;
     std::vector<Step> steps;
     std::vector<CopyJob> copies;
     std::vector<void*> allocations;
@@ -455,8 +461,8 @@ AexrtConv2DDesc desc_of(const EngineCommand& c);
 // output (its only consumer), both fp16: the 1x1 runs in the 3x3 conv's
 // epilogue on the 32x32-MFMA kernel (every 3x3 output channel of a position
 // in one block, so at most 96), and the 3x3 output is never stored.
-// Sets the pairs for m->fuse_1x1 (clears them when off); returns the number of
-// pairs the plan has with fusion on.
+// Fuses the pairs of m->fuse_mask (clears the others) and lists every pair the
+// plan has in m->fuse_pairs; returns their number.
 int fuse_head_1x1(AexrtYoloModel* m) {
     const Engine& e = m->eng;
     auto& V = m->vals;
@@ -466,6 +472,7 @@ int fuse_head_1x1(AexrtYoloModel* m) {
         cs.fused_1x1 = cs.fused_into = -1;
     }
     int pairs = 0;
+    m->fuse_pairs.clear();
     for (size_t ci = 0; ci < e.commands.size(); ++ci) {
         ConvState& cs = m->convs[ci];
         const EngineCommand& c = e.commands[ci];
@@ -492,8 +499,9 @@ int fuse_head_1x1(AexrtYoloModel* m) {
         if (d2.kernel_h != 1 || d2.kernel_w != 1 || d2.stride_h != 1 || d2.pad_top != 0 || d2.out_channels > 96 ||
             d2.out_channels % 8)
             continue;
-        ++pairs;
-        if (!m->fuse_1x1) continue;
+        m->fuse_pairs.emplace_back((int)ci, cj);
+        const int k = pairs++;
+        if (k >= 32 || !((m->fuse_mask >> k) & 1u)) continue;
         cs.fused_1x1 = cj;
         m->convs[cj].fused_into = (int)ci;
         V[c.output].elided = true;
@@ -1001,7 +1009,8 @@ void load_tune_cache(AexrtYoloModel* m) {
         if (line.compare(0, 4, "cmd ") == 0)
             m->refined[line.substr(0, tab)] = c;  // a conv's choice measured in the network
         else if (line.compare(0, 9, "schedule ") == 0)
-            m->schedules[line.substr(0, tab)] = Schedule{c.kind, c.jn, c.pw};  // merge flag, lanes, fusion
+            m->schedules[line.substr(0, tab)] =
+                Schedule{c.kind, c.jn, c.pw, (uint32_t)c.ksw};  // merge flag, lanes, fusion, fused pairs
         else
             m->tuned[line.substr(0, tab)] = c;
     }
@@ -1017,7 +1026,8 @@ void save_tune_cache(AexrtYoloModel* m) {
         };
         for (const auto& [key, c] : m->tuned) put(key, c);
         for (const auto& [key, c] : m->refined) put(key, c);
-        for (const auto& [key, v] : m->schedules) put(key, ConvChoice{v.first, v.second, v.fuse, 0, 0, 0, 0, 0});
+        for (const auto& [key, v] : m->schedules)
+            put(key, ConvChoice{v.first, v.second, v.fuse, (int)v.mask, 0, 0, 0, 0});
         if (!f) return;
     }
     std::rename(tmp.c_str(), m->tune_cache.c_str());
@@ -1712,6 +1722,32 @@ bool refine_in_context(AexrtYoloModel* m) {
     return true;
 }
 
+// Per head 3x3 + 1x1 pair of m->fuse_pairs, the time of the steps of the current
+// build that compute it: the fused step, or the 3x3 step plus the 1x1 step
+// (the least of kContextReps event-profiled passes per step).
+bool pair_step_times(AexrtYoloModel* m, std::vector<float>& out) {
+    out.assign(m->fuse_pairs.size(), 0.0f);
+    if (m->fuse_pairs.empty()) return true;
+    std::vector<float> lo(m->steps.size(), 1e30f);
+    const bool prof = m->profile;
+    m->profile = true;
+    bool ok = true;
+    for (int rep = 0; rep <= kContextReps && ok; ++rep) {
+        ok = run_network(m, m->stream);
+        for (size_t i = 0; ok && rep > 0 && i < m->steps.size() && i < m->prof_ms.size(); ++i)
+            lo[i] = std::min(lo[i], (float)m->prof_ms[i]);
+    }
+    m->profile = prof;
+    m->prof_labels.clear();
+    m->prof_ms.clear();
+    if (!ok) return false;
+    for (size_t k = 0; k < m->fuse_pairs.size(); ++k)
+        for (size_t i = 0; i < m->steps.size(); ++i)
+            if (m->steps[i].cmd == m->fuse_pairs[k].first || m->steps[i].cmd == m->fuse_pairs[k].second)
+                out[k] += lo[i];
+    return true;
+}
+
 // Spreading independent steps over streams pays when kernels are long enough to
 // overlap (large batch) and costs cross-queue synchronization when they are not
 // (batch 1): both schedules are captured and timed at load, the faster one kept.
@@ -1903,8 +1939,8 @@ bool build_model(AexrtYoloModel* m) {
         set_int8_mode(m, ci);
     }
     if (!plan_memory(m, m->copies)) return false;
-    m->fuse_1x1 = false;
-    m->fusable_1x1 = fuse_head_1x1(m);
+    m->fuse_mask = 0;
+    const int fusable = fuse_head_1x1(m);
     mark_slot_readers(m);
     // arena
     size_t total = 0;
@@ -1956,7 +1992,7 @@ bool build_model(AexrtYoloModel* m) {
     // both are measured (with autotuning) or the cached schedule's choice is taken
     const char* f1 = std::getenv("AEXRT_HIP_FUSE_1X1");
     const int fuse_forced = f1 && (f1[0] == '0' || f1[0] == '1') ? f1[0] - '0' : -1;
-    const bool fuse_choice = m->fusable_1x1 > 0 && fuse_forced < 0 && m->autotune && m->use_graph;
+    const bool fuse_choice = fusable > 0 && fuse_forced < 0 && m->autotune && m->use_graph;
     const int merge_variants = pairs && m->autotune && m->use_graph ? 2 : 1;
     const int variants = merge_variants * (fuse_choice ? 2 : 1);
     // without measurement, a schedule cached for this network (same input and
@@ -1968,21 +2004,27 @@ bool build_model(AexrtYoloModel* m) {
     const auto cached_sched = m->schedules.find(skey);
     const bool use_cached_sched = !m->autotune && cached_sched != m->schedules.end();
     float best_ms = 0.0f;
-    bool best_merge = true, best_fuse = false;
+    bool best_merge = true;
+    uint32_t best_fuse = 0;
     int best_lanes = 1;
-    // the schedule cache keeps (merge, lanes, fuse) in a choice's (kind, jn, pw)
-    auto fuse_for = [&](int k) {
-        if (fuse_forced >= 0) return fuse_forced != 0;
-        if (use_cached_sched) return cached_sched->second.fuse != 0;
-        return fuse_choice ? k / merge_variants == 0 : false;
+    // the schedule cache keeps (merge, lanes, fuse, fused pairs) in a choice's
+    // (kind, jn, pw, ksw)
+    auto fuse_for = [&](int k) -> uint32_t {
+        if (fuse_forced >= 0) return fuse_forced ? ~0u : 0u;
+        if (use_cached_sched) return schedule_fuse_mask(cached_sched->second);
+        return fuse_choice && k / merge_variants == 0 ? ~0u : 0u;
     };
+    // per head pair and merge setting: the fused step's time (index 1), the
+    // unfused 3x3 and 1x1 steps' (index 0)
+    std::vector<float> pair_ms[2][2];
     for (int k = 0; k < variants; ++k) {
         m->merge_siblings = use_cached_sched ? cached_sched->second.first != 0 : k % merge_variants == 0;
-        m->fuse_1x1 = fuse_for(k);
+        m->fuse_mask = fuse_for(k);
         fuse_head_1x1(m);
         m->n_lanes = 1;
         if (!build_steps(m, m->copies)) return false;
         if (m->autotune && !refine_in_context(m)) return false;
+        if (fuse_choice && !pair_step_times(m, pair_ms[m->merge_siblings][m->fuse_mask ? 1 : 0])) return false;
         float ms = 0.0f;
         if (fixed_lanes) {
             m->n_lanes = std::min(kLanes, std::atoi(lanes));
@@ -1994,20 +2036,40 @@ bool build_model(AexrtYoloModel* m) {
         if (k == 0 || ms < best_ms) {
             best_ms = ms;
             best_merge = m->merge_siblings;
-            best_fuse = m->fuse_1x1;
+            best_fuse = m->fuse_mask;
             best_lanes = m->n_lanes;
         }
     }
-    if (best_merge != m->merge_siblings || best_fuse != m->fuse_1x1) {
-        // the choices of this build were measured with the first: cached in m->refined
+    // each pair fused or not by its own step times (one launch against two,
+    // under the chosen merge setting); a mixed choice takes its lane count anew
+    bool mixed = false;
+    if (fuse_choice) {
+        const std::vector<float>& f = pair_ms[best_merge][1];
+        const std::vector<float>& u = pair_ms[best_merge][0];
+        uint32_t mask = 0, all = 0;
+        for (size_t q = 0; q < m->fuse_pairs.size() && q < 32; ++q) {
+            all |= 1u << q;
+            if (q < f.size() && q < u.size() && f[q] <= u[q]) mask |= 1u << q;
+        }
+        mask = mask == all ? ~0u : mask;
+        mixed = mask != 0u && mask != ~0u;
+        best_fuse = mask;
+    }
+    if (best_merge != m->merge_siblings || best_fuse != m->fuse_mask) {
+        // the choices of this build were measured with the variants: cached in m->refined
         m->merge_siblings = best_merge;
-        m->fuse_1x1 = best_fuse;
+        m->fuse_mask = best_fuse;
         fuse_head_1x1(m);
         m->n_lanes = 1;
         if (!build_steps(m, m->copies)) return false;
         if (m->autotune && !refine_in_context(m)) return false;
-        m->n_lanes = best_lanes;
-        schedule_steps(m);
+        float ms = 0.0f;
+        if (mixed && !fixed_lanes && m->autotune) {
+            if (!choose_lanes(m, &ms)) return false;
+        } else {
+            m->n_lanes = fixed_lanes ? std::min(kLanes, std::atoi(lanes)) : best_lanes;
+            schedule_steps(m);
+        }
         drop_graph(m);
     }
     if (use_cached_sched && !fixed_lanes) {
@@ -2015,10 +2077,13 @@ bool build_model(AexrtYoloModel* m) {
         schedule_steps(m);
         drop_graph(m);
     }
-    if (m->autotune) m->schedules[skey] = Schedule{m->merge_siblings ? 1 : 0, m->n_lanes, m->fuse_1x1 ? 1 : 0};
+    if (m->autotune)
+        m->schedules[skey] = Schedule{m->merge_siblings ? 1 : 0, m->n_lanes, m->fuse_mask ? 1 : 0,
+                                      m->fuse_mask == ~0u ? 0u : m->fuse_mask};
     if (m->tune_log && variants > 1)
-        std::fprintf(stderr, "aexrt sibling convs: %s, head 1x1 convs: %s\n", best_merge ? "one launch" : "two launches",
-                     best_fuse ? "fused" : "on their own");
+        std::fprintf(stderr, "aexrt sibling convs: %s, head 1x1 convs fused: %s (mask %#x)\n",
+                     best_merge ? "one launch" : "two launches",
+                     best_fuse == ~0u ? "all" : best_fuse ? "some" : "none", best_fuse);
     if (m->autotune && !m->tune_cache.empty()) save_tune_cache(m);
     const char* prof = std::getenv("AEXRT_HIP_PROFILE");
     m->profile = prof && prof[0] == '1';

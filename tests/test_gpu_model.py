@@ -596,3 +596,37 @@ def test_head_1x1_convs_fused_and_on_their_own(cuda, monkeypatch):
             outs[fuse] = m.output()
     err, allowed = tol_range(outs["0"], outs["1"], 1e-2)
     assert err <= allowed, (err, allowed)
+
+
+def test_head_1x1_pairs_fused_one_by_one(cuda, monkeypatch, tmp_path):
+    """The load-time measurement fuses each head 3x3 + 1x1 pair on its own (one launch against
+    two, per pair); a cached schedule keeps the pairs as a bit mask in command order.  With the
+    mask 0b000101 exactly the first and third pairs run fused, and every conv still matches the
+    oracle."""
+    g = build_yolov8n(batch=2, imgsz=160, seed=4)
+    algo = E.w8a8_algo_map(E.lower_graph(g), g.metadata["int8_convs"].split(","))
+    plan = E.compile_plan(g, precision="fp16", algo_overrides=algo)
+    data = E.build_aexrt_engine(g, precision="fp16", algo_overrides=algo, classes=80)
+    x = np.random.default_rng(6).random((2, 3, 160, 160)).astype(np.float32)
+    cmds = plan["replay"]["commands"]
+    n_cmd = len(cmds) + sum(1 for c in cmds if c["kind"] == "CONCAT_CONV1X1")
+
+    def fused_commands():
+        with NativeHipYoloModel(data) as m:
+            m.set_profiling(True)
+            m.run(x)
+            m.set_profiling(False)
+            labels = [lab for lab, _ in m.profile_events() if " then 1x1 cmd#" in lab]
+            checked, _ = _layer_check(m, g, plan)
+            assert checked == 63
+        return sorted(int(lab.split()[0][4:]) for lab in labels)
+
+    monkeypatch.setenv("AEXRT_HIP_FUSE_1X1", "1")
+    every = fused_commands()
+    assert len(every) == 6, every
+    monkeypatch.delenv("AEXRT_HIP_FUSE_1X1")
+    cache = tmp_path / "plan.tune"
+    cache.write_text(f"schedule 2x3x160x160 commands {n_cmd}\t1 1 1 5 0 0 0 0\n")
+    monkeypatch.setenv("AEXRT_HIP_AUTOTUNE", "0")
+    monkeypatch.setenv("AEXRT_HIP_TUNE_CACHE", str(cache))
+    assert fused_commands() == [every[0], every[2]]
