@@ -124,6 +124,9 @@ _SIGS = {
     "aexrt_hip_conv2d_f32": (c_int, [POINTER(ConvDesc), c_uint32, _vp, _vp, _vp, _vp, _vp]),
     "aexrt_hip_conv2d_fused_1x1": (c_int, [POINTER(ConvDesc), c_uint32, POINTER(TensorView), _vp, _vp,
                                            POINTER(ConvDesc), c_uint32, _vp, _vp, POINTER(TensorView), _vp]),
+    "aexrt_hip_conv_chain3": (c_int, [POINTER(ConvDesc), _vp, _vp, POINTER(ConvDesc), _vp, _vp, POINTER(ConvDesc),
+                                      c_uint32, _vp, _vp, POINTER(TensorView), POINTER(TensorView), c_uint32,
+                                      c_uint32, _vp]),
     "aexrt_hip_conv_weight_bytes": (c_int, [POINTER(ConvDesc), c_uint32, POINTER(c_uint64)]),
     "aexrt_hip_pack_conv_weight": (c_int, [POINTER(ConvDesc), c_uint32, c_uint32, _vp, c_uint64, _vp,
                                            c_uint64, _vp]),

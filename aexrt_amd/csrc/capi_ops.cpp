@@ -379,6 +379,50 @@ int aexrt_hip_conv2d_fused_1x1(const AexrtConv2DDesc* desc, uint32_t flags, cons
     return check_hip(launch_conv_igemm(p, false, static_cast<hipStream_t>(stream)), "conv2d_fused_1x1") ? 1 : 0;
 }
 
+int aexrt_hip_conv_chain3(const AexrtConv2DDesc* desc_a, const void* weight_a, const float* bias_a,
+                          const AexrtConv2DDesc* desc_b, const void* weight_b, const float* bias_b,
+                          const AexrtConv2DDesc* desc_c, uint32_t flags_c, const void* weight_c, const float* bias_c,
+                          const AexrtHipTensorView* x, const AexrtHipTensorView* y, uint32_t tile_rows,
+                          uint32_t tile_cols, void* stream) {
+    if (!desc_a || !desc_b || !desc_c || !weight_a || !weight_b || !weight_c || !bias_a || !bias_b || !bias_c || !x ||
+        !y || !x->data || !y->data) {
+        set_error("conv_chain3: null argument");
+        return 0;
+    }
+    if (tile_rows > 4096 || tile_cols > 4096 || (tile_rows == 0) != (tile_cols == 0)) {
+        set_error("conv_chain3: tile rows and columns both 0 (chosen) or both in 1..4096");
+        return 0;
+    }
+    // the intermediates are never stored: dense views of their shapes over
+    // y's memory stand in for them in the parameter checks
+    const AexrtConv2DDesc& a = *desc_a;
+    const AexrtConv2DDesc& b = *desc_b;
+    AexrtHipTensorView t1{}, t2{};
+    t1.data = t2.data = y->data;
+    t1.c_stride = (int32_t)a.out_channels;
+    t1.n_stride = int64_t(a.out_h) * a.out_w * a.out_channels;
+    t2.c_stride = (int32_t)b.out_channels;
+    t2.n_stride = int64_t(b.out_h) * b.out_w * b.out_channels;
+    std::string why;
+    ConvParams pa{}, pb{}, pc{};
+    if (!build_conv_params(a, 5u, AEXRT_HIP_CONV_SILU, *x, weight_a, nullptr, bias_a, nullptr, t1, nullptr, pa, why) ||
+        !build_conv_params(b, 5u, AEXRT_HIP_CONV_SILU, t1, weight_b, nullptr, bias_b, nullptr, t2, nullptr, pb, why) ||
+        !build_conv_params(*desc_c, 5u, flags_c, t2, weight_c, nullptr, bias_c, nullptr, *y, nullptr, pc, why)) {
+        set_error("conv_chain3: " + why);
+        return 0;
+    }
+    if (const char* e = chain_shape_error(pa, pb, pc)) {
+        set_error(std::string("conv_chain3: ") + e);
+        return 0;
+    }
+    int tr = (int)tile_rows, tc = (int)tile_cols;
+    if (!chain_tile(pa, pb, pc, tr, tc)) {
+        set_error("conv_chain3: the tile does not fit the kernel (at most 256 positions per region, LDS)");
+        return 0;
+    }
+    return check_hip(launch_conv_chain(pa, pb, pc, tr, tc, static_cast<hipStream_t>(stream)), "conv_chain3") ? 1 : 0;
+}
+
 int aexrt_hip_conv2d_f32(const AexrtConv2DDesc* desc, uint32_t flags, const float* x, const float* weight,
                          const float* bias, float* y, void* stream) {
     if (!desc || !x || !weight || !bias || !y) {

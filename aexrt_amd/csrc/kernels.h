@@ -132,6 +132,20 @@ LaunchProbe* launch_probe();
 // Kernel and tile launch_conv_igemm(p, int8, ...) runs, as "family tile".
 void conv_kernel_name(const ConvParams& p, bool int8, char* out, size_t n);
 
+// Detect-head branch in one launch (conv_chain.hip): fp16 3x3 SiLU conv a,
+// 3x3 SiLU conv b over a's output, 1x1 conv c over b's output (y), the two
+// intermediate maps kept in LDS.  chain_shape_error: null when the three
+// convs fit the kernel, else the reason.  chain_tile: the tile (rows tr x
+// columns tc) the kernel runs (the given one when it fits; 0 x 0: chosen);
+// false when none fits.
+const char* chain_shape_error(const ConvParams& a, const ConvParams& b, const ConvParams& c);
+bool chain_tile(const ConvParams& a, const ConvParams& b, const ConvParams& c, int& tr, int& tc);
+hipError_t launch_conv_chain(const ConvParams& a, const ConvParams& b, const ConvParams& c, int tr, int tc,
+                             hipStream_t stream);
+// Two branches over one input (br0, br1: their a, b, c) in one launch on one
+// tile (0 x 0: the one that fits the branch with more channels).
+hipError_t launch_conv_chain2(const ConvParams* br0, const ConvParams* br1, int tr, int tc, hipStream_t stream);
+
 // Implicit-GEMM conv (int8 or fp16 MFMA).  Requires C % 8 == 0, OC % 4 == 0,
 // Kp % 64 == 0, OCp % 16 == 0 and 16-byte aligned views.
 hipError_t launch_conv_igemm(const ConvParams& p, bool int8, hipStream_t stream);

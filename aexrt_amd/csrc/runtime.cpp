@@ -19,6 +19,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -103,6 +104,9 @@ struct ConvState {
     // parameters (its input is this conv's output, which is not stored)
     int fused_1x1 = -1, fused_into = -1;
     ConvParams f2p{};
+    // a head branch run in one launch with this 3x3 conv first: the 3x3 conv
+    // over its output (chain_b) and the 1x1 conv over that one's (chain_c)
+    int chain_b = -1, chain_c = -1;
     // sibling pair (this conv first): weights and bias of both convs, rows of
     // this conv then the sibling's, built from the w of each named here
     void* w_pair = nullptr;
@@ -130,10 +134,12 @@ struct Step {
 // Schedule of a network measured at load: sibling convs as one launch, lane
 // count, head 1x1 convs fused into their 3x3 producers.
 struct Schedule {
-    int first = 1;      // sibling pairs in one launch
-    int second = 1;     // lanes
-    int fuse = 0;       // head 3x3 + 1x1 pairs in one launch: 0 none, else the pairs of mask
-    uint32_t mask = 0;  // bit k: the k-th pair in command order (0 with fuse set: every pair)
+    int first = 1;        // sibling pairs in one launch
+    int second = 1;       // lanes
+    int fuse = 0;         // head 3x3 + 1x1 pairs in one launch: 0 none, else the pairs of mask
+    uint32_t mask = 0;    // bit k: the k-th pair in command order (0 with fuse set: every pair)
+    uint32_t chains = 0;  // bit k: the k-th head branch (3x3, 3x3, 1x1) in one launch
+    uint32_t dual = 0;    // bit k: ... sharing its launch with the level's other branch
 };
 
 // Pairs a schedule fuses (bit k: the k-th head pair in command order).
@@ -210,6 +216,12 @@ struct AexrtYoloModel {
     // order; measured at load), and every such pair of the plan (3x3, 1x1 command)
     uint32_t fuse_mask = 0;
     std::vector<std::pair<int, int>> fuse_pairs;
+    // head branches (3x3 SiLU, 3x3 SiLU, 1x1 commands) that can run in one
+    // launch, and those that do (bit k: the k-th in command order; measured
+    // at load per head level)
+    std::vector<std::array<int, 3>> chains;
+    uint32_t chain_mask = 0;
+    uint32_t chain_dual = 0;  // branches of chain_mask that share a launch with another over their input
     std::vector<Step> steps;
     std::vector<CopyJob> copies;
     std::vector<void*> allocations;
@@ -507,6 +519,69 @@ int fuse_head_1x1(AexrtYoloModel* m) {
         V[c.output].elided = true;
     }
     return pairs;
+}
+
+// Head branches that can run in one launch: a fp16 3x3 stride-1 SiLU conv
+// whose output only a second such conv reads, whose output only a 1x1 fp16
+// conv reads, every channel count <= 96.  Lists them in m->chains; those of
+// m->chain_mask take over their convs (the two intermediates are not stored,
+// and a head pair fused by fuse_head_1x1 inside such a branch is undone).
+// Returns the number of branches.
+int setup_chains(AexrtYoloModel* m) {
+    const Engine& e = m->eng;
+    auto& V = m->vals;
+    for (size_t ci = 0; ci < e.commands.size(); ++ci) {
+        ConvState& cs = m->convs[ci];
+        if (cs.chain_b >= 0) {
+            V[e.commands[ci].output].elided = false;
+            V[e.commands[cs.chain_b].output].elided = m->convs[cs.chain_b].fused_1x1 >= 0;
+        }
+        cs.chain_b = cs.chain_c = -1;
+    }
+    m->chains.clear();
+    auto fp16_conv = [&](size_t ci, uint32_t k) {
+        const ConvState& cs = m->convs[ci];
+        const EngineCommand& c = e.commands[ci];
+        if (!cs.is_conv || cs.fused_residual || cs.pg16 || is_int8_algorithm(cs.algorithm) ||
+            is_winograd_algorithm(cs.algorithm))
+            return false;
+        const AexrtConv2DDesc d = desc_of(c);
+        const ValueInfo& x = V[c.inputs[0]];
+        return d.kernel_h == k && d.kernel_w == k && d.stride_h == 1 && d.stride_w == 1 && d.pad_top == k / 2 &&
+               d.out_channels <= 96 && !x.is_input && (k == 1 || (c.kind == kCmdConvSilu && d.in_channels % 16 == 0));
+    };
+    auto only_consumer = [&](size_t ci) {
+        const ValueInfo& y = V[e.commands[ci].output];
+        if (y.consumers.size() != 1 || y.redirect >= 0 || y.rank != 4 || e.commands[ci].output == e.manifest.output_value)
+            return -1;
+        const int cj = y.consumers[0];
+        return e.commands[cj].inputs[0] == e.commands[ci].output ? cj : -1;
+    };
+    for (size_t ci = 0; ci < e.commands.size(); ++ci) {
+        if (!fp16_conv(ci, 3)) continue;
+        const int cb = only_consumer(ci);
+        if (cb < 0 || !fp16_conv((size_t)cb, 3)) continue;
+        const int cc = only_consumer((size_t)cb);
+        if (cc < 0 || !fp16_conv((size_t)cc, 1) || m->convs[cb].fused_residual) continue;
+        bool sib_b = false;  // the second conv must not be half of a sibling pair
+        for (size_t k = 0; k < m->sibling.size(); ++k)
+            sib_b = sib_b || m->sibling[k] == cb || (k == (size_t)cb && m->sibling[k] >= 0);
+        if (sib_b) continue;
+        const int k = (int)m->chains.size();
+        m->chains.push_back({(int)ci, cb, cc});
+        if (k >= 32 || !((m->chain_mask >> k) & 1u)) continue;
+        ConvState& cs = m->convs[ci];
+        ConvState& bs = m->convs[cb];
+        if (bs.fused_1x1 >= 0) {  // the branch's 1x1 pair: now part of the branch
+            m->convs[bs.fused_1x1].fused_into = -1;
+            bs.fused_1x1 = -1;
+        }
+        cs.chain_b = cb;
+        cs.chain_c = cc;
+        V[e.commands[ci].output].elided = true;
+        V[e.commands[cb].output].elided = true;
+    }
+    return (int)m->chains.size();
 }
 
 bool is_fused_add(AexrtYoloModel* m, size_t ci) {
@@ -1010,7 +1085,8 @@ void load_tune_cache(AexrtYoloModel* m) {
             m->refined[line.substr(0, tab)] = c;  // a conv's choice measured in the network
         else if (line.compare(0, 9, "schedule ") == 0)
             m->schedules[line.substr(0, tab)] =
-                Schedule{c.kind, c.jn, c.pw, (uint32_t)c.ksw};  // merge flag, lanes, fusion, fused pairs
+                Schedule{c.kind, c.jn, c.pw, (uint32_t)c.ksw, (uint32_t)c.tr,
+                         (uint32_t)c.tc};  // merge, lanes, fusion, pairs, branches, paired branches
         else
             m->tuned[line.substr(0, tab)] = c;
     }
@@ -1027,7 +1103,7 @@ void save_tune_cache(AexrtYoloModel* m) {
         for (const auto& [key, c] : m->tuned) put(key, c);
         for (const auto& [key, c] : m->refined) put(key, c);
         for (const auto& [key, v] : m->schedules)
-            put(key, ConvChoice{v.first, v.second, v.fuse, (int)v.mask, 0, 0, 0, 0});
+            put(key, ConvChoice{v.first, v.second, v.fuse, (int)v.mask, (int)v.chains, (int)v.dual, 0, 0});
         if (!f) return;
     }
     std::rename(tmp.c_str(), m->tune_cache.c_str());
@@ -1186,6 +1262,114 @@ void label_steps(AexrtYoloModel* m) {
         if (st.family) st.label = st.head + " kernel=" + st.family() + st.tail;
 }
 
+// Kernel parameters of the head branch led by 3x3 conv ci (its a, b, c);
+// false when the three convs do not fit the chain kernel.
+bool chain_params_of(AexrtYoloModel* m, size_t ci, ConvParams (&br)[3]) {
+    const Engine& e = m->eng;
+    const ConvState& cs = m->convs[ci];
+    const int ib = cs.chain_b, ic = cs.chain_c;
+    const ConvState& bs = m->convs[ib];
+    const ConvState& ccs = m->convs[ic];
+    const AexrtHipTensorView xv = view_of(m, (int)e.commands[ci].inputs[0]);
+    const AexrtHipTensorView t1 = view_of(m, cs.out_value), t2 = view_of(m, bs.out_value);
+    const AexrtHipTensorView yv = view_of(m, ccs.out_value);
+    const uint32_t flags_c = (e.commands[ic].kind == kCmdConvSilu ? AEXRT_HIP_CONV_SILU : 0u) |
+                             (is_f32(m, ccs.out_value) ? AEXRT_HIP_CONV_OUT_F32 : 0u);
+    std::string why;
+    int tr = 0, tc = 0;
+    return !is_f32(m, cs.out_value) && !is_f32(m, bs.out_value) &&
+           build_conv_params(conv_desc_padded(m, ci), cs.algorithm, AEXRT_HIP_CONV_SILU, xv, cs.w, nullptr, cs.bias,
+                             nullptr, t1, nullptr, br[0], why) &&
+           build_conv_params(conv_desc_padded(m, (size_t)ib), bs.algorithm, AEXRT_HIP_CONV_SILU, t1, bs.w, nullptr,
+                             bs.bias, nullptr, t2, nullptr, br[1], why) &&
+           build_conv_params(conv_desc_padded(m, (size_t)ic), ccs.algorithm, flags_c, t2, ccs.w, nullptr, ccs.bias,
+                             nullptr, yv, nullptr, br[2], why) &&
+           !chain_shape_error(br[0], br[1], br[2]) && chain_tile(br[0], br[1], br[2], tr, tc);
+}
+
+// Undoes the head branch led by ci (its convs then run on their own).
+void unchain(AexrtYoloModel* m, size_t ci) {
+    const Engine& e = m->eng;
+    ConvState& cs = m->convs[ci];
+    m->vals[e.commands[ci].output].elided = false;
+    m->vals[e.commands[cs.chain_b].output].elided = m->convs[cs.chain_b].fused_1x1 >= 0;
+    cs.chain_b = cs.chain_c = -1;
+}
+
+// The step of the head branch led by 3x3 conv ci (3x3 chain_b, 1x1
+// chain_c), with the branch of another 3x3 conv over the same input in the
+// same launch when there is one (the level's box and class branches);
+// built = false (and the branch undone) when it does not fit the kernel.
+bool build_chain_step(AexrtYoloModel* m, size_t ci, std::vector<bool>& done, bool& built) {
+    built = false;
+    const Engine& e = m->eng;
+    auto& V = m->vals;
+    ConvState& cs = m->convs[ci];
+    ConvParams br0[3];
+    if (!chain_params_of(m, ci, br0)) {
+        unchain(m, ci);
+        return true;
+    }
+    auto dual = [&](size_t c) {
+        for (size_t k = 0; k < m->chains.size() && k < 32; ++k)
+            if (m->chains[k][0] == (int)c) return ((m->chain_dual >> k) & 1u) != 0;
+        return false;
+    };
+    int partner = -1;
+    ConvParams br1[3];
+    for (size_t cj = ci + 1; cj < e.commands.size() && partner < 0 && dual(ci); ++cj) {
+        if (done[cj] || m->convs[cj].chain_b < 0 || e.commands[cj].inputs[0] != e.commands[ci].inputs[0] || !dual(cj))
+            continue;
+        if (!chain_params_of(m, cj, br1)) continue;
+        LaunchProbe probe{};
+        set_launch_probe(&probe);
+        const hipError_t pe = launch_conv_chain2(br0, br1, 0, 0, nullptr);
+        set_launch_probe(nullptr);
+        if (pe == hipSuccess) partner = (int)cj;
+    }
+    const int ib = cs.chain_b, ic = cs.chain_c;
+    std::string tail = " then cmd#" + std::to_string(e.src_cmd[ib]) + " then 1x1 cmd#" + std::to_string(e.src_cmd[ic]);
+    std::vector<int> writes = {V[m->convs[ic].out_value].pl.root};
+    if (partner >= 0) {
+        const ConvState& ps = m->convs[partner];
+        const std::array<ConvParams, 3> a0{br0[0], br0[1], br0[2]}, a1{br1[0], br1[1], br1[2]};
+        m->steps.push_back(Step{(int)ci, "", [a0, a1](hipStream_t s) {
+                                    return launch_conv_chain2(a0.data(), a1.data(), 0, 0, s);
+                                }});
+        m->steps.back().family = [a0, a1] {
+            LaunchProbe probe{};
+            set_launch_probe(&probe);
+            (void)launch_conv_chain2(a0.data(), a1.data(), 0, 0, nullptr);
+            set_launch_probe(nullptr);
+            return std::string(probe.name);
+        };
+        tail += " + cmd#" + std::to_string(e.src_cmd[partner]) + " then cmd#" + std::to_string(e.src_cmd[ps.chain_b]) +
+                " then 1x1 cmd#" + std::to_string(e.src_cmd[ps.chain_c]);
+        writes.push_back(V[m->convs[ps.chain_c].out_value].pl.root);
+        done[partner] = done[ps.chain_b] = done[ps.chain_c] = true;
+    } else {
+        const std::array<ConvParams, 3> a0{br0[0], br0[1], br0[2]};
+        m->steps.push_back(Step{(int)ci, "", [a0](hipStream_t s) {
+                                    return launch_conv_chain(a0[0], a0[1], a0[2], 0, 0, s);
+                                }});
+        m->steps.back().family = [a0] {
+            LaunchProbe probe{};
+            set_launch_probe(&probe);
+            (void)launch_conv_chain(a0[0], a0[1], a0[2], 0, 0, nullptr);
+            set_launch_probe(nullptr);
+            return std::string(probe.name);
+        };
+    }
+    Step& st = m->steps.back();
+    st.head = conv_label(e.commands[ci], e.src_cmd[ci], cs.algorithm);
+    st.tail = tail;
+    st.reads = {V[e.commands[ci].inputs[0]].pl.root};
+    st.writes = writes;
+    done[ib] = done[ic] = true;
+    built = true;
+    return true;
+}
+
 bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
     Engine& e = m->eng;
     auto& V = m->vals;
@@ -1231,8 +1415,13 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                 AexrtConv2DDesc d = conv_desc_padded(m, ci);
                 // a sibling pair whose weights still are those the pair was built from
                 const int sib = m->sibling.empty() ? -1 : m->sibling[ci];
+                if (cs.chain_b >= 0) {
+                    bool built = false;
+                    if (!build_chain_step(m, ci, done, built)) return false;
+                    if (built) break;
+                }
                 const bool pair = m->merge_siblings && sib >= 0 && !done[sib] && cs.w_pair && cs.pair_src[0] == cs.w &&
-                                  cs.pair_src[1] == m->convs[sib].w;
+                                  cs.pair_src[1] == m->convs[sib].w && cs.chain_b < 0 && m->convs[sib].chain_b < 0;
                 if (pair) d.out_channels += desc_of(e.commands[sib]).out_channels;
                 uint32_t flags = c.kind == kCmdConvSilu ? AEXRT_HIP_CONV_SILU : 0u;
                 AexrtHipTensorView xvw{};
@@ -1940,7 +2129,9 @@ bool build_model(AexrtYoloModel* m) {
     }
     if (!plan_memory(m, m->copies)) return false;
     m->fuse_mask = 0;
+    m->chain_mask = 0;
     const int fusable = fuse_head_1x1(m);
+    setup_chains(m);
     mark_slot_readers(m);
     // arena
     size_t total = 0;
@@ -1992,6 +2183,11 @@ bool build_model(AexrtYoloModel* m) {
     // both are measured (with autotuning) or the cached schedule's choice is taken
     const char* f1 = std::getenv("AEXRT_HIP_FUSE_1X1");
     const int fuse_forced = f1 && (f1[0] == '0' || f1[0] == '1') ? f1[0] - '0' : -1;
+    // AEXRT_HIP_CHAIN=0 / 1: head branches (3x3, 3x3, 1x1) never / always in one
+    // launch; otherwise measured per head level (with autotuning) or cached
+    const char* ch = std::getenv("AEXRT_HIP_CHAIN");
+    const int chain_forced = ch && (ch[0] == '0' || ch[0] == '1') ? ch[0] - '0' : -1;
+    const bool chain_choice = !m->chains.empty() && chain_forced < 0 && m->autotune && m->use_graph;
     const bool fuse_choice = fusable > 0 && fuse_forced < 0 && m->autotune && m->use_graph;
     const int merge_variants = pairs && m->autotune && m->use_graph ? 2 : 1;
     const int variants = merge_variants * (fuse_choice ? 2 : 1);
@@ -2014,6 +2210,12 @@ bool build_model(AexrtYoloModel* m) {
         if (use_cached_sched) return schedule_fuse_mask(cached_sched->second);
         return fuse_choice && k / merge_variants == 0 ? ~0u : 0u;
     };
+    // head branches while the schedule variants are measured: forced, cached
+    // or none (measured afterwards)
+    const uint32_t chains0 = chain_forced >= 0 ? (chain_forced ? ~0u : 0u)
+                             : use_cached_sched ? cached_sched->second.chains
+                                                : 0u;
+    m->chain_dual = chain_forced >= 0 ? (chain_forced ? ~0u : 0u) : use_cached_sched ? cached_sched->second.dual : 0u;
     // per head pair and merge setting: the fused step's time (index 1), the
     // unfused 3x3 and 1x1 steps' (index 0)
     std::vector<float> pair_ms[2][2];
@@ -2021,6 +2223,8 @@ bool build_model(AexrtYoloModel* m) {
         m->merge_siblings = use_cached_sched ? cached_sched->second.first != 0 : k % merge_variants == 0;
         m->fuse_mask = fuse_for(k);
         fuse_head_1x1(m);
+        m->chain_mask = chains0;
+        setup_chains(m);
         m->n_lanes = 1;
         if (!build_steps(m, m->copies)) return false;
         if (m->autotune && !refine_in_context(m)) return false;
@@ -2060,6 +2264,7 @@ bool build_model(AexrtYoloModel* m) {
         m->merge_siblings = best_merge;
         m->fuse_mask = best_fuse;
         fuse_head_1x1(m);
+        setup_chains(m);
         m->n_lanes = 1;
         if (!build_steps(m, m->copies)) return false;
         if (m->autotune && !refine_in_context(m)) return false;
@@ -2077,9 +2282,65 @@ bool build_model(AexrtYoloModel* m) {
         schedule_steps(m);
         drop_graph(m);
     }
+    // head branches on the chain kernel, per head level (the branches reading
+    // one input): the captured schedule timed with the level's branches as a
+    // launch each and as one launch together, against the current steps; the
+    // fastest kept
+    if (chain_choice) {
+        auto rebuild = [&]() {
+            const int lanes_kept = m->n_lanes;
+            fuse_head_1x1(m);
+            setup_chains(m);
+            m->n_lanes = 1;
+            if (!build_steps(m, m->copies)) return false;
+            if (!refine_in_context(m)) return false;
+            m->n_lanes = lanes_kept;
+            schedule_steps(m);
+            drop_graph(m);
+            return true;
+        };
+        float base = 0.0f;
+        if (!time_schedule(m, &base)) return false;
+        std::vector<uint32_t> levels;  // input value of each level, in command order
+        for (const auto& c3 : m->chains) {
+            const uint32_t in = e.commands[c3[0]].inputs[0];
+            if (std::find(levels.begin(), levels.end(), in) == levels.end()) levels.push_back(in);
+        }
+        for (uint32_t lv : levels) {
+            uint32_t bits = 0;
+            for (size_t k = 0; k < m->chains.size() && k < 32; ++k)
+                if (e.commands[m->chains[k][0]].inputs[0] == lv) bits |= 1u << k;
+            // the level's branches one launch each (side by side on the lanes), then
+            // both in one launch
+            const uint32_t kept = m->chain_mask, kept_dual = m->chain_dual;
+            uint32_t best_mask = kept, best_dual = kept_dual;
+            for (int variant = 0; variant < 2; ++variant) {
+                m->chain_mask = kept | bits;
+                m->chain_dual = variant ? (kept_dual | bits) : (kept_dual & ~bits);
+                if (!rebuild()) return false;
+                float ms = 0.0f;
+                if (!time_schedule(m, &ms)) return false;
+                const bool faster = ms < base * 0.995f;
+                if (m->tune_log)
+                    std::fprintf(stderr, "aexrt head branches on value %u %s: %.1f us against %.1f us%s\n", lv,
+                                 variant ? "in one launch" : "one launch each", ms * 100.0f, base * 100.0f,
+                                 faster ? " (kept)" : "");
+                if (faster) {
+                    base = ms;
+                    best_mask = m->chain_mask;
+                    best_dual = m->chain_dual;
+                }
+            }
+            if (best_mask != m->chain_mask || best_dual != m->chain_dual) {
+                m->chain_mask = best_mask;
+                m->chain_dual = best_dual;
+                if (!rebuild()) return false;
+            }
+        }
+    }
     if (m->autotune)
         m->schedules[skey] = Schedule{m->merge_siblings ? 1 : 0, m->n_lanes, m->fuse_mask ? 1 : 0,
-                                      m->fuse_mask == ~0u ? 0u : m->fuse_mask};
+                                      m->fuse_mask == ~0u ? 0u : m->fuse_mask, m->chain_mask, m->chain_dual};
     if (m->tune_log && variants > 1)
         std::fprintf(stderr, "aexrt sibling convs: %s, head 1x1 convs fused: %s (mask %#x)\n",
                      best_merge ? "one launch" : "two launches",

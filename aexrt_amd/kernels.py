@@ -304,6 +304,19 @@ def conv2d_fused_1x1(pc: PreparedConv, pc2: PreparedConv, x, y2, *, flags2: int 
         pc2.weight.data_ptr(), pc2.bias.data_ptr(), ctypes.byref(yv), _stream(stream)), "conv2d_fused_1x1")
 
 
+def conv_chain3(pa: PreparedConv, pb: PreparedConv, pc: PreparedConv, x, y, *, flags_c: int = 0, tile=(0, 0),
+                stream=None) -> None:
+    """A detect-head branch in one launch: y = conv_c(fp16(silu(conv_b(fp16(silu(conv_a(x))))))) with
+    a, b fp16 3x3 SiLU convs and c a 1x1 conv (SiLU with flags_c SILU, fp32 y with OUT_F32); the two
+    intermediate maps stay in LDS.  tile = (rows, cols) of a block's output tile, (0, 0): chosen."""
+    da, db, dc = (ConvDesc.from_params(p.params) for p in (pa, pb, pc))
+    xv, yv = view(x), view(y)
+    check(_lib.lib().aexrt_hip_conv_chain3(
+        ctypes.byref(da), pa.weight.data_ptr(), pa.bias.data_ptr(), ctypes.byref(db), pb.weight.data_ptr(),
+        pb.bias.data_ptr(), ctypes.byref(dc), flags_c, pc.weight.data_ptr(), pc.bias.data_ptr(), ctypes.byref(xv),
+        ctypes.byref(yv), int(tile[0]), int(tile[1]), _stream(stream)), "conv_chain3")
+
+
 def conv2d_int8(pc: PreparedConv, x, y, *, flags: int = SILU, residual=None, stream=None) -> None:
     """The reference's int8 conv command on a plain fp16 NHWC input: dynamic below 4096 input
     elements, else the input's amax (strips with INT8_PG16) then the int8 conv."""

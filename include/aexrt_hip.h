@@ -327,6 +327,22 @@ int aexrt_hip_conv2d_fused_1x1(const AexrtConv2DDesc* desc, uint32_t flags, cons
                                const void* weight, const float* bias, const AexrtConv2DDesc* desc2, uint32_t flags2,
                                const void* weight2, const float* bias2, const AexrtHipTensorView* y2, void* stream);
 
+/* A detect-head branch in one launch: y = conv_c(t2), t2 = fp16(silu(conv_b(t1)
+ * + bias_b)), t1 = fp16(silu(conv_a(x) + bias_a)); a and b fp16 3x3 stride-1
+ * pad-1 convs (algorithm 5 weights), b over a's output, c a 1x1 conv over b's
+ * output (flags_c: SILU, OUT_F32; y without amax slots); every conv at most 96
+ * output channels, the 3x3 inputs in 16-channel steps.  t1 and t2 stay in the
+ * kernel's LDS (one tile of tile_rows x tile_cols outputs per block plus the
+ * border conv b needs, recomputed by neighbouring tiles; 0 x 0: chosen) and
+ * are never stored.  The reference runs these three convs of each head
+ * branch inside its fused head replay group (fusion kinds 4/5,
+ * src/aexrt/engine.py:78-79).  Returns 0 and sets the error otherwise. */
+int aexrt_hip_conv_chain3(const AexrtConv2DDesc* desc_a, const void* weight_a, const float* bias_a,
+                          const AexrtConv2DDesc* desc_b, const void* weight_b, const float* bias_b,
+                          const AexrtConv2DDesc* desc_c, uint32_t flags_c, const void* weight_c, const float* bias_c,
+                          const AexrtHipTensorView* x, const AexrtHipTensorView* y, uint32_t tile_rows,
+                          uint32_t tile_cols, void* stream);
+
 /* Tuning/test hook, no reference counterpart: mode 1 runs every int8 1x1
  * stride-1 conv launched without a measured kernel choice on the streaming
  * 1x1 kernel (weights resident in LDS, each tile's input loaded at once and

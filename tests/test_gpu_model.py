@@ -90,17 +90,18 @@ def _layer_check(model: NativeHipYoloModel, graph: Graph, plan: dict, tol=1e-2, 
         fused = rank_y == 0
         nxt = cmds[consumers[out][0]] if fused else None
         convs_in_check = 1
-        if fused and nxt["kind"] in ("CONV", "CONV_SILU"):
-            # a 1x1 conv applied in this conv's epilogue: the pair against the oracle's two convs
-            # with this conv's output rounded to fp16 in between
+        while fused and nxt["kind"] in ("CONV", "CONV_SILU"):
+            # convs run in this conv's launch (a 1x1 in its epilogue, or a head branch's 3x3 and
+            # 1x1): against the oracle's convs with each unstored output rounded to fp16 between
             w2 = names[nxt["inputs"][1]]
             node2 = convs[w2.rsplit(".w", 1)[0]]
             y_ref = ON.conv_layer(O.round_f16(y_ref), graph.constants[w2], graph.constants[names[nxt["inputs"][2]]],
                                   node2.attrs, int8=False, silu=nxt["kind"] == "CONV_SILU", threads=threads)
             out = nxt["output"]
-            fused = False
-            convs_in_check = 2
-        elif fused:  # fused into the residual add that consumes it
+            convs_in_check += 1
+            fused = model.value_info(out)[0] == 0
+            nxt = cmds[consumers[out][0]] if fused else None
+        if fused:  # fused into the residual add that consumes it
             add = cmds[consumers[out][0]]
             other = [v for v in add["inputs"] if v != out][0]
             conv_ref = O.round_f16(y_ref)
@@ -522,6 +523,7 @@ def test_plan_counters_describe_the_prepared_step_list(cuda, monkeypatch):
     supported, the fused residual adds, the paired head convs, the head's 1x1 convs in their 3x3
     producers' epilogues, convs per kernel family adding up."""
     monkeypatch.setenv("AEXRT_HIP_FUSE_1X1", "1")
+    monkeypatch.setenv("AEXRT_HIP_CHAIN", "0")
     g, names, plan, data = _yolo_engine(2, 320)
     with NativeHipYoloModel(data) as m:
         c = m.counter
@@ -580,6 +582,7 @@ def test_head_1x1_convs_fused_and_on_their_own(cuda, monkeypatch):
     data = E.build_aexrt_engine(g, precision="fp16", algo_overrides=algo, classes=80)
     x = np.random.default_rng(6).random((2, 3, 160, 160)).astype(np.float32)
     outs = {}
+    monkeypatch.setenv("AEXRT_HIP_CHAIN", "0")  # the pairs, not whole head branches
     for fuse in ("1", "0"):
         monkeypatch.setenv("AEXRT_HIP_FUSE_1X1", fuse)
         with NativeHipYoloModel(data) as m:
@@ -588,12 +591,43 @@ def test_head_1x1_convs_fused_and_on_their_own(cuda, monkeypatch):
             m.set_profiling(False)
             fused = [lab for lab, _ in m.profile_events() if " then 1x1 cmd#" in lab]
             assert len(fused) == (6 if fuse == "1" else 0), fused
-            assert all("conv3x3_m32_kernel<false," in lab and ",true>" in lab for lab in fused), fused
+            # the fused-1x1 (F2) instances: one wave group ("...,true>") or two ("...,true,2>")
+            assert all("conv3x3_m32_kernel<false," in lab and (",true>" in lab or ",true,2>" in lab)
+                       for lab in fused), fused
             assert m.counter("head_final_conv_fusion_enabled") == (1 if fuse == "1" else 0)
             checked, _ = _layer_check(m, g, plan)
             assert checked == 63
             m.run(x)
             outs[fuse] = m.output()
+    err, allowed = tol_range(outs["0"], outs["1"], 1e-2)
+    assert err <= allowed, (err, allowed)
+
+
+def test_head_branches_in_one_launch(cuda, monkeypatch):
+    """Each head branch (3x3 SiLU, 3x3 SiLU, 1x1) on the chain kernel, a level's two branches in
+    one launch, the intermediate maps never stored: every conv matches the oracle (each branch
+    against the oracle's three convs with the unstored outputs rounded to fp16), and the raw head
+    outputs agree with the separate launches."""
+    g = build_yolov8n(batch=2, imgsz=160, seed=4)
+    algo = E.w8a8_algo_map(E.lower_graph(g), g.metadata["int8_convs"].split(","))
+    plan = E.compile_plan(g, precision="fp16", algo_overrides=algo)
+    data = E.build_aexrt_engine(g, precision="fp16", algo_overrides=algo, classes=80)
+    x = np.random.default_rng(6).random((2, 3, 160, 160)).astype(np.float32)
+    outs = {}
+    for chain in ("1", "0"):
+        monkeypatch.setenv("AEXRT_HIP_CHAIN", chain)
+        with NativeHipYoloModel(data) as m:
+            m.set_profiling(True)
+            m.run(x)
+            m.set_profiling(False)
+            # one launch per head level: its box and class branches together
+            labels = [lab for lab, _ in m.profile_events() if "conv_chain" in lab]
+            assert len(labels) == (3 if chain == "1" else 0), labels
+            assert all("conv_chain2_kernel<" in lab and lab.count(" then 1x1 cmd#") == 2 for lab in labels), labels
+            checked, _ = _layer_check(m, g, plan)
+            assert checked == 63
+            m.run(x)
+            outs[chain] = m.output()
     err, allowed = tol_range(outs["0"], outs["1"], 1e-2)
     assert err <= allowed, (err, allowed)
 
@@ -622,6 +656,7 @@ def test_head_1x1_pairs_fused_one_by_one(cuda, monkeypatch, tmp_path):
         return sorted(int(lab.split()[0][4:]) for lab in labels)
 
     monkeypatch.setenv("AEXRT_HIP_FUSE_1X1", "1")
+    monkeypatch.setenv("AEXRT_HIP_CHAIN", "0")
     every = fused_commands()
     assert len(every) == 6, every
     monkeypatch.delenv("AEXRT_HIP_FUSE_1X1")
