@@ -9,7 +9,10 @@
 // the input window X (G's in-image part plus one more pixel, zero outside
 // the image): neighbouring tiles recompute their shared border of conv a.
 //
-//   prologue  biases -> LDS; X -> LDS (buffer_load ... lds, zeros outside the
+//   prologue  this block's slice of a's and b's weights towards L2 (the blocks
+//             of one XCD together cover all of them; LDS-DMA loads into a
+//             sink, the data dropped), so that the ring's loads hit L2;
+//             biases -> LDS; X -> LDS (buffer_load ... lds, zeros outside the
 //             image); G zeroed; tap tables
 //   conv a    k steps of a in chunks of KC; the chunks' weights stream
 //             through an LDS ring of D slots (loads of D - 1 chunks in
@@ -43,6 +46,7 @@ struct ChainParams {
     int ka, kb;          // k steps of a (9 * a.C / 16) and of b (9 * b.C / 16)
     int nchunk_a, nchunk;  // weight chunks of a, of a and b
     int x_off, g_off;    // LDS byte offsets of the window X and the grid G (after the ring)
+    int sink_off;        // LDS byte offset of the prefetch sink (1 KB per wave, after G)
     uint32_t x_img, y_img;  // bytes of one image's input / output view
     FastDiv fd_tpi, fd_ntc;
 };
@@ -70,10 +74,10 @@ __device__ __forceinline__ int small_div(int a, float inv) { return (int)(((floa
 // MQ: position subtiles per wave and region (regions of up to 128 MQ
 // positions); with MQ = 1 the operands of the next chunk are read from LDS
 // while the MFMAs of the current one run.  blk: the block's tile; lds: the
-// dynamic LDS [ring: kD * CB][X][G]; the tap tables (2 * kChainMaxSteps ints
-// each) and biases (128 floats each) in LDS too.
+// dynamic LDS [ring: kD * CB][X][G][sink]; the biases (128 floats each) in
+// LDS too.
 template <int NQ, int MQ>
-__device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8_t* lds, int* l_toff_a, int* l_toff_b,
+__device__ __forceinline__ void chain_block(const ChainParams& h, int blk, int slice, int nslice, uint8_t* lds,
                                             float* l_bias_a, float* l_bias, float* l_bias2) {
     constexpr int NOCB = NQ * 32;                // output channels of the block (every channel of a, b, c)
     constexpr int CB = kKC * 2 * NOCB * 16;      // LDS bytes of one weight chunk
@@ -107,6 +111,19 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
     const rsrc_t rx = make_rsrc(static_cast<const uint8_t*>(pa.x) + (int64_t)n * pa.x_nstride * 2, h.x_img);
     const rsrc_t rwa = make_rsrc(pa.w, (uint32_t)pa.OCp * (uint32_t)pa.Kp * 2u);
     const rsrc_t rwb = make_rsrc(pb.w, (uint32_t)pb.OCp * (uint32_t)pb.Kp * 2u);
+
+    // ---- slice `slice` of nslice of a's and b's weights towards L2 -----------
+    {
+        uint8_t* const sink = lds + h.sink_off + wave * 1024;
+        auto warm = [&](rsrc_t r, uint32_t bytes) {
+            const uint32_t per = ((bytes + (uint32_t)nslice - 1) / (uint32_t)nslice + 1023u) & ~1023u;
+            const uint32_t lo = (uint32_t)slice * per, hi = min(bytes, lo + per);
+            for (uint32_t o = lo + (uint32_t)wave * 1024u; o < hi; o += 4096u)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)sink, 16, o + (uint32_t)lane * 16u, 0, 0, 0);
+        };
+        warm(rwa, (uint32_t)pa.OCp * (uint32_t)pa.Kp * 2u);
+        warm(rwb, (uint32_t)pb.OCp * (uint32_t)pb.Kp * 2u);
+    }
 
     // ---- biases -> LDS (loads straight into LDS: no register waits) ---------
     if (wave < 2) {
@@ -169,17 +186,22 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
         const int ng = NQ * 4 * GNPIX;
         for (int e = tid; e < ng; e += kNT) *reinterpret_cast<v4i*>(gb + e * 16) = v4i{0, 0, 0, 0};
     }
-    // k step s, half hi: byte offset of its plane and tap relative to the
-    // position's (0, 0) tap pixel (k = tap * C + c); past the last step any
-    // in-map offset (its weights are zero)
-    for (int e = tid; e < 2 * h.ka; e += kNT) {
-        const int k0 = 16 * (e >> 1), tap = k0 / pa.C, c0 = k0 - tap * pa.C;
-        l_toff_a[e] = (((c0 >> 3) + (e & 1)) * XNPIX + (tap / 3) * XW + tap % 3) * 16;
-    }
-    for (int e = tid; e < 2 * h.kb; e += kNT) {
-        const int k0 = 16 * (e >> 1), tap = k0 / pb.C, c0 = k0 - tap * pb.C;
-        l_toff_b[e] = (((c0 >> 3) + (e & 1)) * GNPIX + (tap / 3) * GW + tap % 3) * 16;
-    }
+    // k step s (k = tap * C + c, 16 channels of one tap), half hi: byte offset
+    // of its plane and tap relative to the position's (0, 0) tap pixel in a map
+    // of npix pixels, w per row; past the last step the last one's (its
+    // weights are zero).  Block-uniform but for hi: no table, no LDS read on
+    // the way to the operand reads.
+    struct Taps {
+        int cs16, npix, w, hi_off;
+        float inv_cs16;
+    };
+    const Taps taps_a{pa.C / 16, XNPIX, XW, hi * XNPIX * 16, 1.0f / (float)(pa.C / 16)};
+    const Taps taps_b{pb.C / 16, GNPIX, GW, hi * GNPIX * 16, 1.0f / (float)(pb.C / 16)};
+    auto tap_off = [](const Taps& t, int s) {
+        const int tap = small_div(s, t.inv_cs16);
+        const int ky = (tap * 11) >> 5;  // tap / 3 for tap < 9
+        return (((s - tap * t.cs16) * 2) * t.npix + ky * t.w + (tap - 3 * ky)) * 16 + t.hi_off;
+    };
     // this wave's position subtiles: window / grid byte offset of each
     // position (clamped to the region), conv b's output offsets
     int bofs_a[MQ], bofs_b[MQ], yo[MQ];
@@ -216,9 +238,12 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
     // too, since LDS-DMA loads count as LDS writes.
     auto ring_wait = [&](int c) {
         __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS reads and writes done
         if (c + kD - 2 < h.nchunk) {
-            static_assert(PT * (kD - 2) < 16, "vmcnt in the low field");
-            __builtin_amdgcn_s_waitcnt(0x0070 | (PT * (kD - 2)));  // vmcnt(PT * (kD - 2)) lgkmcnt(0)
+            // s_waitcnt vmcnt(PT * (kD - 2)) lgkmcnt(0): vmcnt bits 3:0 and 15:14, expcnt 7
+            constexpr int vm = PT * (kD - 2);
+            static_assert(vm < 64, "vmcnt field");
+            __builtin_amdgcn_s_waitcnt((vm & 15) | ((vm >> 4) << 14) | 0x0070);
         } else {
             __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
         }
@@ -232,12 +257,12 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
     struct Ops {
         v4i A[kKC][NQ], B[kKC][MQ];
     };
-    auto fetch = [&](int c, int s0, int ks, const uint8_t* map, const int* toff, const int (&bofs)[MQ], Ops& o) {
+    auto fetch = [&](int c, int s0, int ks, const uint8_t* map, const Taps& taps, const int (&bofs)[MQ], Ops& o) {
         const uint8_t* const ws = lds + (c & (kD - 1)) * CB + abase;
 #pragma unroll
         for (int sl = 0; sl < kKC; ++sl) {
             const int s = min(s0 + sl, ks - 1);
-            const int to = toff[s * 2 + hi];
+            const int to = tap_off(taps, s);
 #pragma unroll
             for (int j = 0; j < NQ; ++j) o.A[sl][j] = *reinterpret_cast<const v4i*>(ws + sl * (2 * NOCB * 16) + j * 512);
 #pragma unroll
@@ -259,25 +284,48 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
             }
         }
     };
+    // one k step: the MFMAs of step sl of `cur` (every one, straight-line: past
+    // the last k step the weights are zero, and a wave past the region
+    // computes clamped positions it never stores), then the operand reads of
+    // step sl of the next chunk into `nxt`, so that the reads run while the
+    // matrix core works
+    auto mma_fetch = [&](const Ops& cur, int cn, int s0n, int ks, const uint8_t* map, const Taps& taps,
+                         const int (&bofs)[MQ], Ops& nxt, bool more) {
+        const uint8_t* const ws = lds + (cn & (kD - 1)) * CB + abase;
+#pragma unroll
+        for (int sl = 0; sl < kKC; ++sl) {
+#pragma unroll
+            for (int q = 0; q < MQ; ++q)
+#pragma unroll
+                for (int j = 0; j < NQ; ++j)
+                    acc[q][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, cur.A[sl][j]),
+                                                                       __builtin_bit_cast(v8h, cur.B[sl][q]), acc[q][j],
+                                                                       0, 0, 0);
+            if (more) {  // block-uniform
+                const int s = min(s0n + sl, ks - 1);
+                const int to = tap_off(taps, s);
+#pragma unroll
+                for (int j = 0; j < NQ; ++j)
+                    nxt.A[sl][j] = *reinterpret_cast<const v4i*>(ws + sl * (2 * NOCB * 16) + j * 512);
+#pragma unroll
+                for (int q = 0; q < MQ; ++q) nxt.B[sl][q] = *reinterpret_cast<const v4i*>(map + bofs[q] + to);
+            }
+        }
+    };
     // chunks [cb, ce) of one conv (k steps from (c - cb) * kKC)
-    auto conv = [&](int cb, int ce, int ks, const uint8_t* map, const int* toff, const int (&bofs)[MQ], int myq) {
+    auto conv = [&](int cb, int ce, int ks, const uint8_t* map, const Taps& toff, const int (&bofs)[MQ], int myq) {
         if constexpr (MQ == 1) {
-            // the next chunk's barrier and operand reads before this chunk's MFMAs
+            // the next chunk's barrier, then this chunk's MFMAs interleaved with
+            // the next chunk's operand reads
             Ops o0, o1;
             ring_wait(cb);
             fetch(cb, 0, ks, map, toff, bofs, o0);
             for (int c = cb; c < ce; c += 2) {
+                if (c + 1 < ce) ring_wait(c + 1);
+                mma_fetch(o0, c + 1, (c + 1 - cb) * kKC, ks, map, toff, bofs, o1, c + 1 < ce);
                 if (c + 1 < ce) {
-                    ring_wait(c + 1);
-                    fetch(c + 1, (c + 1 - cb) * kKC, ks, map, toff, bofs, o1);
-                }
-                mma((c - cb) * kKC, ks, myq, o0);
-                if (c + 1 < ce) {
-                    if (c + 2 < ce) {
-                        ring_wait(c + 2);
-                        fetch(c + 2, (c + 2 - cb) * kKC, ks, map, toff, bofs, o0);
-                    }
-                    mma((c + 1 - cb) * kKC, ks, myq, o1);
+                    if (c + 2 < ce) ring_wait(c + 2);
+                    mma_fetch(o1, c + 2, (c + 2 - cb) * kKC, ks, map, toff, bofs, o0, c + 2 < ce);
                 }
             }
         } else {
@@ -291,7 +339,7 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
     };
 
     // ---- conv a --------------------------------------------------------------
-    conv(0, h.nchunk_a, h.ka, lds + h.x_off, l_toff_a, bofs_a, myq1);
+    conv(0, h.nchunk_a, h.ka, lds + h.x_off, taps_a, bofs_a, myq1);
     // epilogue a: fp16(silu(acc + bias)) -> G at the position's grid pixel
     {
         uint8_t* const gb = lds + h.g_off;
@@ -323,7 +371,7 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
         }
     }
     // ---- conv b (its first barrier orders the G writes before its reads) -----
-    conv(h.nchunk_a, h.nchunk, h.kb, lds + h.g_off, l_toff_b, bofs_b, myq2);
+    conv(h.nchunk_a, h.nchunk, h.kb, lds + h.g_off, taps_b, bofs_b, myq2);
 
     // ---- epilogue b + the 1x1 conv c -------------------------------------------
     // y1 = fp16(silu(acc + bias_b)) is the B operand of c: k step k2 of c takes
@@ -402,9 +450,10 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
 template <int NQ, int MQ>
 __global__ __launch_bounds__(kNT) void conv_chain_kernel(ChainParams h) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    __shared__ int l_toff_a[2 * kChainMaxSteps], l_toff_b[2 * kChainMaxSteps];
     __shared__ __attribute__((aligned(16))) float l_bias_a[128], l_bias[128], l_bias2[128];
-    chain_block<NQ, MQ>(h, xcd_remap(blockIdx.x, gridDim.x), lds, l_toff_a, l_toff_b, l_bias_a, l_bias, l_bias2);
+    const int blk = xcd_remap(blockIdx.x, gridDim.x);
+    const int per_xcd = max(1, (int)gridDim.x / 8);  // blocks of one XCD share the weight prefetch
+    chain_block<NQ, MQ>(h, blk, blk % per_xcd, per_xcd, lds, l_bias_a, l_bias, l_bias2);
 }
 
 // Two branches over one input (the head level's box and class branches): the
@@ -413,13 +462,14 @@ __global__ __launch_bounds__(kNT) void conv_chain_kernel(ChainParams h) {
 template <int NQ0, int NQ1, int MQ>
 __global__ __launch_bounds__(kNT) void conv_chain2_kernel(ChainParams h0, ChainParams h1) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    __shared__ int l_toff_a[2 * kChainMaxSteps], l_toff_b[2 * kChainMaxSteps];
     __shared__ __attribute__((aligned(16))) float l_bias_a[128], l_bias[128], l_bias2[128];
     const int blk = xcd_remap(blockIdx.x, gridDim.x);
+    const int per_xcd = max(1, (int)gridDim.x / 8);  // blocks of one XCD share the weight prefetch
     if (blk < h0.ntile)
-        chain_block<NQ0, MQ>(h0, blk, lds, l_toff_a, l_toff_b, l_bias_a, l_bias, l_bias2);
+        chain_block<NQ0, MQ>(h0, blk, blk % per_xcd, per_xcd, lds, l_bias_a, l_bias, l_bias2);
     else
-        chain_block<NQ1, MQ>(h1, blk - h0.ntile, lds, l_toff_a, l_toff_b, l_bias_a, l_bias, l_bias2);
+        chain_block<NQ1, MQ>(h1, blk - h0.ntile, blk % per_xcd, per_xcd, lds, l_bias_a, l_bias,
+                             l_bias2);
 }
 
 }  // namespace chain
