@@ -72,9 +72,9 @@ def _steps_after_calibration(disp: List[dict], nsteps: int) -> tuple:
 
 
 def short_name(kernel: str) -> str:
-    k = re.sub(r"^void ", "", kernel)
+    k = re.sub(r"^void ", "", kernel).replace("(anonymous namespace)::", "")
     k = re.sub(r"\(.*$", "", k)
-    return k.replace("aexrt::", "").replace("(anonymous namespace)::", "").replace("igemm::", "")
+    return k.replace("aexrt::", "").replace("igemm::", "")
 
 
 def traffic_table(fetch_dir: str, write_dir: str, pass_log: str, trace_dir: Optional[str] = None) -> List[dict]:

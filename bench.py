@@ -31,6 +31,7 @@ single-conv benchmark configurations, GPU and single-thread CPU, as JSON lines).
 from __future__ import annotations
 
 import argparse
+import re
 import json
 import os
 import platform
@@ -138,23 +139,30 @@ def parse_label(label: str):
 
 
 def launch_work(label: str, replay):
-    """(ops, algorithmic bytes) of one conv launch (a sibling pair reads its input once; a fused
-    1x1 reads the 3x3 output in registers, so neither that output nor its read is HBM traffic)."""
-    ci, _, int8, sibs, fused = parse_label(label)
+    """(ops, algorithmic bytes) of one conv launch: every conv the label names (a sibling pair,
+    a fused 1x1, a head branch of three convs or a level's two branches); HBM bytes are each
+    distinct input read once, the outputs no conv of the launch reads written once, and every
+    weight once (the intermediates a launch keeps on chip are neither)."""
+    ci, _, int8, _, _ = parse_label(label)
     cmds = replay["commands"]
-    ops, nbytes = conv_work(cmds[ci]["params"], int8)
-    for s in sibs:
-        p = cmds[s]["params"]
-        s_ops, s_bytes = conv_work(p, int8)
-        b, ic, ih, iw = (int(v) for v in p[:4])
-        ops += s_ops
-        nbytes += s_bytes - b * ic * ih * iw * (2 if ic > 3 else 4)
-    for f in fused:
-        p = cmds[f]["params"]
-        f_ops, f_bytes = conv_work(p, False)
-        b, ic, ih, iw = (int(v) for v in p[:4])
-        ops += f_ops
-        nbytes += f_bytes - 2 * b * ic * ih * iw * 2  # the 3x3 output, written and read, is neither
+    idx = [ci] + [int(m) for m in re.findall(r"cmd#(\d+)", label.split(" kernel=", 1)[1])]
+    ops = nbytes = 0
+    produced = {cmds[i]["output"] for i in idx}
+    consumed = {cmds[i]["inputs"][0] for i in idx}
+    inputs_seen = set()
+    for i in idx:
+        p = cmds[i]["params"]
+        c_int8 = int8 and i == ci or (int8 and cmds[i]["inputs"][0] == cmds[ci]["inputs"][0])
+        c_ops, _ = conv_work(p, c_int8)
+        b, ic, ih, iw, oc, oh, ow, kh, kw = (int(v) for v in p[:9])
+        ops += c_ops
+        nbytes += oc * ic * kh * kw * (1 if c_int8 else 2)
+        x = cmds[i]["inputs"][0]
+        if x not in produced and x not in inputs_seen:
+            inputs_seen.add(x)
+            nbytes += b * ic * ih * iw * (2 if ic > 3 else 4)
+        if cmds[i]["output"] not in consumed:
+            nbytes += b * oc * oh * ow * 2
     return ops, nbytes
 
 
