@@ -49,6 +49,7 @@ struct ChainParams {
     int sink_off;        // LDS byte offset of the prefetch sink (1 KB per wave, after G)
     uint32_t x_img, y_img;  // bytes of one image's input / output view
     FastDiv fd_tpi, fd_ntc;
+    FastDiv fd_cs16a, fd_cs16b;  // 16-channel steps of a's and b's input (a.C / 16, b.C / 16)
 };
 
 namespace chain {
@@ -78,7 +79,8 @@ __device__ __forceinline__ int small_div(int a, float inv) { return (int)(((floa
 // LDS too.
 template <int NQ, int MQ>
 __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, int slice, int nslice, uint8_t* lds,
-                                            float* l_bias_a, float* l_bias, float* l_bias2) {
+                                            float* l_bias_a, float* l_bias, float* l_bias2, int* l_tap_a,
+                                            int* l_tap_b) {
     constexpr int NOCB = NQ * 32;                // output channels of the block (every channel of a, b, c)
     constexpr int CB = kKC * 2 * NOCB * 16;      // LDS bytes of one weight chunk
     constexpr int PT = kKC * 2 * NOCB / kNT;     // chunk loads per thread
@@ -154,26 +156,33 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, int s
     }
 
     // ---- weight ring: chunk g (a's chunks, then b's) into slot g % kD -------
+    // piece e = i * kNT + tid of a chunk: k step sl, half, weight row; the
+    // per-lane part of its byte offset in a's and b's weights (kOob past the
+    // rows), fixed for every chunk
+    int w_sl[PT];
+    uint32_t w_a[PT], w_b[PT];
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+        const int e = i * kNT + tid;
+        const int sl = e / (2 * NOCB);
+        const int rem = e - sl * (2 * NOCB);
+        const int half = rem / NOCB;
+        const int row = rem - half * NOCB;
+        w_sl[i] = sl;
+        w_a[i] = row < pa.OCp ? (uint32_t)(row * pa.Kp + 16 * sl + 8 * half) * 2u : kOob;
+        w_b[i] = row < pb.OCp ? (uint32_t)(row * pb.Kp + 16 * sl + 8 * half) * 2u : kOob;
+    }
     auto issue = [&](int g) {
         const bool isb = g >= h.nchunk_a;  // block-uniform
         const int s0 = (isb ? g - h.nchunk_a : g) * kKC;
-        const int ks = isb ? h.kb : h.ka;
-        const int Kp = isb ? pb.Kp : pa.Kp;
-        const int OCp = isb ? pb.OCp : pa.OCp;
+        const int left = (isb ? h.kb : h.ka) - s0;  // k steps of the conv from this chunk on
         uint8_t* const slot = lds + (g & (kD - 1)) * CB;
 #pragma unroll
         for (int i = 0; i < PT; ++i) {
-            const int e0 = i * kNT + wave * 64;
-            const int e = e0 + lane;
-            const int sl = e / (2 * NOCB);
-            const int rem = e - sl * (2 * NOCB);
-            const int half = rem / NOCB;
-            const int row = rem - half * NOCB;
-            const int s = s0 + sl;
-            const bool ok = s < ks && row < OCp;
-            const uint32_t off = (uint32_t)(row * Kp + 16 * s + 8 * half) * 2u;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(isb ? rwb : rwa, (lds_ptr_t)(slot + e0 * 16), 16, ok ? off : kOob,
-                                                      0, 0, 0);
+            const uint32_t base = isb ? w_b[i] : w_a[i];
+            const bool ok = w_sl[i] < left && base != kOob;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(isb ? rwb : rwa, (lds_ptr_t)(slot + (i * kNT + wave * 64) * 16), 16,
+                                                      ok ? base + (uint32_t)s0 * 32u : kOob, 0, 0, 0);
         }
     };
 #pragma unroll
@@ -188,20 +197,19 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, int s
     }
     // k step s (k = tap * C + c, 16 channels of one tap), half hi: byte offset
     // of its plane and tap relative to the position's (0, 0) tap pixel in a map
-    // of npix pixels, w per row; past the last step the last one's (its
-    // weights are zero).  Block-uniform but for hi: no table, no LDS read on
-    // the way to the operand reads.
-    struct Taps {
-        int cs16, npix, w, hi_off;
-        float inv_cs16;
+    // of npix pixels, w per row (past the last step the last one's: its
+    // weights are zero).  Tables [chunk][hi][k step of the chunk], one 16-byte
+    // read per chunk and lane instead of the arithmetic per k step.
+    auto tap_table = [&](int* tab, int C, int ks, int npix, int w) {
+        const int nchunk = (ks + kKC - 1) / kKC;
+        for (int e = tid; e < nchunk * 2 * kKC; e += kNT) {
+            const int c = e / (2 * kKC), r = e - c * (2 * kKC), hh = r / kKC, sl = r - hh * kKC;
+            const int k0 = 16 * min(c * kKC + sl, ks - 1), tap = k0 / C, c0 = k0 - tap * C;
+            tab[e] = (((c0 >> 3) + hh) * npix + (tap / 3) * w + tap % 3) * 16;
+        }
     };
-    const Taps taps_a{pa.C / 16, XNPIX, XW, hi * XNPIX * 16, 1.0f / (float)(pa.C / 16)};
-    const Taps taps_b{pb.C / 16, GNPIX, GW, hi * GNPIX * 16, 1.0f / (float)(pb.C / 16)};
-    auto tap_off = [](const Taps& t, int s) {
-        const int tap = small_div(s, t.inv_cs16);
-        const int ky = (tap * 11) >> 5;  // tap / 3 for tap < 9
-        return (((s - tap * t.cs16) * 2) * t.npix + ky * t.w + (tap - 3 * ky)) * 16 + t.hi_off;
-    };
+    tap_table(l_tap_a, pa.C, h.ka, XNPIX, XW);
+    tap_table(l_tap_b, pb.C, h.kb, GNPIX, GW);
     // this wave's position subtiles: window / grid byte offset of each
     // position (clamped to the region), conv b's output offsets
     int bofs_a[MQ], bofs_b[MQ], yo[MQ];
@@ -257,12 +265,13 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, int s
     struct Ops {
         v4i A[kKC][NQ], B[kKC][MQ];
     };
-    auto fetch = [&](int c, int s0, int ks, const uint8_t* map, const Taps& taps, const int (&bofs)[MQ], Ops& o) {
+    auto fetch = [&](int c, int s0, int ks, const uint8_t* map, const int* taps, const int (&bofs)[MQ], Ops& o) {
         const uint8_t* const ws = lds + (c & (kD - 1)) * CB + abase;
+        const v4i tt = *reinterpret_cast<const v4i*>(taps + ((s0 / kKC) * 2 + hi) * kKC);
+        (void)ks;
 #pragma unroll
         for (int sl = 0; sl < kKC; ++sl) {
-            const int s = min(s0 + sl, ks - 1);
-            const int to = tap_off(taps, s);
+            const int to = tt[sl];
 #pragma unroll
             for (int j = 0; j < NQ; ++j) o.A[sl][j] = *reinterpret_cast<const v4i*>(ws + sl * (2 * NOCB * 16) + j * 512);
 #pragma unroll
@@ -289,9 +298,12 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, int s
     // computes clamped positions it never stores), then the operand reads of
     // step sl of the next chunk into `nxt`, so that the reads run while the
     // matrix core works
-    auto mma_fetch = [&](const Ops& cur, int cn, int s0n, int ks, const uint8_t* map, const Taps& taps,
+    auto mma_fetch = [&](const Ops& cur, int cn, int s0n, int ks, const uint8_t* map, const int* taps,
                          const int (&bofs)[MQ], Ops& nxt, bool more) {
         const uint8_t* const ws = lds + (cn & (kD - 1)) * CB + abase;
+        v4i tt{};
+        if (more) tt = *reinterpret_cast<const v4i*>(taps + ((s0n / kKC) * 2 + hi) * kKC);
+        (void)ks;
 #pragma unroll
         for (int sl = 0; sl < kKC; ++sl) {
 #pragma unroll
@@ -302,8 +314,7 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, int s
                                                                        __builtin_bit_cast(v8h, cur.B[sl][q]), acc[q][j],
                                                                        0, 0, 0);
             if (more) {  // block-uniform
-                const int s = min(s0n + sl, ks - 1);
-                const int to = tap_off(taps, s);
+                const int to = tt[sl];
 #pragma unroll
                 for (int j = 0; j < NQ; ++j)
                     nxt.A[sl][j] = *reinterpret_cast<const v4i*>(ws + sl * (2 * NOCB * 16) + j * 512);
@@ -313,7 +324,7 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, int s
         }
     };
     // chunks [cb, ce) of one conv (k steps from (c - cb) * kKC)
-    auto conv = [&](int cb, int ce, int ks, const uint8_t* map, const Taps& toff, const int (&bofs)[MQ], int myq) {
+    auto conv = [&](int cb, int ce, int ks, const uint8_t* map, const int* toff, const int (&bofs)[MQ], int myq) {
         if constexpr (MQ == 1) {
             // the next chunk's barrier, then this chunk's MFMAs interleaved with
             // the next chunk's operand reads
@@ -339,7 +350,7 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, int s
     };
 
     // ---- conv a --------------------------------------------------------------
-    conv(0, h.nchunk_a, h.ka, lds + h.x_off, taps_a, bofs_a, myq1);
+    conv(0, h.nchunk_a, h.ka, lds + h.x_off, l_tap_a, bofs_a, myq1);
     // epilogue a: fp16(silu(acc + bias)) -> G at the position's grid pixel
     {
         uint8_t* const gb = lds + h.g_off;
@@ -371,7 +382,7 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, int s
         }
     }
     // ---- conv b (its first barrier orders the G writes before its reads) -----
-    conv(h.nchunk_a, h.nchunk, h.kb, lds + h.g_off, taps_b, bofs_b, myq2);
+    conv(h.nchunk_a, h.nchunk, h.kb, lds + h.g_off, l_tap_b, bofs_b, myq2);
 
     // ---- epilogue b + the 1x1 conv c -------------------------------------------
     // y1 = fp16(silu(acc + bias_b)) is the B operand of c: k step k2 of c takes
@@ -451,9 +462,10 @@ template <int NQ, int MQ>
 __global__ __launch_bounds__(kNT) void conv_chain_kernel(ChainParams h) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ __attribute__((aligned(16))) float l_bias_a[128], l_bias[128], l_bias2[128];
+    __shared__ __attribute__((aligned(16))) int l_tap_a[2 * kChainMaxSteps], l_tap_b[2 * kChainMaxSteps];
     const int blk = xcd_remap(blockIdx.x, gridDim.x);
     const int per_xcd = max(1, (int)gridDim.x / 8);  // blocks of one XCD share the weight prefetch
-    chain_block<NQ, MQ>(h, blk, blk % per_xcd, per_xcd, lds, l_bias_a, l_bias, l_bias2);
+    chain_block<NQ, MQ>(h, blk, blk % per_xcd, per_xcd, lds, l_bias_a, l_bias, l_bias2, l_tap_a, l_tap_b);
 }
 
 // Two branches over one input (the head level's box and class branches): the
@@ -463,13 +475,14 @@ template <int NQ0, int NQ1, int MQ>
 __global__ __launch_bounds__(kNT) void conv_chain2_kernel(ChainParams h0, ChainParams h1) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ __attribute__((aligned(16))) float l_bias_a[128], l_bias[128], l_bias2[128];
+    __shared__ __attribute__((aligned(16))) int l_tap_a[2 * kChainMaxSteps], l_tap_b[2 * kChainMaxSteps];
     const int blk = xcd_remap(blockIdx.x, gridDim.x);
     const int per_xcd = max(1, (int)gridDim.x / 8);  // blocks of one XCD share the weight prefetch
     if (blk < h0.ntile)
-        chain_block<NQ0, MQ>(h0, blk, blk % per_xcd, per_xcd, lds, l_bias_a, l_bias, l_bias2);
+        chain_block<NQ0, MQ>(h0, blk, blk % per_xcd, per_xcd, lds, l_bias_a, l_bias, l_bias2, l_tap_a, l_tap_b);
     else
-        chain_block<NQ1, MQ>(h1, blk - h0.ntile, blk % per_xcd, per_xcd, lds, l_bias_a, l_bias,
-                             l_bias2);
+        chain_block<NQ1, MQ>(h1, blk - h0.ntile, blk % per_xcd, per_xcd, lds, l_bias_a, l_bias, l_bias2, l_tap_a,
+                             l_tap_b);
 }
 
 }  // namespace chain

@@ -123,6 +123,8 @@ bool make_chain_params(const ConvParams& a, const ConvParams& b, const ConvParam
     h.y_img = (uint32_t)y_img;
     h.fd_tpi = make_fastdiv((uint32_t)h.tpi);
     h.fd_ntc = make_fastdiv((uint32_t)h.ntc);
+    h.fd_cs16a = make_fastdiv((uint32_t)(a.C / 16));
+    h.fd_cs16b = make_fastdiv((uint32_t)(b.C / 16));
     // one position subtile per wave when both regions have at most 128 positions
     mq = region_extent(a.H, h.TR) * region_extent(a.W, h.TC) <= 128 && h.TR * h.TC <= 128 ? 1 : 2;
     return true;
