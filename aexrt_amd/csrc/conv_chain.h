@@ -9,10 +9,7 @@
 // the input window X (G's in-image part plus one more pixel, zero outside
 // the image): neighbouring tiles recompute their shared border of conv a.
 //
-//   prologue  this block's slice of a's and b's weights towards L2 (the blocks
-//             of one XCD together cover all of them; LDS-DMA loads into a
-//             sink, the data dropped), so that the ring's loads hit L2;
-//             biases -> LDS; X -> LDS (buffer_load ... lds, zeros outside the
+//   prologue  biases -> LDS; X -> LDS (buffer_load ... lds, zeros outside the
 //             image); G zeroed; tap tables
 //   conv a    k steps of a in chunks of KC; the chunks' weights stream
 //             through an LDS ring of D slots (loads of D - 1 chunks in
@@ -46,7 +43,6 @@ struct ChainParams {
     int ka, kb;          // k steps of a (9 * a.C / 16) and of b (9 * b.C / 16)
     int nchunk_a, nchunk;  // weight chunks of a, of a and b
     int x_off, g_off;    // LDS byte offsets of the window X and the grid G (after the ring)
-    int sink_off;        // LDS byte offset of the prefetch sink (1 KB per wave, after G)
     uint32_t x_img, y_img;  // bytes of one image's input / output view
     FastDiv fd_tpi, fd_ntc;
     FastDiv fd_cs16a, fd_cs16b;  // 16-channel steps of a's and b's input (a.C / 16, b.C / 16)
@@ -75,10 +71,10 @@ __device__ __forceinline__ int small_div(int a, float inv) { return (int)(((floa
 // MQ: position subtiles per wave and region (regions of up to 128 MQ
 // positions); with MQ = 1 the operands of the next chunk are read from LDS
 // while the MFMAs of the current one run.  blk: the block's tile; lds: the
-// dynamic LDS [ring: kD * CB][X][G][sink]; the biases (128 floats each) in
-// LDS too.
+// dynamic LDS [ring: kD * CB][X][G]; the biases (128 floats each) and the
+// tap tables in LDS too.
 template <int NQ, int MQ>
-__device__ __forceinline__ void chain_block(const ChainParams& h, int blk, int slice, int nslice, uint8_t* lds,
+__device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8_t* lds,
                                             float* l_bias_a, float* l_bias, float* l_bias2, int* l_tap_a,
                                             int* l_tap_b) {
     constexpr int NOCB = NQ * 32;                // output channels of the block (every channel of a, b, c)
@@ -113,19 +109,6 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, int s
     const rsrc_t rx = make_rsrc(static_cast<const uint8_t*>(pa.x) + (int64_t)n * pa.x_nstride * 2, h.x_img);
     const rsrc_t rwa = make_rsrc(pa.w, (uint32_t)pa.OCp * (uint32_t)pa.Kp * 2u);
     const rsrc_t rwb = make_rsrc(pb.w, (uint32_t)pb.OCp * (uint32_t)pb.Kp * 2u);
-
-    // ---- slice `slice` of nslice of a's and b's weights towards L2 -----------
-    {
-        uint8_t* const sink = lds + h.sink_off + wave * 1024;
-        auto warm = [&](rsrc_t r, uint32_t bytes) {
-            const uint32_t per = ((bytes + (uint32_t)nslice - 1) / (uint32_t)nslice + 1023u) & ~1023u;
-            const uint32_t lo = (uint32_t)slice * per, hi = min(bytes, lo + per);
-            for (uint32_t o = lo + (uint32_t)wave * 1024u; o < hi; o += 4096u)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)sink, 16, o + (uint32_t)lane * 16u, 0, 0, 0);
-        };
-        warm(rwa, (uint32_t)pa.OCp * (uint32_t)pa.Kp * 2u);
-        warm(rwb, (uint32_t)pb.OCp * (uint32_t)pb.Kp * 2u);
-    }
 
     // ---- biases -> LDS (loads straight into LDS: no register waits) ---------
     if (wave < 2) {
@@ -464,8 +447,7 @@ __global__ __launch_bounds__(kNT) void conv_chain_kernel(ChainParams h) {
     __shared__ __attribute__((aligned(16))) float l_bias_a[128], l_bias[128], l_bias2[128];
     __shared__ __attribute__((aligned(16))) int l_tap_a[2 * kChainMaxSteps], l_tap_b[2 * kChainMaxSteps];
     const int blk = xcd_remap(blockIdx.x, gridDim.x);
-    const int per_xcd = max(1, (int)gridDim.x / 8);  // blocks of one XCD share the weight prefetch
-    chain_block<NQ, MQ>(h, blk, blk % per_xcd, per_xcd, lds, l_bias_a, l_bias, l_bias2, l_tap_a, l_tap_b);
+    chain_block<NQ, MQ>(h, blk, lds, l_bias_a, l_bias, l_bias2, l_tap_a, l_tap_b);
 }
 
 // Two branches over one input (the head level's box and class branches): the
@@ -477,11 +459,10 @@ __global__ __launch_bounds__(kNT) void conv_chain2_kernel(ChainParams h0, ChainP
     __shared__ __attribute__((aligned(16))) float l_bias_a[128], l_bias[128], l_bias2[128];
     __shared__ __attribute__((aligned(16))) int l_tap_a[2 * kChainMaxSteps], l_tap_b[2 * kChainMaxSteps];
     const int blk = xcd_remap(blockIdx.x, gridDim.x);
-    const int per_xcd = max(1, (int)gridDim.x / 8);  // blocks of one XCD share the weight prefetch
     if (blk < h0.ntile)
-        chain_block<NQ0, MQ>(h0, blk, blk % per_xcd, per_xcd, lds, l_bias_a, l_bias, l_bias2, l_tap_a, l_tap_b);
+        chain_block<NQ0, MQ>(h0, blk, lds, l_bias_a, l_bias, l_bias2, l_tap_a, l_tap_b);
     else
-        chain_block<NQ1, MQ>(h1, blk - h0.ntile, blk % per_xcd, per_xcd, lds, l_bias_a, l_bias, l_bias2, l_tap_a,
+        chain_block<NQ1, MQ>(h1, blk - h0.ntile, lds, l_bias_a, l_bias, l_bias2, l_tap_a,
                              l_tap_b);
 }
 

@@ -49,7 +49,7 @@ int region_extent(int n, int t) {
 }
 
 // LDS bytes of one block for tile (tr, tc): weight ring, largest window X,
-// largest grid G, prefetch sink; 0 when a region exceeds 256 positions or LDS.
+// largest grid G; 0 when a region exceeds 256 positions or LDS.
 int chain_lds(const ConvParams& a, int nq, int tr, int tc, int* x_bytes) {
     tr = std::min(tr, a.H);
     tc = std::min(tc, a.W);
@@ -59,7 +59,7 @@ int chain_lds(const ConvParams& a, int nq, int tr, int tc, int* x_bytes) {
     const int64_t xb = (xp + 63) / 64 * 64 * 16;
     const int64_t gb = (int64_t)nq * 4 * (tr + 2) * (tc + 2) * 16;
     const int64_t ring = (int64_t)chain::kD * chain::kKC * 2 * nq * 32 * 16;
-    const int64_t total = ring + xb + gb + 4 * 1024;  // + the prefetch sink
+    const int64_t total = ring + xb + gb;
     if (total > kChainLdsBudget) return 0;
     if (x_bytes) *x_bytes = (int)xb;
     return (int)total;
@@ -111,7 +111,6 @@ bool make_chain_params(const ConvParams& a, const ConvParams& b, const ConvParam
     if (!lds) return false;
     h.x_off = chain::kD * chain::kKC * 2 * nq * 32 * 16;
     h.g_off = h.x_off + xb;
-    h.sink_off = h.g_off + nq * 4 * (h.TR + 2) * (h.TC + 2) * 16;
     // one image's views (the kernel addresses each image from its own base)
     const int esz = (c.flags & kConvOutF32) ? 4 : 2;
     const uint64_t x_img = ((uint64_t)(a.H * a.W - 1) * a.x_cstride + a.C) * 2;
