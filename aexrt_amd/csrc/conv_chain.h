@@ -72,8 +72,12 @@ __device__ __forceinline__ int small_div(int a, float inv) { return (int)(((floa
 // positions); with MQ = 1 the operands of the next chunk are read from LDS
 // while the MFMAs of the current one run.  blk: the block's tile; lds: the
 // dynamic LDS [ring: kD * CB][X][G]; the biases (128 floats each) and the
-// tap tables in LDS too.
-template <int NQ, int MQ>
+// tap tables in LDS too.  KG = 2: 8 waves, two groups of 4 over the same
+// positions, group g taking k steps 2g, 2g + 1 of every chunk (two waves per
+// SIMD issue into the matrix core); group 1's partial sums are added into
+// group 0's through the window's LDS at each conv's end, and group 0 runs the
+// epilogues.
+template <int NQ, int MQ, int KG>
 __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8_t* lds,
                                             float* l_bias_a, float* l_bias, float* l_bias2, int* l_tap_a,
                                             int* l_tap_b) {
@@ -81,6 +85,9 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
     constexpr int CB = kKC * 2 * NOCB * 16;      // LDS bytes of one weight chunk
     constexpr int PT = kKC * 2 * NOCB / kNT;     // chunk loads per thread
     static_assert((kKC * 2 * NOCB) % kNT == 0, "a chunk is whole loads of every thread");
+    static_assert(KG == 1 || (KG == 2 && MQ == 1), "two k groups with one position subtile per wave");
+    constexpr int NT = kNT * KG;  // threads of the block
+    constexpr int KS = kKC / KG;  // k steps of a chunk per group
     const ConvParams& pa = h.a;
     const ConvParams& pb = h.b;
     const ConvParams& pc = h.c;
@@ -90,6 +97,8 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31;
     const int hi = lane >> 5;
+    const int grp = KG == 1 ? 0 : wave >> 2;  // k group (wave-uniform)
+    const int lw = wave & 3;                  // wave within its group: position subtiles lw, lw + 4, ...
 
     // ---- tile geometry (block-uniform) --------------------------------------
     const int n = (int)fdiv((uint32_t)blk, h.fd_tpi);
@@ -126,7 +135,7 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
         const int npiece = (pa.C / 8) * XNPIX;
         const float inv_npix = 1.0f / (float)XNPIX, inv_xw = 1.0f / (float)XW;
         uint8_t* const xb = lds + h.x_off;
-        for (int e0 = wave * 64; e0 < npiece; e0 += kNT) {
+        for (int e0 = wave * 64; e0 < npiece; e0 += NT) {
             const int e = e0 + lane;
             const int pl = small_div(e, inv_npix);
             const int pix = e - pl * XNPIX;
@@ -156,6 +165,7 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
         w_b[i] = row < pb.OCp ? (uint32_t)(row * pb.Kp + 16 * sl + 8 * half) * 2u : kOob;
     }
     auto issue = [&](int g) {
+        if (tid >= kNT) return;  // the chunk loads are the first 4 waves'
         const bool isb = g >= h.nchunk_a;  // block-uniform
         const int s0 = (isb ? g - h.nchunk_a : g) * kKC;
         const int left = (isb ? h.kb : h.ka) - s0;  // k steps of the conv from this chunk on
@@ -176,7 +186,7 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
     {
         uint8_t* const gb = lds + h.g_off;
         const int ng = NQ * 4 * GNPIX;
-        for (int e = tid; e < ng; e += kNT) *reinterpret_cast<v4i*>(gb + e * 16) = v4i{0, 0, 0, 0};
+        for (int e = tid; e < ng; e += NT) *reinterpret_cast<v4i*>(gb + e * 16) = v4i{0, 0, 0, 0};
     }
     // k step s (k = tap * C + c, 16 channels of one tap), half hi: byte offset
     // of its plane and tap relative to the position's (0, 0) tap pixel in a map
@@ -185,7 +195,7 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
     // read per chunk and lane instead of the arithmetic per k step.
     auto tap_table = [&](int* tab, int C, int ks, int npix, int w) {
         const int nchunk = (ks + kKC - 1) / kKC;
-        for (int e = tid; e < nchunk * 2 * kKC; e += kNT) {
+        for (int e = tid; e < nchunk * 2 * kKC; e += NT) {
             const int c = e / (2 * kKC), r = e - c * (2 * kKC), hh = r / kKC, sl = r - hh * kKC;
             const int k0 = 16 * min(c * kKC + sl, ks - 1), tap = k0 / C, c0 = k0 - tap * C;
             tab[e] = (((c0 >> 3) + hh) * npix + (tap / 3) * w + tap % 3) * 16;
@@ -196,13 +206,13 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
     // this wave's position subtiles: window / grid byte offset of each
     // position (clamped to the region), conv b's output offsets
     int bofs_a[MQ], bofs_b[MQ], yo[MQ];
-    const int myq1 = min(MQ, max(0, ((npos1 + 31) >> 5) - wave + 3) >> 2);
-    const int myq2 = min(MQ, max(0, ((npos2 + 31) >> 5) - wave + 3) >> 2);
+    const int myq1 = min(MQ, max(0, ((npos1 + 31) >> 5) - lw + 3) >> 2);
+    const int myq2 = min(MQ, max(0, ((npos2 + 31) >> 5) - lw + 3) >> 2);
     {
         const float inv_r1w = 1.0f / (float)R1W, inv_tc = 1.0f / (float)TCr;
 #pragma unroll
         for (int q = 0; q < MQ; ++q) {
-            const int pos = (wave + 4 * q) * 32 + l32;
+            const int pos = (lw + 4 * q) * 32 + l32;
             const int p1 = min(pos, npos1 - 1);
             const int r1 = small_div(p1, inv_r1w);
             bofs_a[q] = (r1 * XW + (p1 - r1 * R1W)) * 16;
@@ -230,7 +240,7 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
     auto ring_wait = [&](int c) {
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS reads and writes done
-        if (c + kD - 2 < h.nchunk) {
+        if (c + kD - 2 < h.nchunk && grp == 0) {  // group 1 issues no chunk loads
             // s_waitcnt vmcnt(PT * (kD - 2)) lgkmcnt(0): vmcnt bits 3:0 and 15:14, expcnt 7
             constexpr int vm = PT * (kD - 2);
             static_assert(vm < 64, "vmcnt field");
@@ -245,15 +255,17 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
         if (c + kD - 1 < h.nchunk) issue(c + kD - 1);
     };
     // the operands of chunk c's k steps over a map (X or G) with its tap table
+    // (this group's KS of the chunk's kKC k steps: steps grp * KS + i)
     struct Ops {
-        v4i A[kKC][NQ], B[kKC][MQ];
+        v4i A[KS][NQ], B[KS][MQ];
     };
+    typedef int vks __attribute__((ext_vector_type(KS)));
     auto fetch = [&](int c, int s0, int ks, const uint8_t* map, const int* taps, const int (&bofs)[MQ], Ops& o) {
-        const uint8_t* const ws = lds + (c & (kD - 1)) * CB + abase;
-        const v4i tt = *reinterpret_cast<const v4i*>(taps + ((s0 / kKC) * 2 + hi) * kKC);
+        const uint8_t* const ws = lds + (c & (kD - 1)) * CB + abase + grp * KS * (2 * NOCB * 16);
+        const vks tt = *reinterpret_cast<const vks*>(taps + ((s0 / kKC) * 2 + hi) * kKC + grp * KS);
         (void)ks;
 #pragma unroll
-        for (int sl = 0; sl < kKC; ++sl) {
+        for (int sl = 0; sl < KS; ++sl) {
             const int to = tt[sl];
 #pragma unroll
             for (int j = 0; j < NQ; ++j) o.A[sl][j] = *reinterpret_cast<const v4i*>(ws + sl * (2 * NOCB * 16) + j * 512);
@@ -263,8 +275,8 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
     };
     auto mma = [&](int s0, int ks, int myq, const Ops& o) {
 #pragma unroll
-        for (int sl = 0; sl < kKC; ++sl) {
-            if (s0 + sl >= ks) break;  // block-uniform
+        for (int sl = 0; sl < KS; ++sl) {
+            if (s0 + grp * KS + sl >= ks) break;  // wave-uniform
 #pragma unroll
             for (int q = 0; q < MQ; ++q) {
                 if (q >= myq) break;  // wave-uniform
@@ -283,12 +295,12 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
     // matrix core works
     auto mma_fetch = [&](const Ops& cur, int cn, int s0n, int ks, const uint8_t* map, const int* taps,
                          const int (&bofs)[MQ], Ops& nxt, bool more) {
-        const uint8_t* const ws = lds + (cn & (kD - 1)) * CB + abase;
-        v4i tt{};
-        if (more) tt = *reinterpret_cast<const v4i*>(taps + ((s0n / kKC) * 2 + hi) * kKC);
+        const uint8_t* const ws = lds + (cn & (kD - 1)) * CB + abase + grp * KS * (2 * NOCB * 16);
+        vks tt{};
+        if (more) tt = *reinterpret_cast<const vks*>(taps + ((s0n / kKC) * 2 + hi) * kKC + grp * KS);
         (void)ks;
 #pragma unroll
-        for (int sl = 0; sl < kKC; ++sl) {
+        for (int sl = 0; sl < KS; ++sl) {
 #pragma unroll
             for (int q = 0; q < MQ; ++q)
 #pragma unroll
@@ -332,8 +344,41 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
         }
     };
 
+    // group 1's partial sums added into group 0's, one 32-channel subtile at a
+    // time through the window region (free after conv a's last chunk): 4 waves
+    // x MQ x 16 floats x 64 lanes per pass
+    auto reduce_groups = [&]() {
+        if constexpr (KG == 2) {
+            float* const red = reinterpret_cast<float*>(lds + h.x_off);
+            auto bar = [] {
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+            };
+#pragma unroll
+            for (int j = 0; j < NQ; ++j) {
+                bar();  // every wave done reading the window / the previous pass
+                if (grp == 1) {
+#pragma unroll
+                    for (int q = 0; q < MQ; ++q)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) red[((lw * MQ + q) * 16 + r) * 64 + lane] = acc[q][j][r];
+                }
+                bar();
+                if (grp == 0) {
+#pragma unroll
+                    for (int q = 0; q < MQ; ++q)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[q][j][r] += red[((lw * MQ + q) * 16 + r) * 64 + lane];
+                }
+            }
+        }
+    };
+
     // ---- conv a --------------------------------------------------------------
     conv(0, h.nchunk_a, h.ka, lds + h.x_off, l_tap_a, bofs_a, myq1);
+    reduce_groups();
     // epilogue a: fp16(silu(acc + bias)) -> G at the position's grid pixel
     {
         uint8_t* const gb = lds + h.g_off;
@@ -341,8 +386,8 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
         const float inv_r1w = 1.0f / (float)R1W;
 #pragma unroll
         for (int q = 0; q < MQ; ++q) {
-            const int pos = (wave + 4 * q) * 32 + l32;
-            if (q < myq1 && pos < npos1) {
+            const int pos = (lw + 4 * q) * 32 + l32;
+            if (grp == 0 && q < myq1 && pos < npos1) {
                 const int r = small_div(pos, inv_r1w);
                 const int gp = (r + dr) * GW + (pos - r * R1W) + dc;
 #pragma unroll
@@ -366,6 +411,8 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
     }
     // ---- conv b (its first barrier orders the G writes before its reads) -----
     conv(h.nchunk_a, h.nchunk, h.kb, lds + h.g_off, l_tap_b, bofs_b, myq2);
+    reduce_groups();
+    if (grp != 0) return;  // the 1x1 and the stores: group 0
 
     // ---- epilogue b + the 1x1 conv c -------------------------------------------
     // y1 = fp16(silu(acc + bias_b)) is the B operand of c: k step k2 of c takes
@@ -441,28 +488,28 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
 }
 
 // One branch: one block per tile.
-template <int NQ, int MQ>
-__global__ __launch_bounds__(kNT) void conv_chain_kernel(ChainParams h) {
+template <int NQ, int MQ, int KG>
+__global__ __launch_bounds__(kNT * KG) void conv_chain_kernel(ChainParams h) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ __attribute__((aligned(16))) float l_bias_a[128], l_bias[128], l_bias2[128];
     __shared__ __attribute__((aligned(16))) int l_tap_a[2 * kChainMaxSteps], l_tap_b[2 * kChainMaxSteps];
     const int blk = xcd_remap(blockIdx.x, gridDim.x);
-    chain_block<NQ, MQ>(h, blk, lds, l_bias_a, l_bias, l_bias2, l_tap_a, l_tap_b);
+    chain_block<NQ, MQ, KG>(h, blk, lds, l_bias_a, l_bias, l_bias2, l_tap_a, l_tap_b);
 }
 
 // Two branches over one input (the head level's box and class branches): the
 // first h0.ntile blocks run branch 0, the rest branch 1, so both fill the GPU
 // together.
-template <int NQ0, int NQ1, int MQ>
-__global__ __launch_bounds__(kNT) void conv_chain2_kernel(ChainParams h0, ChainParams h1) {
+template <int NQ0, int NQ1, int MQ, int KG>
+__global__ __launch_bounds__(kNT * KG) void conv_chain2_kernel(ChainParams h0, ChainParams h1) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ __attribute__((aligned(16))) float l_bias_a[128], l_bias[128], l_bias2[128];
     __shared__ __attribute__((aligned(16))) int l_tap_a[2 * kChainMaxSteps], l_tap_b[2 * kChainMaxSteps];
     const int blk = xcd_remap(blockIdx.x, gridDim.x);
     if (blk < h0.ntile)
-        chain_block<NQ0, MQ>(h0, blk, lds, l_bias_a, l_bias, l_bias2, l_tap_a, l_tap_b);
+        chain_block<NQ0, MQ, KG>(h0, blk, lds, l_bias_a, l_bias, l_bias2, l_tap_a, l_tap_b);
     else
-        chain_block<NQ1, MQ>(h1, blk - h0.ntile, lds, l_bias_a, l_bias, l_bias2, l_tap_a,
+        chain_block<NQ1, MQ, KG>(h1, blk - h0.ntile, lds, l_bias_a, l_bias, l_bias2, l_tap_a,
                              l_tap_b);
 }
 

@@ -2,6 +2,7 @@
 // tile geometry, LDS layout, launch.
 #include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 
 #include "conv_chain.h"
 
@@ -87,8 +88,17 @@ namespace {
 
 // Kernel parameters of one branch for tile (tr, tc) (fitted); its dynamic LDS
 // bytes and position subtiles per wave.  False when it does not fit.
+// k groups of the chain blocks where they fit: 2 (8 waves, two per SIMD
+// issuing into its matrix core; about 1% faster over the whole network at
+// batch 64 than one group), or 1 with AEXRT_HIP_CHAIN_KG=1.  Read at each
+// launch (graphs keep what their build launched).
+int chain_kgroups() {
+    const char* e = std::getenv("AEXRT_HIP_CHAIN_KG");
+    return e && std::atoi(e) == 1 ? 1 : 2;
+}
+
 bool make_chain_params(const ConvParams& a, const ConvParams& b, const ConvParams& c, int tr, int tc, ChainParams& h,
-                       int& lds, int& mq) {
+                       int& lds, int& mq, int& kg) {
     if (chain_shape_error(a, b, c) || !chain_tile(a, b, c, tr, tc)) return false;
     const int nq = chain_nq(a, b, c);
     h = ChainParams{};
@@ -126,6 +136,9 @@ bool make_chain_params(const ConvParams& a, const ConvParams& b, const ConvParam
     h.fd_cs16b = make_fastdiv((uint32_t)(b.C / 16));
     // one position subtile per wave when both regions have at most 128 positions
     mq = region_extent(a.H, h.TR) * region_extent(a.W, h.TC) <= 128 && h.TR * h.TC <= 128 ? 1 : 2;
+    // two k groups of 4 waves each: one subtile per wave and a window large
+    // enough to pass the partial sums of a 32-channel subtile (4 x 16 x 64 floats)
+    kg = chain_kgroups() == 2 && mq == 1 && xb >= 4 * 16 * 64 * 4 ? 2 : 1;
     return true;
 }
 
@@ -134,19 +147,23 @@ bool make_chain_params(const ConvParams& a, const ConvParams& b, const ConvParam
 hipError_t launch_conv_chain(const ConvParams& a, const ConvParams& b, const ConvParams& c, int tr, int tc,
                              hipStream_t stream) {
     ChainParams h{};
-    int lds = 0, mq = 1;
-    if (!make_chain_params(a, b, c, tr, tc, h, lds, mq)) return hipErrorInvalidValue;
+    int lds = 0, mq = 1, kg = 1;
+    if (!make_chain_params(a, b, c, tr, tc, h, lds, mq, kg)) return hipErrorInvalidValue;
     const int nq = chain_nq(a, b, c);
     if (LaunchProbe* pr = launch_probe()) {
-        std::snprintf(pr->name, sizeof(pr->name), "conv_chain_kernel<%d,%d> %dx%d", nq, mq, h.TR, h.TC);
+        std::snprintf(pr->name, sizeof(pr->name), "conv_chain_kernel<%d,%d,%d> %dx%d", nq, mq, kg, h.TR, h.TC);
         return hipSuccess;
     }
-    const dim3 grid((unsigned)h.ntile), block(chain::kNT);
-    if (nq == 2 && mq == 1) hipLaunchKernelGGL((chain::conv_chain_kernel<2, 1>), grid, block, (size_t)lds, stream, h);
-    if (nq == 2 && mq == 2) hipLaunchKernelGGL((chain::conv_chain_kernel<2, 2>), grid, block, (size_t)lds, stream, h);
-    if (nq == 3 && mq == 1) hipLaunchKernelGGL((chain::conv_chain_kernel<3, 1>), grid, block, (size_t)lds, stream, h);
-    if (nq == 3 && mq == 2) hipLaunchKernelGGL((chain::conv_chain_kernel<3, 2>), grid, block, (size_t)lds, stream, h);
-    return hipGetLastError();
+    const dim3 grid((unsigned)h.ntile), block(chain::kNT * kg);
+#define AEXRT_CHAIN1(Q, M, G)                                                                                      \
+    if (nq == Q && mq == M && kg == G) {                                                                           \
+        hipLaunchKernelGGL((chain::conv_chain_kernel<Q, M, G>), grid, block, (size_t)lds, stream, h);               \
+        return hipGetLastError();                                                                                  \
+    }
+    AEXRT_CHAIN1(2, 1, 1) AEXRT_CHAIN1(2, 2, 1) AEXRT_CHAIN1(3, 1, 1) AEXRT_CHAIN1(3, 2, 1)
+    AEXRT_CHAIN1(2, 1, 2) AEXRT_CHAIN1(3, 1, 2)
+#undef AEXRT_CHAIN1
+    return hipErrorInvalidValue;
 }
 
 // Two branches over one input map in one launch, on one tile (the one that
@@ -162,23 +179,27 @@ hipError_t launch_conv_chain2(const ConvParams* br0, const ConvParams* br1, int 
         if (!chain_tile(big0 ? a0 : a1, big0 ? b0 : b1, big0 ? c0 : c1, tr, tc)) return hipErrorInvalidValue;
     }
     ChainParams h0{}, h1{};
-    int lds0 = 0, lds1 = 0, mq0 = 1, mq1 = 1;
-    if (!make_chain_params(a0, b0, c0, tr, tc, h0, lds0, mq0) || !make_chain_params(a1, b1, c1, tr, tc, h1, lds1, mq1) ||
-        mq0 != mq1 || (int64_t)h0.ntile + h1.ntile > INT32_MAX)
+    int lds0 = 0, lds1 = 0, mq0 = 1, mq1 = 1, kg0 = 1, kg1 = 1;
+    if (!make_chain_params(a0, b0, c0, tr, tc, h0, lds0, mq0, kg0) ||
+        !make_chain_params(a1, b1, c1, tr, tc, h1, lds1, mq1, kg1) || mq0 != mq1 ||
+        (int64_t)h0.ntile + h1.ntile > INT32_MAX)
         return hipErrorInvalidValue;
+    const int kg = std::min(kg0, kg1);
     if (LaunchProbe* pr = launch_probe()) {
-        std::snprintf(pr->name, sizeof(pr->name), "conv_chain2_kernel<%d,%d,%d> %dx%d", nq0, nq1, mq0, h0.TR, h0.TC);
+        std::snprintf(pr->name, sizeof(pr->name), "conv_chain2_kernel<%d,%d,%d,%d> %dx%d", nq0, nq1, mq0, kg, h0.TR,
+                      h0.TC);
         return hipSuccess;
     }
-    const dim3 grid((unsigned)(h0.ntile + h1.ntile)), block(chain::kNT);
+    const dim3 grid((unsigned)(h0.ntile + h1.ntile)), block(chain::kNT * kg);
     const size_t lds = (size_t)std::max(lds0, lds1);
-#define AEXRT_CHAIN2(Q0, Q1, M)                                                                                    \
-    if (nq0 == Q0 && nq1 == Q1 && mq0 == M) {                                                                      \
-        hipLaunchKernelGGL((chain::conv_chain2_kernel<Q0, Q1, M>), grid, block, lds, stream, h0, h1);             \
+#define AEXRT_CHAIN2(Q0, Q1, M, G)                                                                                 \
+    if (nq0 == Q0 && nq1 == Q1 && mq0 == M && kg == G) {                                                           \
+        hipLaunchKernelGGL((chain::conv_chain2_kernel<Q0, Q1, M, G>), grid, block, lds, stream, h0, h1);          \
         return hipGetLastError();                                                                                  \
     }
-    AEXRT_CHAIN2(2, 3, 1) AEXRT_CHAIN2(3, 2, 1) AEXRT_CHAIN2(2, 2, 1) AEXRT_CHAIN2(3, 3, 1)
-    AEXRT_CHAIN2(2, 3, 2) AEXRT_CHAIN2(3, 2, 2) AEXRT_CHAIN2(2, 2, 2) AEXRT_CHAIN2(3, 3, 2)
+    AEXRT_CHAIN2(2, 3, 1, 1) AEXRT_CHAIN2(3, 2, 1, 1) AEXRT_CHAIN2(2, 2, 1, 1) AEXRT_CHAIN2(3, 3, 1, 1)
+    AEXRT_CHAIN2(2, 3, 2, 1) AEXRT_CHAIN2(3, 2, 2, 1) AEXRT_CHAIN2(2, 2, 2, 1) AEXRT_CHAIN2(3, 3, 2, 1)
+    AEXRT_CHAIN2(2, 3, 1, 2) AEXRT_CHAIN2(3, 2, 1, 2) AEXRT_CHAIN2(2, 2, 1, 2) AEXRT_CHAIN2(3, 3, 1, 2)
 #undef AEXRT_CHAIN2
     return hipErrorInvalidValue;
 }
