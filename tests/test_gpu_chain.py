@@ -36,7 +36,8 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("kg", ["1", "2"])
+@pytest.mark.parametrize("kg", ["1", pytest.param("2", marks=pytest.mark.skip(
+    reason="two-group chain blocks switched off: a model load that ran them aborted, cause not found"))])
 @pytest.mark.parametrize("case", CASES, ids=[f"c{t[1]}_{t[2]}x{t[3]}_b{t[4]}_o{t[5]}_t{t[6][0]}x{t[6][1]}_{t[7]}"
                                              f"{'_slice' if t[8] else ''}" for t in CASES])
 def test_chain_matches_three_convs(cuda, case, kg, monkeypatch):
