@@ -8,10 +8,15 @@ on a CPU path instead.
 from __future__ import annotations
 
 import ctypes
+import os
 from ctypes import POINTER, Structure, c_float, c_int, c_int32, c_int64, c_uint32, c_uint64, c_void_p
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libaexrt_hip.so"
+# A host-sanitizer build of the same sources (``make -C aexrt_amd/csrc asan``)
+# can be loaded instead for CPU runs of the host paths.
+if os.environ.get("AEXRT_HIP_LIBRARY"):
+    LIB_PATH = Path(os.environ["AEXRT_HIP_LIBRARY"]).resolve()
 
 _lib = None
 
@@ -132,6 +137,8 @@ _SIGS = {
                                            c_uint64, _vp]),
     "aexrt_hip_conv2d": (c_int, [POINTER(ConvDesc), c_uint32, c_uint32, POINTER(TensorView), _vp, _vp, _vp,
                                  POINTER(TensorView), POINTER(TensorView), _vp, _vp]),
+    "aexrt_hip_conv_candidates": (c_uint32, [POINTER(ConvDesc), c_uint32, c_uint32, POINTER(TensorView),
+                                             POINTER(TensorView), POINTER(TensorView), _vp, c_uint32, c_uint32]),
     "aexrt_hip_can_use_conv_int8": (c_int, [POINTER(ConvDesc), c_uint32]),
     "aexrt_hip_set_conv_tile": (c_int, [c_int32, c_int32, c_int32]),
     "aexrt_hip_set_conv3x3_halo": (c_int, [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32]),
@@ -175,6 +182,7 @@ _MODEL_SIGS = {
     "aexrt_yolo_debug_output": (c_int, [_vp, _vp, c_uint64]),
     "aexrt_yolo_debug_value": (c_int, [_vp, c_uint32, _vp, c_uint64]),
     "aexrt_yolo_value_info": (c_int, [_vp, c_uint32, POINTER(c_uint32)]),
+    "aexrt_yolo_debug_conv_int8": (c_int, [_vp, c_uint32, _vp, c_uint64, _vp, c_uint32]),
     "aexrt_yolo_get_last_error": (ctypes.c_char_p, [_vp]),
     "aexrt_yolo_get_last_run_timing": (c_int, [_vp, POINTER(RunTiming)]),
     "aexrt_yolo_profile_event_count": (c_uint32, [_vp]),

@@ -2,6 +2,7 @@
 // repack, and dispatch of one hot-path kernel per call.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -333,6 +334,46 @@ int aexrt_hip_conv2d(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t f
         return 0;
     }
     return launch_conv(p, algorithm, static_cast<hipStream_t>(stream)) ? 1 : 0;
+}
+
+uint32_t aexrt_hip_conv_candidates(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t flags,
+                                   const AexrtHipTensorView* x, const AexrtHipTensorView* residual,
+                                   const AexrtHipTensorView* y, char* names, uint32_t name_len, uint32_t cap) {
+    if (!desc || !x || !y || !x->data || !y->data || (cap && (!names || name_len < 2))) {
+        set_error("conv_candidates: null argument");
+        return 0;
+    }
+    if (is_winograd_algorithm(algorithm) ||
+        (flags & (AEXRT_HIP_CONV_INT8_PG16 | AEXRT_HIP_CONV_INT8_DYNAMIC))) {
+        set_error("conv_candidates: Winograd, pg16 and dynamic int8 convs have one kernel each, no tile choice");
+        return 0;
+    }
+    // the launchers check the pointers only for presence and alignment: any
+    // aligned non-null placeholder stands in for the weights
+    static const float placeholder[4] __attribute__((aligned(16))) = {0, 0, 0, 0};
+    const bool int8 = is_int8_algorithm(algorithm);
+    std::string why;
+    ConvParams p{};
+    if (!build_conv_params(*desc, algorithm, flags, *x, placeholder, int8 ? placeholder : nullptr, placeholder,
+                           residual, *y, nullptr, p, why)) {
+        set_error("conv_candidates: " + why);
+        return 0;
+    }
+    std::vector<ConvChoice> all(kMaxConvChoices);
+    const int n = enumerate_conv_choices(p, int8, all.data(), kMaxConvChoices);
+    const uint32_t out_n = std::min<uint32_t>((uint32_t)n, cap);
+    for (uint32_t i = 0; i < out_n; ++i) {
+        LaunchProbe probe{};
+        ConvParams q = p;
+        q.choice = all[i];
+        set_launch_probe(&probe);
+        const hipError_t e = launch_conv_igemm(q, int8, nullptr);
+        set_launch_probe(nullptr);
+        char* dst = names + (size_t)i * name_len;
+        if (e != hipSuccess) probe.name[0] = '\0';
+        std::snprintf(dst, name_len, "%s", probe.name);
+    }
+    return (uint32_t)n;
 }
 
 int aexrt_hip_conv2d_fused_1x1(const AexrtConv2DDesc* desc, uint32_t flags, const AexrtHipTensorView* x,

@@ -140,6 +140,7 @@ int enumerate_conv_choices(const ConvParams& p, bool int8, ConvChoice* out, int 
             out[n++] = c;
         }
     }
+    if (n < cap && int8 && p.KH == 1 && p.KW == 1) n += enumerate_s1x1_choices(p, int8, out + n, cap - n);
     if (n < cap && nchw && !int8) n += enumerate_stem_choices(p, out + n, cap - n);
     if (n < cap && !nchw) n += enumerate_m32_choices(p, int8, out + n, cap - n);
     if (n < cap && !nchw && !int8) n += enumerate_wide_choices(p, out + n, cap - n);

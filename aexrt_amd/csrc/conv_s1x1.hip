@@ -95,6 +95,35 @@ bool forced_s1x1_choice(ConvChoice& c) {
     return true;
 }
 
+int enumerate_s1x1_choices(const ConvParams& p, bool int8, ConvChoice* out, int cap) {
+    // the launcher sets p.lin per batch slice; the strides decide it
+    ConvParams q = p;
+    q.lin = 0;
+    if (p.KH == 1 && p.KW == 1 && p.S == 1 && p.P == 0 && p.M < (1 << 24) &&
+        p.x_nstride == (int64_t)p.H * p.W * p.x_cstride && p.x_cstride < (1 << 24) &&
+        p.y_nstride == (int64_t)p.OH * p.OW * p.y_cstride && p.y_cstride < (1 << 24))
+        q.lin = kLinX | kLinY;
+    if (!s1x1_shape_ok(q, int8)) return 0;
+    const int ocj = (p.OCp + 15) / 16;
+    int n = 0;
+    for (int pq : {1, 2}) {
+        for (int jq : {1, 2, 4, 8}) {
+            if (n >= cap) return n;
+            if (jq > 1 && jq / 2 >= ocj) continue;  // a channel tile past every channel
+            S1x1Params h{};
+            h.c = q;
+            S1x1Tile t{jq, pq, 0};
+            if (!s1x1_geometry(h, t)) continue;
+            ConvChoice c;
+            c.kind = 6;
+            c.jn = jq;
+            c.pw = pq;
+            out[n++] = c;
+        }
+    }
+    return n;
+}
+
 // One batch slice of a conv with a kind-6 choice (views already inside
 // 32-bit spans, p.lin set).  A choice that does not fit the conv is an error.
 hipError_t launch_conv_s1x1(const ConvParams& p, bool int8, int epi, hipStream_t stream) {

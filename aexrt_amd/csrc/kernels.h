@@ -150,7 +150,10 @@ hipError_t launch_conv_chain2(const ConvParams* br0, const ConvParams* br1, int 
 // Kp % 64 == 0, OCp % 16 == 0 and 16-byte aligned views.
 hipError_t launch_conv_igemm(const ConvParams& p, bool int8, hipStream_t stream);
 // Every kernel/tile choice that can run conv p (implicit-GEMM tiles, and
-// halo tiles for 3x3 convs), at most cap; returns the count.
+// halo tiles for 3x3 convs), at most cap; returns the count.  Callers size
+// their candidate arrays kMaxConvChoices, which no conv of the supported
+// shapes reaches (a count equal to it means some were dropped).
+constexpr int kMaxConvChoices = 256;
 int enumerate_conv_choices(const ConvParams& p, bool int8, ConvChoice* out, int cap);
 int enumerate_halo_choices(const ConvParams& p, bool int8, ConvChoice* out, int cap);
 // Halo-tile 3x3 conv (pad 1, stride 1/2, C % 16 == 0) on one batch slice whose
@@ -187,10 +190,9 @@ bool forced_m32_choice(ConvChoice& c);
 // strided in both views, no residual): weights resident in LDS, every tile's
 // input loaded at once and quantized once into an int8 LDS tile, the next
 // tile in flight during the current one's MFMAs.  epi 0 any flags / 1 SiLU.
-// hipErrorInvalidValue when the choice does not fit the conv.  Not among the
-// load-time candidates (enumerate_conv_choices): the one load that measured it
-// there ended in a host segmentation fault whose cause is not found; it runs
-// only when forced (set_conv1x1_stream).
+// hipErrorInvalidValue when the choice does not fit the conv.
+// enumerate_s1x1_choices: the streaming tiles that fit conv p, at most cap.
+int enumerate_s1x1_choices(const ConvParams& p, bool int8, ConvChoice* out, int cap);
 hipError_t launch_conv_s1x1(const ConvParams& p, bool int8, int epi, hipStream_t stream);
 // Forces every int8 1x1 conv the kind-0 heuristics would run onto one
 // streaming tile (on = false: off).  False for a tile without an instance.

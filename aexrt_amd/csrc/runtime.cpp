@@ -129,6 +129,9 @@ struct Step {
     // runs can change after the step is built: measured tile choices)
     std::string head, tail;
     std::function<std::string()> family;
+    // per-tensor int8 conv steps: the launch parameters as they run now (for
+    // the accumulator debug tap)
+    std::function<ConvParams()> conv_params;
 };
 
 // Schedule of a network measured at load: sibling convs as one launch, lane
@@ -1114,8 +1117,11 @@ constexpr int kContextCands = 4;
 
 bool tune_conv(AexrtYoloModel* m, ConvParams& p, bool int8, std::vector<ConvChoice>* top) {
     const std::string key = tune_key(p, int8);
-    ConvChoice cand[128];
-    const int n = enumerate_conv_choices(p, int8, cand, 128);
+    std::vector<ConvChoice> cand(kMaxConvChoices);
+    const int n = enumerate_conv_choices(p, int8, cand.data(), kMaxConvChoices);
+    if (n >= kMaxConvChoices)
+        std::fprintf(stderr, "aexrt tune %s: %d candidates, the enumeration cap; the rest are not measured\n",
+                     key.c_str(), n);
     auto it = m->tuned.find(key);
     if (it != m->tuned.end()) {
         for (int i = 0; i < n; ++i)
@@ -1235,8 +1241,8 @@ std::string refined_key(size_t ci, uint32_t alg, const ConvParams& p, bool int8)
 // the network first, else its shape's isolated measurement; otherwise the
 // heuristics (choice kind 0).
 void apply_cached_choice(AexrtYoloModel* m, size_t ci, uint32_t alg, ConvParams& p, bool int8) {
-    ConvChoice all[128];
-    const int na = enumerate_conv_choices(p, int8, all, 128);
+    std::vector<ConvChoice> all(kMaxConvChoices);
+    const int na = enumerate_conv_choices(p, int8, all.data(), kMaxConvChoices);
     // a fused 1x1 runs on the 32x32-MFMA kernel only: without a measured
     // choice, the first tile that fits
     if (p.fuse_1x1 && na > 0) p.choice = all[0];
@@ -1572,8 +1578,8 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                         if (!tc->done) {
                             // a choice of an earlier measurement in the network: kept when this
                             // build still offers it for the conv
-                            ConvChoice all[128];
-                            const int na = enumerate_conv_choices(p, tc->int8, all, 128);
+                            std::vector<ConvChoice> all(kMaxConvChoices);
+                            const int na = enumerate_conv_choices(p, tc->int8, all.data(), kMaxConvChoices);
                             for (int k = 0; k < na; ++k) tc->done = tc->done || same_choice(all[k], rf->second);
                         }
                         if (tc->done) p.choice = rf->second;
@@ -1594,6 +1600,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                         conv_kernel_name(t->p, t->int8, name, sizeof(name));
                         return std::string(name);
                     };
+                    if (int8) m->steps.back().conv_params = [t] { return t->p; };
                 } else {
                     if (!is_winograd_algorithm(alg)) apply_cached_choice(m, ci, alg, p, int8);
                     m->steps.push_back(Step{(int)ci, "", [p, alg, pre](hipStream_t s) {
@@ -1612,6 +1619,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                             conv_kernel_name(p, int8, name, sizeof(name));
                             return std::string(name);
                         };
+                        if (int8) m->steps.back().conv_params = [p] { return p; };
                     }
                 }
                 if (own_pass) head += " own-amax";
@@ -2748,6 +2756,55 @@ int aexrt_yolo_debug_value(AexrtYoloModel* m, uint32_t value_id, float* out, uin
         return hipMemcpy(out, m->input_dev, n * 4, hipMemcpyDeviceToHost) == hipSuccess ? 1 : 0;
     }
     return copy_value_to_host(m, v, out, elements) ? 1 : 0;
+}
+
+int aexrt_yolo_debug_conv_int8(AexrtYoloModel* m, uint32_t command_index, int32_t* acc, uint64_t acc_elements,
+                               uint32_t* slots, uint32_t slot_count) {
+    if (!m || !acc) return 0;
+    std::lock_guard<std::mutex> lock(m->mutex);
+    const Step* st = nullptr;
+    for (const Step& s : m->steps)
+        if (s.cmd >= 0 && s.conv_params && m->eng.src_cmd[s.cmd] == command_index) st = &s;
+    if (!st) return fail(m, "debug_conv_int8: command " + std::to_string(command_index) +
+                                " is not a per-tensor int8 conv of the prepared steps") ? 1 : 0;
+    ConvParams q = st->conv_params();
+    const uint64_t n_acc = (uint64_t)q.M * (uint64_t)q.OC;
+    if (acc_elements < n_acc || (slots && slot_count < (uint32_t)q.x_nslots))
+        return fail(m, "debug_conv_int8: output buffers too small") ? 1 : 0;
+    if (!check_hip(hipStreamSynchronize(m->stream), "debug_conv_int8 sync")) return fail(m, last_error()) ? 1 : 0;
+    // the conv again on the input the last run left in memory, with the same
+    // kernel and tile: accumulators on, its output into a dense scratch view,
+    // no amax slot updates (the model's memory is left as the run left it)
+    const int esz = (q.flags & kConvOutF32) ? 4 : 2;
+    void *acc_dev = nullptr, *y_dev = nullptr;
+    bool ok = check_hip(hipMalloc(&acc_dev, n_acc * 4), "debug_conv_int8 alloc") &&
+              check_hip(hipMalloc(&y_dev, n_acc * esz), "debug_conv_int8 alloc");
+    if (ok) {
+        q.acc_out = static_cast<int32_t*>(acc_dev);
+        q.y = y_dev;
+        q.y_nstride = (int64_t)q.OH * q.OW * q.OC;
+        q.y_cstride = q.OC;
+        q.y_slots = SlotRef{nullptr, 1u, 0u};
+        ok = check_hip(launch_conv_igemm(q, true, m->stream), "debug_conv_int8 launch") &&
+             check_hip(hipStreamSynchronize(m->stream), "debug_conv_int8 sync") &&
+             check_hip(hipMemcpy(acc, acc_dev, n_acc * 4, hipMemcpyDeviceToHost), "debug_conv_int8 copy");
+    }
+    // the input's slot words, max over the stripes (what the conv quantized with)
+    if (ok && slots) {
+        const uint32_t stripes = q.x_slots.stripes ? q.x_slots.stripes : 1u;
+        std::vector<uint32_t> w((size_t)q.x_nslots);
+        for (uint32_t g = 0; g < (uint32_t)q.x_nslots; ++g) slots[g] = 0u;
+        for (uint32_t s = 0; s < stripes && ok; ++s) {
+            ok = check_hip(hipMemcpy(w.data(), q.x_slots.p + (size_t)s * q.x_slots.stride, w.size() * 4,
+                                     hipMemcpyDeviceToHost),
+                           "debug_conv_int8 slots");
+            for (size_t g = 0; ok && g < w.size(); ++g) slots[g] = std::max(slots[g], w[g]);
+        }
+    }
+    if (acc_dev) (void)hipFree(acc_dev);
+    if (y_dev) (void)hipFree(y_dev);
+    if (!ok) return fail(m, last_error()) ? 1 : 0;
+    return 1;
 }
 
 // The reference reads back a D3D12 arena page (native/aexrt.h:403); values

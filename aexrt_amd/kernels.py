@@ -399,3 +399,34 @@ def add(a, b, y, y_slots=None, stream=None) -> None:
     av, bv, yv = view(a), view(b), view(y, y_slots)
     check(_lib.lib().aexrt_hip_add(ctypes.byref(av), ctypes.byref(bv), ctypes.byref(yv), n, h * w, c,
                                     _stream(stream)), "add")
+
+
+def conv_candidates(desc: ConvDesc, algorithm: int, flags: int = SILU, *, x_cstride: Optional[int] = None,
+                    y_cstride: Optional[int] = None, residual: bool = False, cap: int = 512) -> list[str]:
+    """Kernel instance and tile of every candidate the model loader measures for one conv with
+    dense NHWC views (channel strides ``x_cstride`` / ``y_cstride`` for channel slices); ``""``
+    marks a candidate its launcher rejects.  With ``IN_NCHW_F32`` in flags the input is the
+    network's fp32 NCHW tensor of ``x_cstride`` channels (desc.in_channels 8).  Host only: no
+    kernel runs, no device is needed."""
+    d = desc
+    xc = x_cstride or d.in_channels
+    yc = y_cstride or d.out_channels
+    base = 1 << 20  # aligned placeholder addresses: nothing is dereferenced
+    xv = TensorView(data=base, n_stride=d.in_h * d.in_w * xc, c_stride=xc, amax_stripes=0, amax_slots=base,
+                    amax_stripe_stride=0)
+    if flags & IN_NCHW_F32:
+        xv.c_stride = 1
+    yv = TensorView(data=base, n_stride=d.out_h * d.out_w * yc, c_stride=yc, amax_stripes=0, amax_slots=None,
+                    amax_stripe_stride=0)
+    rv = TensorView(data=base, n_stride=d.out_h * d.out_w * yc, c_stride=yc, amax_stripes=0, amax_slots=None,
+                    amax_stripe_stride=0)
+    name_len = 128
+    buf = ctypes.create_string_buffer(name_len * cap)
+    n = _lib.lib().aexrt_hip_conv_candidates(ctypes.byref(d), algorithm, flags, ctypes.byref(xv),
+                                             ctypes.byref(rv) if residual else None, ctypes.byref(yv), buf,
+                                             name_len, cap)
+    if n == 0:
+        raise RuntimeError(f"conv_candidates failed: {_lib.last_error()}")
+    raw = buf.raw
+    return [raw[i * name_len:(i + 1) * name_len].split(b"\0", 1)[0].decode() for i in range(min(n, cap))] + \
+        [None] * max(0, n - cap)

@@ -169,6 +169,18 @@ class NativeHipYoloModel:
         shape = dims if rank == 4 else dims[:3]
         return out.reshape(shape)
 
+    def debug_conv_int8(self, command_index: int, batch: int, out_hw: tuple, out_channels: int,
+                        in_channels: int):
+        """The int32 accumulators ([N, OH, OW, OC]) of per-tensor int8 conv ``command_index`` as
+        the last run computed them, and its input's per-16-channel amax words (uint32)."""
+        oh, ow = out_hw
+        acc = np.empty((batch, oh, ow, out_channels), dtype=np.int32)
+        slots = np.empty(in_channels // 16, dtype=np.uint32)
+        if not self.lib.aexrt_yolo_debug_conv_int8(self.model, command_index, acc.ctypes.data_as(ctypes.c_void_p),
+                                                   acc.size, slots.ctypes.data_as(ctypes.c_void_p), slots.size):
+            raise RuntimeError(f"debug_conv_int8 failed: {self.last_error()}")
+        return acc, slots
+
     def last_run_timing(self) -> Optional[dict]:
         t = RunTiming()
         t.struct_size = ctypes.sizeof(RunTiming)

@@ -192,6 +192,21 @@ int aexrt_hip_conv2d(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t f
                      const float* bias, const AexrtHipTensorView* residual,
                      const AexrtHipTensorView* y, int32_t* acc_out, void* stream);
 
+/* The kernel and tile candidates the model loader measures for one conv
+ * (no reference counterpart; the tile-level analogue of the algorithm
+ * candidates of aexrt_yolo_conv_plan_info, native/aexrt.h:435-445, and of
+ * replay_conv_algorithm's candidate list, RT:9510-9576).  x, residual and y
+ * give the views' strides (pointers only need to be 16-byte aligned and
+ * non-null; nothing is read).  For each candidate i < cap, names + i *
+ * name_len receives the kernel instance and tile its launcher would run
+ * ("" when the launcher rejects it).  Returns the candidate count, which
+ * can exceed cap; no kernel runs and no HIP call is made.  Winograd, pg16
+ * and dynamic int8 convs have no tile choice: 0 with a diagnostic. */
+uint32_t aexrt_hip_conv_candidates(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t flags,
+                                   const AexrtHipTensorView* x, const AexrtHipTensorView* residual,
+                                   const AexrtHipTensorView* y, char* names, uint32_t name_len,
+                                   uint32_t cap);
+
 /* a15 on the GPU: fp32 direct convolution of dense NCHW tensors, the
  * reference's aexrt_d3d12_conv2d_float32 / aexrt_d3d12_conv2d_silu_float32
  * (native/aexrt.h:175-189; shader native/aexrt_d3d12_runtime.cpp:1554-1622)
@@ -586,6 +601,20 @@ int aexrt_yolo_debug_value(AexrtYoloModel* model, uint32_t value_id, float* out,
 /* native/aexrt.h:403 reads a D3D12 arena page; values here live in one NHWC
  * arena read through debug_value: returns 0 with a diagnostic. */
 int aexrt_yolo_debug_page(AexrtYoloModel* model, uint32_t page_id, float* out, uint64_t elements);
+/* Debug tap of a per-tensor int8 conv of the loaded model (no reference
+ * counterpart; it exposes the reference's bit-exact quantities,
+ * native/aexrt_d3d12_runtime.cpp:3219-3259 and 4614-4762, at network
+ * level): runs engine command `command_index` again exactly as the last run
+ * did (same kernel and tile, the input and its amax slots as the run left
+ * them) with the int32 accumulators on, into acc ([N][OH][OW][OC] exact
+ * sums of the quantized input times the int8 weights, acc_elements at
+ * least N*OH*OW*OC), and, when slots is non-NULL, the input's per-16-channel
+ * amax words (bit patterns of max|x| over each channel group, the max over
+ * the slot copies: what the conv quantized with; slot_count >= C/16).  The
+ * model's tensors and slots are not modified.  Returns 0 for commands that
+ * are not per-tensor int8 convs (pg16, dynamic, fp16) or before a run. */
+int aexrt_yolo_debug_conv_int8(AexrtYoloModel* model, uint32_t command_index, int32_t* acc,
+                               uint64_t acc_elements, uint32_t* slots, uint32_t slot_count);
 /* Logical dims of a value: out4 = {N, C, H, W} ({N, C, A, 1} for rank 3);
  * returns the rank, 0 when the value has no device storage. */
 int aexrt_yolo_value_info(AexrtYoloModel* model, uint32_t value_id, uint32_t* out4);

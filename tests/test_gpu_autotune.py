@@ -16,6 +16,7 @@ import pytest
 from aexrt_amd import engine as E
 from aexrt_amd.runtime import NativeHipYoloModel
 from aexrt_amd.yolov8 import build_yolov8n
+from tests.test_gpu_model import _layer_check
 
 pytestmark = pytest.mark.gpu
 
@@ -40,9 +41,19 @@ def test_conv_autotune_emits_gated_algo_map(cuda, tmp_path):
     kinds = {i: c["kind"] for i, c in enumerate(plan["replay"]["commands"])}
     assert all(kinds[k] in ("CONV", "CONV_SILU") for k in m)
     assert "kAexrtTunedConvCount" in hdr.read_text()
-    # the map rebuilds into an engine that runs (Winograd targets are refused by the compiler)
-    data = E.build_aexrt_engine(g, precision="fp16", classes=80,
-                                algo_overrides={k: v for k, v in m.items() if v not in (40, 46)})
+    # the map rebuilds into an engine (Winograd targets are refused by the compiler) whose every
+    # conv matches the oracle fed the GPU's own layer inputs, on the algorithm the map chose
+    # (conv_autotune.cpp:300-351 keeps a choice only when the detections pass its gate; here each
+    # layer is held to the backend's parity bounds)
+    overrides = {k: v for k, v in m.items() if v not in (40, 46)}
+    data = E.build_aexrt_engine(g, precision="fp16", classes=80, algo_overrides=overrides)
+    plan = E.compile_plan(g, precision="fp16", algo_overrides=overrides)
     x = np.random.default_rng(1).random((1, 3, 160, 160)).astype(np.float32)
     with NativeHipYoloModel(data) as model:
         model.run(x)
+        current = {i["command_index"]: i["current_algorithm"] for i in model.conv_plan()}
+        for k, v in overrides.items():
+            assert current[k] == v, (k, v, current[k])
+        checked, worst = _layer_check(model, g, plan, threads=8)
+        assert checked == 63, checked
+        assert worst <= 1.0

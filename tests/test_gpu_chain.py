@@ -28,7 +28,7 @@ CASES = [
     (1, 64, 40, 40, 64, 64, (8, 8), "f16", None),     # 40x40 box branch, interior tiles
     (2, 64, 40, 40, 80, 80, (6, 8), "f16", None),     # partial last tile row
     (1, 64, 13, 11, 80, 64, (5, 4), "silu", None),    # ragged map, partial tiles, SiLU on the 1x1
-    (1, 128, 13, 11, 80, 64, (5, 4), "silu", None),   # the same with a 16 KB window (two k groups)
+    (1, 128, 13, 11, 80, 64, (5, 4), "silu", None),   # the same with a 16 KB window
     (2, 32, 9, 7, 48, 32, (0, 0), "f16", None),       # 48 channels in a 64-channel block
     (2, 128, 20, 20, 64, 64, (10, 10), "f32", (80, 144, 144)),  # box outputs in a 144-channel tensor
     (1, 64, 40, 40, 80, 80, (8, 12), "f16", None),    # 140-position regions: two subtiles per wave
@@ -36,16 +36,12 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("kg", ["1", pytest.param("2", marks=pytest.mark.skip(
-    reason="two-group chain blocks switched off: a model load that ran them aborted, cause not found"))])
 @pytest.mark.parametrize("case", CASES, ids=[f"c{t[1]}_{t[2]}x{t[3]}_b{t[4]}_o{t[5]}_t{t[6][0]}x{t[6][1]}_{t[7]}"
                                              f"{'_slice' if t[8] else ''}" for t in CASES])
-def test_chain_matches_three_convs(cuda, case, kg, monkeypatch):
-    """kg 2: two groups of four waves splitting each chunk's k steps, where the
-    block has one position subtile per wave and a window of at least 16 KB."""
+def test_chain_matches_three_convs(cuda, case):
+    """One group of four waves per block (the library launches no other form)."""
     import torch
 
-    monkeypatch.setenv("AEXRT_HIP_CHAIN_KG", kg)
     n, c, h, w, cb, oc, tile, out, sl = case
     rng = np.random.default_rng(701 + c + h + cb + oc)
     x = O.round_f16(rng.standard_normal((n, c, h, w)).astype(np.float32))

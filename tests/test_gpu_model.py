@@ -413,6 +413,60 @@ def test_yolov8n_320_bs64_w8a8_layers(cuda, monkeypatch, tmp_path):
         assert checked == 63
 
 
+def _int8_tensor_check(model, graph, plan, images, threads=16):
+    """Every per-tensor int8 conv of the run, bit for bit: the amax words the conv quantized its
+    input with equal max|x| of each 16-channel group of the GPU's own stored input (and their
+    max equals the oracle's per-tensor amax, RT:3219-3259), and the conv's int32 accumulators of
+    `images` equal the oracle's exact int8 conv of that input quantized with the batch-global
+    amax and of the engine's int8 weights (RT:3314-3346, 4614-4762).  Returns the convs checked."""
+    replay = plan["replay"]
+    names, cmds = replay["names"], replay["commands"]
+    current = {i["command_index"]: i["current_algorithm"] for i in model.conv_plan()}
+    checked = 0
+    for i, c in enumerate(cmds):
+        if c["kind"] not in ("CONV", "CONV_SILU") or current[i] not in E.INT8_KERNELS:
+            continue
+        if plan["plans"][i]["flags"] & E.PLAN_FLAG_INT8_PERGROUP:
+            continue
+        xin, wid, _ = c["inputs"]
+        x = model.value(xin)  # the stored fp16 input, widened exactly
+        if x.size < ON.PREQUANT_MIN_ELEMENTS:
+            continue  # quantized per position in the dynamic kernel: no tensor amax
+        prm = [int(v) for v in c["params"][:16]]
+        n, cin, oc, oh, ow = prm[0], prm[1], prm[4], prm[5], prm[6]
+        acc, slots = model.debug_conv_int8(i, n, (oh, ow), oc, cin)
+        groups = np.abs(x).reshape(n, cin // 16, 16, -1).max(axis=(0, 2, 3)).astype(np.float32)
+        np.testing.assert_array_equal(slots, groups.view(np.uint32), err_msg=f"cmd {i} amax words")
+        amax = float(slots.view(np.float32).max())
+        assert amax == O.amax(x), (i, amax)
+        qw, _ = O.weight_quant(graph.constants[names[wid]], fp16_round=True)
+        sel = list(images)
+        qa = O.quantize(x[sel], amax)
+        desc = np.array(prm, dtype=np.uint32)
+        desc[0] = len(sel)
+        ref = O.conv_int8_acc(qa, qw, desc, threads=threads)
+        got = acc[sel].transpose(0, 3, 1, 2)
+        assert np.array_equal(got, ref), (i, int(np.abs(got.astype(np.int64) - ref).max()))
+        checked += 1
+    return checked
+
+
+@pytest.mark.parametrize("batch,images", [(1, (0,)), (64, (0, 29, 63))])
+def test_yolov8n_320_w8a8_int8_tensors_bit_exact(cuda, monkeypatch, tmp_path, batch, images):
+    """The benchmark network on the benchmark's kernel plan: amax words and int32 accumulators
+    of all 44 int8 convs bit-exact against the oracle."""
+    _use_bench_plan(monkeypatch, tmp_path)
+    g, names, plan, data = _yolo_engine(batch, 320)
+    x = np.random.default_rng(4).random((batch, 3, 320, 320)).astype(np.float32)
+    with NativeHipYoloModel(data) as m:
+        m.run(x)
+        assert _int8_tensor_check(m, g, plan, images) == 44
+        # the tap leaves the model's memory as the run left it
+        out1 = m.output()
+        m.run(x)
+        np.testing.assert_array_equal(m.output(), out1)
+
+
 def test_override_round_trip_restores_identical_outputs(cuda):
     """Overriding convs to other algorithms and back reuses the kernel choices measured first, so
     the restored model's output is bit-identical to the original (a no-op round trip cannot move

@@ -77,3 +77,47 @@ def test_noalloc_refuses_more_channels_than_its_scratch(cuda):
                     ctypes.byref(yv), None)
     assert not ok
     assert "4096 input channels" in _lib.last_error()
+
+
+def test_noalloc_replays_under_graph_capture(cuda):
+    """The entry recorded inside a HIP graph capture (where a caller cannot allocate) on a shape no
+    other test of this file uses, then replayed three times with eager work and synchronizations
+    between the replays: every replay equals the allocating command's eager output bit for bit."""
+    import torch
+
+    n, c, h, w, oc = 2, 96, 14, 14, 48
+    rng = np.random.default_rng(53)
+    x = O.round_f16(rng.standard_normal((n, c, h, w)).astype(np.float32))
+    x[:, 32:48] *= 3.0
+    wt = he_weight(rng, oc, c, 3)
+    b = packing.fp16_round(rng.uniform(-0.1, 0.1, oc).astype(np.float32))
+    desc = O.conv_desc(n, c, h, w, oc, 3, 1, 1)
+    pc = K.prepare_conv(desc, 52, K.SRC_LAYOUT_INT8, packing.pack_conv_int8(wt, fp16_engine=True), b, device=cuda)
+    xd = torch.from_numpy(nchw_to_nhwc(x.astype(np.float16))).to(cuda)
+    y_ref = torch.empty((n, h, w, oc), dtype=torch.float16, device=cuda)
+    y = torch.empty_like(y_ref)
+    K.conv2d_int8(pc, xd, y_ref, flags=K.SILU)
+    torch.cuda.synchronize()
+    ref = y_ref.cpu().numpy()
+    d = _lib.ConvDesc.from_params(pc.params)
+    xv, yv = K.view(xd), K.view(y)
+    args = (ctypes.byref(d), pc.algorithm, K.SILU, ctypes.byref(xv), pc.weight.data_ptr(), pc.w_scale.data_ptr(),
+            pc.bias.data_ptr(), None, ctypes.byref(yv))
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):  # the first call on a device looks up the array's address
+        assert _noalloc()(*args, ctypes.c_void_p(side.cuda_stream)), _lib.last_error()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        ok = _noalloc()(*args, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert ok, _lib.last_error()
+    other = torch.empty_like(y_ref)
+    for _ in range(3):
+        y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(y.cpu().numpy(), ref)
+        K.conv2d_int8(pc, xd, other, flags=K.SILU)  # eager work between the replays
+        torch.cuda.synchronize()
+    np.testing.assert_array_equal(other.cpu().numpy(), ref)
