@@ -137,6 +137,9 @@ _SIGS = {
                                            c_uint64, _vp]),
     "aexrt_hip_conv2d": (c_int, [POINTER(ConvDesc), c_uint32, c_uint32, POINTER(TensorView), _vp, _vp, _vp,
                                  POINTER(TensorView), POINTER(TensorView), _vp, _vp]),
+    "aexrt_hip_conv_pair": (c_int, [POINTER(ConvDesc), c_uint32, c_uint32, POINTER(TensorView), _vp, _vp, _vp, _vp,
+                                    _vp, _vp, POINTER(TensorView), c_uint32, _vp, _vp, _vp, _vp]),
+    "aexrt_hip_conv_pair_barrier_timeouts": (c_uint32, []),
     "aexrt_hip_conv_candidates": (c_uint32, [POINTER(ConvDesc), c_uint32, c_uint32, POINTER(TensorView),
                                              POINTER(TensorView), POINTER(TensorView), _vp, c_uint32, c_uint32]),
     "aexrt_hip_can_use_conv_int8": (c_int, [POINTER(ConvDesc), c_uint32]),

@@ -6,6 +6,8 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -157,6 +159,28 @@ static bool source_to_f32(const AexrtConv2DDesc& d, uint32_t layout, const void*
         return true;
     }
     return false;
+}
+
+// Sync words of the op-level pair entry (and its barrier-timeout word after
+// them), one allocation per device kept for the process; overlapping int8
+// pair calls on one device share them and race.
+constexpr uint32_t kPairSyncWordsAbi = 512;
+static_assert(kPairSyncWordsAbi == (uint32_t)kPairSyncWordsHost, "sync area size");
+
+static uint32_t* pair_sync_words() {
+    static std::mutex mu;
+    static std::map<int, uint32_t*> per_dev;
+    int dev = 0;
+    if (!check_hip(hipGetDevice(&dev), "conv_pair: current device")) return nullptr;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = per_dev.find(dev);
+    if (it != per_dev.end()) return it->second;
+    void* p = nullptr;
+    if (!check_hip(hipMalloc(&p, (kPairSyncWordsAbi + 64) * 4), "conv_pair: sync allocation") ||
+        !check_hip(hipMemset(p, 0, (kPairSyncWordsAbi + 64) * 4), "conv_pair: sync clear"))
+        return nullptr;
+    per_dev[dev] = static_cast<uint32_t*>(p);
+    return static_cast<uint32_t*>(p);
 }
 
 }  // namespace aexrt
@@ -374,6 +398,75 @@ uint32_t aexrt_hip_conv_candidates(const AexrtConv2DDesc* desc, uint32_t algorit
         std::snprintf(dst, name_len, "%s", probe.name);
     }
     return (uint32_t)n;
+}
+
+int aexrt_hip_conv_pair(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t flags, const AexrtHipTensorView* x,
+                        const void* weight_a, const float* w_scale_a, const float* bias_a, const void* weight_b,
+                        const float* w_scale_b, const float* bias_b, const AexrtHipTensorView* y, uint32_t band_rows,
+                        void* t_out, int32_t* acc_a, int32_t* acc_b, void* stream) {
+    if (!desc || !x || !y || !x->data || !y->data || !weight_a || !weight_b || !bias_a || !bias_b) {
+        set_error("conv_pair: null argument");
+        return 0;
+    }
+    if (flags & ~(uint32_t)AEXRT_HIP_CONV_RESIDUAL) {
+        set_error("conv_pair: the only flag is AEXRT_HIP_CONV_RESIDUAL (both convs apply SiLU, fp16 output)");
+        return 0;
+    }
+    const bool int8 = is_int8_algorithm(algorithm);
+    if ((int8 && algorithm != 52u) || is_winograd_algorithm(algorithm) || (!int8 && (acc_a || acc_b))) {
+        set_error("conv_pair: algorithm 52 (int8) or an fp16 MFMA id; accumulators with int8 only");
+        return 0;
+    }
+    if (band_rows > 4096) {
+        set_error("conv_pair: band_rows 0 (chosen) or at most 4096");
+        return 0;
+    }
+    std::string why;
+    ConvParams pa{}, pb{};
+    AexrtHipTensorView t{};  // the intermediate's view (its pointer is never used)
+    t.data = y->data;
+    t.n_stride = int64_t(desc->out_h) * desc->out_w * desc->out_channels;
+    t.c_stride = (int32_t)desc->out_channels;
+    t.amax_slots = x->amax_slots;  // read by the kernel only through the barrier's amax words
+    if (!build_conv_params(*desc, algorithm, AEXRT_HIP_CONV_SILU, *x, weight_a, w_scale_a, bias_a, nullptr, t, nullptr,
+                           pa, why) ||
+        !build_conv_params(*desc, algorithm, AEXRT_HIP_CONV_SILU | (flags & AEXRT_HIP_CONV_RESIDUAL), t, weight_b,
+                           w_scale_b, bias_b, (flags & AEXRT_HIP_CONV_RESIDUAL) ? x : nullptr, *y, acc_b, pb, why)) {
+        set_error("conv_pair: " + why);
+        return 0;
+    }
+    if (const char* e = pair_shape_error(pa, pb, int8)) {
+        set_error(e);
+        return 0;
+    }
+    uint32_t* sync = nullptr;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (int8) {
+        sync = pair_sync_words();
+        if (!sync || !check_hip(launch_fill_u32(sync, kPairSyncWordsAbi, 0u, s), "conv_pair: clear sync words"))
+            return 0;
+    }
+    const hipError_t e = launch_conv_pair(pa, pb, int8, (int)band_rows, sync, sync ? sync + kPairSyncWordsAbi : nullptr,
+                                          static_cast<__half*>(t_out), acc_a, s);
+    if (e == hipErrorInvalidConfiguration) {
+        set_error("conv_pair: the grid of this batch and band height does not fit the GPU at once");
+        return 0;
+    }
+    if (e == hipErrorInvalidValue) {
+        set_error("conv_pair: no band of this height fits the kernel (LDS, positions per block, views)");
+        return 0;
+    }
+    return check_hip(e, "conv_pair") ? 1 : 0;
+}
+
+uint32_t aexrt_hip_conv_pair_barrier_timeouts(void) {
+    uint32_t* sync = pair_sync_words();
+    if (!sync) return 0xFFFFFFFFu;
+    uint32_t err = 0;
+    if (!check_hip(hipDeviceSynchronize(), "conv_pair: sync") ||
+        !check_hip(hipMemcpy(&err, sync + kPairSyncWordsAbi, 4, hipMemcpyDeviceToHost), "conv_pair: read error word"))
+        return 0xFFFFFFFFu;
+    return err;
 }
 
 int aexrt_hip_conv2d_fused_1x1(const AexrtConv2DDesc* desc, uint32_t flags, const AexrtHipTensorView* x,

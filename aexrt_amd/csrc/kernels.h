@@ -146,6 +146,20 @@ hipError_t launch_conv_chain(const ConvParams& a, const ConvParams& b, const Con
 // tile (0 x 0: the one that fits the branch with more channels).
 hipError_t launch_conv_chain2(const ConvParams* br0, const ConvParams* br1, int tr, int tc, hipStream_t stream);
 
+// C2f bottleneck pair in one launch (conv_pair.h): conv a (3x3 s1 p1 SiLU,
+// C -> C) then conv b (the same, + b.res when b.flags has kConvResidual) over
+// a's output, which stays in LDS (t_out: optional dense NHWC copy of it;
+// acc_a / b.acc_out: optional int32 sums, int8).  Bands of tr output rows
+// (0: chosen).  int8: a grid barrier exchanges the intermediate's amax, so
+// the whole grid must be resident (hipErrorInvalidConfiguration otherwise);
+// sync: kPairSyncWords uint32 zero at launch (a generation word excepted),
+// err: set to 1 if a barrier wait timed out.
+constexpr int kPairSyncWordsHost = 512;
+const char* pair_shape_error(const ConvParams& a, const ConvParams& b, bool int8);
+int enumerate_pair_bands(const ConvParams& a, const ConvParams& b, bool int8, int* out, int cap);
+hipError_t launch_conv_pair(const ConvParams& a, const ConvParams& b, bool int8, int tr, uint32_t* sync,
+                            uint32_t* err, __half* t_out, int32_t* acc_a, hipStream_t stream);
+
 // Implicit-GEMM conv (int8 or fp16 MFMA).  Requires C % 8 == 0, OC % 4 == 0,
 // Kp % 64 == 0, OCp % 16 == 0 and 16-byte aligned views.
 hipError_t launch_conv_igemm(const ConvParams& p, bool int8, hipStream_t stream);

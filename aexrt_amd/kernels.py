@@ -317,6 +317,25 @@ def conv_chain3(pa: PreparedConv, pb: PreparedConv, pc: PreparedConv, x, y, *, f
         ctypes.byref(yv), int(tile[0]), int(tile[1]), _stream(stream)), "conv_chain3")
 
 
+def conv_pair(pa: PreparedConv, pb: PreparedConv, x, y, *, x_slots=None, y_slots=None, residual: bool = False,
+              band_rows: int = 0, t_out=None, acc_a=None, acc_b=None, stream=None) -> None:
+    """A C2f bottleneck in one launch: y = silu(conv_b(fp16(silu(conv_a(x))))) (+ x with residual), both
+    3x3 C -> C convs on int8 (algorithm 52: x_slots hold x's amax; the intermediate is quantized with
+    its own batch-global amax) or fp16; the intermediate stays on chip (t_out: an optional copy).
+    acc_a / acc_b: optional int32 [N*H*W, C] sums of the two int8 convs."""
+    d = ConvDesc.from_params(pa.params)
+    xv, yv = view(x, x_slots), view(y, y_slots)
+    check(_lib.lib().aexrt_hip_conv_pair(
+        ctypes.byref(d), pa.algorithm, RESIDUAL if residual else 0, ctypes.byref(xv), pa.weight.data_ptr(),
+        _ptr(pa.w_scale), pa.bias.data_ptr(), pb.weight.data_ptr(), _ptr(pb.w_scale), pb.bias.data_ptr(),
+        ctypes.byref(yv), int(band_rows), _ptr(t_out), _ptr(acc_a), _ptr(acc_b), _stream(stream)), "conv_pair")
+
+
+def conv_pair_barrier_timeouts() -> int:
+    """Synchronizes the device; nonzero when an int8 pair launch's grid barrier wait timed out."""
+    return int(_lib.lib().aexrt_hip_conv_pair_barrier_timeouts())
+
+
 def conv2d_int8(pc: PreparedConv, x, y, *, flags: int = SILU, residual=None, stream=None) -> None:
     """The reference's int8 conv command on a plain fp16 NHWC input: dynamic below 4096 input
     elements, else the input's amax (strips with INT8_PG16) then the int8 conv."""

@@ -207,6 +207,33 @@ uint32_t aexrt_hip_conv_candidates(const AexrtConv2DDesc* desc, uint32_t algorit
                                    const AexrtHipTensorView* y, char* names, uint32_t name_len,
                                    uint32_t cap);
 
+/* C2f bottleneck superblock (the reference's fusion kind 1,
+ * src/aexrt/engine.py:75-76, shader native/aexrt_d3d12_runtime.cpp:
+ * 12205-12563, there in fp32): conv a (3x3 s1 p1 SiLU, C -> C) and conv b
+ * (the same, plus x as residual with AEXRT_HIP_CONV_RESIDUAL) in one
+ * launch, a's output kept on chip.  desc is conv a's (and b's) descriptor:
+ * C = in = out channels, a multiple of 32 up to 128.  algorithm 52: W8A8
+ * (x->amax_slots give x's per-tensor scale; the intermediate is quantized
+ * with its own per-tensor amax over the whole batch, exchanged between the
+ * workgroups through a grid barrier, exactly as two int8 convs would), or
+ * an fp16 id.  Weights packed for `algorithm` (aexrt_hip_pack_conv_weight),
+ * w_scale_* for int8.  y: fp16 NHWC view, its amax slots folded when set.
+ * band_rows: output rows per workgroup (0: chosen).  Optional: t_out (fp16
+ * dense NHWC copy of the intermediate), acc_a / acc_b (int32 [N*H*W][C]
+ * sums of the two convs, int8).  Returns 0 with a diagnostic when the
+ * shape, the band or (int8) the whole grid at once does not fit the GPU.
+ * Asynchronous on `stream`; the int8 form uses a per-device sync area
+ * (overlapping int8 calls on one device race). */
+int aexrt_hip_conv_pair(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t flags,
+                        const AexrtHipTensorView* x, const void* weight_a, const float* w_scale_a,
+                        const float* bias_a, const void* weight_b, const float* w_scale_b,
+                        const float* bias_b, const AexrtHipTensorView* y, uint32_t band_rows,
+                        void* t_out, int32_t* acc_a, int32_t* acc_b, void* stream);
+/* Synchronizes the device and returns the barrier-timeout word of the int8
+ * pair entry's sync area on the current device (0: every grid barrier
+ * completed; the wait is bounded and sets this word instead of hanging). */
+uint32_t aexrt_hip_conv_pair_barrier_timeouts(void);
+
 /* a15 on the GPU: fp32 direct convolution of dense NCHW tensors, the
  * reference's aexrt_d3d12_conv2d_float32 / aexrt_d3d12_conv2d_silu_float32
  * (native/aexrt.h:175-189; shader native/aexrt_d3d12_runtime.cpp:1554-1622)
