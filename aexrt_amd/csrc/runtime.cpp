@@ -107,6 +107,10 @@ struct ConvState {
     // a head branch run in one launch with this 3x3 conv first: the 3x3 conv
     // over its output (chain_b) and the 1x1 conv over that one's (chain_c)
     int chain_b = -1, chain_c = -1;
+    // C2f bottleneck superblock: this 3x3 conv and the 3x3 conv over its
+    // output (pair_b) in one launch, the intermediate never stored; pair_a:
+    // the first conv of the pair this one completes
+    int pair_b = -1, pair_a = -1;
     // sibling pair (this conv first): weights and bias of both convs, rows of
     // this conv then the sibling's, built from the w of each named here
     void* w_pair = nullptr;
@@ -132,6 +136,9 @@ struct Step {
     // per-tensor int8 conv steps: the launch parameters as they run now (for
     // the accumulator debug tap)
     std::function<ConvParams()> conv_params;
+    // a launch whose workgroups meet in a grid barrier (int8 superblock): never
+    // concurrent with another such launch, which could hold the CUs it waits for
+    bool grid_sync = false;
 };
 
 // Schedule of a network measured at load: sibling convs as one launch, lane
@@ -177,6 +184,7 @@ struct PlanStats {
     uint32_t exact_40_64x64 = 0, exact_20_64x64 = 0, exact_10_128x128 = 0, exact_20_128x64 = 0,
              exact_10_256x64 = 0;
     uint32_t native_fp16 = 0;
+    uint32_t c2f_superblocks = 0;       // C2f bottleneck pairs run as one launch
 };
 
 // A CONCAT input that could not be placed inside its concat: copied there.
@@ -227,6 +235,12 @@ struct AexrtYoloModel {
     uint32_t chain_dual = 0;  // branches of chain_mask that share a launch with another over their input
     std::vector<Step> steps;
     std::vector<CopyJob> copies;
+    // C2f bottleneck superblocks (AEXRT_HIP_C2F_SUPERBLOCK=1): their grid
+    // barriers' sync words (cleared every run) and the barrier-timeout word
+    bool c2f_superblock = false;
+    uint32_t* pair_sync = nullptr;
+    int n_pair_sync = 0;
+    uint32_t* pair_err = nullptr;
     std::vector<void*> allocations;
     uint8_t* arena = nullptr;
     uint32_t* slots = nullptr;
@@ -585,6 +599,59 @@ int setup_chains(AexrtYoloModel* m) {
         V[e.commands[cb].output].elided = true;
     }
     return (int)m->chains.size();
+}
+
+// C2f bottlenecks whose two 3x3 convs can run as one superblock launch: a
+// 3x3 stride-1 SiLU conv C -> C (int8 per-tensor or fp16, 32 <= C <= 128 in
+// steps of 32) whose output only a second such conv of the same arithmetic
+// reads, that second conv taking the first one's input as its fused residual
+// or no residual.  With m->c2f_superblock the pairs are marked (their
+// intermediate is then never stored); returns how many the plan has.
+int setup_pairs(AexrtYoloModel* m) {
+    const Engine& e = m->eng;
+    auto& V = m->vals;
+    int n = 0;
+    auto conv3 = [&](size_t ci, int C) {
+        const ConvState& cs = m->convs[ci];
+        const EngineCommand& c = e.commands[ci];
+        if (!cs.is_conv || c.kind != kCmdConvSilu || cs.pg16 || cs.dynamic || cs.own_slots ||
+            is_winograd_algorithm(cs.algorithm) || cs.fused_1x1 >= 0 || cs.fused_into >= 0 || cs.chain_b >= 0 ||
+            cs.chain_c >= 0 || m->sibling[ci] >= 0)
+            return false;
+        const AexrtConv2DDesc d = desc_of(c);
+        return d.kernel_h == 3 && d.kernel_w == 3 && d.stride_h == 1 && d.pad_top == 1 && d.in_channels == (uint32_t)C &&
+               d.out_channels == (uint32_t)C && d.in_h == d.out_h && d.in_w == d.out_w && C % 32 == 0 && C <= 128;
+    };
+    for (size_t ci = 0; ci < e.commands.size(); ++ci) {
+        ConvState& cs = m->convs[ci];
+        if (cs.pair_b >= 0) V[e.commands[ci].output].elided = false;
+        cs.pair_a = cs.pair_b = -1;
+    }
+    for (size_t ci = 0; ci < e.commands.size(); ++ci) {
+        const EngineCommand& c = e.commands[ci];
+        ConvState& cs = m->convs[ci];
+        if (!cs.is_conv || cs.fused_residual || cs.pair_a >= 0) continue;
+        const int C = (int)desc_of(c).in_channels;
+        if (!conv3(ci, C)) continue;
+        const ValueInfo& t = V[c.output];
+        const ValueInfo& x = V[c.inputs[0]];
+        if (t.consumers.size() != 1 || t.redirect >= 0 || c.output == e.manifest.output_value || x.is_input ||
+            !x.pl.valid)
+            continue;
+        const int cj = t.consumers[0];
+        ConvState& bs = m->convs[cj];
+        if (e.commands[cj].inputs[0] != c.output || !conv3((size_t)cj, C) ||
+            is_int8_algorithm(bs.algorithm) != is_int8_algorithm(cs.algorithm))
+            continue;
+        if (bs.fused_residual && bs.residual_value != (int)c.inputs[0]) continue;
+        if (is_int8_algorithm(cs.algorithm) && !m->roots[x.pl.root].slots_complete) continue;
+        ++n;
+        if (!m->c2f_superblock) continue;
+        cs.pair_b = cj;
+        bs.pair_a = (int)ci;
+        V[c.output].elided = true;
+    }
+    return n;
 }
 
 bool is_fused_add(AexrtYoloModel* m, size_t ci) {
@@ -1197,7 +1264,7 @@ void schedule_steps(AexrtYoloModel* m) {
         st[i].deps.clear();
         st[i].signal = false;
         for (int j = i - 1; j >= 0; --j) {
-            bool dep = st[i].all || st[j].all;
+            bool dep = st[i].all || st[j].all || (st[i].grid_sync && st[j].grid_sync);
             for (int r : st[i].reads)
                 for (int w : st[j].writes) dep = dep || r == w;
             if (dep) st[i].deps.push_back(j);
@@ -1376,6 +1443,65 @@ bool build_chain_step(AexrtYoloModel* m, size_t ci, std::vector<bool>& done, boo
     return true;
 }
 
+// The superblock step of bottleneck pair (ci, its pair_b): both 3x3 convs in
+// one launch (conv_pair.h); built = false (and the pair undone: both convs
+// then run on their own) when the launcher refuses it, e.g. an int8 grid
+// that the GPU cannot hold at once.
+bool build_pair_step(AexrtYoloModel* m, size_t ci, int k, std::vector<bool>& done, bool& built) {
+    built = false;
+    const Engine& e = m->eng;
+    auto& V = m->vals;
+    ConvState& cs = m->convs[ci];
+    const int cj = cs.pair_b;
+    ConvState& bs = m->convs[cj];
+    const bool int8 = is_int8_algorithm(cs.algorithm);
+    auto undo = [&] {
+        V[e.commands[ci].output].elided = false;
+        bs.pair_a = -1;
+        cs.pair_b = -1;
+        return true;
+    };
+    const int xv = (int)e.commands[ci].inputs[0], tv = (int)e.commands[ci].output;
+    AexrtHipTensorView xvw = view_of(m, xv), tvw = view_of(m, tv), yvw = view_of(m, bs.out_value);
+    if (int8 && !tvw.amax_slots) tvw.amax_slots = xvw.amax_slots;  // read only through the barrier's amax words
+    const uint32_t fa = AEXRT_HIP_CONV_SILU, fb = AEXRT_HIP_CONV_SILU | (bs.fused_residual ? AEXRT_HIP_CONV_RESIDUAL : 0u);
+    ConvParams pa{}, pb{};
+    std::string why;
+    if (!build_conv_params(conv_desc_padded(m, ci), cs.algorithm, fa, xvw, cs.w, cs.scale, cs.bias, nullptr, tvw,
+                           nullptr, pa, why) ||
+        !build_conv_params(conv_desc_padded(m, (size_t)cj), bs.algorithm, fb, tvw, bs.w, bs.scale, bs.bias,
+                           bs.fused_residual ? &xvw : nullptr, yvw, nullptr, pb, why))
+        return undo();
+    uint32_t* sync = int8 ? m->pair_sync + (size_t)k * kPairSyncWordsHost : nullptr;
+    uint32_t* err = int8 ? m->pair_err : nullptr;
+    {
+        LaunchProbe probe{};
+        set_launch_probe(&probe);
+        const hipError_t pe = launch_conv_pair(pa, pb, int8, 0, sync, err, nullptr, nullptr, nullptr);
+        set_launch_probe(nullptr);
+        if (pe != hipSuccess) return undo();
+    }
+    m->steps.push_back(Step{(int)ci, "", [pa, pb, int8, sync, err](hipStream_t s) {
+                                return launch_conv_pair(pa, pb, int8, 0, sync, err, nullptr, nullptr, s);
+                            }});
+    Step& st = m->steps.back();
+    st.family = [pa, pb, int8, sync, err] {
+        LaunchProbe probe{};
+        set_launch_probe(&probe);
+        (void)launch_conv_pair(pa, pb, int8, 0, sync, err, nullptr, nullptr, nullptr);
+        set_launch_probe(nullptr);
+        return std::string(probe.name);
+    };
+    st.head = conv_label(e.commands[ci], e.src_cmd[ci], cs.algorithm);
+    st.tail = " then cmd#" + std::to_string(e.src_cmd[cj]) + " (C2f bottleneck superblock)";
+    st.reads = {V[xv].pl.root};
+    st.writes = {V[bs.out_value].pl.root};
+    st.grid_sync = int8;
+    done[cj] = true;
+    built = true;
+    return true;
+}
+
 bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
     Engine& e = m->eng;
     auto& V = m->vals;
@@ -1389,6 +1515,29 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                                 }});
         m->steps.back().all = true;
     }
+    {
+        int npairs = 0;
+        for (const ConvState& cs : m->convs) npairs += cs.pair_b >= 0 && is_int8_algorithm(cs.algorithm) ? 1 : 0;
+        if (npairs > m->n_pair_sync) {
+            m->pair_sync = static_cast<uint32_t*>(dev_alloc(m, (size_t)npairs * kPairSyncWordsHost * 4));
+            if (!m->pair_sync) return fail(m, "out of device memory for superblock sync words");
+            m->n_pair_sync = npairs;
+        }
+        if (npairs > 0 && !m->pair_err) {
+            m->pair_err = static_cast<uint32_t*>(dev_alloc(m, 256));
+            if (!m->pair_err || hipMemset(m->pair_err, 0, 256) != hipSuccess)
+                return fail(m, "out of device memory for the superblock error word");
+        }
+        if (npairs > 0) {
+            uint32_t* sync = m->pair_sync;
+            const int64_t n = (int64_t)npairs * kPairSyncWordsHost;
+            m->steps.push_back(Step{-1, "superblock sync clear", [sync, n](hipStream_t s) {
+                                        return launch_fill_u32(sync, n, 0u, s);
+                                    }});
+            m->steps.back().all = true;
+        }
+    }
+    int pair_k = 0;  // int8 superblock steps built so far (their sync areas)
     const uint32_t in_v = e.manifest.input_value;
     if (m->input_needs_nhwc) {
         const ValueInfo& x = V[in_v];
@@ -1425,6 +1574,15 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                     bool built = false;
                     if (!build_chain_step(m, ci, done, built)) return false;
                     if (built) break;
+                }
+                if (cs.pair_b >= 0) {
+                    bool built = false;
+                    const bool int8_pair = is_int8_algorithm(cs.algorithm);
+                    if (!build_pair_step(m, ci, pair_k, done, built)) return false;
+                    if (built) {
+                        if (int8_pair) ++pair_k;
+                        break;
+                    }
                 }
                 const bool pair = m->merge_siblings && sib >= 0 && !done[sib] && cs.w_pair && cs.pair_src[0] == cs.w &&
                                   cs.pair_src[1] == m->convs[sib].w && cs.chain_b < 0 && m->convs[sib].chain_b < 0;
@@ -2067,10 +2225,15 @@ void compute_stats(AexrtYoloModel* m) {
         const std::string f = x.family();
         const uint8_t k = f.rfind("conv_int8_dynamic", 0) == 0 ? 3
                           : (f.rfind("conv3x3_halo", 0) == 0 || f.rfind("conv3x3_wide", 0) == 0 ||
-                             f.rfind("conv3x3_stem", 0) == 0 || f.rfind("conv3x3_m32", 0) == 0)
+                             f.rfind("conv3x3_stem", 0) == 0 || f.rfind("conv3x3_m32", 0) == 0 ||
+                             f.rfind("conv_pair", 0) == 0)
                               ? 2
                               : 1;
         conv_kind[x.cmd] = k;
+        if (x.tail.find("superblock") != std::string::npos) {
+            ++st.c2f_superblocks;
+            if (m->convs[x.cmd].pair_b >= 0) conv_kind[m->convs[x.cmd].pair_b] = k;
+        }
         if (x.tail.rfind(" + cmd#", 0) == 0) {  // a sibling pair in one launch
             st.paired_conv3x3 += desc_of(e.commands[x.cmd]).kernel_h == 3;
             if (m->sibling[x.cmd] >= 0) conv_kind[m->sibling[x.cmd]] = k;
@@ -2140,6 +2303,8 @@ bool build_model(AexrtYoloModel* m) {
     m->chain_mask = 0;
     const int fusable = fuse_head_1x1(m);
     setup_chains(m);
+    if (const char* v = std::getenv("AEXRT_HIP_C2F_SUPERBLOCK")) m->c2f_superblock = v[0] == '1';
+    setup_pairs(m);
     mark_slot_readers(m);
     // arena
     size_t total = 0;
@@ -2593,7 +2758,7 @@ uint32_t aexrt_yolo_late_concat_conv1x1_fusion_count(AexrtYoloModel* m) { return
 // D3D12-only fusions this backend does not form: 0.
 uint32_t aexrt_yolo_concat_residual_conv1x1_fusion_count(AexrtYoloModel* m) { (void)m; return 0; }
 uint32_t aexrt_yolo_paired_conv3x3_fusion_count(AexrtYoloModel* m) { return m ? m->stats.paired_conv3x3 : 0; }
-uint32_t aexrt_yolo_c2f_bottleneck_superblock_count(AexrtYoloModel* m) { (void)m; return 0; }
+uint32_t aexrt_yolo_c2f_bottleneck_superblock_count(AexrtYoloModel* m) { return m ? m->stats.c2f_superblocks : 0; }
 uint32_t aexrt_yolo_c2f_tail_residual_fusion_count(AexrtYoloModel* m) { return m ? m->stats.tail_residual : 0; }
 uint32_t aexrt_yolo_head_fusion_enabled(AexrtYoloModel* m) { (void)m; return 0; }
 uint32_t aexrt_yolo_head_final_conv_fusion_enabled(AexrtYoloModel* m) { return m && m->stats.head_final_conv ? 1u : 0u; }
@@ -2718,6 +2883,12 @@ int aexrt_yolo_run(AexrtDevice* device, AexrtYoloModel* m, const float* input, u
     }
     auto t2 = clk::now();
     if (!check_hip(hipStreamSynchronize(m->stream), "run sync")) return fail(m, last_error()) ? 1 : 0;
+    if (m->pair_err) {  // a superblock's grid barrier wait that timed out leaves wrong outputs
+        uint32_t err = 0;
+        if (!check_hip(hipMemcpy(&err, m->pair_err, 4, hipMemcpyDeviceToHost), "superblock status") || err)
+            return fail(m, err ? "run: a C2f superblock's grid barrier timed out (the outputs are not valid)"
+                               : last_error()) ? 1 : 0;
+    }
     auto t3 = clk::now();
     uint32_t cap = 0;
     if (m->post_ok && detections)

@@ -55,12 +55,13 @@ TUNE_FILE = os.path.join(ROOT, "aexrt_amd", "tuned", "yolov8n320.tune")
 TRAFFIC_TABLE = os.path.join(ROOT, "profiles", "hbm_traffic_yolov8n320_bs64.md")
 
 
-def use_tune_plan(retune: bool) -> str | None:
-    """Points AEXRT_HIP_TUNE_CACHE at a scratch copy of the committed plan (the runtime rewrites
-    the file it is given after a measuring load).  Returns the scratch path."""
+def use_tune_plan(retune: bool, source: str | None = None) -> str | None:
+    """Points AEXRT_HIP_TUNE_CACHE at a scratch copy of the committed plan (or of `source`; the
+    runtime rewrites the file it is given after a measuring load).  Returns the scratch path."""
     path = os.path.join(tempfile.mkdtemp(prefix="aexrt_tune_"), "plan.tune")
-    if os.path.exists(TUNE_FILE) and not retune:
-        shutil.copyfile(TUNE_FILE, path)
+    source = source or TUNE_FILE
+    if os.path.exists(source) and not retune:
+        shutil.copyfile(source, path)
         os.environ["AEXRT_HIP_AUTOTUNE"] = "0"
     else:
         os.environ.pop("AEXRT_HIP_AUTOTUNE", None)
@@ -502,6 +503,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--retune", action="store_true", help="measure the kernel plan at load instead of the committed one")
     ap.add_argument("--save-tune-cache", help="write the kernel plan the run used to this file")
+    ap.add_argument("--tune-plan", help="run this kernel plan file instead of the committed one")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="one calibration copy and one profiled forward at --batch, for rocprofv3 --pmc")
     ap.add_argument("--trace-pass", action="store_true", help="--steps graph replays at --batch, for a kernel trace")
@@ -511,7 +513,7 @@ def main() -> int:
         print(json.dumps({"error": "this benchmark runs on exactly one GPU; multi-GPU runs are not part of this "
                                    "build (per-tensor amax would need a batch-wide max-reduce across GPUs)"}))
         return 2
-    plan = use_tune_plan(args.retune)
+    plan = use_tune_plan(args.retune, args.tune_plan)
     if args.pmc_pass:
         return pmc_pass(args.batch)
     if args.trace_pass:
