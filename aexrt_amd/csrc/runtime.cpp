@@ -150,6 +150,7 @@ struct Schedule {
     uint32_t mask = 0;    // bit k: the k-th pair in command order (0 with fuse set: every pair)
     uint32_t chains = 0;  // bit k: the k-th head branch (3x3, 3x3, 1x1) in one launch
     uint32_t dual = 0;    // bit k: ... sharing its launch with the level's other branch
+    int super = 0;        // C2f bottleneck superblocks on: bit 0 fp16 pairs, bit 1 int8 pairs
 };
 
 // Pairs a schedule fuses (bit k: the k-th head pair in command order).
@@ -237,7 +238,7 @@ struct AexrtYoloModel {
     std::vector<CopyJob> copies;
     // C2f bottleneck superblocks (AEXRT_HIP_C2F_SUPERBLOCK=1): their grid
     // barriers' sync words (cleared every run) and the barrier-timeout word
-    bool c2f_superblock = false;
+    uint32_t superblock_mask = 0;  // bit 0: fp16 pairs as superblocks, bit 1: int8 pairs
     uint32_t* pair_sync = nullptr;
     int n_pair_sync = 0;
     uint32_t* pair_err = nullptr;
@@ -605,8 +606,9 @@ int setup_chains(AexrtYoloModel* m) {
 // 3x3 stride-1 SiLU conv C -> C (int8 per-tensor or fp16, 32 <= C <= 128 in
 // steps of 32) whose output only a second such conv of the same arithmetic
 // reads, that second conv taking the first one's input as its fused residual
-// or no residual.  With m->c2f_superblock the pairs are marked (their
-// intermediate is then never stored); returns how many the plan has.
+// or no residual.  The pairs of the arithmetics in m->superblock_mask (bit 0
+// fp16, bit 1 int8) are marked (their intermediate is then never stored);
+// returns the arithmetics the plan has pairs of, as such bits.
 int setup_pairs(AexrtYoloModel* m) {
     const Engine& e = m->eng;
     auto& V = m->vals;
@@ -645,8 +647,9 @@ int setup_pairs(AexrtYoloModel* m) {
             continue;
         if (bs.fused_residual && bs.residual_value != (int)c.inputs[0]) continue;
         if (is_int8_algorithm(cs.algorithm) && !m->roots[x.pl.root].slots_complete) continue;
-        ++n;
-        if (!m->c2f_superblock) continue;
+        const int bit = is_int8_algorithm(cs.algorithm) ? 2 : 1;
+        n |= bit;
+        if (!(m->superblock_mask & (uint32_t)bit)) continue;
         cs.pair_b = cj;
         bs.pair_a = (int)ci;
         V[c.output].elided = true;
@@ -1155,8 +1158,8 @@ void load_tune_cache(AexrtYoloModel* m) {
             m->refined[line.substr(0, tab)] = c;  // a conv's choice measured in the network
         else if (line.compare(0, 9, "schedule ") == 0)
             m->schedules[line.substr(0, tab)] =
-                Schedule{c.kind, c.jn, c.pw, (uint32_t)c.ksw, (uint32_t)c.tr,
-                         (uint32_t)c.tc};  // merge, lanes, fusion, pairs, branches, paired branches
+                Schedule{c.kind, c.jn, c.pw, (uint32_t)c.ksw, (uint32_t)c.tr, (uint32_t)c.tc,
+                         c.cc & 3};  // merge, lanes, fusion, pairs, branches, paired branches, superblocks
         else
             m->tuned[line.substr(0, tab)] = c;
     }
@@ -1173,7 +1176,7 @@ void save_tune_cache(AexrtYoloModel* m) {
         for (const auto& [key, c] : m->tuned) put(key, c);
         for (const auto& [key, c] : m->refined) put(key, c);
         for (const auto& [key, v] : m->schedules)
-            put(key, ConvChoice{v.first, v.second, v.fuse, (int)v.mask, (int)v.chains, (int)v.dual, 0, 0});
+            put(key, ConvChoice{v.first, v.second, v.fuse, (int)v.mask, (int)v.chains, (int)v.dual, v.super, 0});
         if (!f) return;
     }
     std::rename(tmp.c_str(), m->tune_cache.c_str());
@@ -1510,7 +1513,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
     {
         uint32_t* slots = m->slots;
         const int64_t n = int64_t(kSlotStripes) * m->slot_stride;
-        m->steps.push_back(Step{-1, "amax slots clear", [slots, n](hipStream_t s) {
+        m->steps.push_back(Step{-1, "amax slots clear " + std::to_string(n) + " words", [slots, n](hipStream_t s) {
                                     return launch_fill_u32(slots, n, 0u, s);
                                 }});
         m->steps.back().all = true;
@@ -1531,7 +1534,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
         if (npairs > 0) {
             uint32_t* sync = m->pair_sync;
             const int64_t n = (int64_t)npairs * kPairSyncWordsHost;
-            m->steps.push_back(Step{-1, "superblock sync clear", [sync, n](hipStream_t s) {
+            m->steps.push_back(Step{-1, "superblock sync clear " + std::to_string(n) + " words", [sync, n](hipStream_t s) {
                                         return launch_fill_u32(sync, n, 0u, s);
                                     }});
             m->steps.back().all = true;
@@ -2303,7 +2306,8 @@ bool build_model(AexrtYoloModel* m) {
     m->chain_mask = 0;
     const int fusable = fuse_head_1x1(m);
     setup_chains(m);
-    if (const char* v = std::getenv("AEXRT_HIP_C2F_SUPERBLOCK")) m->c2f_superblock = v[0] == '1';
+    // the superblocks start off; the schedule choice turns them on where faster
+    m->superblock_mask = 0;
     setup_pairs(m);
     mark_slot_readers(m);
     // arena
@@ -2511,9 +2515,59 @@ bool build_model(AexrtYoloModel* m) {
             }
         }
     }
+    // C2f bottleneck superblocks (AEXRT_HIP_C2F_SUPERBLOCK=0 / 1: never / always):
+    // per arithmetic, the captured schedule timed with its pairs as superblocks
+    // against the current steps, the faster kept; without measurement the cached
+    // schedule's choice
+    {
+        const char* sb = std::getenv("AEXRT_HIP_C2F_SUPERBLOCK");
+        const int sb_forced = sb && (sb[0] == '0' || sb[0] == '1') ? sb[0] - '0' : -1;
+        m->superblock_mask = 3u;
+        const uint32_t avail = (uint32_t)setup_pairs(m);
+        m->superblock_mask = 0;
+        setup_pairs(m);
+        uint32_t want = 0;
+        if (sb_forced >= 0) want = sb_forced ? avail : 0u;
+        else if (use_cached_sched) want = (uint32_t)cached_sched->second.super & avail;
+        auto rebuild_pairs = [&]() {
+            const int lanes_kept = m->n_lanes;
+            setup_pairs(m);
+            m->n_lanes = 1;
+            if (!build_steps(m, m->copies)) return false;
+            if (m->autotune && !refine_in_context(m)) return false;
+            m->n_lanes = lanes_kept;
+            schedule_steps(m);
+            drop_graph(m);
+            return true;
+        };
+        if (sb_forced < 0 && !use_cached_sched && avail && m->autotune && m->use_graph) {
+            float base = 0.0f;
+            if (!time_schedule(m, &base)) return false;
+            for (uint32_t bit : {1u, 2u}) {
+                if (!(avail & bit)) continue;
+                m->superblock_mask = want | bit;
+                if (!rebuild_pairs()) return false;
+                float ms = 0.0f;
+                if (!time_schedule(m, &ms)) return false;
+                const bool faster = ms < base * 0.995f;
+                if (m->tune_log)
+                    std::fprintf(stderr, "aexrt %s C2f superblocks: %.1f us against %.1f us%s\n",
+                                 bit == 1u ? "fp16" : "int8", ms * 100.0f, base * 100.0f, faster ? " (kept)" : "");
+                if (faster) {
+                    want |= bit;
+                    base = ms;
+                }
+            }
+        }
+        if (m->superblock_mask != want) {
+            m->superblock_mask = want;
+            if (!rebuild_pairs()) return false;
+        }
+    }
     if (m->autotune)
         m->schedules[skey] = Schedule{m->merge_siblings ? 1 : 0, m->n_lanes, m->fuse_mask ? 1 : 0,
-                                      m->fuse_mask == ~0u ? 0u : m->fuse_mask, m->chain_mask, m->chain_dual};
+                                      m->fuse_mask == ~0u ? 0u : m->fuse_mask, m->chain_mask, m->chain_dual,
+                                      (int)m->superblock_mask};
     if (m->tune_log && variants > 1)
         std::fprintf(stderr, "aexrt sibling convs: %s, head 1x1 convs fused: %s (mask %#x)\n",
                      best_merge ? "one launch" : "two launches",

@@ -239,6 +239,14 @@ def analyse(steps, replay, batch: int):
     rec = roofline_record(e["ops"], e["bytes"], e["ms"] / 1e3, PEAK_INT8_OPS if e["int8"] else PEAK_FP16_FLOPS,
                           "TOPS" if e["int8"] else "TFLOP/s")
     rec["traffic"] = measured_traffic(inst, e["labels"], batch)
+    t_ms = trace_launch_ms(inst) if batch == 64 else None
+    if t_ms:
+        # the same algorithmic work over the kernel-trace mean duration (no event boundaries)
+        per = (e["ops"] if rec["bound"] == "mfma" else e["bytes"]) / n
+        ach = per / (t_ms / 1e3) / (1e12 if rec["bound"] == "mfma" else 1e9)
+        rec["trace_avg_launch_ms"] = round(t_ms, 5)
+        rec["achieved_trace"] = round(ach, 1)
+        rec["frac_trace"] = round(ach / rec["peak"], 4)
     rec.update(kernel=inst, launches_per_step=n, ms_per_step=round(e["ms"], 5), avg_launch_ms=round(e["ms"] / n, 5),
                ops_per_launch=e["ops"] // n, algorithmic_bytes_per_launch=e["bytes"] // n,
                layers=[lab.split(" alg=")[0] for lab in e["labels"]])
@@ -256,6 +264,62 @@ def analyse(steps, replay, batch: int):
             "frac_of_layer_rooflines": round(f["roof"] / f["secs"], 4)}
     ranking = sorted(((k, round(v["ms"], 4), len(v["labels"])) for k, v in by_inst.items()), key=lambda t: -t[1])
     return rec, families, ranking
+
+
+def bandwidth_launches(steps, replay):
+    """The HBM-bound launches that are not convs: the amax-slot clear (one fill of the slot words),
+    the 2x nearest upsamples and the fused SPPF pools, each against 8 TB/s with its algorithmic
+    bytes (fp16 tensors read once and written once; the fill writes its words)."""
+    cmds = replay["commands"]
+    groups = {}
+    for label, ms in steps:
+        kind = nbytes = None
+        m = re.match(r"amax slots clear (\d+) words", label) or re.match(r"superblock sync clear (\d+) words", label)
+        if m:
+            kind, nbytes = ("slot clear" if label.startswith("amax") else "superblock sync clear"), int(m.group(1)) * 4
+        elif label.startswith("cmd#") and " RESIZE" in label:
+            n, c, h, w, oh, ow = (int(v) for v in cmds[int(label.split()[0][4:])]["params"][:6])
+            kind, nbytes = "resize 2x nearest", n * c * (h * w + oh * ow) * 2
+        elif label.startswith("cmd#") and " SPPF" in label:
+            n, c, h, w = (int(v) for v in cmds[int(label.split()[0][4:])]["params"][:4])
+            kind, nbytes = "SPPF three 5x5 pools", 4 * n * c * h * w * 2  # one read, three pooled maps written
+        if kind is None:
+            continue
+        g = groups.setdefault(kind, dict(ms=0.0, bytes=0, n=0, layers=[]))
+        g["ms"] += ms
+        g["bytes"] += nbytes
+        g["n"] += 1
+        g["layers"].append(label.split(" alg=")[0])
+    out = []
+    for kind, g in groups.items():
+        gbs = g["bytes"] / (g["ms"] / 1e3) / 1e9
+        out.append({"launch": kind, "launches_per_step": g["n"], "algorithmic_bytes_per_launch": g["bytes"] // g["n"],
+                    "avg_launch_ms": round(g["ms"] / g["n"], 5), "achieved": round(gbs, 1), "unit": "GB/s",
+                    "peak": PEAK_HBM / 1e9, "frac": round(gbs / (PEAK_HBM / 1e9), 4), "layers": g["layers"]})
+    return out
+
+
+TRACE_TABLE = os.path.join(ROOT, "profiles", "kernel_stats_yolov8n320_bs64.md")
+
+
+def trace_launch_ms(instance: str):
+    """Mean duration per launch (ms) of a kernel instance in the committed kernel-trace summary (the
+    rocprofv3 trace of this plan's graph replays), or None."""
+    if not os.path.exists(TRACE_TABLE):
+        return None
+    want = instance.replace(" ", "")
+    with open(TRACE_TABLE) as f:
+        for line in f:
+            cells = [c.strip().strip("`") for c in line.strip().strip("|").split("|")]
+            if len(cells) == 4 and cells[0] and cells[0][0].isalpha():
+                name = cells[0].split("::")[-1].replace(" ", "")
+                # the trace names a template's defaulted trailing arguments too
+                if name == want or name.startswith(want[:-1] + ","):
+                    try:
+                        return float(cells[3]) / 1e3
+                    except ValueError:
+                        return None
+    return None
 
 
 def cpu_model() -> str:
@@ -465,6 +529,18 @@ def configs_bench() -> int:
         emit(f"C3 W8A8 3x3 s2 64->128 @160->80 bs{n}", ms_i8, ops, nb, PEAK_INT8_OPS, c3_int8 * n,
              "oracle W8A8 chain, 1 thread" + ("" if n == 1 else f" (batch 1 time x {n})"),
              {"dtype": "int8", "gpu_includes": "amax pass + conv"})
+        # the command's amax pass on its own: one read of the fp16 input, a few slot words written
+        xin = nhwc(x3[:n])
+        slots = K.new_slots(64, dev, stripes=16)
+        ms_amax = _gpu_ms(lambda: K.amax_slots(xin, slots))
+        amax_bytes = n * 64 * 160 * 160 * 2
+        gbs = amax_bytes / (ms_amax / 1e3) / 1e9
+        rec = {"config": f"C3 W8A8 amax pass (a1) 64x160x160 bs{n}", "gpu_ms": round(ms_amax, 5),
+               "algorithmic_bytes": amax_bytes, "achieved": round(gbs, 1), "unit": "GB/s",
+               "peak": PEAK_HBM / 1e9, "frac": round(gbs / (PEAK_HBM / 1e9), 4),
+               "kernel": "amax_slots_nhwc_kernel", "dtype": "fp16 in"}
+        out.append(rec)
+        print(json.dumps(rec), flush=True)
         ms_f = fp16_conv(n, 64, 160, 160, 128, 3, 2, x3[:n], w3, b3)
         ops, nb = conv_work(d3, False)
         emit(f"C3 fp16 3x3 s2 64->128 @160->80 bs{n}", ms_f, ops, nb, PEAK_FP16_FLOPS, c3_fp16 * n,
@@ -480,15 +556,19 @@ def configs_bench() -> int:
     c4 = _cpu_ms(lambda: ON.run_graph(g4, x4, threads=1), reps=3)
     ops4 = sum(conv_work(c["params"], False)[0] for c in E.lower_graph(g4)["commands"] if c["kind"].startswith("CONV"))
     bytes4 = 128 * 40 * 40 * 2 * 2
-    for wino in (False, True):
+    for wino in (False, True, "superblock"):
+        if wino == "superblock":
+            os.environ["AEXRT_HIP_C2F_SUPERBLOCK"] = "1"
         with NativeHipYoloModel(data4) as m:
-            if wino:
+            os.environ.pop("AEXRT_HIP_C2F_SUPERBLOCK", None)
+            if wino is True:
                 for info in m.conv_plan():
                     if info["desc"][7] == 3 and 40 in info["candidates"]:
                         m.override_conv_algorithm(info["command_index"], 40)
             m.run(x4)
             ms4 = _gpu_ms(lambda: m.run_device(), reps=100)
-        emit(f"C4 C2f fp16 @40x40 bs1 ({'Winograd F(2x2,3x3)' if wino else 'direct'} 3x3)", ms4, ops4, bytes4,
+        form = {False: "direct 3x3", True: "Winograd F(2x2,3x3) 3x3", "superblock": "bottleneck superblocks"}[wino]
+        emit(f"C4 C2f fp16 @40x40 bs1 ({form})", ms4, ops4, bytes4,
              PEAK_FP16_FLOPS, c4, "oracle network (fp16-stored values), 1 thread",
              {"dtype": "fp16", "gpu_includes": "the whole block (6 convs) as one engine, graph replay"})
     return 0
@@ -536,6 +616,7 @@ def main() -> int:
         results[bs] = dict(ms=ms, ips=bs / (ms / 1e3), steps=steps, graph=g, model=model, replay=replay)
     big = results[args.batch]
     roof, families, ranking = analyse(big["steps"], big["replay"], args.batch)
+    bw = bandwidth_launches(big["steps"], big["replay"])
     i8 = families.get("int8_convs", {})
     line = {
         "metric": "YOLOv8n-320 W8A8 images/s (bs1, bs64); int8 conv TOPS vs MFMA peak",
@@ -562,6 +643,7 @@ def main() -> int:
         "roofline": roof,
         "families": families,
         "kernel_ranking_ms_per_step": ranking[:8],
+        "bandwidth_bound_launches": bw,
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(results[1]["graph"])
