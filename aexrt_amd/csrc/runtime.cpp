@@ -1259,6 +1259,15 @@ bool tune_conv(AexrtYoloModel* m, ConvParams& p, bool int8, std::vector<ConvChoi
 // orders it after that lane's last step too); dependencies on other lanes become
 // event waits.  The captured graph thus has parallel branches (the head's box and
 // class chains, the finest head level beside the rest of the neck).
+// Whether step i must follow the earlier step j: it reads a root j writes,
+// either one touches every root, or both meet in a grid barrier.
+bool step_depends(const Step& i, const Step& j) {
+    bool dep = i.all || j.all || (i.grid_sync && j.grid_sync);
+    for (int r : i.reads)
+        for (int w : j.writes) dep = dep || r == w;
+    return dep;
+}
+
 void schedule_steps(AexrtYoloModel* m) {
     auto& st = m->steps;
     const int nl = std::max(1, std::min(kLanes, m->n_lanes));
@@ -1266,12 +1275,8 @@ void schedule_steps(AexrtYoloModel* m) {
     for (int i = 0; i < n; ++i) {
         st[i].deps.clear();
         st[i].signal = false;
-        for (int j = i - 1; j >= 0; --j) {
-            bool dep = st[i].all || st[j].all || (st[i].grid_sync && st[j].grid_sync);
-            for (int r : st[i].reads)
-                for (int w : st[j].writes) dep = dep || r == w;
-            if (dep) st[i].deps.push_back(j);
-        }
+        for (int j = i - 1; j >= 0; --j)
+            if (step_depends(st[i], st[j])) st[i].deps.push_back(j);
     }
     int last[kLanes];
     for (int l = 0; l < kLanes; ++l) last[l] = -1;
