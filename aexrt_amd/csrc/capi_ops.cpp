@@ -360,6 +360,46 @@ int aexrt_hip_conv2d(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t f
     return launch_conv(p, algorithm, static_cast<hipStream_t>(stream)) ? 1 : 0;
 }
 
+int aexrt_hip_conv2d_upsample_copy(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t flags,
+                                   const AexrtHipTensorView* x, const void* weight, const float* w_scale,
+                                   const float* bias, const AexrtHipTensorView* y, const AexrtHipTensorView* y_up,
+                                   void* stream) {
+    if (!desc || !x || !y || !y_up || !weight || !bias || !x->data || !y->data || !y_up->data) {
+        set_error("conv2d_upsample_copy: null argument");
+        return 0;
+    }
+    if (!is_int8_algorithm(algorithm) || (flags & (AEXRT_HIP_CONV_INT8_PG16 | AEXRT_HIP_CONV_INT8_DYNAMIC))) {
+        set_error("conv2d_upsample_copy: a per-tensor int8 1x1 conv (algorithm 51/52/53)");
+        return 0;
+    }
+    if (!slot_ref_ok(*y_up) || y_up->c_stride <= 0 || y_up->n_stride <= 0 ||
+        reinterpret_cast<uintptr_t>(y_up->data) % 8) {
+        set_error("conv2d_upsample_copy: bad upsample view");
+        return 0;
+    }
+    std::string why;
+    ConvParams p{};
+    if (!build_conv_params(*desc, algorithm, flags, *x, weight, w_scale, bias, nullptr, *y, nullptr, p, why)) {
+        set_error("conv2d_upsample_copy: " + why);
+        return 0;
+    }
+    p.yup = y_up->data;
+    p.yup_nstride = y_up->n_stride;
+    p.yup_cstride = (int32_t)y_up->c_stride;
+    p.yup_slots = slot_ref(y_up);
+    // the streaming 1x1 kernel: a forced tile, else the first that fits
+    ConvChoice forced;
+    if (!forced_s1x1_choice(forced)) {
+        std::vector<ConvChoice> all(kMaxConvChoices);
+        if (enumerate_conv_choices(p, true, all.data(), kMaxConvChoices) == 0) {
+            set_error("conv2d_upsample_copy: no streaming 1x1 tile fits this conv and view");
+            return 0;
+        }
+        p.choice = all[0];
+    }
+    return launch_conv(p, algorithm, static_cast<hipStream_t>(stream)) ? 1 : 0;
+}
+
 uint32_t aexrt_hip_conv_candidates(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t flags,
                                    const AexrtHipTensorView* x, const AexrtHipTensorView* residual,
                                    const AexrtHipTensorView* y, char* names, uint32_t name_len, uint32_t cap) {

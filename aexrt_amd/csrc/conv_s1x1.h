@@ -23,6 +23,11 @@
 //     so the memory latency of a tile overlaps the previous tile's work, with
 //     one barrier per tile; a launch whose blocks own one tile each gets one
 //     tile buffer (half the LDS, twice the resident blocks for small maps).
+// UP: the epilogue also writes each output value to the 2 x 2 positions of
+// the output's nearest 2x upsample (p.yup, e.g. a channel slice of a concat
+// that a resize of this conv's output used to fill) and folds the block's
+// maxima into that view's slots too: the resize's values and amax without
+// its launch or its re-read of this output.
 // Every iteration issues the same memory operations (the epilogue's stores,
 // then the next tile's loads; out-of-range offsets when there is nothing to
 // do) and the prologue issues an iteration's stores as dropped ones, so the
@@ -45,6 +50,7 @@ struct S1x1Params {
     int wbytes;    // LDS bytes of the block's weights: nks * OCB * 64
     int tbytes;    // LDS bytes of one int8 tile: nks * TP * 64
     FastDiv fd_c16;
+    FastDiv fd_hw, fd_w;  // UP: output positions of an image, columns
 };
 
 namespace s1x1 {
@@ -58,7 +64,7 @@ using igemm::v2i;
 using igemm::xcd_remap;
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-template <int JQ, int PQ, int NP, int EPI>
+template <int JQ, int PQ, int NP, int EPI, bool UP = false>
 __global__ __launch_bounds__(256) void conv1x1_stream_kernel(S1x1Params h) {
     constexpr int OCB = JQ * 16;  // output channels of the block
     constexpr int TP = PQ * 64;   // positions of a tile
@@ -151,7 +157,8 @@ __global__ __launch_bounds__(256) void conv1x1_stream_kernel(S1x1Params h) {
     const bool acc_on = EPI == igemm::kEpiAny && p.acc_out != nullptr;
     const rsrc_t ry = make_rsrc(p.y, p.y_bytes);
     const rsrc_t racc = make_rsrc(p.acc_out, acc_on ? (uint32_t)p.M * (uint32_t)p.OC * 4u : 0u);
-    constexpr int NST = JQ * PQ * (EPI == igemm::kEpiAny ? 2 : 1);  // stores of one tile
+    const rsrc_t ryu = make_rsrc(UP ? p.yup : nullptr, UP ? p.yup_bytes : 0u);
+    constexpr int NST = JQ * PQ * ((EPI == igemm::kEpiAny ? 2 : 1) + (UP ? 4 : 0));  // stores of one tile
     // the stores of an iteration, dropped: both edges into the loop then
     // carry the same memory operations after the first tile's loads
 #pragma unroll
@@ -243,6 +250,23 @@ __global__ __launch_bounds__(256) void conv1x1_stream_kernel(S1x1Params h) {
                     __builtin_memcpy(&o, oh, 8);
                     __builtin_amdgcn_raw_buffer_store_b64(o, ry, ok ? yoff * 2u : kOob, 0, 0);
                 }
+                if constexpr (UP) {
+                    // position m = (n, y, x) -> (n, 2y + dy, 2x + dx), dy, dx in {0, 1}
+                    const uint32_t n = fdiv((uint32_t)m, h.fd_hw);
+                    const uint32_t r = (uint32_t)m - n * (uint32_t)(p.OH * p.OW);
+                    const uint32_t yy = fdiv(r, h.fd_w);
+                    const uint32_t xx = r - yy * (uint32_t)p.OW;
+                    const uint32_t ucs = (uint32_t)p.yup_cstride;
+                    const uint32_t u0 = n * (uint32_t)p.yup_nstride + ((2u * yy) * (2u * p.OW) + 2u * xx) * ucs + oc0;
+                    const uint32_t drow = 2u * p.OW * ucs;
+                    const __half2 uh[2] = {__floats2half2_rn(v[0], v[1]), __floats2half2_rn(v[2], v[3])};
+                    v2i uo;
+                    __builtin_memcpy(&uo, uh, 8);
+                    __builtin_amdgcn_raw_buffer_store_b64(uo, ryu, ok ? u0 * 2u : kOob, 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b64(uo, ryu, ok ? (u0 + ucs) * 2u : kOob, 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b64(uo, ryu, ok ? (u0 + drow) * 2u : kOob, 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b64(uo, ryu, ok ? (u0 + drow + ucs) * 2u : kOob, 0, 0);
+                }
                 if constexpr (EPI == igemm::kEpiAny) {
                     // int32 accumulators (acc_out; a zero-byte view drops them)
                     __builtin_amdgcn_raw_buffer_store_b128(
@@ -260,14 +284,20 @@ __global__ __launch_bounds__(256) void conv1x1_stream_kernel(S1x1Params h) {
     }
 
     igemm::flush_slots<JQ>(p, gmax, n0, jmax, 0xFFFFFFFFu, out_f32, l_slots);
+    if constexpr (UP) {
+        // the upsample holds the same values: the same maxima (l_slots as
+        // reduced above, read by the threads that read them there)
+        if (p.yup_slots.p && tid < jmax && n0 + tid * 16 < p.OC && l_slots[tid])
+            atomicMax(slot_copy(p.yup_slots, blockIdx.x) + (n0 >> 4) + tid, l_slots[tid]);
+    }
 }
 
 // Blocks of one instance the GPU holds at once with lds_bytes of dynamic LDS.
-template <int JQ, int PQ, int NP, int EPI>
+template <int JQ, int PQ, int NP, int EPI, bool UP>
 int s1x1_resident_blocks(int lds_bytes) {
     int per_cu = 0, cus = 0, dev = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv1x1_stream_kernel<JQ, PQ, NP, EPI>, 256,
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv1x1_stream_kernel<JQ, PQ, NP, EPI, UP>, 256,
                                                      (size_t)lds_bytes) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu < 1 ||
         cus < 1)
@@ -277,15 +307,15 @@ int s1x1_resident_blocks(int lds_bytes) {
 
 // Persistent grid: every resident block slot gets one contiguous run of
 // position tiles of one channel tile.
-template <int JQ, int PQ, int NP, int EPI>
+template <int JQ, int PQ, int NP, int EPI, bool UP = false>
 hipError_t s1x1_launch_cfg(S1x1Params h, hipStream_t stream) {
     // one tile buffer when the single-buffer footprint already gives every
     // tile its own resident block
     int lds_bytes = h.wbytes + h.tbytes;
-    int cap = s1x1_resident_blocks<JQ, PQ, NP, EPI>(lds_bytes);
+    int cap = s1x1_resident_blocks<JQ, PQ, NP, EPI, UP>(lds_bytes);
     if ((int64_t)h.ntile * h.c.ntn > cap) {
         lds_bytes = h.wbytes + 2 * h.tbytes;
-        cap = s1x1_resident_blocks<JQ, PQ, NP, EPI>(lds_bytes);
+        cap = s1x1_resident_blocks<JQ, PQ, NP, EPI, UP>(lds_bytes);
     }
     int groups = h.ntile;
     if ((int64_t)h.ntile * h.c.ntn > cap) groups = std::max(1, cap / h.c.ntn);
@@ -293,14 +323,25 @@ hipError_t s1x1_launch_cfg(S1x1Params h, hipStream_t stream) {
     groups = (h.ntile + h.c.per - 1) / h.c.per;
     const int64_t blocks = (int64_t)groups * h.c.ntn;
     if (blocks > INT32_MAX) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((conv1x1_stream_kernel<JQ, PQ, NP, EPI>), dim3((unsigned)blocks), dim3(256),
+    hipLaunchKernelGGL((conv1x1_stream_kernel<JQ, PQ, NP, EPI, UP>), dim3((unsigned)blocks), dim3(256),
                        (size_t)lds_bytes, stream, h);
     return hipGetLastError();
 }
 
-// Every (JQ, PQ, NP) of one epilogue family.
+// Every (JQ, PQ, NP) of one epilogue family; with the upsample copy (up),
+// the one-subtile-per-wave tiles (PQ 1).
 template <int EPI>
-hipError_t s1x1_launch_family(const S1x1Params& h, int jq, int pq, int np, hipStream_t stream) {
+hipError_t s1x1_launch_family(const S1x1Params& h, int jq, int pq, int np, bool up, hipStream_t stream) {
+#define AEXRT_S1X1_UP_CASE(J, N) \
+    if (jq == J && pq == 1 && np == N) return s1x1_launch_cfg<J, 1, N, EPI, true>(h, stream);
+    if (up) {
+        AEXRT_S1X1_UP_CASE(1, 1) AEXRT_S1X1_UP_CASE(1, 2) AEXRT_S1X1_UP_CASE(1, 4) AEXRT_S1X1_UP_CASE(1, 8)
+        AEXRT_S1X1_UP_CASE(2, 1) AEXRT_S1X1_UP_CASE(2, 2) AEXRT_S1X1_UP_CASE(2, 4) AEXRT_S1X1_UP_CASE(2, 8)
+        AEXRT_S1X1_UP_CASE(4, 1) AEXRT_S1X1_UP_CASE(4, 2) AEXRT_S1X1_UP_CASE(4, 4) AEXRT_S1X1_UP_CASE(4, 8)
+        AEXRT_S1X1_UP_CASE(8, 1) AEXRT_S1X1_UP_CASE(8, 2) AEXRT_S1X1_UP_CASE(8, 4) AEXRT_S1X1_UP_CASE(8, 8)
+        return hipErrorInvalidValue;
+    }
+#undef AEXRT_S1X1_UP_CASE
 #define AEXRT_S1X1_CASE(J, P, N) \
     if (jq == J && pq == P && np == N) return s1x1_launch_cfg<J, P, N, EPI>(h, stream);
     AEXRT_S1X1_CASE(1, 1, 1) AEXRT_S1X1_CASE(1, 1, 2) AEXRT_S1X1_CASE(1, 1, 4) AEXRT_S1X1_CASE(1, 1, 8)
@@ -314,8 +355,10 @@ hipError_t s1x1_launch_family(const S1x1Params& h, int jq, int pq, int np, hipSt
     return hipErrorInvalidValue;
 }
 
-#define AEXRT_S1X1_EXTERN(E) extern template hipError_t s1x1_launch_family<E>(const S1x1Params&, int, int, int, hipStream_t);
-#define AEXRT_S1X1_INSTANCE(E) template hipError_t s1x1_launch_family<E>(const S1x1Params&, int, int, int, hipStream_t);
+#define AEXRT_S1X1_EXTERN(E) \
+    extern template hipError_t s1x1_launch_family<E>(const S1x1Params&, int, int, int, bool, hipStream_t);
+#define AEXRT_S1X1_INSTANCE(E) \
+    template hipError_t s1x1_launch_family<E>(const S1x1Params&, int, int, int, bool, hipStream_t);
 
 }  // namespace s1x1
 }  // namespace aexrt

@@ -24,17 +24,21 @@ struct S1x1Tile {
 
 // int8 1x1 stride-1 convs on views whose positions are evenly strided, with
 // the SiLU or run-time-flag epilogue and no residual.
+// An upsample copy (yup) takes an fp16 output and a view of 4x the
+// positions with 8-byte aligned channel groups.
 bool s1x1_shape_ok(const ConvParams& p, bool int8) {
+    const bool up_ok = !p.yup || (!(p.flags & kConvOutF32) && p.yup_cstride % 4 == 0 && p.yup_cstride >= p.OC &&
+                                  p.yup_nstride >= (int64_t)4 * p.OH * p.OW * p.yup_cstride);
     return int8 && p.loader == kLoaderNhwc && p.KH == 1 && p.KW == 1 && p.S == 1 && p.P == 0 && p.OH == p.H &&
            p.OW == p.W && p.C % 16 == 0 && p.x_cstride % 8 == 0 && (p.lin & kLinX) && (p.lin & kLinY) &&
-           !(p.flags & kConvResidual) && p.res == nullptr && p.fuse_1x1 == nullptr && p.M < (1 << 24);
+           !(p.flags & kConvResidual) && p.res == nullptr && p.fuse_1x1 == nullptr && p.M < (1 << 24) && up_ok;
 }
 
-bool s1x1_instantiated(int jq, int pq, int np) {
+bool s1x1_instantiated(int jq, int pq, int np, bool up) {
     if (jq != 1 && jq != 2 && jq != 4 && jq != 8) return false;
     if (np != 1 && np != 2 && np != 4 && np != 8) return false;
     if (pq == 1) return true;
-    return pq == 2 && jq <= 4 && np <= 4;
+    return !up && pq == 2 && jq <= 4 && np <= 4;
 }
 
 // Fills the geometry of tile (jq, pq) into h and the piece count into t.np;
@@ -47,7 +51,7 @@ bool s1x1_geometry(S1x1Params& h, S1x1Tile& t) {
     h.npiece = h.TP * h.c16;
     const int need = (h.npiece + 255) / 256;
     t.np = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : need <= 8 ? 8 : 0;
-    if (!t.np || !s1x1_instantiated(t.jq, t.pq, t.np)) return false;
+    if (!t.np || !s1x1_instantiated(t.jq, t.pq, t.np, p.yup != nullptr)) return false;
     const int64_t ntile = ((int64_t)p.M + h.TP - 1) / h.TP;
     if (ntile > INT32_MAX / 2) return false;
     h.ntile = (int)ntile;
@@ -58,18 +62,22 @@ bool s1x1_geometry(S1x1Params& h, S1x1Tile& t) {
     h.c.ntn = (p.OCp + ocb - 1) / ocb;
     h.c.fd_ntn = make_fastdiv((uint32_t)h.c.ntn);
     h.fd_c16 = make_fastdiv((uint32_t)h.c16);
+    h.fd_hw = make_fastdiv((uint32_t)(p.OH * p.OW));
+    h.fd_w = make_fastdiv((uint32_t)p.OW);
     return true;
 }
 
 std::atomic<int> g_s1x1_force{0};  // jq | pq << 8, 0 = off
 
 hipError_t s1x1_launch(const S1x1Params& h, int epi, const S1x1Tile& t, hipStream_t s) {
+    const bool up = h.c.yup != nullptr;
     if (LaunchProbe* pr = launch_probe()) {
-        std::snprintf(pr->name, sizeof(pr->name), "conv1x1_stream_kernel<%d,%d,%d,%d>", t.jq, t.pq, t.np, epi);
+        std::snprintf(pr->name, sizeof(pr->name), "conv1x1_stream_kernel<%d,%d,%d,%d%s>", t.jq, t.pq, t.np, epi,
+                      up ? ",true" : "");
         return hipSuccess;
     }
-    if (epi == igemm::kEpiSilu) return s1x1::s1x1_launch_family<igemm::kEpiSilu>(h, t.jq, t.pq, t.np, s);
-    if (epi == igemm::kEpiAny) return s1x1::s1x1_launch_family<igemm::kEpiAny>(h, t.jq, t.pq, t.np, s);
+    if (epi == igemm::kEpiSilu) return s1x1::s1x1_launch_family<igemm::kEpiSilu>(h, t.jq, t.pq, t.np, up, s);
+    if (epi == igemm::kEpiAny) return s1x1::s1x1_launch_family<igemm::kEpiAny>(h, t.jq, t.pq, t.np, up, s);
     return hipErrorInvalidValue;
 }
 
@@ -80,7 +88,7 @@ bool set_conv1x1_stream(bool on, int jq, int pq) {
         g_s1x1_force.store(0);
         return true;
     }
-    if (!s1x1_instantiated(jq, pq, 1)) return false;
+    if (!s1x1_instantiated(jq, pq, 1, false)) return false;
     g_s1x1_force.store(jq | (pq << 8));
     return true;
 }
@@ -107,6 +115,7 @@ int enumerate_s1x1_choices(const ConvParams& p, bool int8, ConvChoice* out, int 
     const int ocj = (p.OCp + 15) / 16;
     int n = 0;
     for (int pq : {1, 2}) {
+        if (pq > 1 && p.yup) break;  // the upsample copy runs on one-subtile tiles
         for (int jq : {1, 2, 4, 8}) {
             if (n >= cap) return n;
             if (jq > 1 && jq / 2 >= ocj) continue;  // a channel tile past every channel

@@ -99,6 +99,15 @@ struct ConvParams {
     // the epilogue (its weights, bias, flags and output view; the input view
     // is this conv's output, which is then not stored).  Null: none.
     const struct ConvParams* fuse_1x1 = nullptr;
+    // int8 1x1 convs on the streaming kernel: when yup is set, the output's
+    // nearest 2x upsample (2 OH x 2 OW positions per image, NHWC view of
+    // OC channels, e.g. a channel slice of a concat) is written there too,
+    // and its amax folded into yup_slots.  Null: none.
+    void* yup = nullptr;
+    int64_t yup_nstride = 0;
+    int32_t yup_cstride = 0;
+    SlotRef yup_slots{};
+    uint32_t yup_bytes = 0;  // filled in by the igemm launcher
     // filled in by the igemm launcher
     uint32_t x_bytes = 0, y_bytes = 0, r_bytes = 0;  // byte spans of the views
     uint32_t x_slot_bytes = 0;                       // byte span of the input slots

@@ -239,6 +239,10 @@ struct AexrtYoloModel {
     // C2f bottleneck superblocks (AEXRT_HIP_C2F_SUPERBLOCK=1): their grid
     // barriers' sync words (cleared every run) and the barrier-timeout word
     uint32_t superblock_mask = 0;  // bit 0: fp16 pairs as superblocks, bit 1: int8 pairs
+    // per command: a nearest 2x resize folded into the int8 1x1 conv that
+    // produces its input (the conv's entry names the resize, the resize's
+    // the conv); -1: none
+    std::vector<int> up_fold;
     uint32_t* pair_sync = nullptr;
     int n_pair_sync = 0;
     uint32_t* pair_err = nullptr;
@@ -1131,6 +1135,11 @@ std::string tune_key(const ConvParams& p, bool int8) {
                       (long long)p.fuse_1x1->y_nstride, p.fuse_1x1->y_cstride);
         k += buf;
     }
+    if (p.yup) {
+        // the upsample copy: its view
+        std::snprintf(buf, sizeof(buf), "|u%lld,%d", (long long)p.yup_nstride, p.yup_cstride);
+        k += buf;
+    }
     return k;
 }
 
@@ -1318,9 +1327,9 @@ std::string refined_key(size_t ci, uint32_t alg, const ConvParams& p, bool int8)
 void apply_cached_choice(AexrtYoloModel* m, size_t ci, uint32_t alg, ConvParams& p, bool int8) {
     std::vector<ConvChoice> all(kMaxConvChoices);
     const int na = enumerate_conv_choices(p, int8, all.data(), kMaxConvChoices);
-    // a fused 1x1 runs on the 32x32-MFMA kernel only: without a measured
-    // choice, the first tile that fits
-    if (p.fuse_1x1 && na > 0) p.choice = all[0];
+    // a fused 1x1 runs on the 32x32-MFMA kernel only, an upsample copy on the
+    // streaming 1x1 kernel: without a measured choice, the first tile that fits
+    if ((p.fuse_1x1 || p.yup) && na > 0) p.choice = all[0];
     if (m->tune_cache.empty()) return;
     auto offered = [&](const ConvChoice& c) {
         for (int k = 0; k < na; ++k)
@@ -1333,7 +1342,23 @@ void apply_cached_choice(AexrtYoloModel* m, size_t ci, uint32_t alg, ConvParams&
         return;
     }
     auto tu = m->tuned.find(tune_key(p, int8));
-    if (tu != m->tuned.end() && offered(tu->second)) p.choice = tu->second;
+    if (tu != m->tuned.end() && offered(tu->second)) {
+        p.choice = tu->second;
+        return;
+    }
+    if (p.yup) {
+        // the same conv measured without the upsample copy: its tile, when the
+        // copy's kernel instances include it
+        ConvParams q = p;
+        q.yup = nullptr;
+        auto rq = m->refined.find(refined_key(ci, alg, q, int8));
+        if (rq != m->refined.end() && offered(rq->second)) {
+            p.choice = rq->second;
+            return;
+        }
+        auto tq = m->tuned.find(tune_key(q, int8));
+        if (tq != m->tuned.end() && offered(tq->second)) p.choice = tq->second;
+    }
 }
 
 // Labels of the conv steps name the kernel and tile that runs (it changes as
@@ -1510,11 +1535,40 @@ bool build_pair_step(AexrtYoloModel* m, size_t ci, int k, std::vector<bool>& don
     return true;
 }
 
+// Nearest 2x resizes folded into the int8 1x1 conv that produces their input
+// (AEXRT_HIP_FOLD_UPSAMPLE=0: never): the conv's launch writes the upsample
+// too (ConvParams::yup, the streaming 1x1 kernel), so the resize neither
+// launches nor reads the conv output again.  Candidates here; a conv whose
+// shape and views the kernel does not take keeps its resize (build_steps).
+void setup_upsample_folds(AexrtYoloModel* m) {
+    const Engine& e = m->eng;
+    m->up_fold.assign(e.commands.size(), -1);
+    const char* env = std::getenv("AEXRT_HIP_FOLD_UPSAMPLE");
+    if (env && env[0] == '0') return;
+    for (size_t ci = 0; ci < e.commands.size(); ++ci) {
+        const EngineCommand& c = e.commands[ci];
+        if (c.kind != kCmdResize || c.inputs.empty()) continue;
+        const ValueInfo& x = m->vals[c.inputs[0]];
+        const ValueInfo& o = m->vals[c.output];
+        if (x.producer < 0 || o.N != x.N || o.C != x.C || o.H != 2 * x.H || o.W != 2 * x.W) continue;
+        const int pc = x.producer;
+        const ConvState& cs = m->convs[pc];
+        if (!cs.is_conv || cs.out_value != (int)c.inputs[0] || !is_int8_algorithm(cs.algorithm) || cs.pg16 ||
+            cs.dynamic || cs.fused_residual || cs.pair_a >= 0 || cs.pair_b >= 0 || m->up_fold[pc] >= 0)
+            continue;
+        const AexrtConv2DDesc d = desc_of(e.commands[pc]);
+        if (d.kernel_h != 1 || d.kernel_w != 1 || is_f32(m, cs.out_value) || is_f32(m, c.output)) continue;
+        m->up_fold[pc] = (int)ci;
+        m->up_fold[ci] = pc;
+    }
+}
+
 bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
     Engine& e = m->eng;
     auto& V = m->vals;
     m->steps.clear();
     m->tunables.clear();
+    setup_upsample_folds(m);
     {
         uint32_t* slots = m->slots;
         const int64_t n = int64_t(kSlotStripes) * m->slot_stride;
@@ -1658,6 +1712,23 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                                        pair ? cs.bias_pair : cs.bias, cs.fused_residual ? &rvw : nullptr, yvw, nullptr,
                                        p, why))
                     return fail(m, "command " + std::to_string(ci) + ": " + why);
+                int upv = -1;  // output value of a resize folded into this conv
+                if (m->up_fold[ci] >= 0) {
+                    const EngineCommand& rc = e.commands[m->up_fold[ci]];
+                    const AexrtHipTensorView uv = view_of(m, (int)rc.output);
+                    p.yup = uv.data;
+                    p.yup_nstride = uv.n_stride;
+                    p.yup_cstride = (int32_t)uv.c_stride;
+                    p.yup_slots = slot_ref(uv);
+                    ConvChoice probe[4];
+                    if (own_pass || enumerate_conv_choices(p, int8, probe, 4) == 0) {
+                        p.yup = nullptr;  // the kernel does not take it: the resize runs
+                        m->up_fold[m->up_fold[ci]] = -1;
+                        m->up_fold[ci] = -1;
+                    } else {
+                        upv = (int)rc.output;
+                    }
+                }
                 int f2v = -1;  // output value of a 1x1 conv fused into this conv's epilogue
                 if (cs.fused_1x1 >= 0) {
                     // fused only where a 32x32-MFMA tile holds every output channel of the
@@ -1796,6 +1867,10 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                 if (cs.fused_residual) st.reads.push_back(V[cs.residual_value].pl.root);
                 st.writes = {V[f2v >= 0 ? f2v : yv].pl.root};
                 if (f2v >= 0) st.tail = " then 1x1 cmd#" + std::to_string(e.src_cmd[cs.fused_1x1]);
+                if (upv >= 0) {
+                    st.writes.push_back(V[upv].pl.root);
+                    st.tail = " + 2x upsample cmd#" + std::to_string(e.src_cmd[m->up_fold[ci]]);
+                }
                 if (pair) {
                     done[sib] = true;
                     st.tail = " + cmd#" + std::to_string(e.src_cmd[sib]);
@@ -1870,6 +1945,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                 break;
             }
             case kCmdResize: {
+                if (m->up_fold[ci] >= 0) break;  // written by the conv producing its input
                 const ValueInfo& x = V[c.inputs[0]];
                 const ValueInfo& o = V[c.output];
                 AexrtHipTensorView xv = view_of(m, (int)c.inputs[0]), yv = view_of(m, (int)c.output);

@@ -292,6 +292,18 @@ def conv2d(pc: PreparedConv, x, y, *, flags: int = SILU, x_slots=None, y_slots=N
         _ptr(acc_out), _stream(stream)), "conv2d")
 
 
+def conv2d_upsample_copy(pc: PreparedConv, x, y, y_up, *, flags: int = SILU, x_slots=None, y_slots=None,
+                         y_up_slots=None, stream=None) -> None:
+    """int8 1x1 conv ``pc`` (per-tensor) that also writes its output's nearest 2x upsample into the
+    NHWC view ``y_up`` ([N, 2 OH, 2 OW, OC], e.g. a channel slice of a concat) and folds its amax into
+    ``y_up_slots``: the resize after the conv, in the conv's launch."""
+    d = ConvDesc.from_params(pc.params)
+    xv, yv, uv = view(x, x_slots), view(y, y_slots), view(y_up, y_up_slots)
+    check(_lib.lib().aexrt_hip_conv2d_upsample_copy(
+        ctypes.byref(d), pc.algorithm, flags, ctypes.byref(xv), pc.weight.data_ptr(), _ptr(pc.w_scale),
+        pc.bias.data_ptr(), ctypes.byref(yv), ctypes.byref(uv), _stream(stream)), "conv2d_upsample_copy")
+
+
 def conv2d_fused_1x1(pc: PreparedConv, pc2: PreparedConv, x, y2, *, flags2: int = 0, y2_slots=None,
                      stream=None) -> None:
     """fp16 3x3 SiLU conv ``pc`` with the 1x1 conv ``pc2`` of its output fused into its epilogue:

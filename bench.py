@@ -146,8 +146,16 @@ def launch_work(label: str, replay):
     weight once (the intermediates a launch keeps on chip are neither)."""
     ci, _, int8, _, _ = parse_label(label)
     cmds = replay["commands"]
-    idx = [ci] + [int(m) for m in re.findall(r"cmd#(\d+)", label.split(" kernel=", 1)[1])]
+    tail = label.split(" kernel=", 1)[1]
+    # "+ 2x upsample cmd#R": the launch also writes the nearest 2x upsample of its output (the
+    # resize R it replaces), 4x the output's positions
+    up = re.search(r" \+ 2x upsample cmd#(\d+)", tail)
+    tail = tail[:up.start()] + tail[up.end():] if up else tail
+    idx = [ci] + [int(m) for m in re.findall(r"cmd#(\d+)", tail)]
     ops = nbytes = 0
+    if up:
+        b, _, _, _, oc, oh, ow = (int(v) for v in cmds[ci]["params"][:7])
+        nbytes += b * oc * 4 * oh * ow * 2
     produced = {cmds[i]["output"] for i in idx}
     consumed = {cmds[i]["inputs"][0] for i in idx}
     inputs_seen = set()

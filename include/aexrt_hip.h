@@ -192,6 +192,22 @@ int aexrt_hip_conv2d(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t f
                      const float* bias, const AexrtHipTensorView* residual,
                      const AexrtHipTensorView* y, int32_t* acc_out, void* stream);
 
+/* An int8 1x1 conv (algorithm 51/52/53, per-tensor, the arguments of
+ * aexrt_hip_conv2d without residual and accumulators) that also writes the
+ * nearest 2x upsample of its fp16 output into y_up (2 OH x 2 OW positions per
+ * image, OC channels: e.g. the channel slice of a concat that a resize of y
+ * used to fill) and folds its amax into y_up's slots.  Replaces the
+ * reference's RESIZE command on a conv output (src/aexrt/yolo.py:830-834;
+ * the nearest resize shader native/aexrt_d3d12_runtime.cpp:14851-14872, which
+ * reads y again and writes y_up) with stores in the conv's own launch.
+ * Runs on the streaming 1x1 kernel (a tile forced with
+ * aexrt_hip_set_conv1x1_stream, else the first that fits); 0 with a
+ * diagnostic when none fits (fp32 output, views). */
+int aexrt_hip_conv2d_upsample_copy(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t flags,
+                                   const AexrtHipTensorView* x, const void* weight, const float* w_scale,
+                                   const float* bias, const AexrtHipTensorView* y, const AexrtHipTensorView* y_up,
+                                   void* stream);
+
 /* The kernel and tile candidates the model loader measures for one conv
  * (no reference counterpart; the tile-level analogue of the algorithm
  * candidates of aexrt_yolo_conv_plan_info, native/aexrt.h:435-445, and of

@@ -222,6 +222,42 @@ def test_yolov8n_320_w8a8_superblocks_equal_separate_convs(cuda, monkeypatch, tm
     assert err <= allowed, (err, allowed)
 
 
+@pytest.mark.parametrize("batch", [1, 64])
+def test_yolov8n_320_w8a8_upsample_folded_into_its_conv(cuda, monkeypatch, tmp_path, batch):
+    """The neck's two nearest 2x upsamples written by the int8 1x1 convs that produce their inputs
+    (no resize launch, aexrt_hip_conv2d_upsample_copy) against the network with the resize kernels:
+    every stored value (conv outputs, the upsamples in their concat slices, the concats) and the
+    network output bit for bit, on the bench's kernel plan.  The producing convs run the same tile
+    with or without the copy."""
+    _use_bench_plan(monkeypatch, tmp_path)
+    g, names, plan, data = _yolo_engine(batch, 320)
+    x = np.random.default_rng(4).random((batch, 3, 320, 320)).astype(np.float32)
+    outs = []
+    for on in ("0", "1"):
+        monkeypatch.setenv("AEXRT_HIP_FOLD_UPSAMPLE", on)
+        with NativeHipYoloModel(data) as m:
+            m.set_profiling(True)
+            m.run(x)
+            labels = [lab for lab, _ in m.profile_events()]
+            m.set_profiling(False)
+            folded = [lab for lab in labels if "2x upsample" in lab]
+            resizes = [lab for lab in labels if lab.endswith("RESIZE")]
+            assert (len(folded), len(resizes)) == ((2, 0) if on == "1" else (0, 2)), labels
+            m.run(x)
+            out = m.output()
+            stored = {}
+            for i, c in enumerate(plan["replay"]["commands"]):
+                if c["kind"] in ("CONV", "CONV_SILU", "BINARY", "RESIZE", "CONCAT", "MAXPOOL") and \
+                        m.value_info(c["output"])[0] == 4:
+                    stored[i] = m.value(c["output"])
+            outs.append((out, stored))
+    (o0, s0), (o1, s1) = outs
+    assert set(s0) == set(s1) and len(s0) >= 40
+    for i in sorted(s0):
+        np.testing.assert_array_equal(s1[i], s0[i], err_msg=f"command {i} ({plan['replay']['commands'][i]['kind']})")
+    np.testing.assert_array_equal(o1, o0)
+
+
 @pytest.mark.parametrize("batch", [1, 3])
 def test_c2f_w8a8_block_layer_parity(cuda, batch):
     g = _c2f_graph(batch=batch, c=64, dim=20, seed=5)

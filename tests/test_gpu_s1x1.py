@@ -119,3 +119,84 @@ def test_s1x1_rejects_tiles_without_instance(cuda):
     with pytest.raises(RuntimeError, match="set_conv1x1_stream"):
         K.set_conv1x1_stream(True, 8, 2)
     K.set_conv1x1_stream(False)
+
+
+# (n, c, h, w, oc, upsample root width, channel offset there, jq or 0 for the first fitting tile, seed)
+S1X1_UPSAMPLE = [
+    (2, 192, 20, 20, 128, 192, 0, 4, 431),   # YOLO's top-down path at 20x20: 128 of the 192 concat channels
+    (3, 512, 10, 10, 256, 384, 0, 4, 432),   # SPPF's conv at 10x10 feeding a 384-channel concat
+    (2, 64, 7, 9, 32, 96, 48, 0, 433),       # ragged tail, a slice at a channel offset, first tile that fits
+    (1, 32, 5, 6, 16, 16, 0, 1, 434),        # one 16-channel group, dense upsample view
+]
+
+
+@pytest.mark.parametrize("case", S1X1_UPSAMPLE,
+                         ids=[f"n{t[0]}_c{t[1]}_{t[2]}x{t[3]}_oc{t[4]}_up{t[5]}at{t[6]}_jq{t[7]}" for t in S1X1_UPSAMPLE])
+def test_s1x1_upsample_copy_equals_resize(cuda, case):
+    """The conv with its output's nearest 2x upsample written in the same launch
+    (aexrt_hip_conv2d_upsample_copy): y bit-identical to the plain conv's, the upsample
+    view bit-identical to the resize kernel's output of y (the reference's RESIZE), its slots
+    equal to the resize's, and the rest of the upsample root untouched."""
+    import torch
+
+    n, c, h, w, oc, uw, u0, jq, seed = case
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((n, c, h, w)).astype(np.float16).astype(np.float32)
+    wt = group16_weight(rng, oc, c, 1)
+    b = packing.fp16_round(rng.uniform(-0.1, 0.1, oc).astype(np.float32))
+    desc = O.conv_desc(n, c, h, w, oc, 1, 1, 0)
+    pc = K.prepare_conv(desc, 51, K.SRC_LAYOUT_INT8, packing.pack_conv_int8(wt, fp16_engine=True), b, device=cuda)
+    xd = torch.from_numpy(nchw_to_nhwc(x.astype(np.float16))).to(cuda)
+    xs = K.new_slots(c, cuda, stripes=16)
+    K.amax_slots(xd, xs)
+    # the plain conv, then the resize kernel into a root of the same layout
+    y_ref = torch.empty((n, h, w, oc), dtype=torch.float16, device=cuda)
+    ys_ref = K.new_slots(oc, cuda, stripes=16)
+    if jq:
+        K.set_conv1x1_stream(True, jq, 1)
+    try:
+        K.conv2d(pc, xd, y_ref, flags=K.SILU, x_slots=xs, y_slots=ys_ref)
+        up_ref = torch.full((n, 2 * h, 2 * w, uw), 5.0, dtype=torch.float16, device=cuda)
+        us_ref = K.new_slots(uw, cuda, stripes=16)
+        K.resize_nearest(y_ref, up_ref[..., u0:u0 + oc], y_slots=us_ref[:, u0 // 16:(u0 + oc) // 16])
+        # the conv with the upsample copy
+        y = torch.empty_like(y_ref)
+        ys = K.new_slots(oc, cuda, stripes=16)
+        up = torch.full_like(up_ref, 5.0)
+        us = K.new_slots(uw, cuda, stripes=16)
+        K.conv2d_upsample_copy(pc, xd, y, up[..., u0:u0 + oc], x_slots=xs, y_slots=ys,
+                               y_up_slots=us[:, u0 // 16:(u0 + oc) // 16])
+        torch.cuda.synchronize()
+    finally:
+        K.set_conv1x1_stream(False)
+    if jq:
+        # the same tile on both sides: the same kernel arithmetic, bit for bit
+        assert torch.equal(y, y_ref)
+        assert torch.equal(up, up_ref)
+        np.testing.assert_array_equal(_u32(ys).max(axis=0), _u32(ys_ref).max(axis=0))
+        np.testing.assert_array_equal(_u32(us).max(axis=0), _u32(us_ref).max(axis=0))
+    # against the oracle: y within one fp16 ulp; the upsample is y repeated 2 x 2 bit for bit, with
+    # the max |y| of each group in its slots, and the rest of its root untouched
+    _, _, _, _, _, yo = O.w8a8_conv(x, wt, b, desc, silu=True, fp16_engine=True)
+    got = nhwc_to_nchw(y.float().cpu().numpy())
+    assert (np.abs(got.astype(np.float64) - yo) <= _ulp16(yo)).all()
+    upn = up.float().cpu().numpy()
+    np.testing.assert_array_equal(upn[..., u0:u0 + oc], np.repeat(np.repeat(nchw_to_nhwc(got), 2, axis=1), 2, axis=2))
+    assert (upn[..., :u0] == 5.0).all() and (upn[..., u0 + oc:] == 5.0).all()
+    np.testing.assert_array_equal(_u32(us).max(axis=0)[u0 // 16:(u0 + oc) // 16], _slots_of(got, oc))
+
+
+def test_s1x1_upsample_copy_refuses_fp32_output(cuda):
+    import torch
+
+    desc = O.conv_desc(1, 32, 4, 4, 16, 1, 1, 0)
+    rng = np.random.default_rng(1)
+    pc = K.prepare_conv(desc, 51, K.SRC_LAYOUT_INT8,
+                        packing.pack_conv_int8(group16_weight(rng, 16, 32, 1), fp16_engine=True),
+                        np.zeros(16, np.float32), device=cuda)
+    x = torch.zeros((1, 4, 4, 32), dtype=torch.float16, device=cuda)
+    xs = K.new_slots(32, cuda)
+    y = torch.zeros((1, 4, 4, 16), dtype=torch.float32, device=cuda)
+    up = torch.zeros((1, 8, 8, 16), dtype=torch.float16, device=cuda)
+    with pytest.raises(RuntimeError, match="conv2d_upsample_copy"):
+        K.conv2d_upsample_copy(pc, x, y, up, flags=K.OUT_F32, x_slots=xs)

@@ -108,6 +108,17 @@ def test_committed_plan_loads_runs_and_closes(stub, batch):
     convs = _conv_labels(res)
     assert len(convs) > 40
     assert all(" kernel=" in lab for lab in convs if "CONV" in lab)
+    # the neck's two 2x upsamples are written by the convs producing their inputs
+    folded = [lab for lab in convs if "+ 2x upsample" in lab]
+    assert len(folded) == 2 and all("conv1x1_stream_kernel<" in lab and ",true>" in lab for lab in folded)
+    assert not any(lab.endswith("RESIZE") for lab in convs)
+
+
+def test_upsample_fold_can_be_switched_off(stub):
+    res = _run({"batch": 64, "env": {"AEXRT_HIP_FOLD_UPSAMPLE": "0"}})
+    convs = _conv_labels(res)
+    assert sum(lab.endswith("RESIZE") for lab in convs) == 2
+    assert not any("2x upsample" in lab for lab in convs)
 
 
 def test_load_time_tuning_writes_a_plan_that_reloads(stub, tmp_path):
@@ -128,8 +139,12 @@ def test_forced_superblocks_build_one_launch_per_bottleneck(stub):
     assert fp16["superblocks"] == 2
 
 
-@pytest.mark.skipif(not ASAN_LIB.exists() or _asan_runtime() is None,
-                    reason="host-ASan library not built (make -C aexrt_amd/csrc asan)")
+def _asan_current():
+    return ASAN_LIB.exists() and LIB.exists() and ASAN_LIB.stat().st_mtime >= LIB.stat().st_mtime
+
+
+@pytest.mark.skipif(not _asan_current() or _asan_runtime() is None,
+                    reason="host-ASan library not built, or older than libaexrt_hip.so (make -C aexrt_amd/csrc asan)")
 def test_host_paths_under_address_sanitizer(stub, tmp_path):
     _run({"batch": 64}, asan=True)
     _run({"batch": 64, "plan": str(tmp_path / "plan.tune")}, asan=True)
