@@ -400,6 +400,58 @@ int aexrt_hip_conv2d_upsample_copy(const AexrtConv2DDesc* desc, uint32_t algorit
     return launch_conv(p, algorithm, static_cast<hipStream_t>(stream)) ? 1 : 0;
 }
 
+int aexrt_hip_conv2d_upsampled_input(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t flags,
+                                     const AexrtHipTensorView* x, const AexrtHipTensorView* x_up, uint32_t up_c0,
+                                     uint32_t up_channels, const void* weight, const float* w_scale,
+                                     const float* bias, const AexrtHipTensorView* y, int32_t* acc_out, void* stream) {
+    if (!desc || !x || !x_up || !y || !weight || !bias || !x->data || !x_up->data || !y->data) {
+        set_error("conv2d_upsampled_input: null argument");
+        return 0;
+    }
+    if (!is_int8_algorithm(algorithm) || (flags & (AEXRT_HIP_CONV_INT8_PG16 | AEXRT_HIP_CONV_INT8_DYNAMIC))) {
+        set_error("conv2d_upsampled_input: a per-tensor int8 1x1 conv (algorithm 51/52/53)");
+        return 0;
+    }
+    if (!slot_ref_ok(*x_up) || !x_up->amax_slots || x_up->c_stride <= 0 || x_up->n_stride <= 0 ||
+        reinterpret_cast<uintptr_t>(x_up->data) % 16 || up_channels == 0 || up_channels % 16 || up_c0 % 16) {
+        set_error("conv2d_upsampled_input: bad source view (16-byte aligned, amax slots, 16-channel groups)");
+        return 0;
+    }
+    std::string why;
+    ConvParams p{};
+    if (!build_conv_params(*desc, algorithm, flags, *x, weight, w_scale, bias, nullptr, *y, acc_out, p, why)) {
+        set_error("conv2d_upsampled_input: " + why);
+        return 0;
+    }
+    {
+        // the kernel reads both views through one 32-bit buffer resource
+        const uintptr_t xa = reinterpret_cast<uintptr_t>(x->data), ua = reinterpret_cast<uintptr_t>(x_up->data);
+        const uintptr_t xe = xa + (uintptr_t)(desc->batch * x->n_stride) * 2;
+        const uintptr_t ue = ua + (uintptr_t)(desc->batch * x_up->n_stride) * 2;
+        if (std::max(xe, ue) - std::min(xa, ua) > 0xFFFFFFF0ull) {
+            set_error("conv2d_upsampled_input: x and x_up must lie within one 4 GB span (e.g. one arena)");
+            return 0;
+        }
+    }
+    p.xup = x_up->data;
+    p.xup_nstride = x_up->n_stride;
+    p.xup_cstride = (int32_t)x_up->c_stride;
+    p.xup_c0 = (int32_t)up_c0;
+    p.xup_cn = (int32_t)up_channels;
+    p.xup_slots = slot_ref(x_up);
+    p.xup_nslots = (int32_t)(up_channels / 16);
+    ConvChoice forced;
+    if (!forced_s1x1_choice(forced)) {
+        std::vector<ConvChoice> all(kMaxConvChoices);
+        if (enumerate_conv_choices(p, true, all.data(), kMaxConvChoices) == 0) {
+            set_error("conv2d_upsampled_input: no streaming 1x1 tile fits this conv and its source");
+            return 0;
+        }
+        p.choice = all[0];
+    }
+    return launch_conv(p, algorithm, static_cast<hipStream_t>(stream)) ? 1 : 0;
+}
+
 uint32_t aexrt_hip_conv_candidates(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t flags,
                                    const AexrtHipTensorView* x, const AexrtHipTensorView* residual,
                                    const AexrtHipTensorView* y, char* names, uint32_t name_len, uint32_t cap) {

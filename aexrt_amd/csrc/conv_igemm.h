@@ -138,11 +138,27 @@ __device__ __forceinline__ void in_slot_loads(const ConvParams& p, int lane, uin
             rs, e < tot ? ((uint32_t)c * p.x_slots.stride + (uint32_t)(e - c * ns)) * 4u : kOob, 0, 0);
     }
 }
+// Slot words of an upsampled input source (ConvParams::xup): up to
+// kMaxUpSlotReads (stripes x groups), spread over the lanes as above.
+constexpr int kMaxUpSlotReads = 256;
+__device__ __forceinline__ void up_slot_loads(const ConvParams& p, uint32_t slot_bytes, FastDiv fd_ns, int lane,
+                                              uint32_t (&raw)[kMaxUpSlotReads / 64]) {
+    const rsrc_t rs = make_rsrc(p.xup_slots.p, slot_bytes);
+    const int ns = p.xup_nslots;
+    const int tot = (int)p.xup_slots.stripes * ns;
+#pragma unroll
+    for (int r = 0; r < kMaxUpSlotReads / 64; ++r) {
+        const int e = lane + r * 64;
+        const int c = (int)fdiv((uint32_t)e, fd_ns);
+        raw[r] = __builtin_amdgcn_raw_buffer_load_b32(
+            rs, e < tot ? ((uint32_t)c * p.xup_slots.stride + (uint32_t)(e - c * ns)) * 4u : kOob, 0, 0);
+    }
+}
 // s_q = 127 / amax (quantizer), in_scale = amax / 127 (dequant); both 0 for
 // an all-zero input, whose quantized values are then all 0.
 __device__ __forceinline__ void in_slot_scale(const uint32_t (&raw)[kMaxSlotReads / 64], float& s_q,
-                                              float& in_scale) {
-    uint32_t am = 0;
+                                              float& in_scale, uint32_t also = 0u) {
+    uint32_t am = also;  // also: slot words of further input channels this lane read
 #pragma unroll
     for (int r = 0; r < kMaxSlotReads / 64; ++r) am = max(am, raw[r]);
     const float a_max = u2f(wave_umax(am));

@@ -122,7 +122,7 @@ int enumerate_conv_choices(const ConvParams& p, bool int8, ConvChoice* out, int 
     // a fused 1x1 runs only in the 32x32-MFMA kernel's epilogue
     if (p.fuse_1x1) return p.loader == kLoaderNhwc ? enumerate_m32_choices(p, int8, out, cap) : 0;
     // an upsample copy of the output: the streaming 1x1 kernel only
-    if (p.yup) return int8 && p.KH == 1 && p.KW == 1 ? enumerate_s1x1_choices(p, int8, out, cap) : 0;
+    if (p.yup || p.xup) return int8 && p.KH == 1 && p.KW == 1 ? enumerate_s1x1_choices(p, int8, out, cap) : 0;
     int n = 0;
     const bool nchw = p.loader == kLoaderNchwF32;
     if (!nchw && p.Kp / 64 <= igemm::kMaxSteps) {
@@ -171,7 +171,8 @@ hipError_t launch_conv_igemm(const ConvParams& p0, bool int8, hipStream_t stream
                                        p0.fuse_1x1 ? (uint64_t)p0.fuse_1x1->y_nstride *
                                                          ((p0.fuse_1x1->flags & kConvOutF32) ? 4 : 2)
                                                    : 0,
-                                       p0.yup ? (uint64_t)p0.yup_nstride * 2 : 0});
+                                       p0.yup ? (uint64_t)p0.yup_nstride * 2 : 0,
+                                       p0.xup ? (uint64_t)p0.xup_nstride * 2 : 0});
     if ((uint64_t)p0.OCp * p0.Kp * 2 > kMaxViewBytes || per_img == 0) return hipErrorInvalidValue;
     const int per_launch = (int)std::min<uint64_t>((uint64_t)p0.N, kMaxViewBytes / per_img);
     if (per_launch < 1) return hipErrorInvalidValue;
@@ -190,7 +191,8 @@ hipError_t launch_conv_igemm(const ConvParams& p0, bool int8, hipStream_t stream
     if (p0.fuse_1x1 && (p0.choice.kind != 5 || int8)) return hipErrorInvalidValue;
     // the upsample copy: a streaming 1x1 choice (measured, or forced)
     ConvChoice forced_up;
-    if (p0.yup && !(int8 && (p0.choice.kind == 6 || (p0.choice.kind == 0 && forced_s1x1_choice(forced_up)))))
+    if ((p0.yup || p0.xup) &&
+        !(int8 && (p0.choice.kind == 6 || (p0.choice.kind == 0 && forced_s1x1_choice(forced_up)))))
         return hipErrorInvalidValue;
     for (int nb = 0; nb < p0.N; nb += per_launch) {
         ConvParams p = p0;
@@ -216,6 +218,10 @@ hipError_t launch_conv_igemm(const ConvParams& p0, bool int8, hipStream_t stream
         if (p0.yup) {
             p.yup = static_cast<__half*>(p0.yup) + (int64_t)nb * p0.yup_nstride;
             p.yup_bytes = (uint32_t)view_span(p.N, p.yup_nstride, p.yup_cstride, 4 * HWo, p.OC, 2);
+        }
+        if (p0.xup) {
+            p.xup = static_cast<const __half*>(p0.xup) + (int64_t)nb * p0.xup_nstride;
+            p.xup_bytes = (uint32_t)view_span(p.N, p.xup_nstride, p.xup_cstride, HWi / 4, p.xup_cn, 2);
         }
         p.x_bytes = nchw ? (uint32_t)((uint64_t)p.N * p.x_nstride * 4)
                          : (uint32_t)view_span(p.N, p.x_nstride, p.x_cstride, HWi, p.C, 2);

@@ -28,6 +28,11 @@
 // that a resize of this conv's output used to fill) and folds the block's
 // maxima into that view's slots too: the resize's values and amax without
 // its launch or its re-read of this output.
+// XUP: the input pieces of channels [xup_c0, xup_c0 + xup_cn) are loaded
+// from p.xup at the position's (y / 2, x / 2): the conv reads a nearest 2x
+// upsample (a concat slice a resize would fill) straight from its source,
+// through one buffer resource over both views (xbase, byte offsets x_off0,
+// xup_off0); the source's amax slots are read with the input's.
 // Every iteration issues the same memory operations (the epilogue's stores,
 // then the next tile's loads; out-of-range offsets when there is nothing to
 // do) and the prologue issues an iteration's stores as dropped ones, so the
@@ -50,7 +55,12 @@ struct S1x1Params {
     int wbytes;    // LDS bytes of the block's weights: nks * OCB * 64
     int tbytes;    // LDS bytes of one int8 tile: nks * TP * 64
     FastDiv fd_c16;
-    FastDiv fd_hw, fd_w;  // UP: output positions of an image, columns
+    FastDiv fd_hw, fd_w;  // UP, XUP: positions of an image, columns
+    // XUP: one resource over the input and the upsampled source
+    const void* xbase;
+    uint32_t xspan, x_off0, xup_off0;
+    uint32_t xup_slot_bytes;
+    FastDiv fd_uns;
 };
 
 namespace s1x1 {
@@ -64,7 +74,7 @@ using igemm::v2i;
 using igemm::xcd_remap;
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-template <int JQ, int PQ, int NP, int EPI, bool UP = false>
+template <int JQ, int PQ, int NP, int EPI, bool UP = false, bool XUP = false>
 __global__ __launch_bounds__(256) void conv1x1_stream_kernel(S1x1Params h) {
     constexpr int OCB = JQ * 16;  // output channels of the block
     constexpr int TP = PQ * 64;   // positions of a tile
@@ -92,12 +102,14 @@ __global__ __launch_bounds__(256) void conv1x1_stream_kernel(S1x1Params h) {
     const int ntl = min(p.per, h.ntile - pt0);
     const int jmax = min(JQ, (p.OCp - n0) >> 4);
 
-    const rsrc_t rx = make_rsrc(p.x, p.x_bytes);
+    const rsrc_t rx = XUP ? make_rsrc(h.xbase, h.xspan) : make_rsrc(p.x, p.x_bytes);
     const rsrc_t rw = make_rsrc(p.w, (uint32_t)p.OCp * (uint32_t)p.Kp);
 
     // ---- prologue loads: input scale, per-channel constants ----------------
     uint32_t slot_raw[igemm::kMaxSlotReads / 64];
     igemm::in_slot_loads(p, lane, slot_raw);
+    uint32_t up_raw[XUP ? igemm::kMaxUpSlotReads / 64 : 1];
+    if constexpr (XUP) igemm::up_slot_loads(p, h.xup_slot_bytes, h.fd_uns, lane, up_raw);
     const rsrc_t rb = make_rsrc(p.bias, (uint32_t)p.OC * 4u);
     const rsrc_t rsc = make_rsrc(p.w_scale, (uint32_t)p.OC * 4u);
     const uint32_t cofs = tid < OCB && n0 + tid < p.OC ? (uint32_t)(n0 + tid) * 4u : kOob;
@@ -110,14 +122,19 @@ __global__ __launch_bounds__(256) void conv1x1_stream_kernel(S1x1Params h) {
     int ppos[NP];
     uint32_t poff[NP];
     int plds[NP];
+    uint32_t pup[XUP ? NP : 1];  // XUP: the piece's channel in the source, ~0 for the input's own
 #pragma unroll
     for (int k = 0; k < NP; ++k) {
         const int e = tid + k * 256;
         const int pos = (int)fdiv((uint32_t)e, h.fd_c16);
         const int c = e - pos * h.c16;
         ppos[k] = e < h.npiece ? pos : 0x40000000;  // past every tile's last position
-        poff[k] = ((uint32_t)pos * (uint32_t)p.x_cstride + (uint32_t)c * 16u) * 2u;
+        poff[k] = (XUP ? h.x_off0 : 0u) + ((uint32_t)pos * (uint32_t)p.x_cstride + (uint32_t)c * 16u) * 2u;
         plds[k] = ((c >> 2) * TP + pos) * 64 + (((c & 3) ^ ((pos >> 2) & 3)) << 4);
+        if constexpr (XUP) {
+            const int cu = c * 16 - p.xup_c0;
+            pup[k] = cu >= 0 && cu < p.xup_cn ? (uint32_t)cu : 0xFFFFFFFFu;
+        }
     }
     v4i pf[NP][2];
     // all loads of tile tl (out of range when !live or past the map)
@@ -126,8 +143,21 @@ __global__ __launch_bounds__(256) void conv1x1_stream_kernel(S1x1Params h) {
         const uint32_t base = (uint32_t)m0 * (uint32_t)p.x_cstride * 2u;
 #pragma unroll
         for (int k = 0; k < NP; ++k) {
-            const bool ok = live && m0 + ppos[k] < p.M;
-            const uint32_t off = ok ? base + poff[k] : kOob;
+            const int m = m0 + ppos[k];
+            const bool ok = live && m < p.M;
+            uint32_t off = base + poff[k];
+            if constexpr (XUP) {
+                // position m = (n, y, x) of the input -> (n, y / 2, x / 2) of the source
+                const uint32_t n = fdiv((uint32_t)m, h.fd_hw);
+                const uint32_t r = (uint32_t)m - n * (uint32_t)(p.H * p.W);
+                const uint32_t yy = fdiv(r, h.fd_w);
+                const uint32_t xx = r - yy * (uint32_t)p.W;
+                const uint32_t uo = h.xup_off0 + (n * (uint32_t)p.xup_nstride +
+                                                  ((yy >> 1) * (uint32_t)(p.W >> 1) + (xx >> 1)) * (uint32_t)p.xup_cstride +
+                                                  pup[k]) * 2u;
+                off = pup[k] != 0xFFFFFFFFu ? uo : off;
+            }
+            off = ok ? off : kOob;
             pf[k][0] = bload16(rx, off);
             pf[k][1] = bload16(rx, off + 16u);
         }
@@ -169,7 +199,12 @@ __global__ __launch_bounds__(256) void conv1x1_stream_kernel(S1x1Params h) {
     // the first tile are needed before the first barrier
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     float s_q = 0.0f, in_scale = 0.0f;
-    igemm::in_slot_scale(slot_raw, s_q, in_scale);
+    uint32_t up_am = 0u;
+    if constexpr (XUP) {
+#pragma unroll
+        for (int r = 0; r < igemm::kMaxUpSlotReads / 64; ++r) up_am = max(up_am, up_raw[r]);
+    }
+    igemm::in_slot_scale(slot_raw, s_q, in_scale, up_am);
     if (tid < OCB) {
         l_bias[tid] = bias_v;
         // dequant factor amax/127 * w_scale[oc] (one fma in the epilogue)
@@ -293,11 +328,11 @@ __global__ __launch_bounds__(256) void conv1x1_stream_kernel(S1x1Params h) {
 }
 
 // Blocks of one instance the GPU holds at once with lds_bytes of dynamic LDS.
-template <int JQ, int PQ, int NP, int EPI, bool UP>
+template <int JQ, int PQ, int NP, int EPI, bool UP, bool XUP>
 int s1x1_resident_blocks(int lds_bytes) {
     int per_cu = 0, cus = 0, dev = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv1x1_stream_kernel<JQ, PQ, NP, EPI, UP>, 256,
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv1x1_stream_kernel<JQ, PQ, NP, EPI, UP, XUP>, 256,
                                                      (size_t)lds_bytes) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu < 1 ||
         cus < 1)
@@ -307,15 +342,15 @@ int s1x1_resident_blocks(int lds_bytes) {
 
 // Persistent grid: every resident block slot gets one contiguous run of
 // position tiles of one channel tile.
-template <int JQ, int PQ, int NP, int EPI, bool UP = false>
+template <int JQ, int PQ, int NP, int EPI, bool UP = false, bool XUP = false>
 hipError_t s1x1_launch_cfg(S1x1Params h, hipStream_t stream) {
     // one tile buffer when the single-buffer footprint already gives every
     // tile its own resident block
     int lds_bytes = h.wbytes + h.tbytes;
-    int cap = s1x1_resident_blocks<JQ, PQ, NP, EPI, UP>(lds_bytes);
+    int cap = s1x1_resident_blocks<JQ, PQ, NP, EPI, UP, XUP>(lds_bytes);
     if ((int64_t)h.ntile * h.c.ntn > cap) {
         lds_bytes = h.wbytes + 2 * h.tbytes;
-        cap = s1x1_resident_blocks<JQ, PQ, NP, EPI, UP>(lds_bytes);
+        cap = s1x1_resident_blocks<JQ, PQ, NP, EPI, UP, XUP>(lds_bytes);
     }
     int groups = h.ntile;
     if ((int64_t)h.ntile * h.c.ntn > cap) groups = std::max(1, cap / h.c.ntn);
@@ -323,15 +358,26 @@ hipError_t s1x1_launch_cfg(S1x1Params h, hipStream_t stream) {
     groups = (h.ntile + h.c.per - 1) / h.c.per;
     const int64_t blocks = (int64_t)groups * h.c.ntn;
     if (blocks > INT32_MAX) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((conv1x1_stream_kernel<JQ, PQ, NP, EPI, UP>), dim3((unsigned)blocks), dim3(256),
+    hipLaunchKernelGGL((conv1x1_stream_kernel<JQ, PQ, NP, EPI, UP, XUP>), dim3((unsigned)blocks), dim3(256),
                        (size_t)lds_bytes, stream, h);
     return hipGetLastError();
 }
 
-// Every (JQ, PQ, NP) of one epilogue family; with the upsample copy (up),
-// the one-subtile-per-wave tiles (PQ 1).
+// Every (JQ, PQ, NP) of one epilogue family; with the upsample copy (up) or
+// an upsampled input source (xup), the one-subtile-per-wave tiles (PQ 1).
 template <int EPI>
-hipError_t s1x1_launch_family(const S1x1Params& h, int jq, int pq, int np, bool up, hipStream_t stream) {
+hipError_t s1x1_launch_family(const S1x1Params& h, int jq, int pq, int np, bool up, bool xup, hipStream_t stream) {
+#define AEXRT_S1X1_XUP_CASE(J, N) \
+    if (jq == J && pq == 1 && np == N) return s1x1_launch_cfg<J, 1, N, EPI, false, true>(h, stream);
+    if (xup) {
+        if (up) return hipErrorInvalidValue;
+        AEXRT_S1X1_XUP_CASE(1, 1) AEXRT_S1X1_XUP_CASE(1, 2) AEXRT_S1X1_XUP_CASE(1, 4) AEXRT_S1X1_XUP_CASE(1, 8)
+        AEXRT_S1X1_XUP_CASE(2, 1) AEXRT_S1X1_XUP_CASE(2, 2) AEXRT_S1X1_XUP_CASE(2, 4) AEXRT_S1X1_XUP_CASE(2, 8)
+        AEXRT_S1X1_XUP_CASE(4, 1) AEXRT_S1X1_XUP_CASE(4, 2) AEXRT_S1X1_XUP_CASE(4, 4) AEXRT_S1X1_XUP_CASE(4, 8)
+        AEXRT_S1X1_XUP_CASE(8, 1) AEXRT_S1X1_XUP_CASE(8, 2) AEXRT_S1X1_XUP_CASE(8, 4) AEXRT_S1X1_XUP_CASE(8, 8)
+        return hipErrorInvalidValue;
+    }
+#undef AEXRT_S1X1_XUP_CASE
 #define AEXRT_S1X1_UP_CASE(J, N) \
     if (jq == J && pq == 1 && np == N) return s1x1_launch_cfg<J, 1, N, EPI, true>(h, stream);
     if (up) {
@@ -356,9 +402,9 @@ hipError_t s1x1_launch_family(const S1x1Params& h, int jq, int pq, int np, bool 
 }
 
 #define AEXRT_S1X1_EXTERN(E) \
-    extern template hipError_t s1x1_launch_family<E>(const S1x1Params&, int, int, int, bool, hipStream_t);
+    extern template hipError_t s1x1_launch_family<E>(const S1x1Params&, int, int, int, bool, bool, hipStream_t);
 #define AEXRT_S1X1_INSTANCE(E) \
-    template hipError_t s1x1_launch_family<E>(const S1x1Params&, int, int, int, bool, hipStream_t);
+    template hipError_t s1x1_launch_family<E>(const S1x1Params&, int, int, int, bool, bool, hipStream_t);
 
 }  // namespace s1x1
 }  // namespace aexrt

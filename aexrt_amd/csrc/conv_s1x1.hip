@@ -25,13 +25,22 @@ struct S1x1Tile {
 // int8 1x1 stride-1 convs on views whose positions are evenly strided, with
 // the SiLU or run-time-flag epilogue and no residual.
 // An upsample copy (yup) takes an fp16 output and a view of 4x the
-// positions with 8-byte aligned channel groups.
+// positions with 8-byte aligned channel groups; an upsampled input source
+// (xup) whole 16-channel pieces of the input, an even map and the source's
+// slots, and not both at once.
 bool s1x1_shape_ok(const ConvParams& p, bool int8) {
     const bool up_ok = !p.yup || (!(p.flags & kConvOutF32) && p.yup_cstride % 4 == 0 && p.yup_cstride >= p.OC &&
                                   p.yup_nstride >= (int64_t)4 * p.OH * p.OW * p.yup_cstride);
+    const bool xup_ok =
+        !p.xup || (!p.yup && p.H % 2 == 0 && p.W % 2 == 0 && p.xup_c0 % 16 == 0 && p.xup_cn % 16 == 0 &&
+                   p.xup_cn > 0 && p.xup_c0 + p.xup_cn <= p.C && p.xup_cstride % 8 == 0 && p.xup_cstride >= p.xup_cn &&
+                   p.xup_nstride >= (int64_t)(p.H / 2) * (p.W / 2) * p.xup_cstride && p.xup_slots.p &&
+                   p.xup_nslots == p.xup_cn / 16 &&
+                   (int64_t)p.xup_slots.stripes * p.xup_nslots <= igemm::kMaxUpSlotReads);
     return int8 && p.loader == kLoaderNhwc && p.KH == 1 && p.KW == 1 && p.S == 1 && p.P == 0 && p.OH == p.H &&
            p.OW == p.W && p.C % 16 == 0 && p.x_cstride % 8 == 0 && (p.lin & kLinX) && (p.lin & kLinY) &&
-           !(p.flags & kConvResidual) && p.res == nullptr && p.fuse_1x1 == nullptr && p.M < (1 << 24) && up_ok;
+           !(p.flags & kConvResidual) && p.res == nullptr && p.fuse_1x1 == nullptr && p.M < (1 << 24) && up_ok &&
+           xup_ok;
 }
 
 bool s1x1_instantiated(int jq, int pq, int np, bool up) {
@@ -51,7 +60,7 @@ bool s1x1_geometry(S1x1Params& h, S1x1Tile& t) {
     h.npiece = h.TP * h.c16;
     const int need = (h.npiece + 255) / 256;
     t.np = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : need <= 8 ? 8 : 0;
-    if (!t.np || !s1x1_instantiated(t.jq, t.pq, t.np, p.yup != nullptr)) return false;
+    if (!t.np || !s1x1_instantiated(t.jq, t.pq, t.np, p.yup != nullptr || p.xup != nullptr)) return false;
     const int64_t ntile = ((int64_t)p.M + h.TP - 1) / h.TP;
     if (ntile > INT32_MAX / 2) return false;
     h.ntile = (int)ntile;
@@ -64,20 +73,24 @@ bool s1x1_geometry(S1x1Params& h, S1x1Tile& t) {
     h.fd_c16 = make_fastdiv((uint32_t)h.c16);
     h.fd_hw = make_fastdiv((uint32_t)(p.OH * p.OW));
     h.fd_w = make_fastdiv((uint32_t)p.OW);
+    if (p.xup) {
+        h.fd_uns = make_fastdiv((uint32_t)std::max(p.xup_nslots, 1));
+        h.xup_slot_bytes = ((p.xup_slots.stripes - 1) * p.xup_slots.stride + (uint32_t)p.xup_nslots) * 4u;
+    }
     return true;
 }
 
 std::atomic<int> g_s1x1_force{0};  // jq | pq << 8, 0 = off
 
 hipError_t s1x1_launch(const S1x1Params& h, int epi, const S1x1Tile& t, hipStream_t s) {
-    const bool up = h.c.yup != nullptr;
+    const bool up = h.c.yup != nullptr, xup = h.c.xup != nullptr;
     if (LaunchProbe* pr = launch_probe()) {
         std::snprintf(pr->name, sizeof(pr->name), "conv1x1_stream_kernel<%d,%d,%d,%d%s>", t.jq, t.pq, t.np, epi,
-                      up ? ",true" : "");
+                      up ? ",true" : xup ? ",false,true" : "");
         return hipSuccess;
     }
-    if (epi == igemm::kEpiSilu) return s1x1::s1x1_launch_family<igemm::kEpiSilu>(h, t.jq, t.pq, t.np, up, s);
-    if (epi == igemm::kEpiAny) return s1x1::s1x1_launch_family<igemm::kEpiAny>(h, t.jq, t.pq, t.np, up, s);
+    if (epi == igemm::kEpiSilu) return s1x1::s1x1_launch_family<igemm::kEpiSilu>(h, t.jq, t.pq, t.np, up, xup, s);
+    if (epi == igemm::kEpiAny) return s1x1::s1x1_launch_family<igemm::kEpiAny>(h, t.jq, t.pq, t.np, up, xup, s);
     return hipErrorInvalidValue;
 }
 
@@ -115,7 +128,7 @@ int enumerate_s1x1_choices(const ConvParams& p, bool int8, ConvChoice* out, int 
     const int ocj = (p.OCp + 15) / 16;
     int n = 0;
     for (int pq : {1, 2}) {
-        if (pq > 1 && p.yup) break;  // the upsample copy runs on one-subtile tiles
+        if (pq > 1 && (p.yup || p.xup)) break;  // the upsample variants run on one-subtile tiles
         for (int jq : {1, 2, 4, 8}) {
             if (n >= cap) return n;
             if (jq > 1 && jq / 2 >= ocj) continue;  // a channel tile past every channel
@@ -143,6 +156,16 @@ hipError_t launch_conv_s1x1(const ConvParams& p, bool int8, int epi, hipStream_t
     h.c = p;
     S1x1Tile t{p.choice.jn, p.choice.pw, 0};
     if (!s1x1_geometry(h, t)) return hipErrorInvalidValue;
+    if (p.xup) {
+        // one buffer resource over the input view and the source: 32-bit offsets from the lower
+        const uintptr_t xa = reinterpret_cast<uintptr_t>(p.x), ua = reinterpret_cast<uintptr_t>(p.xup);
+        const uintptr_t lo = std::min(xa, ua), hi = std::max(xa + p.x_bytes, ua + p.xup_bytes);
+        if (hi - lo > 0xFFFFFFF0ull) return hipErrorInvalidValue;
+        h.xbase = reinterpret_cast<const void*>(lo);
+        h.xspan = (uint32_t)(hi - lo);
+        h.x_off0 = (uint32_t)(xa - lo);
+        h.xup_off0 = (uint32_t)(ua - lo);
+    }
     return s1x1_launch(h, epi, t, stream);
 }
 

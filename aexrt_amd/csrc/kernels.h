@@ -108,6 +108,17 @@ struct ConvParams {
     int32_t yup_cstride = 0;
     SlotRef yup_slots{};
     uint32_t yup_bytes = 0;  // filled in by the igemm launcher
+    // int8 1x1 convs on the streaming kernel: input channels [xup_c0, xup_c0
+    // + xup_cn) are read from xup, a map of H/2 x W/2 positions (NHWC view),
+    // as its nearest 2x upsample, so that upsample is never stored (the input
+    // view's memory for those channels is not read); xup_slots / xup_nslots:
+    // that map's amax slots, read besides the input's.  Null: none.
+    const void* xup = nullptr;
+    int64_t xup_nstride = 0;
+    int32_t xup_cstride = 0, xup_c0 = 0, xup_cn = 0;
+    SlotRef xup_slots{};
+    int32_t xup_nslots = 0;
+    uint32_t xup_bytes = 0;  // filled in by the igemm launcher
     // filled in by the igemm launcher
     uint32_t x_bytes = 0, y_bytes = 0, r_bytes = 0;  // byte spans of the views
     uint32_t x_slot_bytes = 0;                       // byte span of the input slots

@@ -243,6 +243,11 @@ struct AexrtYoloModel {
     // produces its input (the conv's entry names the resize, the resize's
     // the conv); -1: none
     std::vector<int> up_fold;
+    // per command: a nearest 2x resize whose output (a concat slice) the
+    // int8 1x1 conv reading the concat reads from the resize's input instead,
+    // so the upsample is never stored (the conv's entry names the resize, the
+    // resize's the conv); -1: none
+    std::vector<int> up_read;
     uint32_t* pair_sync = nullptr;
     int n_pair_sync = 0;
     uint32_t* pair_err = nullptr;
@@ -1535,32 +1540,131 @@ bool build_pair_step(AexrtYoloModel* m, size_t ci, int k, std::vector<bool>& don
     return true;
 }
 
-// Nearest 2x resizes folded into the int8 1x1 conv that produces their input
-// (AEXRT_HIP_FOLD_UPSAMPLE=0: never): the conv's launch writes the upsample
-// too (ConvParams::yup, the streaming 1x1 kernel), so the resize neither
-// launches nor reads the conv output again.  Candidates here; a conv whose
-// shape and views the kernel does not take keeps its resize (build_steps).
+void set_upsampled_input(AexrtYoloModel* m, ConvParams& p, int ci);
+
+// The int8 1x1 conv that reads nearest 2x resize ci's output, a 16-channel
+// aligned slice of a concat root, as its only reader (the concat over the
+// whole root read by that conv alone, placed without a copy): -1 when there
+// is none or the streaming kernel does not take the conv with the source.
+int upsample_reader(AexrtYoloModel* m, size_t ci) {
+    const Engine& e = m->eng;
+    const EngineCommand& c = e.commands[ci];
+    const int src = (int)c.inputs[0], o = (int)c.output;
+    const ValueInfo& ov = m->vals[o];
+    if (!ov.pl.valid || ov.C % 16 || ov.pl.offset % 16) return -1;
+    for (int u : ov.consumers)
+        if (e.commands[u].kind != kCmdConcat) return -1;
+    for (const CopyJob& j : m->copies)
+        if (j.src == o) return -1;
+    const int R = ov.pl.root;
+    int cat = -1;
+    for (size_t v = 0; v < m->vals.size(); ++v) {
+        const ValueInfo& x = m->vals[v];
+        if (x.pl.valid && x.pl.root == R && x.pl.offset == 0 && x.C == m->roots[R].C && (int)v != o) cat = (int)v;
+    }
+    if (cat < 0 || m->vals[cat].consumers.size() != 1) return -1;
+    const int k = m->vals[cat].consumers[0];
+    const ConvState& ks = m->convs[k];
+    if (!ks.is_conv || (int)e.commands[k].inputs[0] != cat || !is_int8_algorithm(ks.algorithm) || ks.pg16 ||
+        ks.dynamic || ks.fused_residual || !m->roots[R].slots_complete || m->up_read[k] >= 0)
+        return -1;
+    const AexrtConv2DDesc d = desc_of(e.commands[k]);
+    if (d.kernel_h != 1 || d.kernel_w != 1 || is_f32(m, ks.out_value)) return -1;
+    const AexrtHipTensorView xv = view_of(m, cat), sv = view_of(m, src), yv = view_of(m, ks.out_value);
+    if (!xv.amax_slots || !sv.amax_slots) return -1;
+    // the kernel reads both views through one resource: within 4 GB of each other
+    const uintptr_t xa = reinterpret_cast<uintptr_t>(xv.data), sa = reinterpret_cast<uintptr_t>(sv.data);
+    const ValueInfo& cv = m->vals[cat];
+    const ValueInfo& srcv = m->vals[src];
+    const uintptr_t xe = xa + (uintptr_t)(cv.N * xv.n_stride) * 2, se = sa + (uintptr_t)(srcv.N * sv.n_stride) * 2;
+    if (std::max(xe, se) - std::min(xa, sa) > 0xFFFFFFF0ull) return -1;
+    ConvParams p{};
+    std::string why;
+    const uint32_t flags = e.commands[k].kind == kCmdConvSilu ? AEXRT_HIP_CONV_SILU : 0u;
+    if (!build_conv_params(conv_desc_padded(m, (size_t)k), ks.algorithm, flags, xv, ks.w, ks.scale, ks.bias, nullptr,
+                           yv, nullptr, p, why))
+        return -1;
+    set_upsampled_input(m, p, (int)ci);
+    ConvChoice probe[4];
+    return enumerate_conv_choices(p, true, probe, 4) > 0 ? k : -1;
+}
+
+// Nearest 2x resizes that never launch (AEXRT_HIP_FOLD_UPSAMPLE=0: every
+// resize launches; =copy: the producer form only).  Where the one reader of
+// the resize's output is an int8 1x1 conv over its concat, that conv reads
+// the resize's input at half resolution instead (ConvParams::xup): the
+// upsample is never stored.  Otherwise, where the resize's input comes from
+// an int8 1x1 conv, that conv writes the upsample too (ConvParams::yup), so
+// the resize neither launches nor reads the conv output again.  Candidates
+// here; a producer whose shape and views the kernel does not take keeps its
+// resize (build_steps).
 void setup_upsample_folds(AexrtYoloModel* m) {
     const Engine& e = m->eng;
     m->up_fold.assign(e.commands.size(), -1);
+    m->up_read.assign(e.commands.size(), -1);
     const char* env = std::getenv("AEXRT_HIP_FOLD_UPSAMPLE");
     if (env && env[0] == '0') return;
+    const bool reader_form = !(env && std::strcmp(env, "copy") == 0);
     for (size_t ci = 0; ci < e.commands.size(); ++ci) {
         const EngineCommand& c = e.commands[ci];
         if (c.kind != kCmdResize || c.inputs.empty()) continue;
         const ValueInfo& x = m->vals[c.inputs[0]];
         const ValueInfo& o = m->vals[c.output];
-        if (x.producer < 0 || o.N != x.N || o.C != x.C || o.H != 2 * x.H || o.W != 2 * x.W) continue;
+        if (o.N != x.N || o.C != x.C || o.H != 2 * x.H || o.W != 2 * x.W || is_f32(m, c.output)) continue;
+        if (reader_form) {
+            const int k = upsample_reader(m, ci);
+            if (k >= 0) {
+                m->up_read[k] = (int)ci;
+                m->up_read[ci] = k;
+                continue;
+            }
+        }
+        if (x.producer < 0) continue;
         const int pc = x.producer;
         const ConvState& cs = m->convs[pc];
         if (!cs.is_conv || cs.out_value != (int)c.inputs[0] || !is_int8_algorithm(cs.algorithm) || cs.pg16 ||
             cs.dynamic || cs.fused_residual || cs.pair_a >= 0 || cs.pair_b >= 0 || m->up_fold[pc] >= 0)
             continue;
         const AexrtConv2DDesc d = desc_of(e.commands[pc]);
-        if (d.kernel_h != 1 || d.kernel_w != 1 || is_f32(m, cs.out_value) || is_f32(m, c.output)) continue;
+        if (d.kernel_h != 1 || d.kernel_w != 1 || is_f32(m, cs.out_value)) continue;
         m->up_fold[pc] = (int)ci;
         m->up_fold[ci] = pc;
     }
+}
+
+// Fills conv p's upsampled input source from resize ci: the resize's input,
+// read at half resolution for the channels of its output's slice.
+void set_upsampled_input(AexrtYoloModel* m, ConvParams& p, int ci) {
+    const EngineCommand& rc = m->eng.commands[ci];
+    const ValueInfo& o = m->vals[rc.output];
+    const AexrtHipTensorView sv = view_of(m, (int)rc.inputs[0]);
+    p.xup = sv.data;
+    p.xup_nstride = sv.n_stride;
+    p.xup_cstride = (int32_t)sv.c_stride;
+    p.xup_c0 = (int32_t)o.pl.offset;
+    p.xup_cn = o.C;
+    p.xup_slots = slot_ref(sv);
+    p.xup_nslots = o.C / 16;
+}
+
+// Writes the upsamples that folded convs read from their sources into their
+// concat slices (synchronously), for reads of those values outside a run.
+bool store_folded_upsamples(AexrtYoloModel* m, int root) {
+    const Engine& e = m->eng;
+    for (size_t ci = 0; ci < e.commands.size(); ++ci) {
+        if (e.commands[ci].kind != kCmdResize || m->up_read.size() <= ci || m->up_read[ci] < 0) continue;
+        const ValueInfo& x = m->vals[e.commands[ci].inputs[0]];
+        const ValueInfo& o = m->vals[e.commands[ci].output];
+        if (o.pl.root != root) continue;
+        const AexrtHipTensorView xv = view_of(m, (int)e.commands[ci].inputs[0]), yv = view_of(m, (int)e.commands[ci].output);
+        if (!check_hip(launch_resize_nearest_nhwc(static_cast<const __half*>(xv.data), xv.n_stride, xv.c_stride,
+                                                  static_cast<__half*>(yv.data), yv.n_stride, yv.c_stride, x.N, x.H,
+                                                  x.W, x.C, o.H, o.W, SlotRef{nullptr, 1u, 0u}, m->stream),
+                       "store upsample") ||
+            !check_hip(hipStreamSynchronize(m->stream), "store upsample sync"))
+            return false;
+    }
+    return true;
 }
 
 bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
@@ -1712,6 +1816,10 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                                        pair ? cs.bias_pair : cs.bias, cs.fused_residual ? &rvw : nullptr, yvw, nullptr,
                                        p, why))
                     return fail(m, "command " + std::to_string(ci) + ": " + why);
+                if (m->up_read[ci] >= 0) {
+                    set_upsampled_input(m, p, m->up_read[ci]);
+                    if (own_pass) return fail(m, "command " + std::to_string(ci) + ": upsampled input without slots");
+                }
                 int upv = -1;  // output value of a resize folded into this conv
                 if (m->up_fold[ci] >= 0) {
                     const EngineCommand& rc = e.commands[m->up_fold[ci]];
@@ -1871,6 +1979,10 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                     st.writes.push_back(V[upv].pl.root);
                     st.tail = " + 2x upsample cmd#" + std::to_string(e.src_cmd[m->up_fold[ci]]);
                 }
+                if (m->up_read[ci] >= 0) {
+                    st.reads.push_back(V[e.commands[m->up_read[ci]].inputs[0]].pl.root);
+                    st.tail = " reading 2x upsample cmd#" + std::to_string(e.src_cmd[m->up_read[ci]]);
+                }
                 if (pair) {
                     done[sib] = true;
                     st.tail = " + cmd#" + std::to_string(e.src_cmd[sib]);
@@ -1945,7 +2057,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
                 break;
             }
             case kCmdResize: {
-                if (m->up_fold[ci] >= 0) break;  // written by the conv producing its input
+                if (m->up_fold[ci] >= 0 || m->up_read[ci] >= 0) break;  // folded into a conv
                 const ValueInfo& x = V[c.inputs[0]];
                 const ValueInfo& o = V[c.output];
                 AexrtHipTensorView xv = view_of(m, (int)c.inputs[0]), yv = view_of(m, (int)c.output);
@@ -3061,6 +3173,8 @@ int aexrt_yolo_debug_value(AexrtYoloModel* m, uint32_t value_id, float* out, uin
         if (elements < n) return 0;
         return hipMemcpy(out, m->input_dev, n * 4, hipMemcpyDeviceToHost) == hipSuccess ? 1 : 0;
     }
+    // upsamples that the convs reading them take from their sources are stored now
+    if (m->vals[v].pl.valid && !store_folded_upsamples(m, m->vals[v].pl.root)) return fail(m, last_error()) ? 1 : 0;
     return copy_value_to_host(m, v, out, elements) ? 1 : 0;
 }
 
@@ -3105,6 +3219,18 @@ int aexrt_yolo_debug_conv_int8(AexrtYoloModel* m, uint32_t command_index, int32_
                                      hipMemcpyDeviceToHost),
                            "debug_conv_int8 slots");
             for (size_t g = 0; ok && g < w.size(); ++g) slots[g] = std::max(slots[g], w[g]);
+        }
+        // groups read from an upsampled source: its slot words
+        if (ok && q.xup) {
+            const uint32_t us = q.xup_slots.stripes ? q.xup_slots.stripes : 1u;
+            std::vector<uint32_t> u((size_t)q.xup_nslots);
+            const int g0 = q.xup_c0 / 16;
+            for (uint32_t s = 0; s < us && ok; ++s) {
+                ok = check_hip(hipMemcpy(u.data(), q.xup_slots.p + (size_t)s * q.xup_slots.stride, u.size() * 4,
+                                         hipMemcpyDeviceToHost),
+                               "debug_conv_int8 source slots");
+                for (size_t g = 0; ok && g < u.size(); ++g) slots[g0 + g] = std::max(slots[g0 + g], u[g]);
+            }
         }
     }
     if (acc_dev) (void)hipFree(acc_dev);

@@ -292,6 +292,19 @@ def conv2d(pc: PreparedConv, x, y, *, flags: int = SILU, x_slots=None, y_slots=N
         _ptr(acc_out), _stream(stream)), "conv2d")
 
 
+def conv2d_upsampled_input(pc: PreparedConv, x, x_up, up_c0: int, y, *, flags: int = SILU, x_slots=None,
+                           x_up_slots=None, y_slots=None, acc_out=None, stream=None) -> None:
+    """int8 1x1 conv ``pc`` (per-tensor) over ``x`` ([N, H, W, C] NHWC view) whose channels [up_c0,
+    up_c0 + C_up) are the nearest 2x upsample of ``x_up`` ([N, H/2, W/2, C_up]), read from x_up
+    directly (x's memory there is not read); ``x_up_slots``: x_up's amax slots."""
+    d = ConvDesc.from_params(pc.params)
+    xv, uv, yv = view(x, x_slots), view(x_up, x_up_slots), view(y, y_slots)
+    check(_lib.lib().aexrt_hip_conv2d_upsampled_input(
+        ctypes.byref(d), pc.algorithm, flags, ctypes.byref(xv), ctypes.byref(uv), up_c0, x_up.shape[3],
+        pc.weight.data_ptr(), _ptr(pc.w_scale), pc.bias.data_ptr(), ctypes.byref(yv), _ptr(acc_out),
+        _stream(stream)), "conv2d_upsampled_input")
+
+
 def conv2d_upsample_copy(pc: PreparedConv, x, y, y_up, *, flags: int = SILU, x_slots=None, y_slots=None,
                          y_up_slots=None, stream=None) -> None:
     """int8 1x1 conv ``pc`` (per-tensor) that also writes its output's nearest 2x upsample into the

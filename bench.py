@@ -151,11 +151,18 @@ def launch_work(label: str, replay):
     # resize R it replaces), 4x the output's positions
     up = re.search(r" \+ 2x upsample cmd#(\d+)", tail)
     tail = tail[:up.start()] + tail[up.end():] if up else tail
+    # "reading 2x upsample cmd#R": the conv reads that upsampled slice of its input from the resize
+    # R's source, a quarter of the slice's positions
+    rd = re.search(r" reading 2x upsample cmd#(\d+)", tail)
+    tail = tail[:rd.start()] + tail[rd.end():] if rd else tail
     idx = [ci] + [int(m) for m in re.findall(r"cmd#(\d+)", tail)]
     ops = nbytes = 0
     if up:
         b, _, _, _, oc, oh, ow = (int(v) for v in cmds[ci]["params"][:7])
         nbytes += b * oc * 4 * oh * ow * 2
+    if rd:
+        b, c, h, w, oh, ow = (int(v) for v in cmds[int(rd.group(1))]["params"][:6])
+        nbytes -= b * c * oh * ow * 2 - b * c * h * w * 2
     produced = {cmds[i]["output"] for i in idx}
     consumed = {cmds[i]["inputs"][0] for i in idx}
     inputs_seen = set()

@@ -208,6 +208,25 @@ int aexrt_hip_conv2d_upsample_copy(const AexrtConv2DDesc* desc, uint32_t algorit
                                    const float* bias, const AexrtHipTensorView* y, const AexrtHipTensorView* y_up,
                                    void* stream);
 
+/* An int8 1x1 conv (algorithm 51/52/53, per-tensor, the arguments of
+ * aexrt_hip_conv2d without residual) whose input channels [up_c0, up_c0 +
+ * up_channels) are the nearest 2x upsample of x_up (a map of H/2 x W/2
+ * positions with its own amax slots), read from x_up directly: x's memory for
+ * those channels is not read, and the per-tensor amax is the max over x's
+ * other slots and x_up's.  Replaces the reference's RESIZE into a concat
+ * slice followed by the concat's 1x1 conv (src/aexrt/yolo.py:830-834, the
+ * CONCAT_CONV1X1 pattern yolo.py:473-488; shaders
+ * native/aexrt_d3d12_runtime.cpp:14851-14872 and 4614-4762) with the conv
+ * alone, the upsample never stored.  x and x_up must lie within one 4 GB
+ * span (one arena, as a model's values do).  acc_out: optional int32 sums.
+ * Runs on
+ * the streaming 1x1 kernel (a forced tile, else the first that fits); 0 with
+ * a diagnostic when none fits. */
+int aexrt_hip_conv2d_upsampled_input(const AexrtConv2DDesc* desc, uint32_t algorithm, uint32_t flags,
+                                     const AexrtHipTensorView* x, const AexrtHipTensorView* x_up, uint32_t up_c0,
+                                     uint32_t up_channels, const void* weight, const float* w_scale,
+                                     const float* bias, const AexrtHipTensorView* y, int32_t* acc_out, void* stream);
+
 /* The kernel and tile candidates the model loader measures for one conv
  * (no reference counterpart; the tile-level analogue of the algorithm
  * candidates of aexrt_yolo_conv_plan_info, native/aexrt.h:435-445, and of

@@ -222,18 +222,21 @@ def test_yolov8n_320_w8a8_superblocks_equal_separate_convs(cuda, monkeypatch, tm
     assert err <= allowed, (err, allowed)
 
 
+@pytest.mark.parametrize("form", ["read", "copy"])
 @pytest.mark.parametrize("batch", [1, 64])
-def test_yolov8n_320_w8a8_upsample_folded_into_its_conv(cuda, monkeypatch, tmp_path, batch):
-    """The neck's two nearest 2x upsamples written by the int8 1x1 convs that produce their inputs
-    (no resize launch, aexrt_hip_conv2d_upsample_copy) against the network with the resize kernels:
-    every stored value (conv outputs, the upsamples in their concat slices, the concats) and the
-    network output bit for bit, on the bench's kernel plan.  The producing convs run the same tile
-    with or without the copy."""
+def test_yolov8n_320_w8a8_upsample_folded_into_its_conv(cuda, monkeypatch, tmp_path, batch, form):
+    """The neck's two nearest 2x upsamples without a resize launch against the network with the
+    resize kernels: read by the int8 1x1 conv over their concat straight from the resize's input
+    ("read", the default: the upsample is never stored, aexrt_hip_conv2d_upsampled_input), or
+    written by the int8 1x1 conv producing that input ("copy", aexrt_hip_conv2d_upsample_copy).
+    Every stored value (conv outputs, the upsamples in their concat slices, which a value read
+    stores on demand in the "read" form, the concats) and the network output bit for bit, on the
+    bench's kernel plan (the folded convs run the same tile as without the fold)."""
     _use_bench_plan(monkeypatch, tmp_path)
     g, names, plan, data = _yolo_engine(batch, 320)
     x = np.random.default_rng(4).random((batch, 3, 320, 320)).astype(np.float32)
     outs = []
-    for on in ("0", "1"):
+    for on in ("0", "1" if form == "read" else "copy"):
         monkeypatch.setenv("AEXRT_HIP_FOLD_UPSAMPLE", on)
         with NativeHipYoloModel(data) as m:
             m.set_profiling(True)
@@ -242,7 +245,8 @@ def test_yolov8n_320_w8a8_upsample_folded_into_its_conv(cuda, monkeypatch, tmp_p
             m.set_profiling(False)
             folded = [lab for lab in labels if "2x upsample" in lab]
             resizes = [lab for lab in labels if lab.endswith("RESIZE")]
-            assert (len(folded), len(resizes)) == ((2, 0) if on == "1" else (0, 2)), labels
+            assert (len(folded), len(resizes)) == ((2, 0) if on != "0" else (0, 2)), labels
+            assert all(("reading 2x" in lab) == (form == "read") for lab in folded), folded
             m.run(x)
             out = m.output()
             stored = {}

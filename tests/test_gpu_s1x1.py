@@ -200,3 +200,84 @@ def test_s1x1_upsample_copy_refuses_fp32_output(cuda):
     up = torch.zeros((1, 8, 8, 16), dtype=torch.float16, device=cuda)
     with pytest.raises(RuntimeError, match="conv2d_upsample_copy"):
         K.conv2d_upsample_copy(pc, x, y, up, flags=K.OUT_F32, x_slots=xs)
+
+
+# (n, upsample channels, other channels, h, w (of the conv), oc, slice offset, jq or 0, seed)
+S1X1_UPSAMPLED_INPUT = [
+    (2, 128, 64, 40, 40, 64, 0, 4, 441),    # YOLO's P3 top-down concat: upsample first, then the skip feature
+    (3, 256, 128, 20, 20, 128, 0, 8, 442),  # the P4 one (256 + 128 channels)
+    (2, 32, 48, 6, 10, 32, 48, 0, 443),     # the upsample as the last slice, a ragged tail, first tile that fits
+    (1, 16, 16, 4, 4, 16, 16, 1, 444),      # one 16-channel group each
+]
+
+
+@pytest.mark.parametrize("case", S1X1_UPSAMPLED_INPUT,
+                         ids=[f"n{t[0]}_up{t[1]}_c{t[2]}_{t[3]}x{t[4]}_oc{t[5]}_at{t[6]}_jq{t[7]}"
+                              for t in S1X1_UPSAMPLED_INPUT])
+def test_s1x1_upsampled_input_equals_resize_then_conv(cuda, case):
+    """The conv over a concat whose upsampled slice it reads from the resize's source
+    (aexrt_hip_conv2d_upsampled_input; the slice itself left unwritten) against the resize into
+    the slice followed by the same conv: int32 accumulators equal (and equal to the oracle's),
+    outputs and output slots bit-identical on the same tile; the slice's own slot words are not
+    needed (they stay zero)."""
+    import torch
+
+    n, cu, cs, h, w, oc, u0, jq, seed = case
+    c = cu + cs
+    rng = np.random.default_rng(seed)
+    src = rng.standard_normal((n, cu, h // 2, w // 2)).astype(np.float16).astype(np.float32)
+    skip = rng.standard_normal((n, cs, h, w)).astype(np.float16).astype(np.float32)
+    up = np.repeat(np.repeat(src, 2, axis=2), 2, axis=3)
+    cat = np.concatenate([up, skip], axis=1) if u0 == 0 else np.concatenate([skip, up], axis=1)
+    assert cat.shape[1] == c and (u0 == 0 or u0 == cs)
+    wt = group16_weight(rng, oc, c, 1)
+    b = packing.fp16_round(rng.uniform(-0.1, 0.1, oc).astype(np.float32))
+    desc = O.conv_desc(n, c, h, w, oc, 1, 1, 0)
+    pc = K.prepare_conv(desc, 51, K.SRC_LAYOUT_INT8, packing.pack_conv_int8(wt, fp16_engine=True), b, device=cuda)
+    # the source and the folded form's root in one allocation (the kernel reads both through one
+    # buffer resource, as a model's arena holds them)
+    arena = torch.empty(n * (h // 2) * (w // 2) * cu + n * h * w * c, dtype=torch.float16, device=cuda)
+    src_d = arena[:n * (h // 2) * (w // 2) * cu].view(n, h // 2, w // 2, cu)
+    src_d.copy_(torch.from_numpy(nchw_to_nhwc(src.astype(np.float16))).to(cuda))
+    src_s = K.new_slots(cu, cuda, stripes=16)
+    K.amax_slots(src_d, src_s)
+    # the reference order: the skip feature and the resize into one root, then the conv over it
+    root = torch.zeros((n, h, w, c), dtype=torch.float16, device=cuda)
+    root_s = K.new_slots(c, cuda, stripes=16)
+    s0 = 0 if u0 else cu  # the skip slice
+    root[..., s0:s0 + cs] = torch.from_numpy(nchw_to_nhwc(skip.astype(np.float16))).to(cuda)
+    K.amax_slots(root[..., s0:s0 + cs], root_s[:, s0 // 16:(s0 + cs) // 16])
+    K.resize_nearest(src_d, root[..., u0:u0 + cu], y_slots=root_s[:, u0 // 16:(u0 + cu) // 16])
+    y_ref = torch.empty((n, h, w, oc), dtype=torch.float16, device=cuda)
+    ys_ref = K.new_slots(oc, cuda, stripes=16)
+    acc_ref = torch.empty((n * h * w, oc), dtype=torch.int32, device=cuda)
+    # the folded form: a root holding only the skip slice and its slots
+    root2 = arena[n * (h // 2) * (w // 2) * cu:].view(n, h, w, c)
+    root2.fill_(float("nan"))
+    root2_s = K.new_slots(c, cuda, stripes=16)
+    root2[..., s0:s0 + cs] = root[..., s0:s0 + cs]
+    K.amax_slots(root2[..., s0:s0 + cs], root2_s[:, s0 // 16:(s0 + cs) // 16])
+    y = torch.empty_like(y_ref)
+    ys = K.new_slots(oc, cuda, stripes=16)
+    acc = torch.empty_like(acc_ref)
+    K.set_conv1x1_stream(True, jq or 1, 1)
+    try:
+        K.conv2d(pc, root, y_ref, flags=K.SILU, x_slots=root_s, y_slots=ys_ref, acc_out=acc_ref)
+        if not jq:
+            K.set_conv1x1_stream(False)
+        K.conv2d_upsampled_input(pc, root2, src_d, u0, y, x_slots=root2_s, x_up_slots=src_s, y_slots=ys,
+                                 acc_out=acc)
+        torch.cuda.synchronize()
+    finally:
+        K.set_conv1x1_stream(False)
+    np.testing.assert_array_equal(acc.cpu().numpy(), acc_ref.cpu().numpy())
+    _, _, _, _, acc_o, y_o = O.w8a8_conv(cat, wt, b, desc, silu=True, fp16_engine=True)
+    np.testing.assert_array_equal(acc.cpu().numpy().reshape(n, h, w, oc), nchw_to_nhwc(acc_o))
+    got = nhwc_to_nchw(y.float().cpu().numpy())
+    assert (np.abs(got.astype(np.float64) - y_o) <= _ulp16(y_o)).all()
+    np.testing.assert_array_equal(_u32(ys).max(axis=0), _slots_of(got, oc))
+    if jq:
+        assert torch.equal(y, y_ref)
+    # the slice was never written nor its slots
+    assert torch.isnan(root2[..., u0:u0 + cu]).all()
+    assert not _u32(root2_s)[:, u0 // 16:(u0 + cu) // 16].any()

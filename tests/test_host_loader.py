@@ -108,17 +108,23 @@ def test_committed_plan_loads_runs_and_closes(stub, batch):
     convs = _conv_labels(res)
     assert len(convs) > 40
     assert all(" kernel=" in lab for lab in convs if "CONV" in lab)
-    # the neck's two 2x upsamples are written by the convs producing their inputs
-    folded = [lab for lab in convs if "+ 2x upsample" in lab]
-    assert len(folded) == 2 and all("conv1x1_stream_kernel<" in lab and ",true>" in lab for lab in folded)
+    # the neck's two 2x upsamples are read from their sources by the convs over their concats
+    folded = [lab for lab in convs if " reading 2x upsample" in lab]
+    assert len(folded) == 2 and all("conv1x1_stream_kernel<" in lab and ",false,true>" in lab for lab in folded)
     assert not any(lab.endswith("RESIZE") for lab in convs)
 
 
-def test_upsample_fold_can_be_switched_off(stub):
+def test_upsample_fold_forms(stub):
     res = _run({"batch": 64, "env": {"AEXRT_HIP_FOLD_UPSAMPLE": "0"}})
     convs = _conv_labels(res)
     assert sum(lab.endswith("RESIZE") for lab in convs) == 2
     assert not any("2x upsample" in lab for lab in convs)
+    # the producer form: the convs producing the upsamples' inputs write them too
+    res = _run({"batch": 64, "env": {"AEXRT_HIP_FOLD_UPSAMPLE": "copy"}})
+    convs = _conv_labels(res)
+    folded = [lab for lab in convs if " + 2x upsample" in lab]
+    assert len(folded) == 2 and all(",true>" in lab and ",false,true>" not in lab for lab in folded)
+    assert not any(lab.endswith("RESIZE") for lab in convs)
 
 
 def test_load_time_tuning_writes_a_plan_that_reloads(stub, tmp_path):
@@ -147,5 +153,5 @@ def _asan_current():
                     reason="host-ASan library not built, or older than libaexrt_hip.so (make -C aexrt_amd/csrc asan)")
 def test_host_paths_under_address_sanitizer(stub, tmp_path):
     _run({"batch": 64}, asan=True)
-    _run({"batch": 64, "plan": str(tmp_path / "plan.tune")}, asan=True)
+    _run({"batch": 1, "plan": str(tmp_path / "plan.tune")}, asan=True)  # load-time tuning (bs 1: quicker)
     _run({"batch": 64, "env": {"AEXRT_HIP_C2F_SUPERBLOCK": "1"}}, asan=True)
