@@ -230,7 +230,7 @@ int aexrt_hip_set_conv_stem(int32_t mode, int32_t tr) {
 }
 
 int aexrt_hip_set_conv1x1_stream(int32_t mode, int32_t jq, int32_t pq) {
-    if (!set_conv1x1_stream(mode != 0, jq, pq)) {
+    if (!set_conv1x1_stream(mode, jq, pq)) {
         set_error("set_conv1x1_stream: no kernel instance for this tile");
         return 0;
     }

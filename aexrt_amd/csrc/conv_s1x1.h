@@ -61,6 +61,7 @@ struct S1x1Params {
     uint32_t xspan, x_off0, xup_off0;
     uint32_t xup_slot_bytes;
     FastDiv fd_uns;
+    int one;  // one tile per block (a grid of every tile) instead of a persistent grid
 };
 
 namespace s1x1 {
@@ -347,7 +348,7 @@ hipError_t s1x1_launch_cfg(S1x1Params h, hipStream_t stream) {
     // one tile buffer when the single-buffer footprint already gives every
     // tile its own resident block
     int lds_bytes = h.wbytes + h.tbytes;
-    int cap = s1x1_resident_blocks<JQ, PQ, NP, EPI, UP, XUP>(lds_bytes);
+    int cap = h.one ? INT32_MAX : s1x1_resident_blocks<JQ, PQ, NP, EPI, UP, XUP>(lds_bytes);
     if ((int64_t)h.ntile * h.c.ntn > cap) {
         lds_bytes = h.wbytes + 2 * h.tbytes;
         cap = s1x1_resident_blocks<JQ, PQ, NP, EPI, UP, XUP>(lds_bytes);

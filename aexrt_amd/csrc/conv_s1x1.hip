@@ -80,13 +80,13 @@ bool s1x1_geometry(S1x1Params& h, S1x1Tile& t) {
     return true;
 }
 
-std::atomic<int> g_s1x1_force{0};  // jq | pq << 8, 0 = off
+std::atomic<int> g_s1x1_force{0};  // jq | pq << 8 | one-tile-per-block << 16, 0 = off
 
 hipError_t s1x1_launch(const S1x1Params& h, int epi, const S1x1Tile& t, hipStream_t s) {
     const bool up = h.c.yup != nullptr, xup = h.c.xup != nullptr;
     if (LaunchProbe* pr = launch_probe()) {
-        std::snprintf(pr->name, sizeof(pr->name), "conv1x1_stream_kernel<%d,%d,%d,%d%s>", t.jq, t.pq, t.np, epi,
-                      up ? ",true" : xup ? ",false,true" : "");
+        std::snprintf(pr->name, sizeof(pr->name), "conv1x1_stream_kernel<%d,%d,%d,%d%s>%s", t.jq, t.pq, t.np, epi,
+                      up ? ",true" : xup ? ",false,true" : "", h.one ? " one tile per block" : "");
         return hipSuccess;
     }
     if (epi == igemm::kEpiSilu) return s1x1::s1x1_launch_family<igemm::kEpiSilu>(h, t.jq, t.pq, t.np, up, xup, s);
@@ -96,13 +96,13 @@ hipError_t s1x1_launch(const S1x1Params& h, int epi, const S1x1Tile& t, hipStrea
 
 }  // namespace
 
-bool set_conv1x1_stream(bool on, int jq, int pq) {
-    if (!on) {
+bool set_conv1x1_stream(int mode, int jq, int pq) {
+    if (!mode) {
         g_s1x1_force.store(0);
         return true;
     }
-    if (!s1x1_instantiated(jq, pq, 1, false)) return false;
-    g_s1x1_force.store(jq | (pq << 8));
+    if ((mode != 1 && mode != 2) || !s1x1_instantiated(jq, pq, 1, false)) return false;
+    g_s1x1_force.store(jq | (pq << 8) | (mode == 2 ? 1 << 16 : 0));
     return true;
 }
 
@@ -113,6 +113,7 @@ bool forced_s1x1_choice(ConvChoice& c) {
     c.kind = 6;
     c.jn = f & 0xFF;
     c.pw = (f >> 8) & 0xFF;
+    c.ksw = (f >> 16) & 1;  // one tile per block
     return true;
 }
 
@@ -141,6 +142,13 @@ int enumerate_s1x1_choices(const ConvParams& p, bool int8, ConvChoice* out, int 
             c.jn = jq;
             c.pw = pq;
             out[n++] = c;
+            // the same tile on a grid of one tile per block: the hardware refills
+            // the CUs as blocks end, so loads and stores of different blocks
+            // interleave instead of all blocks' phases lining up
+            if (n < cap && (int64_t)h.ntile * h.c.ntn > 256) {
+                c.ksw = 1;
+                out[n++] = c;
+            }
         }
     }
     return n;
@@ -156,6 +164,7 @@ hipError_t launch_conv_s1x1(const ConvParams& p, bool int8, int epi, hipStream_t
     h.c = p;
     S1x1Tile t{p.choice.jn, p.choice.pw, 0};
     if (!s1x1_geometry(h, t)) return hipErrorInvalidValue;
+    h.one = p.choice.ksw ? 1 : 0;
     if (p.xup) {
         // one buffer resource over the input view and the source: 32-bit offsets from the lower
         const uintptr_t xa = reinterpret_cast<uintptr_t>(p.x), ua = reinterpret_cast<uintptr_t>(p.xup);

@@ -230,7 +230,7 @@ int enumerate_s1x1_choices(const ConvParams& p, bool int8, ConvChoice* out, int 
 hipError_t launch_conv_s1x1(const ConvParams& p, bool int8, int epi, hipStream_t stream);
 // Forces every int8 1x1 conv the kind-0 heuristics would run onto one
 // streaming tile (on = false: off).  False for a tile without an instance.
-bool set_conv1x1_stream(bool on, int jq, int pq);
+bool set_conv1x1_stream(int mode, int jq, int pq);  // 0 off, 1 persistent, 2 one tile per block
 bool forced_s1x1_choice(ConvChoice& c);
 // Band kernel of the network's first conv (3x3 pad 1, stride 1/2, fp32 NCHW
 // input of at most 3 channels read directly, fp16 SiLU output, OCp <= 64,

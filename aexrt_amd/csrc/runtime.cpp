@@ -1145,6 +1145,12 @@ std::string tune_key(const ConvParams& p, bool int8) {
         std::snprintf(buf, sizeof(buf), "|u%lld,%d", (long long)p.yup_nstride, p.yup_cstride);
         k += buf;
     }
+    if (p.xup) {
+        // the upsampled input source: its channels and view
+        std::snprintf(buf, sizeof(buf), "|x%d,%d,%lld,%d", p.xup_c0, p.xup_cn, (long long)p.xup_nstride,
+                      p.xup_cstride);
+        k += buf;
+    }
     return k;
 }
 
@@ -1332,9 +1338,10 @@ std::string refined_key(size_t ci, uint32_t alg, const ConvParams& p, bool int8)
 void apply_cached_choice(AexrtYoloModel* m, size_t ci, uint32_t alg, ConvParams& p, bool int8) {
     std::vector<ConvChoice> all(kMaxConvChoices);
     const int na = enumerate_conv_choices(p, int8, all.data(), kMaxConvChoices);
-    // a fused 1x1 runs on the 32x32-MFMA kernel only, an upsample copy on the
-    // streaming 1x1 kernel: without a measured choice, the first tile that fits
-    if ((p.fuse_1x1 || p.yup) && na > 0) p.choice = all[0];
+    // a fused 1x1 runs on the 32x32-MFMA kernel only, an upsample copy or an
+    // upsampled input source on the streaming 1x1 kernel: without a measured
+    // choice, the first tile that fits
+    if ((p.fuse_1x1 || p.yup || p.xup) && na > 0) p.choice = all[0];
     if (m->tune_cache.empty()) return;
     auto offered = [&](const ConvChoice& c) {
         for (int k = 0; k < na; ++k)
@@ -1351,11 +1358,12 @@ void apply_cached_choice(AexrtYoloModel* m, size_t ci, uint32_t alg, ConvParams&
         p.choice = tu->second;
         return;
     }
-    if (p.yup) {
-        // the same conv measured without the upsample copy: its tile, when the
-        // copy's kernel instances include it
+    if (p.yup || p.xup) {
+        // the same conv measured without the upsample copy or source: its
+        // tile, when those kernel instances include it
         ConvParams q = p;
         q.yup = nullptr;
+        q.xup = nullptr;
         auto rq = m->refined.find(refined_key(ci, alg, q, int8));
         if (rq != m->refined.end() && offered(rq->second)) {
             p.choice = rq->second;

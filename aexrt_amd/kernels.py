@@ -225,11 +225,12 @@ def set_conv_stem(mode: int = STEM_AUTO, tr: int = 0) -> None:
     check(_lib.lib().aexrt_hip_set_conv_stem(mode, tr), "set_conv_stem")
 
 
-def set_conv1x1_stream(on: bool = False, jq: int = 0, pq: int = 0) -> None:
+def set_conv1x1_stream(on: bool = False, jq: int = 0, pq: int = 0, one_tile: bool = False) -> None:
     """Force the streaming 1x1 int8 kernel (jq 16-channel subtiles per block, pq 16-position
-    subtiles per wave) onto every int8 1x1 conv launched without a measured choice; off restores
-    the automatic choice."""
-    check(_lib.lib().aexrt_hip_set_conv1x1_stream(1 if on else 0, jq, pq), "set_conv1x1_stream")
+    subtiles per wave; one_tile: a grid of one tile per block instead of a persistent one) onto
+    every int8 1x1 conv launched without a measured choice; off restores the automatic choice."""
+    mode = 0 if not on else (2 if one_tile else 1)
+    check(_lib.lib().aexrt_hip_set_conv1x1_stream(mode, jq, pq), "set_conv1x1_stream")
 
 
 def conv_weight_bytes(params: Sequence[int], algorithm: int) -> int:

@@ -426,7 +426,9 @@ int aexrt_hip_conv_chain3(const AexrtConv2DDesc* desc_a, const void* weight_a, c
  * quantized once into an int8 LDS tile) with jq 16-channel subtiles per block
  * (1/2/4/8) and pq 16-position subtiles per wave (1, or 2 with jq <= 4); a
  * conv that tile does not fit (LDS, views not evenly strided, residual) then
- * fails.  mode 0 switches it off.  Returns 0 for a tile without an instance. */
+ * fails.  mode 2: the same on a grid of one tile per block instead of a
+ * persistent grid.  mode 0 switches it off.  Returns 0 for a tile without an
+ * instance. */
 int aexrt_hip_set_conv1x1_stream(int32_t mode, int32_t jq, int32_t pq);
 
 /* Kernel of the network's first conv (3x3 pad 1, stride 1/2, the fp32 NCHW

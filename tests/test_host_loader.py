@@ -100,14 +100,14 @@ def _conv_labels(res):
     return [lab for lab in res["labels"] if lab.startswith("cmd#")]
 
 
-@pytest.mark.parametrize("batch", [1, 64])
+@pytest.mark.parametrize("batch", [1, 2, 64])  # 2: no shape of the plan, every choice by rule
 def test_committed_plan_loads_runs_and_closes(stub, batch):
     res = _run({"batch": batch})
     assert res["output_elements"] == batch * 144 * 2100  # output0 [B][A = 2100 anchors][4 * 16 + 80]
     assert res["labels"][0].startswith("amax slots clear")
     convs = _conv_labels(res)
     assert len(convs) > 40
-    assert all(" kernel=" in lab for lab in convs if "CONV" in lab)
+    assert all(" kernel=" in lab and "not launchable" not in lab for lab in convs if "CONV" in lab)
     # the neck's two 2x upsamples are read from their sources by the convs over their concats
     folded = [lab for lab in convs if " reading 2x upsample" in lab]
     assert len(folded) == 2 and all("conv1x1_stream_kernel<" in lab and ",false,true>" in lab for lab in folded)
