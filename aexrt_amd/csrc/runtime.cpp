@@ -273,6 +273,14 @@ struct AexrtYoloModel {
     std::string tune_cache;                    // AEXRT_HIP_TUNE_CACHE file, empty: none
     hipStream_t lane_stream[kLanes] = {};      // capture-time streams of lanes 1..kLanes-1
     int n_lanes = 1;                           // lanes the schedule uses (measured at load)
+    // how steps are put on lanes: 0 the dependency rule, 1 list scheduling over
+    // step_ms, 2 lane_plan (a plan measured before, read from the tune cache)
+    int lane_policy = 0;
+    int lane_policy_forced = -1;              // AEXRT_HIP_LIST_SCHEDULE=0 / 1, else -1
+    std::vector<float> step_ms;               // per step: its time in the network on one lane
+    std::string lane_plan;                    // per step: its lane as a digit
+    // "lanes <input dims> <commands>" -> lane plan measured at load (list scheduling kept)
+    std::map<std::string, std::string> lane_plans;
     std::vector<hipEvent_t> step_events;      // per step, recorded when a step signals
     std::vector<hipEvent_t> lane_events;      // fork / join events of the captures
     hipStream_t stream = nullptr;
@@ -1163,13 +1171,21 @@ bool same_choice(const ConvChoice& a, const ConvChoice& b) {
 // (each still checked against the shape's candidates) and the file is
 // rewritten with every choice of the model, so that later loads of the same
 // engine (or of another with the same conv shapes) launch the same kernels.
-// One line per conv shape: key, tab, kind jn pw ksw tr tc cc nw.
+// One line per conv shape: key, tab, kind jn pw ksw tr tc cc nw; a measured
+// schedule in the same form; a list-scheduled network's lanes as
+// "lanes <input dims> commands <n>", tab, one digit per step.
 void load_tune_cache(AexrtYoloModel* m) {
     std::ifstream f(m->tune_cache);
     std::string line;
     while (std::getline(f, line)) {
         const size_t tab = line.find('\t');
         if (tab == std::string::npos) continue;
+        if (line.compare(0, 6, "lanes ") == 0) {
+            const std::string plan = line.substr(tab + 1);
+            if (!plan.empty() && plan.find_first_not_of("0123") == std::string::npos)
+                m->lane_plans[line.substr(0, tab)] = plan;
+            continue;
+        }
         ConvChoice c{};
         if (std::sscanf(line.c_str() + tab + 1, "%d %d %d %d %d %d %d %d", &c.kind, &c.jn, &c.pw, &c.ksw, &c.tr,
                         &c.tc, &c.cc, &c.nw) != 8)
@@ -1197,6 +1213,7 @@ void save_tune_cache(AexrtYoloModel* m) {
         for (const auto& [key, c] : m->refined) put(key, c);
         for (const auto& [key, v] : m->schedules)
             put(key, ConvChoice{v.first, v.second, v.fuse, (int)v.mask, (int)v.chains, (int)v.dual, v.super, 0});
+        for (const auto& [key, plan] : m->lane_plans) f << key << '\t' << plan << '\n';
         if (!f) return;
     }
     std::rename(tmp.c_str(), m->tune_cache.c_str());
@@ -1274,11 +1291,18 @@ bool tune_conv(AexrtYoloModel* m, ConvParams& p, bool int8, std::vector<ConvChoi
 // step needs is after the earlier steps that write a root it reads (read after
 // write), and everything after the slot clear.  Two producers of slices of one root
 // touch disjoint bytes and disjoint amax slot groups, so they may run concurrently.
-// Lanes: a step continues the lane of its latest dependency when that lane has not
-// moved on, else takes an idle lane (else the least recently used one, which then
-// orders it after that lane's last step too); dependencies on other lanes become
-// event waits.  The captured graph thus has parallel branches (the head's box and
-// class chains, the finest head level beside the rest of the neck).
+// Lanes, by the dependency rule: a step continues the lane of its latest
+// dependency when that lane has not moved on, else takes an idle lane (else the
+// least recently used one, which then orders it after that lane's last step
+// too); dependencies on other lanes become event waits.  The captured graph thus
+// has parallel branches (the head's box and class chains, the finest head level
+// beside the rest of the neck).  The rule looks at step order only: a head branch
+// whose input was produced early can land behind the rest of the neck.  List
+// scheduling instead takes the steps' times measured in the network on one lane
+// and puts each step on the lane where it can start first (after its
+// dependencies' estimated ends and its lane's last step), preferring a lane that
+// ends with one of its dependencies (no cross-lane wait).  Which of the two runs
+// faster is measured at load.
 // Whether step i must follow the earlier step j: it reads a root j writes,
 // either one touches every root, or both meet in a grid barrier.
 bool step_depends(const Step& i, const Step& j) {
@@ -1300,21 +1324,50 @@ void schedule_steps(AexrtYoloModel* m) {
     }
     int last[kLanes];
     for (int l = 0; l < kLanes; ++l) last[l] = -1;
+    const bool planned = m->lane_policy == 2 && (int)m->lane_plan.size() == n;
+    const bool listed = m->lane_policy == 1 && (int)m->step_ms.size() == n;
+    std::vector<double> end(n, 0.0);  // list scheduling: estimated end of each step
+    double lane_end[kLanes] = {};
     for (int i = 0; i < n; ++i) {
-        int lane = -1, best = -1;
-        for (int l = 0; l < nl; ++l)
-            for (int d : st[i].deps)
-                if (last[l] == d && d > best) {
-                    best = d;
+        int lane = -1;
+        if (nl == 1) {
+            lane = 0;
+        } else if (planned) {
+            lane = std::min(nl - 1, std::max(0, m->lane_plan[i] - '0'));
+        } else if (listed) {
+            double ready = 0.0;
+            for (int d : st[i].deps) ready = std::max(ready, end[d]);
+            double best = 0.0;
+            bool best_follows = false;
+            constexpr double kTie = 1e-4;  // ms: starts this close count as equal
+            for (int l = 0; l < nl; ++l) {
+                const double start = std::max(ready, lane_end[l]);
+                bool follows = false;
+                for (int d : st[i].deps) follows = follows || last[l] == d;
+                if (lane < 0 || start < best - kTie || (start <= best + kTie && follows && !best_follows)) {
                     lane = l;
+                    best = start;
+                    best_follows = follows;
                 }
-        if (lane < 0) {
-            for (int l = 0; l < nl && lane < 0; ++l)
-                if (last[l] < 0) lane = l;
+            }
+            end[i] = best + std::max(0.0f, m->step_ms[i]);
+            lane_end[lane] = end[i];
+        } else {
+            int best = -1;
+            for (int l = 0; l < nl; ++l)
+                for (int d : st[i].deps)
+                    if (last[l] == d && d > best) {
+                        best = d;
+                        lane = l;
+                    }
             if (lane < 0) {
-                lane = 0;
-                for (int l = 1; l < nl; ++l)
-                    if (last[l] < last[lane]) lane = l;
+                for (int l = 0; l < nl && lane < 0; ++l)
+                    if (last[l] < 0) lane = l;
+                if (lane < 0) {
+                    lane = 0;
+                    for (int l = 1; l < nl; ++l)
+                        if (last[l] < last[lane]) lane = l;
+                }
             }
         }
         st[i].lane = lane;
@@ -1322,6 +1375,13 @@ void schedule_steps(AexrtYoloModel* m) {
             if (st[d].lane != lane) st[d].signal = true;
         last[lane] = i;
     }
+}
+
+// The lanes of the current schedule, one digit per step.
+std::string lane_digits(const AexrtYoloModel* m) {
+    std::string s;
+    for (const Step& x : m->steps) s += (char)('0' + x.lane);
+    return s;
 }
 
 // Key of a conv's choice measured in the network: the command, its algorithm
@@ -1679,6 +1739,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
     Engine& e = m->eng;
     auto& V = m->vals;
     m->steps.clear();
+    m->step_ms.clear();  // list scheduling measures the new steps again
     m->tunables.clear();
     setup_upsample_folds(m);
     {
@@ -2284,10 +2345,10 @@ bool refine_in_context(AexrtYoloModel* m) {
 // Per head 3x3 + 1x1 pair of m->fuse_pairs, the time of the steps of the current
 // build that compute it: the fused step, or the 3x3 step plus the 1x1 step
 // (the least of kContextReps event-profiled passes per step).
-bool pair_step_times(AexrtYoloModel* m, std::vector<float>& out) {
-    out.assign(m->fuse_pairs.size(), 0.0f);
-    if (m->fuse_pairs.empty()) return true;
-    std::vector<float> lo(m->steps.size(), 1e30f);
+// Each step's time in the network, launched one by one between events: the
+// least of kContextReps passes after a warm-up pass.
+bool profiled_step_times(AexrtYoloModel* m, std::vector<float>& lo) {
+    lo.assign(m->steps.size(), 1e30f);
     const bool prof = m->profile;
     m->profile = true;
     bool ok = true;
@@ -2299,7 +2360,14 @@ bool pair_step_times(AexrtYoloModel* m, std::vector<float>& out) {
     m->profile = prof;
     m->prof_labels.clear();
     m->prof_ms.clear();
-    if (!ok) return false;
+    return ok;
+}
+
+bool pair_step_times(AexrtYoloModel* m, std::vector<float>& out) {
+    out.assign(m->fuse_pairs.size(), 0.0f);
+    if (m->fuse_pairs.empty()) return true;
+    std::vector<float> lo;
+    if (!profiled_step_times(m, lo)) return false;
     for (size_t k = 0; k < m->fuse_pairs.size(); ++k)
         for (size_t i = 0; i < m->steps.size(); ++i)
             if (m->steps[i].cmd == m->fuse_pairs[k].first || m->steps[i].cmd == m->fuse_pairs[k].second)
@@ -2337,27 +2405,47 @@ bool time_schedule(AexrtYoloModel* m, float* ms_out) {
     return ok;
 }
 
-// The fastest lane count of kLanes down to one (its time of 10 runs in *best_ms).
+// Schedules the current steps anew under the current lane count and policy; list
+// scheduling measures the steps' times first when the step list changed since.
+bool reschedule(AexrtYoloModel* m) {
+    if (m->lane_policy == 1 && m->n_lanes > 1 && m->step_ms.size() != m->steps.size() &&
+        !profiled_step_times(m, m->step_ms))
+        return false;
+    schedule_steps(m);
+    drop_graph(m);
+    return true;
+}
+
+// The fastest lane count of kLanes down to one, each under the dependency rule
+// and under list scheduling (its time of 10 runs in *best_ms).
 bool choose_lanes(AexrtYoloModel* m, float* best_ms) {
     *best_ms = 0.0f;
     if (!m->use_graph) return true;
-    int options[kLanes];
-    for (int k = 0; k < kLanes; ++k) options[k] = kLanes - k;
-    int best = 1;
-    for (int k = 0; k < kLanes; ++k) {
-        m->n_lanes = options[k];
-        schedule_steps(m);
-        float ms = 0.0f;
-        if (!time_schedule(m, &ms)) return false;
-        if (k == 0 || ms < *best_ms) {
-            *best_ms = ms;
-            best = options[k];
+    if (!profiled_step_times(m, m->step_ms)) return false;
+    int best = 1, best_policy = 0;
+    bool first = true;
+    for (int policy = 0; policy < 2; ++policy)
+        for (int lanes = kLanes; lanes >= (policy ? 2 : 1); --lanes) {
+            if (m->lane_policy_forced >= 0 && policy != m->lane_policy_forced && lanes > 1) continue;
+            m->n_lanes = lanes;
+            m->lane_policy = policy;
+            schedule_steps(m);
+            float ms = 0.0f;
+            if (!time_schedule(m, &ms)) return false;
+            if (first || ms < *best_ms) {
+                *best_ms = ms;
+                best = lanes;
+                best_policy = policy;
+            }
+            first = false;
         }
-    }
     m->n_lanes = best;
+    m->lane_policy = best_policy;
     schedule_steps(m);
     drop_graph(m);
-    if (m->tune_log) std::fprintf(stderr, "aexrt lanes: %d (%.1f us per run)\n", best, *best_ms * 100.0f);
+    if (m->tune_log)
+        std::fprintf(stderr, "aexrt lanes: %d, %s (%.1f us per run)\n", best,
+                     best_policy ? "list scheduled" : "dependency rule", *best_ms * 100.0f);
     return true;
 }
 
@@ -2556,6 +2644,12 @@ bool build_model(AexrtYoloModel* m) {
     // schedules are measured and the faster kept.
     const char* lanes = std::getenv("AEXRT_HIP_LANES");
     const bool fixed_lanes = lanes && lanes[0] >= '1' && lanes[0] <= '9';
+    // AEXRT_HIP_LIST_SCHEDULE=0 / 1: steps put on lanes by the dependency rule / by
+    // list scheduling over their measured times; otherwise both are measured (with
+    // autotuning) or the cached lane plan is taken
+    const char* ls = std::getenv("AEXRT_HIP_LIST_SCHEDULE");
+    m->lane_policy_forced = ls && (ls[0] == '0' || ls[0] == '1') ? ls[0] - '0' : -1;
+    const int fixed_policy = std::max(0, m->lane_policy_forced);
     const bool pairs = std::any_of(m->sibling.begin(), m->sibling.end(), [](int s) { return s >= 0; });
     // AEXRT_HIP_FUSE_1X1=0 / 1: head 3x3 + 1x1 pairs never / always in one launch; otherwise
     // both are measured (with autotuning) or the cached schedule's choice is taken
@@ -2580,7 +2674,7 @@ bool build_model(AexrtYoloModel* m) {
     float best_ms = 0.0f;
     bool best_merge = true;
     uint32_t best_fuse = 0;
-    int best_lanes = 1;
+    int best_lanes = 1, best_policy = 0;
     // the schedule cache keeps (merge, lanes, fuse, fused pairs) in a choice's
     // (kind, jn, pw, ksw)
     auto fuse_for = [&](int k) -> uint32_t {
@@ -2610,7 +2704,8 @@ bool build_model(AexrtYoloModel* m) {
         float ms = 0.0f;
         if (fixed_lanes) {
             m->n_lanes = std::min(kLanes, std::atoi(lanes));
-            schedule_steps(m);
+            m->lane_policy = fixed_policy;
+            if (!reschedule(m)) return false;
             if (variants > 1 && !time_schedule(m, &ms)) return false;
         } else if (m->autotune && !choose_lanes(m, &ms)) {
             return false;
@@ -2620,6 +2715,7 @@ bool build_model(AexrtYoloModel* m) {
             best_merge = m->merge_siblings;
             best_fuse = m->fuse_mask;
             best_lanes = m->n_lanes;
+            best_policy = m->lane_policy;
         }
     }
     // each pair fused or not by its own step times (one launch against two,
@@ -2651,14 +2747,19 @@ bool build_model(AexrtYoloModel* m) {
             if (!choose_lanes(m, &ms)) return false;
         } else {
             m->n_lanes = fixed_lanes ? std::min(kLanes, std::atoi(lanes)) : best_lanes;
-            schedule_steps(m);
+            m->lane_policy = fixed_lanes ? fixed_policy : best_policy;
+            if (!reschedule(m)) return false;
         }
         drop_graph(m);
     }
+    // the lane plan of a list-scheduled network is kept beside its schedule
+    const std::string lkey = "lanes" + skey.substr(8);
     if (use_cached_sched && !fixed_lanes) {
         m->n_lanes = std::max(1, std::min(kLanes, cached_sched->second.second));
-        schedule_steps(m);
-        drop_graph(m);
+        const auto plan = m->lane_plans.find(lkey);
+        m->lane_policy = m->lane_policy_forced >= 0 ? m->lane_policy_forced : plan != m->lane_plans.end() ? 2 : 0;
+        m->lane_plan = plan != m->lane_plans.end() ? plan->second : std::string();
+        if (!reschedule(m)) return false;
     }
     // head branches on the chain kernel, per head level (the branches reading
     // one input): the captured schedule timed with the level's branches as a
@@ -2673,9 +2774,7 @@ bool build_model(AexrtYoloModel* m) {
             if (!build_steps(m, m->copies)) return false;
             if (!refine_in_context(m)) return false;
             m->n_lanes = lanes_kept;
-            schedule_steps(m);
-            drop_graph(m);
-            return true;
+            return reschedule(m);
         };
         float base = 0.0f;
         if (!time_schedule(m, &base)) return false;
@@ -2737,9 +2836,7 @@ bool build_model(AexrtYoloModel* m) {
             if (!build_steps(m, m->copies)) return false;
             if (m->autotune && !refine_in_context(m)) return false;
             m->n_lanes = lanes_kept;
-            schedule_steps(m);
-            drop_graph(m);
-            return true;
+            return reschedule(m);
         };
         if (sb_forced < 0 && !use_cached_sched && avail && m->autotune && m->use_graph) {
             float base = 0.0f;
@@ -2765,10 +2862,19 @@ bool build_model(AexrtYoloModel* m) {
             if (!rebuild_pairs()) return false;
         }
     }
-    if (m->autotune)
+    // the lanes measured again over the final steps (the branches and
+    // superblocks chosen above change them)
+    float final_ms = 0.0f;
+    if (m->autotune && !fixed_lanes && !choose_lanes(m, &final_ms)) return false;
+    if (m->autotune) {
         m->schedules[skey] = Schedule{m->merge_siblings ? 1 : 0, m->n_lanes, m->fuse_mask ? 1 : 0,
                                       m->fuse_mask == ~0u ? 0u : m->fuse_mask, m->chain_mask, m->chain_dual,
                                       (int)m->superblock_mask};
+        if (m->lane_policy == 1 && m->n_lanes > 1)
+            m->lane_plans[lkey] = lane_digits(m);
+        else
+            m->lane_plans.erase(lkey);
+    }
     if (m->tune_log && variants > 1)
         std::fprintf(stderr, "aexrt sibling convs: %s, head 1x1 convs fused: %s (mask %#x)\n",
                      best_merge ? "one launch" : "two launches",
@@ -2779,6 +2885,13 @@ bool build_model(AexrtYoloModel* m) {
     setup_postprocess(m);
     label_steps(m);
     compute_stats(m);
+    if (m->tune_log)
+        for (size_t i = 0; i < m->steps.size(); ++i) {
+            std::string deps;
+            for (int d : m->steps[i].deps) deps += " " + std::to_string(d);
+            std::fprintf(stderr, "aexrt step %zu lane %d%s after%s: %s\n", i, m->steps[i].lane,
+                         m->steps[i].signal ? " signals" : "", deps.c_str(), m->steps[i].label.c_str());
+        }
     m->executable = true;
     return true;
 }

@@ -93,7 +93,10 @@ def _run(spec, asan=False, timeout=600):
     assert r.returncode == 0, (spec, r.returncode, r.stdout[-2000:], r.stderr[-4000:])
     line = [ln for ln in r.stdout.splitlines() if ln.startswith("RESULT ")]
     assert line, r.stdout[-2000:]
-    return json.loads(line[-1][len("RESULT "):])
+    res = json.loads(line[-1][len("RESULT "):])
+    # with AEXRT_HIP_TUNE_LOG=1 the library prints each step's lane of the final schedule
+    res["lanes"] = [int(ln.split()[4]) for ln in r.stderr.splitlines() if ln.startswith("aexrt step ")]
+    return res
 
 
 def _conv_labels(res):
@@ -129,11 +132,32 @@ def test_upsample_fold_forms(stub):
 
 def test_load_time_tuning_writes_a_plan_that_reloads(stub, tmp_path):
     plan = tmp_path / "plan.tune"
-    tuned = _run({"batch": 64, "plan": str(plan)})
+    log = {"AEXRT_HIP_TUNE_LOG": "1"}
+    tuned = _run({"batch": 64, "plan": str(plan), "env": log})
     assert plan.exists() and "schedule 64x3x320x320" in plan.read_text()
-    # the measured plan, read back without measuring, gives the same launches
-    again = _run({"batch": 64, "plan": str(plan), "env": {"AEXRT_HIP_AUTOTUNE": "0"}})
+    # the measured plan, read back without measuring, gives the same launches on the same lanes
+    again = _run({"batch": 64, "plan": str(plan), "env": dict(log, AEXRT_HIP_AUTOTUNE="0")})
     assert again["labels"] == tuned["labels"]
+    assert again["lanes"] == tuned["lanes"] and len(tuned["lanes"]) == len(tuned["labels"])
+
+
+def _plan_line(prefix):
+    text = (ROOT / "aexrt_amd" / "tuned" / "yolov8n320.tune").read_text()
+    return [ln.split("\t") for ln in text.splitlines() if ln.startswith(prefix)]
+
+
+def test_committed_lane_plan_is_applied(stub):
+    (sched, fields), = _plan_line("schedule 64x3x320x320")
+    (_, plan), = _plan_line("lanes 64x3x320x320")
+    lanes = int(fields.split()[1])
+    log = {"AEXRT_HIP_TUNE_LOG": "1"}
+    res = _run({"batch": 64, "env": log})
+    assert res["lanes"] == [int(c) for c in plan] and max(res["lanes"]) < lanes
+    # the dependency rule instead (same lane count), and list scheduling over the steps' times
+    for policy in ("0", "1"):
+        other = _run({"batch": 64, "env": dict(log, AEXRT_HIP_LIST_SCHEDULE=policy)})
+        assert other["labels"] == res["labels"] and len(other["lanes"]) == len(plan)
+        assert max(other["lanes"]) < lanes and other["lanes"][:20] == [0] * 20  # the backbone is a chain
 
 
 def test_forced_superblocks_build_one_launch_per_bottleneck(stub):
