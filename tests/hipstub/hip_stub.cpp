@@ -158,6 +158,7 @@ hipError_t hipMemset(void* dst, int value, size_t n) {
     std::memset(dst, value, n);
     return hipSuccess;
 }
+hipError_t hipMemsetAsync(void* dst, int value, size_t n, hipStream_t) { return hipMemset(dst, value, n); }
 
 hipError_t hipGetDevice(int* id) {
     *id = 0;
