@@ -405,6 +405,19 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
             // y1 in a lane: four of them the lane holds (rows 8 j4 + 4 hi + r
             // of subtile k2 / 2, j4 = 2 (k2 % 2) + hi), four its partner lane
             // (lane ^ 32) does.
+            // The W2 rows of an output subtile (all its k steps) are loaded
+            // together, one subtile ahead: the first before y1 is formed, the
+            // next ones under the current subtile's products and stores (loaded
+            // at their use, each product would wait out a load of its own).
+            v4i a2c[NQ * 2], a2n[NQ * 2];
+            auto w2_loads = [&](int j2, v4i (&a)[NQ * 2]) {
+                const int row2 = j2 * 32 + l32;
+#pragma unroll
+                for (int k2 = 0; k2 < NQ * 2; ++k2)
+                    a[k2] = bload16(rw2, row2 < h.c2.OCp ? (uint32_t)(row2 * h.c2.Kp + k2 * 16 + hi * 8) * 2u : kOob);
+            };
+            w2_loads(0, a2c);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int q = 0; q < MQ; ++q) {
                 v4i b2[NQ * 2];
@@ -433,15 +446,13 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
                 }
 #pragma unroll
                 for (int j2 = 0; j2 < NQ; ++j2) {
-                    const int row2 = j2 * 32 + l32;
-                    v4i a2[NQ * 2];
-#pragma unroll
-                    for (int k2 = 0; k2 < NQ * 2; ++k2)
-                        a2[k2] = bload16(rw2, row2 < h.c2.OCp ? (uint32_t)(row2 * h.c2.Kp + k2 * 16 + hi * 8) * 2u : kOob);
+                    if (j2 + 1 < NQ) w2_loads(j2 + 1, a2n);
+                    else if (q + 1 < MQ) w2_loads(0, a2n);
+                    __builtin_amdgcn_sched_barrier(0);
                     v16f acc2{};
 #pragma unroll
                     for (int k2 = 0; k2 < NQ * 2; ++k2)
-                        acc2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a2[k2]),
+                        acc2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a2c[k2]),
                                                                       __builtin_bit_cast(v8h, b2[k2]), acc2, 0, 0, 0);
 #pragma unroll
                     for (int j4 = 0; j4 < 4; ++j4) {
@@ -468,6 +479,8 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_m32_kernel(M32Params h) {
                                                                   0, 0);
                         }
                     }
+#pragma unroll
+                    for (int k2 = 0; k2 < NQ * 2; ++k2) a2c[k2] = a2n[k2];
                 }
             }
 #pragma unroll
