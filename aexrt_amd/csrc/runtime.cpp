@@ -3246,8 +3246,13 @@ int aexrt_yolo_run(AexrtDevice* device, AexrtYoloModel* m, const float* input, u
                        "detection count readback") ||
             !check_hip(hipMemcpyAsync(dets_host.data(), m->dets_dev, dets_host.size() * 4, hipMemcpyDeviceToHost,
                                       m->stream),
-                       "detection readback"))
-            return fail(m, last_error()) ? 1 : 0;
+                       "detection readback")) {
+            // a readback already enqueued writes into raw_count / dets_host: it
+            // completes before they go out of scope
+            const std::string err = last_error();
+            (void)hipStreamSynchronize(m->stream);
+            return fail(m, err) ? 1 : 0;
+        }
     }
     auto t2 = clk::now();
     if (!check_hip(hipStreamSynchronize(m->stream), "run sync")) return fail(m, last_error()) ? 1 : 0;
