@@ -161,6 +161,31 @@ hipError_t launch_conv_chain(const ConvParams& a, const ConvParams& b, const Con
     return hipErrorInvalidValue;
 }
 
+int enumerate_chain_tiles(const ConvParams* br0, const ConvParams* br1, int* tr, int* tc, int cap) {
+    const ConvParams& a = br0[0];
+    const int H = a.H, W = a.W;
+    const int cand[][2] = {{H, W}, {(H + 1) / 2, W}, {(H + 1) / 2, (W + 1) / 2}, {(H + 2) / 3, (W + 2) / 3},
+                           {8, 8}, {6, 8}, {5, 5}, {4, 4}, {3, 3}};
+    int n = 0;
+    for (const auto& t : cand) {
+        const int r = std::min(t[0], H), c = std::min(t[1], W);
+        if (r < 1 || c < 1) continue;
+        bool seen = false;
+        for (int k = 0; k < n; ++k) seen = seen || (tr[k] == r && tc[k] == c);
+        if (seen || n >= cap) continue;
+        ChainParams h0{}, h1{};
+        int lds0 = 0, lds1 = 0, mq0 = 1, mq1 = 1, kg0 = 1, kg1 = 1;
+        if (!make_chain_params(br0[0], br0[1], br0[2], r, c, h0, lds0, mq0, kg0)) continue;
+        if (br1 && (!make_chain_params(br1[0], br1[1], br1[2], r, c, h1, lds1, mq1, kg1) || mq0 != mq1 ||
+                    (int64_t)h0.ntile + h1.ntile > INT32_MAX))
+            continue;
+        tr[n] = r;
+        tc[n] = c;
+        ++n;
+    }
+    return n;
+}
+
 // Two branches over one input map in one launch, on one tile (the one that
 // fits the branch with more channels).
 hipError_t launch_conv_chain2(const ConvParams* br0, const ConvParams* br1, int tr, int tc, hipStream_t stream) {

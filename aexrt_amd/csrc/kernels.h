@@ -165,6 +165,10 @@ hipError_t launch_conv_chain(const ConvParams& a, const ConvParams& b, const Con
 // Two branches over one input (br0, br1: their a, b, c) in one launch on one
 // tile (0 x 0: the one that fits the branch with more channels).
 hipError_t launch_conv_chain2(const ConvParams* br0, const ConvParams* br1, int tr, int tc, hipStream_t stream);
+// Tiles a chain launch can run on (br1 null: one branch; else both branches on
+// the same tile), the largest first: whole map, halves, thirds, then 8x8 down
+// to 3x3; up to cap (rows, columns) pairs written, their count returned.
+int enumerate_chain_tiles(const ConvParams* br0, const ConvParams* br1, int* tr, int* tc, int cap);
 
 // C2f bottleneck pair in one launch (conv_pair.h): conv a (3x3 s1 p1 SiLU,
 // C -> C) then conv b (the same, + b.res when b.flags has kConvResidual) over

@@ -107,6 +107,9 @@ struct ConvState {
     // a head branch run in one launch with this 3x3 conv first: the 3x3 conv
     // over its output (chain_b) and the 1x1 conv over that one's (chain_c)
     int chain_b = -1, chain_c = -1;
+    // the chain launch's tile (rows x columns; 0 x 0: the largest that fits),
+    // measured at load among the tiles the kernel offers
+    int chain_tr = 0, chain_tc = 0;
     // C2f bottleneck superblock: this 3x3 conv and the 3x3 conv over its
     // output (pair_b) in one launch, the intermediate never stored; pair_a:
     // the first conv of the pair this one completes
@@ -265,6 +268,16 @@ struct AexrtYoloModel {
     std::map<std::string, ConvChoice> tuned;  // conv shape -> measured choice
     std::map<std::string, std::vector<ConvChoice>> tuned_top;  // conv shape -> fastest candidates
     std::vector<std::unique_ptr<TunedConv>> tunables;         // convs of the step list with measured choices
+    // chain launches of the step list: first branch's command, the other
+    // branch's (-1: one branch), the step, the key of its tile choice
+    struct ChainStep {
+        size_t ci = 0;
+        int partner = -1;
+        size_t step = 0;
+        std::string key;
+        bool done = false;
+    };
+    std::vector<ChainStep> chain_steps;
     // "cmd <index> <shape key>" -> choice measured in the network (the shape key
     // keeps a cached choice from applying to the same command at another batch)
     std::map<std::string, ConvChoice> refined;
@@ -1190,8 +1203,8 @@ void load_tune_cache(AexrtYoloModel* m) {
         if (std::sscanf(line.c_str() + tab + 1, "%d %d %d %d %d %d %d %d", &c.kind, &c.jn, &c.pw, &c.ksw, &c.tr,
                         &c.tc, &c.cc, &c.nw) != 8)
             continue;
-        if (line.compare(0, 4, "cmd ") == 0)
-            m->refined[line.substr(0, tab)] = c;  // a conv's choice measured in the network
+        if (line.compare(0, 4, "cmd ") == 0 || line.compare(0, 10, "chain cmd ") == 0)
+            m->refined[line.substr(0, tab)] = c;  // a conv's (or a chain's tile) choice measured in the network
         else if (line.compare(0, 9, "schedule ") == 0)
             m->schedules[line.substr(0, tab)] =
                 Schedule{c.kind, c.jn, c.pw, (uint32_t)c.ksw, (uint32_t)c.tr, (uint32_t)c.tc,
@@ -1509,16 +1522,38 @@ bool build_chain_step(AexrtYoloModel* m, size_t ci, std::vector<bool>& done, boo
     const int ib = cs.chain_b, ic = cs.chain_c;
     std::string tail = " then cmd#" + std::to_string(e.src_cmd[ib]) + " then 1x1 cmd#" + std::to_string(e.src_cmd[ic]);
     std::vector<int> writes = {V[m->convs[ic].out_value].pl.root};
+    // the launch's tile: measured before (this load or the tune cache) when the
+    // kernel still offers it, else the largest that fits until measured
+    AexrtYoloModel::ChainStep rec;
+    rec.ci = ci;
+    rec.partner = partner;
+    rec.step = m->steps.size();
+    rec.key = "chain cmd " + std::to_string(ci) + " " + std::to_string(br0[0].N) + "x" + std::to_string(br0[0].C) +
+              "x" + std::to_string(br0[0].H) + "x" + std::to_string(br0[0].W) + (partner >= 0 ? " two" : " one");
+    cs.chain_tr = cs.chain_tc = 0;
+    auto rf = m->refined.find(rec.key);
+    if (rf != m->refined.end()) {
+        int tr[16], tc[16];
+        const int n = enumerate_chain_tiles(br0, partner >= 0 ? br1 : nullptr, tr, tc, 16);
+        for (int k = 0; k < n && !rec.done; ++k)
+            if (tr[k] == rf->second.tr && tc[k] == rf->second.tc) {
+                cs.chain_tr = tr[k];
+                cs.chain_tc = tc[k];
+                rec.done = true;
+            }
+    }
+    m->chain_steps.push_back(rec);
+    const ConvState* tile = &cs;
     if (partner >= 0) {
         const ConvState& ps = m->convs[partner];
         const std::array<ConvParams, 3> a0{br0[0], br0[1], br0[2]}, a1{br1[0], br1[1], br1[2]};
-        m->steps.push_back(Step{(int)ci, "", [a0, a1](hipStream_t s) {
-                                    return launch_conv_chain2(a0.data(), a1.data(), 0, 0, s);
+        m->steps.push_back(Step{(int)ci, "", [a0, a1, tile](hipStream_t s) {
+                                    return launch_conv_chain2(a0.data(), a1.data(), tile->chain_tr, tile->chain_tc, s);
                                 }});
-        m->steps.back().family = [a0, a1] {
+        m->steps.back().family = [a0, a1, tile] {
             LaunchProbe probe{};
             set_launch_probe(&probe);
-            (void)launch_conv_chain2(a0.data(), a1.data(), 0, 0, nullptr);
+            (void)launch_conv_chain2(a0.data(), a1.data(), tile->chain_tr, tile->chain_tc, nullptr);
             set_launch_probe(nullptr);
             return std::string(probe.name);
         };
@@ -1528,13 +1563,13 @@ bool build_chain_step(AexrtYoloModel* m, size_t ci, std::vector<bool>& done, boo
         done[partner] = done[ps.chain_b] = done[ps.chain_c] = true;
     } else {
         const std::array<ConvParams, 3> a0{br0[0], br0[1], br0[2]};
-        m->steps.push_back(Step{(int)ci, "", [a0](hipStream_t s) {
-                                    return launch_conv_chain(a0[0], a0[1], a0[2], 0, 0, s);
+        m->steps.push_back(Step{(int)ci, "", [a0, tile](hipStream_t s) {
+                                    return launch_conv_chain(a0[0], a0[1], a0[2], tile->chain_tr, tile->chain_tc, s);
                                 }});
-        m->steps.back().family = [a0] {
+        m->steps.back().family = [a0, tile] {
             LaunchProbe probe{};
             set_launch_probe(&probe);
-            (void)launch_conv_chain(a0[0], a0[1], a0[2], 0, 0, nullptr);
+            (void)launch_conv_chain(a0[0], a0[1], a0[2], tile->chain_tr, tile->chain_tc, nullptr);
             set_launch_probe(nullptr);
             return std::string(probe.name);
         };
@@ -1739,6 +1774,7 @@ bool build_steps(AexrtYoloModel* m, const std::vector<CopyJob>& copies) {
     Engine& e = m->eng;
     auto& V = m->vals;
     m->steps.clear();
+    m->chain_steps.clear();
     m->step_ms.clear();  // list scheduling measures the new steps again
     m->tunables.clear();
     setup_upsample_folds(m);
@@ -2300,7 +2336,10 @@ bool run_network(AexrtYoloModel* m, hipStream_t s) {
 // candidate with its shortest step.
 constexpr int kContextReps = 3;
 
-bool refine_in_context(AexrtYoloModel* m) {
+bool profiled_step_times(AexrtYoloModel* m, std::vector<float>& lo);
+bool choose_chain_tiles(AexrtYoloModel* m);
+
+bool refine_candidates(AexrtYoloModel* m) {
     size_t rounds = 0;
     for (const auto& t : m->tunables)
         if (!t->done && t->cands.size() > 1) rounds = std::max(rounds, t->cands.size());
@@ -2336,6 +2375,78 @@ bool refine_in_context(AexrtYoloModel* m) {
         if (m->tune_log)
             std::fprintf(stderr, "aexrt in-network %s: candidate %zu of %zu  %.2f us (first %.2f us)\n",
                          m->steps[t.step].label.c_str(), bi, t.cands.size(), ms[k][bi] * 1000.0f, ms[k][0] * 1000.0f);
+    }
+    label_steps(m);
+    drop_graph(m);
+    return true;
+}
+
+bool refine_in_context(AexrtYoloModel* m) { return refine_candidates(m) && choose_chain_tiles(m); }
+
+// The tile of each chain launch not measured yet: the tiles the kernel offers
+// for it (whole map, halves, thirds, 8x8 down to 3x3) timed in the network
+// like the conv candidates above (round r: every chain on its r-th tile, the
+// least of kContextReps event-profiled passes per step), the fastest kept.  A
+// small batch has few tiles of the whole map (one block per image and
+// branch), and smaller tiles spread the chain over more of the GPU at the cost
+// of recomputing their borders; a large batch keeps the large tiles.
+bool choose_chain_tiles(AexrtYoloModel* m) {
+    struct Todo {
+        size_t k;
+        std::vector<std::pair<int, int>> tiles;
+    };
+    std::vector<Todo> todo;
+    size_t rounds = 0;
+    for (size_t k = 0; k < m->chain_steps.size(); ++k) {
+        auto& c = m->chain_steps[k];
+        if (c.done) continue;
+        ConvParams br0[3], br1[3];
+        int tr[16], tc[16];
+        int n = 0;
+        if (chain_params_of(m, c.ci, br0) && (c.partner < 0 || chain_params_of(m, (size_t)c.partner, br1)))
+            n = enumerate_chain_tiles(br0, c.partner >= 0 ? br1 : nullptr, tr, tc, 16);
+        if (n <= 1) {
+            c.done = true;
+            continue;
+        }
+        Todo t{k, {}};
+        for (int i = 0; i < n; ++i) t.tiles.emplace_back(tr[i], tc[i]);
+        rounds = std::max(rounds, t.tiles.size());
+        todo.push_back(std::move(t));
+    }
+    if (todo.empty()) return true;
+    std::vector<std::vector<float>> ms(todo.size());
+    for (size_t r = 0; r < rounds; ++r) {
+        for (const Todo& t : todo) {
+            const auto& tile = t.tiles[std::min(r, t.tiles.size() - 1)];
+            ConvState& cs = m->convs[m->chain_steps[t.k].ci];
+            cs.chain_tr = tile.first;
+            cs.chain_tc = tile.second;
+        }
+        std::vector<float> lo;
+        if (!profiled_step_times(m, lo)) return false;
+        for (size_t i = 0; i < todo.size(); ++i) {
+            const size_t st = m->chain_steps[todo[i].k].step;
+            ms[i].push_back(st < lo.size() ? lo[st] : 1e30f);
+        }
+    }
+    for (size_t i = 0; i < todo.size(); ++i) {
+        auto& c = m->chain_steps[todo[i].k];
+        size_t bi = 0;
+        for (size_t r = 1; r < todo[i].tiles.size(); ++r)
+            if (ms[i][r] < ms[i][bi]) bi = r;
+        ConvState& cs = m->convs[c.ci];
+        cs.chain_tr = todo[i].tiles[bi].first;
+        cs.chain_tc = todo[i].tiles[bi].second;
+        c.done = true;
+        ConvChoice rec{};
+        rec.tr = cs.chain_tr;
+        rec.tc = cs.chain_tc;
+        m->refined[c.key] = rec;
+        if (m->tune_log)
+            std::fprintf(stderr, "aexrt chain tile of %s: %dx%d, %zu of %zu  %.2f us (largest %.2f us)\n",
+                         m->steps[c.step].label.c_str(), cs.chain_tr, cs.chain_tc, bi, todo[i].tiles.size(),
+                         ms[i][bi] * 1000.0f, ms[i][0] * 1000.0f);
     }
     label_steps(m);
     drop_graph(m);

@@ -198,7 +198,10 @@ BRANCHES = [(64, 64, 64), (80, 80, 80)]  # box (reg_max 16 x 4) and class (80) b
 def test_chain_accesses_stay_in_bounds_on_yolov8n_heads(imgsz, batch, kg):
     seen = 0
     for C, hw in HEADS[imgsz]:
-        for tile in [(0, 0), (hw, hw), ((hw + 1) // 2, hw), (8, 8), (6, 8), (5, 4)]:
+        # the rule's tile (0, 0), the tiles the load-time measurement tries (enumerate_chain_tiles),
+        # and a ragged one
+        for tile in [(0, 0), (hw, hw), ((hw + 1) // 2, hw), ((hw + 1) // 2, (hw + 1) // 2),
+                     ((hw + 2) // 3, (hw + 2) // 3), (8, 8), (6, 8), (5, 5), (4, 4), (3, 3), (5, 4)]:
             # the two-branch launch takes the tile that fits the branch with more channels
             t = chain_tile(C, hw, hw, max(chain_nq(*br) for br in BRANCHES), *tile)
             if t is None:

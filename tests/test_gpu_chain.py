@@ -33,6 +33,11 @@ CASES = [
     (2, 128, 20, 20, 64, 64, (10, 10), "f32", (80, 144, 144)),  # box outputs in a 144-channel tensor
     (1, 64, 40, 40, 80, 80, (8, 12), "f16", None),    # 140-position regions: two subtiles per wave
     (2, 64, 24, 24, 64, 64, (12, 12), "f32", None),   # 196 and 144 positions
+    # small tiles the load-time measurement offers (many blocks at batch 1, borders recomputed)
+    (1, 256, 10, 10, 80, 80, (5, 5), "f32", None),
+    (1, 256, 10, 10, 64, 64, (4, 4), "f32", None),    # ragged: tiles of 4, 4 and 2
+    (1, 128, 20, 20, 80, 80, (3, 3), "f32", None),    # 25-position regions, 9-position tiles
+    (1, 64, 40, 40, 64, 64, (14, 14), "f16", None),   # thirds of the map
 ]
 
 

@@ -117,6 +117,26 @@ def test_committed_plan_loads_runs_and_closes(stub, batch):
     assert not any(lab.endswith("RESIZE") for lab in convs)
 
 
+@pytest.mark.parametrize("batch", [1, 64])
+def test_committed_chain_tiles_are_applied(stub, batch):
+    """Each head chain launch runs the tile its plan line records ("chain cmd <command> <dims> one|two":
+    measured at load among the tiles the kernel offers)."""
+    tiles = {}
+    for key, fields in _plan_line("chain cmd "):
+        _, _, cmd, dims, form = key.split()
+        if int(dims.split("x")[0]) == batch:
+            f = fields.split()
+            tiles[(int(cmd), form)] = (int(f[4]), int(f[5]))
+    res = _run({"batch": batch})
+    chains = [lab for lab in _conv_labels(res) if "conv_chain" in lab]
+    assert chains
+    for lab in chains:
+        cmd = int(lab.split()[0][len("cmd#"):])
+        form = "two" if "conv_chain2_kernel" in lab else "one"
+        tr, tc = tiles[(cmd, form)]
+        assert f"> {tr}x{tc} then" in lab, (lab, tr, tc)
+
+
 def test_upsample_fold_forms(stub):
     res = _run({"batch": 64, "env": {"AEXRT_HIP_FOLD_UPSAMPLE": "0"}})
     convs = _conv_labels(res)
