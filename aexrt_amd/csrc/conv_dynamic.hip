@@ -47,12 +47,16 @@ __global__ __launch_bounds__(kDynThreads) void conv_int8_dynamic_kernel(DynConvP
     const int pad = p.K == 3 ? 1 : 0;
     const __half* xn = p.x + (int64_t)n * p.x_nstride;
     for (int g = threadIdx.x; g < G; g += blockDim.x) {
+        // the taps' values in registers: loops over the largest tap count with
+        // constant indices (a runtime-indexed array would live in scratch memory)
         float v[9][4];
         float am = 0.0f;
-        for (int t = 0; t < taps; ++t) {
+#pragma unroll
+        for (int t = 0; t < 9; ++t) {
             const int iy = oh * p.S + t / p.K - pad;
             const int ix = ow * p.S + t % p.K - pad;
-            const bool in = iy >= 0 && iy < p.H && ix >= 0 && ix < p.W;
+            const bool in = t < taps && iy >= 0 && iy < p.H && ix >= 0 && ix < p.W;
+#pragma unroll
             for (int c = 0; c < 4; ++c) {
                 const float val = in ? __half2float(xn[(int64_t)(iy * p.W + ix) * p.x_cstride + g * 4 + c]) : 0.0f;
                 v[t][c] = val;
@@ -61,7 +65,9 @@ __global__ __launch_bounds__(kDynThreads) void conv_int8_dynamic_kernel(DynConvP
         }
         const float s = am > 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
         l_inv[g] = __fdiv_rn(am, 127.0f);
-        for (int t = 0; t < taps; ++t) l_q[t * G + g] = pack4_q(v[t][0], v[t][1], v[t][2], v[t][3], s);
+#pragma unroll
+        for (int t = 0; t < 9; ++t)
+            if (t < taps) l_q[t * G + g] = pack4_q(v[t][0], v[t][1], v[t][2], v[t][3], s);
     }
     __syncthreads();
     const bool out_f32 = (p.flags & kConvOutF32) != 0;

@@ -198,6 +198,11 @@ int enumerate_halo_choices(const ConvParams& p, bool int8, ConvChoice* out, int 
              jn = jn == 4 ? 5 : jn << 1) {
             if (jn == 5 && ocj != 5) continue;
             for (int pw = nchw ? 2 : 1; pw <= (nw == 8 ? 2 : 4) && n < cap; pw <<= 1) {
+                // fp16 tiles of 4-5 channel subtiles with 2 or more position
+                // subtiles per wave need more than 256 registers and spill to
+                // scratch memory (slow, and a first launch has to grow the
+                // queue's scratch): not offered
+                if (!int8 && jn >= 4 && pw >= (nchw ? 4 : 2)) continue;
                 const int npos = 16 * nw * pw;  // positions of a tile
                 const int tcs[7] = {p.OW, ow4, 16, 32, 48, 64, 80};
                 for (int i = 0; i < 7 && n < cap; ++i) {
