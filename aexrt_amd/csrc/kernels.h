@@ -60,7 +60,10 @@ enum Loader : int {
 
 // Kernel and tile of one conv launch.  kind 0: chosen by the heuristics;
 // 1: implicit GEMM with tile (jn, pw, ksw); 2: halo-tile 3x3 with (jn, pw),
-// tr x tc positions, cc channels per chunk and nw waves per block.
+// tr x tc positions, cc channels per chunk and nw waves per block; 5: the
+// 32x32-MFMA 3x3 with nq = jn, mq = pw, the halo fields and its wave groups
+// minus one in ksw; 6: the streaming 1x1 with jq = jn, pq = pw and one tile
+// per block (ksw).
 struct ConvChoice {
     int kind = 0;
     int jn = 0, pw = 0, ksw = 0;
