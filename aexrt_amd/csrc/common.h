@@ -35,6 +35,17 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// A 16-byte MFMA operand gathered across the wave's two lane halves: every
+// lane passes two dword pairs x and y; lane l < 32 gets {x of lane l, x of
+// lane l + 32} and lane l + 32 gets {y of lane l, y of lane l + 32}.
+// v_permlane32_swap exchanges the upper 32 lanes of its first operand with
+// the lower 32 lanes of its second (a VALU op, no LDS round trip).
+__device__ __forceinline__ v4i half_swap_operand(const uint32_t (&x)[2], const uint32_t (&y)[2]) {
+    const auto a = __builtin_amdgcn_permlane32_swap(x[0], y[0], false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(x[1], y[1], false, false);
+    return v4i{(int)a[0], (int)b[0], (int)a[1], (int)b[1]};
+}
+
 // Max of the slot bit patterns over a wave: slots order as unsigned integers
 // (a NaN pattern wins over every finite value, as in the atomicMax producers).
 __device__ __forceinline__ uint32_t wave_umax(uint32_t v) {

@@ -442,14 +442,7 @@ __device__ __forceinline__ void chain_block(const ChainParams& h, int blk, uint8
                 __builtin_memcpy(&h2[j4][1], &x1, 4);
             }
 #pragma unroll
-            for (int m = 0; m < 2; ++m) {
-                const uint32_t s0 = hi ? h2[2 * m][0] : h2[2 * m + 1][0];
-                const uint32_t s1 = hi ? h2[2 * m][1] : h2[2 * m + 1][1];
-                const uint32_t r0 = (uint32_t)__shfl_xor((int)s0, 32, 64);
-                const uint32_t r1 = (uint32_t)__shfl_xor((int)s1, 32, 64);
-                b2[2 * j + m] = hi ? v4i{(int)r0, (int)r1, (int)h2[2 * m + 1][0], (int)h2[2 * m + 1][1]}
-                                   : v4i{(int)h2[2 * m][0], (int)h2[2 * m][1], (int)r0, (int)r1};
-            }
+            for (int m = 0; m < 2; ++m) b2[2 * j + m] = half_swap_operand(h2[2 * m], h2[2 * m + 1]);
         }
 #pragma unroll
         for (int j2 = 0; j2 < NQ; ++j2) {
