@@ -1543,6 +1543,8 @@ bool build_chain_step(AexrtYoloModel* m, size_t ci, std::vector<bool>& done, boo
             }
     }
     m->chain_steps.push_back(rec);
+    // the launch reads the tile when it runs, so a tile measured later applies
+    // (m->convs is sized once at load: the pointer stays valid)
     const ConvState* tile = &cs;
     if (partner >= 0) {
         const ConvState& ps = m->convs[partner];
