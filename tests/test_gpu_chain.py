@@ -41,6 +41,22 @@ CASES = [
 ]
 
 
+# the cases of the two-group blocks (two groups of four waves splitting each chunk's k steps):
+# one block subtile per wave and a window of at least 16 KB
+KG2_CASES = [t for t in CASES if t[1] >= 128]
+
+
+@pytest.mark.skip(reason="two-group chain blocks (KG = 2) switched off: a model load that ran them "
+                         "aborted and no cause was shown; the library launches one group only")
+@pytest.mark.parametrize("case", KG2_CASES, ids=[f"c{t[1]}_{t[2]}x{t[3]}_b{t[4]}_o{t[5]}_t{t[6][0]}x{t[6][1]}"
+                                                 for t in KG2_CASES])
+def test_chain_two_k_groups_matches_three_convs(cuda, case):
+    """Kept skipped while the path is off.  No hook selects the two-group blocks, so the test
+    fails rather than re-test the one-group form: a hook that selects them, and a check of the
+    launched instance's name, come back with the path."""
+    pytest.fail("no hook selects the two-group chain blocks")
+
+
 @pytest.mark.parametrize("case", CASES, ids=[f"c{t[1]}_{t[2]}x{t[3]}_b{t[4]}_o{t[5]}_t{t[6][0]}x{t[6][1]}_{t[7]}"
                                              f"{'_slice' if t[8] else ''}" for t in CASES])
 def test_chain_matches_three_convs(cuda, case):
