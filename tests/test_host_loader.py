@@ -50,6 +50,11 @@ if spec.get("model") == "c2f":
     g = WL.c2f_block(batch=1, c=128, dim=40, seed=3)
     model = NativeHipYoloModel(E.build_aexrt_engine(g, precision="fp16"))
     model.run(np.zeros((1, 128, 40, 40), np.float32))
+elif spec.get("model") == "yolo160_concat_fp16":
+    from aexrt_amd.yolov8 import build_yolov8n
+    g = build_yolov8n(batch=1, imgsz=160, seed=4)
+    model = NativeHipYoloModel(E.build_aexrt_engine(g, precision="fp16", classes=80, fuse_concat_min_h=-1))
+    model.run(np.zeros((1, 3, 160, 160), np.float32))
 else:
     g, model, _ = bench.build_model(spec["batch"])
     bench.fill_input(model, spec["batch"], 320)
@@ -189,6 +194,16 @@ def test_forced_superblocks_build_one_launch_per_bottleneck(stub):
     assert fp16["superblocks"] == 2
 
 
+def test_yolov8n_160_fused_concat_fp16_load_time_tuning(stub, tmp_path):
+    """The load of the fp16 YOLOv8n-160 engine with its 13 fused concat + 1x1 commands, measuring
+    every fp16 candidate at load (the GPU test of this engine is skipped: one of its loads aborted
+    on the GPU with no cause shown); here, and under ASan below, it completes."""
+    plan = tmp_path / "plan.tune"
+    res = _run({"model": "yolo160_concat_fp16", "plan": str(plan)})
+    assert plan.exists() and "schedule 1x3x160x160" in plan.read_text()
+    assert len(_conv_labels(res)) > 50
+
+
 def _asan_current():
     return ASAN_LIB.exists() and LIB.exists() and ASAN_LIB.stat().st_mtime >= LIB.stat().st_mtime
 
@@ -198,4 +213,5 @@ def _asan_current():
 def test_host_paths_under_address_sanitizer(stub, tmp_path):
     _run({"batch": 64}, asan=True)
     _run({"batch": 1, "plan": str(tmp_path / "plan.tune")}, asan=True)  # load-time tuning (bs 1: quicker)
+    _run({"model": "yolo160_concat_fp16", "plan": str(tmp_path / "plan160.tune")}, asan=True)
     _run({"batch": 64, "env": {"AEXRT_HIP_C2F_SUPERBLOCK": "1"}}, asan=True)
